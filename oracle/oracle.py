@@ -1,0 +1,298 @@
+"""ctypes wrapper over the CPU oracle (oracle/gossmx_oracle.cpp).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, always as the checker. The product package never
+imports this module.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libgossmx_oracle.so")
+
+# numpy views of the reference's Q8Block / ResidualQ8Block (lib.rs:732-742):
+# f32 scale + 32 x i8 values, 36 bytes, no padding.
+Q8_DTYPE = np.dtype([("scale", "<f4"), ("values", "i1", (32,))])
+RQ8_DTYPE = np.dtype([("primary", Q8_DTYPE), ("residual", Q8_DTYPE)])
+assert Q8_DTYPE.itemsize == 36 and RQ8_DTYPE.itemsize == 72
+
+OK = 0
+INVALID_DIMENSIONS = 3
+NON_FINITE_INPUT = 4
+NON_FINITE_LOGITS = 8
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+class OracleLayer(C.Structure):
+    _fields_ = [
+        ("router_weight", C.c_void_p), ("router_bias", C.c_void_p),
+        ("gate_up", C.c_void_p), ("gate_up_bias", C.c_void_p),
+        ("down", C.c_void_p), ("down_bias", C.c_void_p),
+        ("experts", C.c_size_t), ("hidden", C.c_size_t), ("intermediate", C.c_size_t), ("top_k", C.c_size_t),
+        ("alpha", C.c_float), ("limit", C.c_float),
+    ]
+
+
+def _declare(L):
+    vp, sz, i32, u32, f32, u64 = C.c_void_p, C.c_size_t, C.c_int, C.c_uint32, C.c_float, C.c_uint64
+    sig = {
+        "oracle_bf16_bits": (C.c_uint16, [f32]),
+        "oracle_e8m0_scale": (f32, [C.c_uint8]),
+        "oracle_decode_mxfp4": (f32, [C.c_uint8]),
+        "oracle_mxfp4_integer": (C.c_int32, [C.c_uint8]),
+        "oracle_expf_glibc": (f32, [f32]),
+        "oracle_expf_restated": (f32, [f32]),
+        "oracle_adjacent_to_split": (None, [vp, vp]),
+        "oracle_split_to_adjacent": (None, [vp, vp]),
+        "oracle_expf_check": (u64, [u32, u32, i32, C.POINTER(u32)]),
+        "oracle_quantize_residual_q8": (i32, [vp, sz, vp]),
+        "oracle_quantize_q8": (i32, [vp, sz, vp]),
+        "oracle_block_dots": (None, [vp, sz, sz, vp, vp]),
+        "oracle_mxfp4_matmul": (i32, [vp, sz, sz, sz, i32, i32, vp, sz, sz, sz, sz, vp, sz, vp, sz, sz]),
+        "oracle_mxfp4_matmul_auto": (i32, [vp, sz, sz, i32, vp, sz, vp, vp, sz, i32]),
+        "oracle_has_avx2": (i32, []),
+        "oracle_bench_weights": (None, [sz, sz, vp]),
+        "oracle_bench_residual": (None, [sz, sz, vp]),
+        "oracle_bench_bias": (None, [sz, vp]),
+        "oracle_pack_x8": (None, [vp, sz, sz, vp]),
+        "oracle_bf16_matvec": (None, [vp, sz, sz, vp, vp]),
+        "oracle_rms_norm": (None, [vp, vp, sz, f32, vp]),
+        "oracle_swiglu": (i32, [vp, sz, f32, f32, vp]),
+        "oracle_stable_top_k": (None, [vp, sz, sz, vp]),
+        "oracle_softmax": (None, [vp, sz, vp]),
+        "oracle_moe_batch": (i32, [C.POINTER(OracleLayer), vp, sz, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32]),
+        "oracle_stream_hash": (u64, [u64, u64, u64]),
+        "oracle_gen_mxfp4": (None, [u64, u64, sz, sz, sz, vp]),
+        "oracle_gen_bf16_normal": (None, [u64, u64, sz, f32, f32, vp]),
+        "oracle_gen_hidden": (None, [u64, u64, sz, sz, i32, vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+# ---------------------------------------------------------------------------
+# Thin numpy helpers.
+
+def bf16_bits(x: float) -> int:
+    return lib().oracle_bf16_bits(float(x))
+
+
+def bf16_round_array(a: np.ndarray) -> np.ndarray:
+    """Vectorised half-2.7.1 bf16 round trip (RNE, NaN quieted)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    rb = 0x8000
+    up = ((u & rb) != 0) & ((u & (3 * rb - 1)) != 0)
+    hi = (u >> 16) + up.astype(np.uint64)
+    hi = np.where(nan, (u >> 16) | 0x40, hi)
+    return ((hi & 0xFFFF) << 16).astype(np.uint32).view(np.float32)
+
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def quantize_residual_q8(x: np.ndarray):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.size // 32, dtype=RQ8_DTYPE)
+    st = lib().oracle_quantize_residual_q8(_p(x), x.size, _p(out))
+    return st, out
+
+
+def quantize_q8(x: np.ndarray):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.size // 32, dtype=Q8_DTYPE)
+    st = lib().oracle_quantize_q8(_p(x), x.size, _p(out))
+    return st, out
+
+
+def bench_fixtures(n: int, blocks: int, m: int):
+    """mxfp4_matrix_bench.rs:524-597 fixtures: canonical, x8, residual, bias."""
+    L = lib()
+    canonical = np.zeros(n * blocks * 17, dtype=np.uint8)
+    L.oracle_bench_weights(n, blocks, _p(canonical))
+    x8 = np.zeros_like(canonical)
+    L.oracle_pack_x8(_p(canonical), n, blocks, _p(x8))
+    residual = np.zeros(m * blocks, dtype=RQ8_DTYPE)
+    L.oracle_bench_residual(m, blocks, _p(residual))
+    bias = np.zeros(n, dtype=np.float32)
+    L.oracle_bench_bias(n, _p(bias))
+    return canonical, x8, residual, bias
+
+
+def pack_x8(canonical: np.ndarray, rows: int, blocks: int) -> np.ndarray:
+    out = np.zeros_like(canonical)
+    lib().oracle_pack_x8(_p(canonical), rows, blocks, _p(out))
+    return out
+
+
+def mxfp4_matmul(data, rows, blocks, layout, act, m, bias, out_stride=None, kind=2, act_stride=None, out=None,
+                 act_bpr=None):
+    """Scalar Kernels::mxfp4_matmul; returns (status, output)."""
+    out_stride = rows if out_stride is None else out_stride
+    act_stride = blocks if act_stride is None else act_stride
+    act_bpr = blocks if act_bpr is None else act_bpr
+    if out is None:
+        out = np.full((m - 1) * out_stride + rows, np.nan, dtype=np.float32)
+    st = lib().oracle_mxfp4_matmul(_p(data), data.size, rows, blocks, layout, kind, _p(act), act.size, m, act_bpr,
+                                   act_stride, _p(bias), 0 if bias is None else bias.size, _p(out), out.size,
+                                   out_stride)
+    return st, out
+
+
+def mxfp4_matmul_auto(data_x8, rows, blocks, act, m, bias, threads=1):
+    out = np.full(m * rows, np.nan, dtype=np.float32)
+    lib().oracle_mxfp4_matmul_auto(_p(data_x8), rows, blocks, 2, _p(act), m, _p(bias), _p(out), rows, threads)
+    return out
+
+
+def block_dots(canonical, rows, blocks, act):
+    out = np.zeros(rows * blocks * 2, dtype=np.int32)
+    lib().oracle_block_dots(_p(canonical), rows, blocks, _p(act), _p(out))
+    return out.reshape(rows, blocks, 2)
+
+
+def gen_mxfp4(seed, stream, experts, rows, blocks):
+    out = np.zeros(experts * rows * blocks * 17, dtype=np.uint8)
+    lib().oracle_gen_mxfp4(seed, stream, experts, rows, blocks, _p(out))
+    return out
+
+
+def gen_bf16_normal(seed, stream, n, mean=0.0, std=1.0):
+    out = np.zeros(n, dtype=np.uint16)
+    lib().oracle_gen_bf16_normal(seed, stream, n, mean, std, _p(out))
+    return out
+
+
+def gen_hidden(seed, stream, m, h, normalise=True):
+    out = np.zeros(m * h, dtype=np.uint16)
+    lib().oracle_gen_hidden(seed, stream, m, h, 1 if normalise else 0, _p(out))
+    return out.reshape(m, h)
+
+
+def swiglu(gate_up, intermediate, alpha=1.702, limit=7.0):
+    g = np.ascontiguousarray(gate_up, dtype=np.float32)
+    out = np.zeros(intermediate, dtype=np.float32)
+    lib().oracle_swiglu(_p(g), intermediate, alpha, limit, _p(out))
+    return out
+
+
+def stable_top_k(v, k):
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    out = np.zeros(min(k, v.size), dtype=np.uint32)
+    lib().oracle_stable_top_k(_p(v), v.size, k, _p(out))
+    return out
+
+
+def softmax(v):
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    out = np.zeros_like(v)
+    lib().oracle_softmax(_p(v), v.size, _p(out))
+    return out
+
+
+class MoeLayerHost:
+    """Host copies of one MoE layer in the reference's tensor formats."""
+
+    def __init__(self, router_weight, router_bias, gate_up, gate_up_bias, down, down_bias, experts, hidden,
+                 intermediate, top_k=4, alpha=1.702, limit=7.0):
+        self.router_weight = np.ascontiguousarray(router_weight, dtype=np.uint16)
+        self.router_bias = np.ascontiguousarray(router_bias, dtype=np.float32)
+        self.gate_up = np.ascontiguousarray(gate_up, dtype=np.uint8)
+        self.gate_up_bias = np.ascontiguousarray(gate_up_bias, dtype=np.float32)
+        self.down = np.ascontiguousarray(down, dtype=np.uint8)
+        self.down_bias = np.ascontiguousarray(down_bias, dtype=np.float32)
+        self.experts, self.hidden, self.intermediate, self.top_k = experts, hidden, intermediate, top_k
+        self.alpha, self.limit = alpha, limit
+
+    def struct(self):
+        s = OracleLayer()
+        s.router_weight = self.router_weight.ctypes.data
+        s.router_bias = self.router_bias.ctypes.data
+        s.gate_up = self.gate_up.ctypes.data
+        s.gate_up_bias = self.gate_up_bias.ctypes.data
+        s.down = self.down.ctypes.data
+        s.down_bias = self.down_bias.ctypes.data
+        s.experts, s.hidden, s.intermediate, s.top_k = self.experts, self.hidden, self.intermediate, self.top_k
+        s.alpha, s.limit = self.alpha, self.limit
+        return s
+
+
+def moe_batch(layer: MoeLayerHost, x_bf16: np.ndarray, injected_logits=None, trace=False, auto_lane=False,
+              threads=1):
+    """CpuModel::moe_batch restated; returns a dict of outputs (or raises)."""
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    m = x.shape[0]
+    E, H, I, K = layer.experts, layer.hidden, layer.intermediate, layer.top_k
+    res = {
+        "router_logits": np.zeros((m, E), np.float32),
+        "selected": np.zeros((m, K), np.uint32),
+        "routing_weights": np.zeros((m, K), np.float32),
+        "output": np.zeros((m, H), np.float32),
+        "route_order": np.zeros(m * K, np.uint32),
+    }
+    if trace:
+        res["gate_up"] = np.zeros((m, K, 2 * I), np.float32)
+        res["swiglu"] = np.zeros((m, K, I), np.float32)
+        res["down"] = np.zeros((m, K, H), np.float32)
+    inj = None if injected_logits is None else np.ascontiguousarray(injected_logits, dtype=np.float32)
+    s = layer.struct()
+    st = lib().oracle_moe_batch(C.byref(s), _p(x), m, _p(inj), _p(res["router_logits"]), _p(res["selected"]),
+                                _p(res["routing_weights"]), _p(res["output"]), _p(res["route_order"]),
+                                _p(res.get("gate_up")), _p(res.get("swiglu")), _p(res.get("down")),
+                                1 if auto_lane else 0, threads)
+    res["status"] = st
+    return res
+
+
+def synthetic_layer(seed: int, layer: int, experts=32, hidden=2880, intermediate=2880, top_k=4,
+                    with_experts=True) -> MoeLayerHost:
+    """The config-0 layer distribution: router bf16 N(0, 0.02) plus bf16 bias,
+    MXFP4 codes uniform over 16 codes, E8M0 exponent uniform in [-8, -4],
+    expert biases bf16 N(0, 0.02). Streams are keyed by layer so any layer can
+    be regenerated independently (the GPU library uses the same MXFP4 streams).
+    """
+    base = 16 * layer
+    rw = gen_bf16_normal(seed, base + 0, experts * hidden, 0.0, 0.02)
+    rb = bf16_to_f32(gen_bf16_normal(seed, base + 1, experts, 0.0, 0.02))
+    gub = bf16_to_f32(gen_bf16_normal(seed, base + 2, experts * 2 * intermediate, 0.0, 0.02))
+    db = bf16_to_f32(gen_bf16_normal(seed, base + 3, experts * hidden, 0.0, 0.02))
+    if with_experts:
+        gu = gen_mxfp4(seed, base + 4, experts, 2 * intermediate, hidden // 32)
+        dn = gen_mxfp4(seed, base + 5, experts, hidden, intermediate // 32)
+    else:
+        gu = np.zeros(0, np.uint8)
+        dn = np.zeros(0, np.uint8)
+    return MoeLayerHost(rw, rb, gu, gub, dn, db, experts, hidden, intermediate, top_k)
+
+
+MXFP4_STREAM_GATE_UP = 4
+MXFP4_STREAM_DOWN = 5
