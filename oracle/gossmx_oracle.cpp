@@ -599,6 +599,19 @@ void oracle_pack_x8(const uint8_t* canonical, size_t rows, size_t blocks, uint8_
     }
 }
 
+// accumulate_mxfp4_bf16_block, lib.rs:932-945 (the exact-BF16 projection
+// lane contract); here it pins bf16_bits against the reference's lane-bit KAT.
+void oracle_accumulate_mxfp4_bf16_block(const uint8_t* record17, const uint16_t* activation, float* lanes16) {
+  const float scale = e8m0_scale(record17[0]);
+  for (int i = 0; i < kPacked; ++i) {
+    const uint8_t packed = record17[1 + i];
+    const float low = bf16_round(kE2M1[packed & 0x0f] * scale);
+    const float high = bf16_round(kE2M1[packed >> 4] * scale);
+    lanes16[(2 * i) % 16] += low * bf16_to_f32(activation[2 * i]);
+    lanes16[(2 * i + 1) % 16] += high * bf16_to_f32(activation[2 * i + 1]);
+  }
+}
+
 void oracle_bf16_matvec(const uint16_t* w, size_t rows, size_t cols, const uint16_t* x, float* out) {
   for (size_t r = 0; r < rows; ++r) out[r] = bf16_dot(w + r * cols, x, cols);
 }

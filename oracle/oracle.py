@@ -81,6 +81,7 @@ def _declare(L):
         "oracle_bench_bias": (None, [sz, vp]),
         "oracle_pack_x8": (None, [vp, sz, sz, vp]),
         "oracle_bf16_matvec": (None, [vp, sz, sz, vp, vp]),
+        "oracle_accumulate_mxfp4_bf16_block": (None, [vp, vp, vp]),
         "oracle_rms_norm": (None, [vp, vp, sz, f32, vp]),
         "oracle_swiglu": (i32, [vp, sz, f32, f32, vp]),
         "oracle_stable_top_k": (None, [vp, sz, sz, vp]),

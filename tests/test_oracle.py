@@ -1,0 +1,362 @@
+"""Pins the CPU oracle (oracle/gossmx_oracle.cpp) before anything is checked
+against it: the reference's golden SHA-256 vectors, its known-answer tests,
+closed forms, and brute force on tiny inputs. CPU only."""
+import ctypes as C
+import hashlib
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "mxfp4_matrix_hashes.json")
+LIBM = C.CDLL("libm.so.6")
+LIBM.sinf.restype = C.c_float
+LIBM.sinf.argtypes = [C.c_float]
+
+
+def f32(x):
+    return np.float32(x)
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a, dtype=np.float32).tobytes()).hexdigest()
+
+
+def golden_cases():
+    with open(GOLDEN) as fh:
+        return json.load(fh)["cases"]
+
+
+# --- golden vectors: mxfp4_matrix_bench.rs:166-372, evidence correctness[] ---
+
+@pytest.mark.parametrize("case", golden_cases(), ids=lambda c: f"{c['role']}-m{c['m']}")
+def test_matmul_golden_hash_canonical_and_x8(case):
+    n, m = case["n"], case["m"]
+    canonical, x8, res, bias = O.bench_fixtures(n, 90, m)
+    for data, layout in ((canonical, 1), (x8, 2)):
+        st, out = O.mxfp4_matmul(data, n, 90, layout, res, m, bias)
+        assert st == O.OK
+        assert sha(out) == case["sha256"]
+
+
+@pytest.mark.parametrize("case", golden_cases(), ids=lambda c: f"{c['role']}-m{c['m']}")
+def test_cpu_baseline_lanes_reproduce_golden_hash(case):
+    """The Auto lane (x8 AVX2 GEMV at M=1, scalar otherwise) and its all-cores
+    variant must be bit-identical to scalar before they are timed
+    (mxfp4_matrix_bench.rs:215-246)."""
+    n, m = case["n"], case["m"]
+    _, x8, res, bias = O.bench_fixtures(n, 90, m)
+    for threads in (1, 4):
+        out = O.mxfp4_matmul_auto(x8, n, 90, res, m, bias, threads=threads)
+        assert sha(out) == case["sha256"]
+
+
+# --- known-answer tests of crates/gpt-oss-cpu-kernels/src/lib.rs ---
+
+def test_e8m0_edges_kat():
+    # lib.rs:1716-1722
+    assert np.float32(O.lib().oracle_e8m0_scale(0)).view(np.uint32) == 0x00400000
+    for s in (1, 2, 126, 127, 128, 254):
+        assert np.float32(O.lib().oracle_e8m0_scale(s)).view(np.uint32) == s << 23
+    assert math.isnan(O.lib().oracle_e8m0_scale(0xFF))
+
+
+def test_all_codes_decode_and_doubled_integers():
+    # lib.rs:1561-1568 (MXFP4_VALUES, lib.rs:37-39) and mxfp4_integer (lib.rs:1067-1074)
+    values = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0]
+    for code, v in enumerate(values):
+        got = O.lib().oracle_decode_mxfp4(code)
+        assert np.float32(got).view(np.uint32) == np.float32(v).view(np.uint32)
+        assert O.lib().oracle_mxfp4_integer(code) == int(2 * v)
+
+
+def test_adjacent_split_round_trip_kat():
+    # lib.rs:1571-1583
+    adjacent = np.array([((2 * i) & 15) | (((2 * i + 1) & 15) << 4) for i in range(16)], np.uint8)
+    split = np.zeros(16, np.uint8)
+    O.lib().oracle_adjacent_to_split(O._p(adjacent), O._p(split))
+    for i, b in enumerate(split):
+        assert b & 15 == i and b >> 4 == i
+    back = np.zeros(16, np.uint8)
+    O.lib().oracle_split_to_adjacent(O._p(split), O._p(back))
+    assert (back == adjacent).all()
+
+
+def _q8(scale, values):
+    a = np.zeros(1, O.Q8_DTYPE)
+    a["scale"] = scale
+    a["values"][0] = values
+    return a
+
+
+def test_block_dot_official_scale_kat():
+    # lib.rs:1790-1806: scale 127, packed 0x11, q = 1 -> integer 32, float 16.0
+    rec = np.array([127] + [0x11] * 16, np.uint8)
+    act = _q8(1.0, [1] * 32)
+    st, out = O.mxfp4_matmul(rec, 1, 1, 1, act, 1, None, kind=1)
+    assert st == O.OK and out[0] == 16.0
+    ract = np.zeros(1, O.RQ8_DTYPE)
+    ract["primary"] = act[0]
+    dots = O.block_dots(rec, 1, 1, ract)
+    assert dots[0, 0, 0] == 32 and dots[0, 0, 1] == 0
+
+
+def test_fused_residual_dot_equals_two_dots_kat():
+    # lib.rs:1808-1832
+    rec = np.array([129] + [(i | ((15 - i) << 4)) for i in range(16)], np.uint8)
+    ract = np.zeros(1, O.RQ8_DTYPE)
+    ract["primary"]["scale"] = 0.125
+    ract["primary"]["values"][0] = [i - 16 for i in range(32)]
+    ract["residual"]["scale"] = 0.001
+    ract["residual"]["values"][0] = [31 - i for i in range(32)]
+    dots = O.block_dots(rec, 1, 1, ract)[0, 0]
+    w = [O.lib().oracle_mxfp4_integer(c) for i in range(16) for c in (rec[1 + i] & 15, rec[1 + i] >> 4)]
+    assert dots[0] == sum(int(a) * int(b) for a, b in zip(w, ract["primary"]["values"][0]))
+    assert dots[1] == sum(int(a) * int(b) for a, b in zip(w, ract["residual"]["values"][0]))
+
+
+def test_extreme_block_dot_closed_form():
+    # matmul.rs:1860-1866: 127 * 12 * 32 = 48,768 at the extremes.
+    rec = np.array([127] + [0x77] * 16, np.uint8)  # every code 7 -> 12
+    ract = np.zeros(1, O.RQ8_DTYPE)
+    ract["primary"]["values"][0] = [127] * 32
+    ract["residual"]["values"][0] = [-127] * 32
+    d = O.block_dots(rec, 1, 1, ract)[0, 0]
+    assert d[0] == 48768 and d[1] == -48768
+
+
+def test_invalid_scale_propagates_nan():
+    # lib.rs:1598-1635
+    rec = np.tile(np.array([0xFF] + [0x11] * 16, np.uint8), 8)
+    act = _q8(1.0, [1] * 32)
+    st, out = O.mxfp4_matmul(rec, 8, 1, 1, act, 1, np.zeros(8, np.float32), kind=1)
+    assert st == O.OK and np.isnan(out).all()
+    x8 = O.pack_x8(rec, 8, 1)
+    st, out = O.mxfp4_matmul(x8, 8, 1, 2, act, 1, np.zeros(8, np.float32), kind=1)
+    assert st == O.OK and np.isnan(out).all()
+
+
+def test_zero_block_quantization_is_stable():
+    # lib.rs:1724-1732, 1764-1775
+    st, q = O.quantize_q8(np.zeros(32, np.float32))
+    assert st == O.OK and q["scale"][0] == 0.0 and (q["values"][0] == 0).all()
+    st, r = O.quantize_residual_q8(np.zeros(32, np.float32))
+    assert st == O.OK
+    for part in ("primary", "residual"):
+        assert r[part]["scale"][0] == 0.0 and (r[part]["values"][0] == 0).all()
+
+
+def test_residual_q8_reconstructs_better_than_one_pass():
+    # lib.rs:1734-1762 (f32 arithmetic as in the Rust test; sinf from libm)
+    x = np.array([f32(LIBM.sinf(f32(i) * f32(0.731))) * f32(9.0) + f32(i) * f32(0.013) for i in range(32)],
+                 np.float32)
+    _, q = O.quantize_q8(x)
+    _, r = O.quantize_residual_q8(x)
+    e1 = np.abs(x - q["values"][0].astype(np.float32) * q["scale"][0]).sum()
+    e2 = np.abs(x - r["primary"]["values"][0].astype(np.float32) * r["primary"]["scale"][0]
+                - r["residual"]["values"][0].astype(np.float32) * r["residual"]["scale"][0]).sum()
+    assert e2 < e1 * 0.02
+
+
+@pytest.mark.parametrize("bad", [float("nan"), float("inf"), float("-inf")])
+def test_residual_q8_rejects_non_finite(bad):
+    # lib.rs:1777-1788
+    x = np.zeros(32, np.float32)
+    x[7] = bad
+    assert O.quantize_residual_q8(x)[0] == O.NON_FINITE_INPUT
+    assert O.quantize_q8(x)[0] == O.NON_FINITE_INPUT
+
+
+def test_quantize_closed_forms():
+    # quantize_q8_block (lib.rs:1051-1065): max 127 gives scale 1 and inverse 1,
+    # so values are rounded half away from zero (f32::round) and clamped.
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0
+    x[1], x[2], x[3], x[4] = 2.5, -2.5, 0.5, -0.49
+    _, q = O.quantize_q8(x)
+    assert q["scale"][0] == 1.0
+    assert list(q["values"][0][:5]) == [127, 3, -3, 1, 0]
+    # Exact multiples of a power-of-two scale reconstruct exactly and leave a
+    # zero residual.
+    k = np.arange(-16, 16, dtype=np.float32)
+    x = k * np.float32(127.0 / 16.0 / 127.0 * 4.0)
+    x[0] = -127 * np.float32(0.25)
+    _, r = O.quantize_residual_q8(x)
+    s = r["primary"]["scale"][0]
+    assert s == np.float32(0.25)
+    assert (r["primary"]["values"][0].astype(np.float32) * s == x).all()
+    assert r["residual"]["scale"][0] == 0.0
+
+
+def test_exact_bf16_lane_bits_kat():
+    # lib.rs:1834-1856: pins bf16 round-to-nearest-even (half 2.7.1).
+    rec = np.array([124, 0x75, 0x31, 0xED, 0xA6, 0x42, 0xF9, 0x8B, 0xC4, 0x17, 0x5E, 0x20, 0xDA, 0x63, 0xBF,
+                    0x94, 0x28], np.uint8)
+    act = np.array([O.bf16_bits(f32(LIBM.sinf((f32(i) - f32(15.5)) * f32(0.137))) * f32(2.25))
+                    for i in range(32)], np.uint16)
+    lanes = np.zeros(16, np.float32)
+    O.lib().oracle_accumulate_mxfp4_bf16_block(O._p(rec), O._p(act), O._p(lanes))
+    assert list(lanes.view(np.uint32)) == [
+        3206160384, 3217183744, 3204644864, 3169845248, 1062731776, 1067950080, 3215392768,
+        3203301376, 1041563648, 1059454976, 3217698816, 1057914880, 1061216256, 3188326400,
+        3186294784, 1049509888]
+
+
+def test_bf16_rounding_ties_and_nan():
+    # half 2.7.1 from_f32: round to nearest, ties to even; NaN stays NaN.
+    assert O.bf16_bits(np.uint32(0x3F808000).view(np.float32)) == 0x3F80  # tie, even stays
+    assert O.bf16_bits(np.uint32(0x3F818000).view(np.float32)) == 0x3F82  # tie, odd rounds up
+    assert O.bf16_bits(np.uint32(0x3F808001).view(np.float32)) == 0x3F81
+    assert O.bf16_bits(np.uint32(0x7F7FFFFF).view(np.float32)) == 0x7F80  # rounds to +inf
+    assert (O.bf16_bits(float("nan")) & 0x7FC0) == 0x7FC0
+    v = np.random.default_rng(1).standard_normal(4096).astype(np.float32)
+    assert (O.bf16_round_array(v).view(np.uint32) >> 16 == np.array([O.bf16_bits(x) for x in v])).all()
+
+
+# --- cpu_runner.rs and gpt-oss-moe-semantics KATs ---
+
+def test_swiglu_kat():
+    # cpu_runner.rs:4406-4409
+    out = O.swiglu(np.array([2.0, 3.0, -1.0, 8.0], np.float32), 2)
+    assert list(out) == [7.75, -1.234375]
+
+
+def test_stable_top_k_kats():
+    # cpu_runner.rs:4412-4414 and moe-semantics/src/lib.rs:196-199
+    assert list(O.stable_top_k(np.array([1, 2, 2, 0], np.float32), 2)) == [1, 2]
+    assert list(O.stable_top_k(np.array([1, 1, 0.5, 1], np.float32), 2)) == [0, 1]
+
+
+def test_route_top_k_kats():
+    # gpu_layer.rs:3284-3291 and moe-semantics/src/lib.rs:229-240
+    v = np.array([1, 1, 0.5, 1], np.float32)
+    sel = O.stable_top_k(v, 2)
+    w = O.softmax(v[sel])
+    assert list(sel) == [0, 1] and list(w) == [0.5, 0.5]
+    v = np.array([0.0, 2.0, 1.0], np.float32)
+    sel = O.stable_top_k(v, 2)
+    w = O.softmax(v[sel])
+    assert list(sel) == [1, 2] and abs(float(w.sum()) - 1.0) < 1e-6
+    w = O.softmax(np.array([1.0, 2.0, 3.0], np.float32))
+    assert abs(float(w.sum()) - 1.0) < 1e-6
+
+
+def tiny_layer(seed=7, experts=3, hidden=64, intermediate=32, top_k=2):
+    return O.synthetic_layer(seed, 0, experts=experts, hidden=hidden, intermediate=intermediate, top_k=top_k)
+
+
+def test_route_grouping_order_kat():
+    # cpu_runner.rs:4417-4452: routes (2,0,0),(1,0,1),(2,1,0),(1,1,1) group to
+    # (1,0,1),(1,1,1),(2,0,0),(2,1,0). Injected logits rank expert 2 then 1.
+    layer = tiny_layer()
+    logits = np.array([[0.0, 1.0, 2.0], [0.0, 1.0, 2.0]], np.float32)
+    x = O.gen_hidden(3, 9, 2, 64)
+    r = O.moe_batch(layer, x, injected_logits=logits)
+    assert r["status"] == O.OK
+    assert [(int(o) // 2, int(o) % 2) for o in r["route_order"]] == [(0, 1), (1, 1), (0, 0), (1, 0)]
+    assert r["selected"].tolist() == [[2, 1], [2, 1]]
+
+
+# --- glibc expf restatement (the device expf follows the same algorithm) ---
+
+def test_expf_restatement_matches_glibc_on_every_float():
+    first = C.c_uint32()
+    bad = O.lib().oracle_expf_check(0, 0xFFFFFFFF, 8, C.byref(first))
+    assert bad == 0, f"first mismatch at bits {first.value:#010x}"
+
+
+# --- composition of moe_batch, checked piece by piece (cpu_runner.rs:2794-3013) ---
+
+def _moe_by_pieces(layer, x):
+    """moe_batch recomposed from separately pinned oracle pieces."""
+    E, H, I, K = layer.experts, layer.hidden, layer.intermediate, layer.top_k
+    m = x.shape[0]
+    lg = np.zeros((m, E), np.float32)
+    O.lib().oracle_bf16_matvec(O._p(layer.router_weight), E, H, O._p(np.ascontiguousarray(x[0])), O._p(lg[0]))
+    for r in range(m):
+        O.lib().oracle_bf16_matvec(O._p(layer.router_weight), E, H, O._p(np.ascontiguousarray(x[r])), O._p(lg[r]))
+    lg = O.bf16_round_array(lg + layer.router_bias[None, :])
+    out = np.zeros((m, H), np.float32)
+    sel_all, w_all = [], []
+    for r in range(m):
+        sel = O.stable_top_k(lg[r], K)
+        w = O.bf16_round_array(O.softmax(lg[r][sel]))
+        sel_all.append(sel)
+        w_all.append(w)
+        acc = np.zeros(H, np.float32)
+        for rank, e in enumerate(sel):
+            _, q = O.quantize_residual_q8(O.bf16_to_f32(x[r]))
+            gu_w = layer.gate_up[e * 2 * I * (H // 32) * 17:(e + 1) * 2 * I * (H // 32) * 17]
+            _, gu = O.mxfp4_matmul(gu_w, 2 * I, H // 32, 1, q, 1, layer.gate_up_bias[e * 2 * I:(e + 1) * 2 * I])
+            a = O.bf16_round_array(O.swiglu(O.bf16_round_array(gu), I))
+            _, q2 = O.quantize_residual_q8(a)
+            dn_w = layer.down[e * H * (I // 32) * 17:(e + 1) * H * (I // 32) * 17]
+            _, y = O.mxfp4_matmul(dn_w, H, I // 32, 1, q2, 1, layer.down_bias[e * H:(e + 1) * H])
+            acc = acc + O.bf16_round_array(y) * w[rank]
+        out[r] = O.bf16_round_array(acc)
+    return lg, np.array(sel_all), np.array(w_all), out
+
+
+def test_moe_batch_equals_composition_of_pieces():
+    layer = tiny_layer(experts=4, hidden=96, intermediate=64, top_k=2)
+    x = O.gen_hidden(11, 1, 5, 96)
+    r = O.moe_batch(layer, x)
+    assert r["status"] == O.OK
+    lg, sel, w, out = _moe_by_pieces(layer, x)
+    assert (r["router_logits"].view(np.uint32) == lg.view(np.uint32)).all()
+    assert (r["selected"] == sel).all()
+    assert (r["routing_weights"].view(np.uint32) == w.view(np.uint32)).all()
+    assert (r["output"].view(np.uint32) == out.view(np.uint32)).all()
+
+
+def test_router_dot_is_exact_on_exact_inputs():
+    # With small-integer bf16 operands every product and partial sum is exact,
+    # so any summation order gives the integer dot (scalar_bf16_dot,
+    # lib.rs:1007-1029).
+    rng = np.random.default_rng(5)
+    w = rng.integers(-8, 9, size=(3, 2880)).astype(np.float32)
+    x = rng.integers(-8, 9, size=2880).astype(np.float32)
+    wb = (w.view(np.uint32) >> 16).astype(np.uint16)
+    xb = (x.view(np.uint32) >> 16).astype(np.uint16)
+    out = np.zeros(3, np.float32)
+    O.lib().oracle_bf16_matvec(O._p(wb), 3, 2880, O._p(xb), O._p(out))
+    assert (out == (w.astype(np.int64) @ x.astype(np.int64)).astype(np.float32)).all()
+    # General inputs stay within a float64 error bound of the true dot.
+    wg = O.gen_bf16_normal(1, 2, 2880, 0.0, 0.02)
+    xg = O.gen_bf16_normal(1, 3, 2880)
+    O.lib().oracle_bf16_matvec(O._p(wg), 1, 2880, O._p(xg), O._p(out))
+    exact = float(O.bf16_to_f32(wg).astype(np.float64) @ O.bf16_to_f32(xg).astype(np.float64))
+    assert abs(out[0] - exact) < 1e-4
+
+
+def test_rms_norm_closed_form():
+    # lib.rs:699-730: a constant vector c normalises to c / sqrt(c^2 + eps).
+    x = np.full(2880, 2.0, np.float32)
+    out = np.zeros_like(x)
+    O.lib().oracle_rms_norm(O._p(x), O._p(np.ones_like(x)), 2880, np.float32(1e-5), O._p(out))
+    assert np.allclose(out, 2.0 / math.sqrt(4.0 + 1e-5), rtol=1e-6)
+
+
+def test_moe_one_hot_and_all_experts_invariants():
+    # top_k == experts: every expert is used once per row, weights sum ~ 1.
+    layer = tiny_layer(experts=3, hidden=64, intermediate=32, top_k=3)
+    x = O.gen_hidden(2, 4, 3, 64)
+    r = O.moe_batch(layer, x)
+    assert r["status"] == O.OK
+    for row in r["selected"]:
+        assert sorted(row.tolist()) == [0, 1, 2]
+    assert np.allclose(r["routing_weights"].sum(1), 1.0, atol=1e-2)
+    # Routing in rank order: logits of the selected experts are non-increasing.
+    for lg, sel in zip(r["router_logits"], r["selected"]):
+        assert (np.diff(lg[sel]) <= 0).all()
+
+
+def test_moe_rejects_non_finite_logits():
+    layer = tiny_layer()
+    x = O.gen_hidden(3, 9, 1, 64)
+    logits = np.array([[0.0, float("inf"), 1.0]], np.float32)
+    assert O.moe_batch(layer, x, injected_logits=logits)["status"] == O.NON_FINITE_LOGITS
