@@ -1,0 +1,750 @@
+// C ABI of libgossmx.so (include/gossmx.h): contexts, resident weights, the
+// kernel-boundary matmul and the MoE block, profiling and the fault hook.
+#include "../../include/gossmx.h"
+#include "gossmx_internal.h"
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+using namespace gossmx;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return status;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(e == hipErrorOutOfMemory ? GOSSMX_ERR_OUT_OF_MEMORY : GOSSMX_ERR_DEVICE, "%s: %s", what,
+              hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                   \
+  do {                                        \
+    hipError_t e_ = (expr);                   \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+// A grow-only device buffer.
+struct DevBuf {
+  void* p = nullptr;
+  size_t cap = 0;
+};
+
+struct ProfileMark {
+  int op;
+  hipEvent_t start, stop;
+};
+
+}  // namespace
+
+struct gossmx_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool own_stream = false;
+  int* err = nullptr;  // device error flags
+  bool fault_armed = false;
+  bool profiling = false;
+  std::vector<ProfileMark> marks;
+  std::vector<hipEvent_t> event_pool;
+  double op_ms[GOSSMX_OP_COUNT] = {0};
+  uint64_t op_launches[GOSSMX_OP_COUNT] = {0};
+  // scratch
+  DevBuf x, injected, logits, selected, weights, act1v, act1s, bucket, route_tok, route_slot, work, act2v, act2s, y,
+      out, trace, rec, bias, mout;
+};
+
+struct gossmx_weights {
+  gossmx_ctx* ctx = nullptr;
+  int device = 0;
+  TiledWeights t;
+};
+
+struct gossmx_layer {
+  gossmx_moe_config cfg;
+  const gossmx_weights* gate_up = nullptr;
+  const gossmx_weights* down = nullptr;
+  uint16_t* router_w = nullptr;
+  float* router_b = nullptr;
+  float* gate_up_bias = nullptr;
+  float* down_bias = nullptr;
+};
+
+namespace {
+
+int ensure(gossmx_ctx* ctx, DevBuf& b, size_t bytes) {
+  if (bytes <= b.cap) return GOSSMX_OK;
+  if (b.p) {
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    HIP_TRY(hipFree(b.p), "hipFree");
+    b.p = nullptr;
+    b.cap = 0;
+  }
+  const size_t cap = std::max<size_t>(bytes, 256) * 5 / 4;
+  HIP_TRY(hipMalloc(&b.p, cap), "hipMalloc(scratch)");
+  b.cap = cap;
+  return GOSSMX_OK;
+}
+
+hipEvent_t take_event(gossmx_ctx* ctx) {
+  if (!ctx->event_pool.empty()) {
+    hipEvent_t e = ctx->event_pool.back();
+    ctx->event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Brackets one launch with events when profiling is on.
+struct OpScope {
+  gossmx_ctx* ctx;
+  int op;
+  hipEvent_t start = nullptr;
+  OpScope(gossmx_ctx* c, int o) : ctx(c), op(o) {
+    if (ctx->profiling) {
+      start = take_event(ctx);
+      if (start) hipEventRecord(start, ctx->stream);
+    }
+  }
+  ~OpScope() {
+    if (start) {
+      hipEvent_t stop = take_event(ctx);
+      if (stop) {
+        hipEventRecord(stop, ctx->stream);
+        ctx->marks.push_back({op, start, stop});
+      } else {
+        ctx->event_pool.push_back(start);
+      }
+    }
+  }
+};
+
+int fold_profile(gossmx_ctx* ctx) {
+  if (ctx->marks.empty()) return GOSSMX_OK;
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  for (const ProfileMark& m : ctx->marks) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, m.start, m.stop) == hipSuccess) {
+      ctx->op_ms[m.op] += ms;
+      ctx->op_launches[m.op] += 1;
+    }
+    ctx->event_pool.push_back(m.start);
+    ctx->event_pool.push_back(m.stop);
+  }
+  ctx->marks.clear();
+  return GOSSMX_OK;
+}
+
+// Reads and clears the sticky device error flags (synchronizes).
+int check_device_errors(gossmx_ctx* ctx) {
+  int flags = 0;
+  HIP_TRY(hipMemcpyAsync(&flags, ctx->err, sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "read error flags");
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  if (flags == 0) return GOSSMX_OK;
+  HIP_TRY(launch_clear_ints(ctx->err, 1, ctx->stream), "clear error flags");
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  if (flags & kErrNonFiniteLogits) return fail(GOSSMX_ERR_NON_FINITE_LOGITS, "router produced non-finite logits");
+  return fail(GOSSMX_ERR_NON_FINITE_INPUT, "kernel input contains a non-finite value");
+}
+
+int set_device(int device) {
+  HIP_TRY(hipSetDevice(device), "hipSetDevice");
+  return GOSSMX_OK;
+}
+
+TiledWeights make_tiled(size_t experts, size_t rows, size_t blocks) {
+  TiledWeights t;
+  t.experts = experts;
+  t.rows = rows;
+  t.blocks = blocks;
+  t.tiles = (rows + kTileRows - 1) / kTileRows;
+  t.nib_stride = t.tiles * 256 * blocks;
+  t.scl_stride = t.tiles * 16 * blocks;
+  return t;
+}
+
+int alloc_tiled(gossmx_ctx* ctx, size_t experts, size_t rows, size_t blocks, gossmx_weights** out) {
+  if (!ctx || !out) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context or output handle");
+  if (experts == 0 || rows == 0 || blocks == 0)
+    return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "invalid MXFP4 tensor shape [%zu, %zu, %zu]", experts, rows, blocks);
+  if (int s = set_device(ctx->device)) return s;
+  auto* w = new gossmx_weights();
+  w->ctx = ctx;
+  w->device = ctx->device;
+  w->t = make_tiled(experts, rows, blocks);
+  hipError_t e = hipMalloc(&w->t.nib, experts * w->t.nib_stride);
+  if (e == hipSuccess) e = hipMalloc(&w->t.scl, experts * w->t.scl_stride);
+  if (e != hipSuccess) {
+    if (w->t.nib) hipFree(w->t.nib);
+    delete w;
+    return hip_fail(e, "hipMalloc(weights)");
+  }
+  hipError_t f = launch_fill_tiled_padding(w->t, ctx->stream);
+  if (f != hipSuccess) {
+    hipFree(w->t.nib);
+    hipFree(w->t.scl);
+    delete w;
+    return hip_fail(f, "padding fill");
+  }
+  *out = w;
+  return GOSSMX_OK;
+}
+
+// Mxfp4MatmulProblem::new + validate_activation_extent (matmul.rs:245-267,
+// 339-369) and the view checks of Mxfp4MatrixView::new (lib.rs:774-796).
+int validate_problem(const gossmx_matmul_problem* p, size_t rows, size_t blocks, size_t experts) {
+  if (!p) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null problem");
+  if (p->activation_kind != GOSSMX_ACT_Q8 && p->activation_kind != GOSSMX_ACT_RESIDUAL_Q8)
+    return fail(GOSSMX_ERR_INVALID_ARGUMENT, "unknown activation kind %d", p->activation_kind);
+  if (p->memory != GOSSMX_MEM_HOST && p->memory != GOSSMX_MEM_DEVICE)
+    return fail(GOSSMX_ERR_INVALID_ARGUMENT, "unknown memory kind %d", p->memory);
+  if (!p->activations || !p->output) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null activations or output");
+  if (p->expert >= experts) return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "expert %zu of %zu", p->expert, experts);
+  const size_t m = p->m;
+  if (m == 0 || p->blocks_per_row == 0 || p->row_stride < p->blocks_per_row ||
+      (m - 1) > (SIZE_MAX - p->blocks_per_row) / std::max<size_t>(p->row_stride, 1) ||
+      (m - 1) * p->row_stride + p->blocks_per_row > p->activations_len)
+    return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "invalid activation matrix view: rows=%zu, blocks=%zu, stride=%zu, len=%zu",
+                m, p->blocks_per_row, p->row_stride, p->activations_len);
+  if (p->blocks_per_row != blocks || p->output_stride < rows ||
+      (m - 1) > (SIZE_MAX - rows) / std::max<size_t>(p->output_stride, 1) ||
+      (m - 1) * p->output_stride + rows > p->output_len || (p->bias && p->bias_len != rows))
+    return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "invalid MXFP4 matmul: M=%zu, N=%zu, K=%zu, output_stride=%zu", m, rows,
+                blocks * kBlock, p->output_stride);
+  if (m > (size_t)INT32_MAX / 2 || rows > (size_t)INT32_MAX / 2)
+    return fail(GOSSMX_ERR_UNSUPPORTED, "matrix too large for this build");
+  return GOSSMX_OK;
+}
+
+}  // namespace
+
+// ===========================================================================
+extern "C" {
+
+const char* gossmx_last_error(void) { return g_last_error.c_str(); }
+int gossmx_version(void) { return 100; }
+
+int gossmx_device_count(int* count) {
+  if (!count) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null count");
+  *count = 0;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return GOSSMX_OK;
+  for (int d = 0; d < n; ++d) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, d) == hipSuccess && std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) ++*count;
+  }
+  return GOSSMX_OK;
+}
+
+int gossmx_ctx_create(int device, void* stream, gossmx_ctx** out) {
+  if (!out) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null output handle");
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n)
+    return fail(GOSSMX_ERR_UNAVAILABLE_BACKEND, "no HIP device %d", device);
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(GOSSMX_ERR_UNAVAILABLE_BACKEND, "device %d is %s, this build needs gfx950", device, prop.gcnArchName);
+  if (int s = set_device(device)) return s;
+  auto* ctx = new gossmx_ctx();
+  ctx->device = device;
+  if (stream) {
+    ctx->stream = static_cast<hipStream_t>(stream);
+  } else {
+    hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      delete ctx;
+      return hip_fail(e, "hipStreamCreate");
+    }
+    ctx->own_stream = true;
+  }
+  hipError_t e = hipMalloc(&ctx->err, 16);
+  if (e == hipSuccess) e = launch_clear_ints(ctx->err, 4, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    gossmx_ctx_destroy(ctx);
+    return hip_fail(e, "context setup");
+  }
+  *out = ctx;
+  return GOSSMX_OK;
+}
+
+void gossmx_ctx_destroy(gossmx_ctx* ctx) {
+  if (!ctx) return;
+  hipSetDevice(ctx->device);
+  if (ctx->stream) hipStreamSynchronize(ctx->stream);
+  for (auto& m : ctx->marks) {
+    hipEventDestroy(m.start);
+    hipEventDestroy(m.stop);
+  }
+  for (auto e : ctx->event_pool) hipEventDestroy(e);
+  DevBuf* bufs[] = {&ctx->x, &ctx->injected, &ctx->logits, &ctx->selected, &ctx->weights, &ctx->act1v,
+                    &ctx->act1s, &ctx->bucket, &ctx->route_tok, &ctx->route_slot, &ctx->work, &ctx->act2v,
+                    &ctx->act2s, &ctx->y, &ctx->out, &ctx->trace, &ctx->rec, &ctx->bias, &ctx->mout};
+  for (DevBuf* b : bufs)
+    if (b->p) hipFree(b->p);
+  if (ctx->err) hipFree(ctx->err);
+  if (ctx->own_stream && ctx->stream) hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+int gossmx_ctx_set_stream(gossmx_ctx* ctx, void* stream) {
+  if (!ctx || !stream) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context or stream");
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  if (int s = fold_profile(ctx)) return s;
+  if (ctx->own_stream) hipStreamDestroy(ctx->stream);
+  ctx->stream = static_cast<hipStream_t>(stream);
+  ctx->own_stream = false;
+  return GOSSMX_OK;
+}
+
+void* gossmx_ctx_stream(gossmx_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int gossmx_synchronize(gossmx_ctx* ctx) {
+  if (!ctx) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context");
+  if (int s = set_device(ctx->device)) return s;
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  return check_device_errors(ctx);
+}
+
+int gossmx_malloc(gossmx_ctx* ctx, size_t bytes, void** out) {
+  if (!ctx || !out) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+  if (int s = set_device(ctx->device)) return s;
+  HIP_TRY(hipMalloc(out, std::max<size_t>(bytes, 1)), "hipMalloc");
+  return GOSSMX_OK;
+}
+int gossmx_free(gossmx_ctx* ctx, void* ptr) {
+  if (!ctx) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context");
+  if (!ptr) return GOSSMX_OK;
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  HIP_TRY(hipFree(ptr), "hipFree");
+  return GOSSMX_OK;
+}
+int gossmx_memcpy_h2d(gossmx_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "hipMemcpy H2D");
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  return GOSSMX_OK;
+}
+int gossmx_memcpy_d2h(gossmx_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpy D2H");
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  return GOSSMX_OK;
+}
+
+// --- weights ---------------------------------------------------------------
+
+int gossmx_weights_upload(gossmx_ctx* ctx, const uint8_t* data, size_t len, size_t experts, size_t rows,
+                          size_t blocks, int layout, gossmx_weights** out) {
+  if (!ctx || !data || !out) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+  if (layout != GOSSMX_LAYOUT_CANONICAL_V1 && layout != GOSSMX_LAYOUT_X8_SPLIT_V2)
+    return fail(GOSSMX_ERR_INVALID_ARGUMENT, "unknown source layout %d", layout);
+  if (experts == 0 || rows == 0 || blocks == 0 || len != experts * rows * blocks * kRecord)
+    return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "invalid MXFP4 matrix view: rows=%zu, blocks=%zu, bytes=%zu", rows,
+                blocks, len);
+  gossmx_weights* w = nullptr;
+  if (int s = alloc_tiled(ctx, experts, rows, blocks, &w)) return s;
+  void* staging = nullptr;
+  hipError_t e = hipMalloc(&staging, len);
+  if (e == hipSuccess) e = hipMemcpyAsync(staging, data, len, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = launch_repack(static_cast<const uint8_t*>(staging), layout, w->t, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (staging) hipFree(staging);
+  if (e != hipSuccess) {
+    gossmx_weights_destroy(w);
+    return hip_fail(e, "weights upload");
+  }
+  *out = w;
+  return GOSSMX_OK;
+}
+
+int gossmx_weights_generate(gossmx_ctx* ctx, uint64_t seed, uint64_t stream, size_t experts, size_t rows,
+                            size_t blocks, gossmx_weights** out) {
+  gossmx_weights* w = nullptr;
+  if (int s = alloc_tiled(ctx, experts, rows, blocks, &w)) return s;
+  hipError_t e = launch_generate(seed, stream, w->t, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    gossmx_weights_destroy(w);
+    return hip_fail(e, "weights generate");
+  }
+  *out = w;
+  return GOSSMX_OK;
+}
+
+int gossmx_weights_export(gossmx_ctx* ctx, const gossmx_weights* w, uint8_t* out, size_t len) {
+  if (!ctx || !w || !out) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+  const size_t need = w->t.experts * w->t.rows * w->t.blocks * kRecord;
+  if (len != need) return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "export needs %zu bytes, got %zu", need, len);
+  if (int s = set_device(ctx->device)) return s;
+  void* dev = nullptr;
+  HIP_TRY(hipMalloc(&dev, len), "hipMalloc(export)");
+  hipError_t e = launch_export(w->t, static_cast<uint8_t*>(dev), ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(out, dev, len, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  hipFree(dev);
+  if (e != hipSuccess) return hip_fail(e, "weights export");
+  return GOSSMX_OK;
+}
+
+int gossmx_weights_shape(const gossmx_weights* w, size_t* experts, size_t* rows, size_t* blocks) {
+  if (!w) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null weights");
+  if (experts) *experts = w->t.experts;
+  if (rows) *rows = w->t.rows;
+  if (blocks) *blocks = w->t.blocks;
+  return GOSSMX_OK;
+}
+
+size_t gossmx_weights_device_bytes(const gossmx_weights* w) {
+  return w ? w->t.experts * (w->t.nib_stride + w->t.scl_stride) : 0;
+}
+
+void gossmx_weights_destroy(gossmx_weights* w) {
+  if (!w) return;
+  hipSetDevice(w->device);
+  if (w->ctx && w->ctx->stream) hipStreamSynchronize(w->ctx->stream);
+  if (w->t.nib) hipFree(w->t.nib);
+  if (w->t.scl) hipFree(w->t.scl);
+  delete w;
+}
+
+// --- kernel boundary ---------------------------------------------------------
+
+int gossmx_mxfp4_matmul_check(const gossmx_matmul_problem* p, size_t rows, size_t blocks, size_t experts) {
+  return validate_problem(p, rows, blocks, experts);
+}
+
+int gossmx_mxfp4_matmul(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
+  if (!ctx) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context");
+  if (!p || !p->weights) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null problem or weights");
+  const TiledWeights& w = p->weights->t;
+  if (int s = validate_problem(p, w.rows, w.blocks, w.experts)) return s;
+  if (ctx->fault_armed) {
+    ctx->fault_armed = false;
+    return fail(GOSSMX_ERR_INJECTED_FAULT, "injected fault before launch");
+  }
+  if (int s = set_device(ctx->device)) return s;
+  const size_t m = p->m, rows = w.rows, B = w.blocks;
+  const size_t rsz = p->activation_kind == GOSSMX_ACT_RESIDUAL_Q8 ? 72 : 36;
+  const size_t rec_count = (m - 1) * p->row_stride + B;
+  const uint8_t* rec = static_cast<const uint8_t*>(p->activations);
+  if (p->memory == GOSSMX_MEM_HOST) {
+    if (int s = ensure(ctx, ctx->rec, rec_count * rsz)) return s;
+    HIP_TRY(hipMemcpyAsync(ctx->rec.p, rec, rec_count * rsz, hipMemcpyHostToDevice, ctx->stream), "H2D activations");
+    rec = static_cast<const uint8_t*>(ctx->rec.p);
+  }
+  if (int s = ensure(ctx, ctx->act1v, m * B * 2 * kBlock * sizeof(_Float16))) return s;
+  if (int s = ensure(ctx, ctx->act1s, m * B * 2 * sizeof(float))) return s;
+  ActBuffers act{static_cast<_Float16*>(ctx->act1v.p), static_cast<float*>(ctx->act1s.p)};
+  HIP_TRY(launch_prep_records(rec, p->activation_kind, m, B, p->row_stride, act, ctx->err, ctx->stream),
+          "prepare activations");
+  const float* bias = p->bias;
+  if (bias && p->memory == GOSSMX_MEM_HOST) {
+    if (int s = ensure(ctx, ctx->bias, rows * sizeof(float))) return s;
+    HIP_TRY(hipMemcpyAsync(ctx->bias.p, p->bias, rows * sizeof(float), hipMemcpyHostToDevice, ctx->stream), "H2D bias");
+    bias = static_cast<const float*>(ctx->bias.p);
+  }
+  float* out = p->output;
+  size_t out_stride = p->output_stride;
+  if (p->memory == GOSSMX_MEM_HOST) {
+    if (int s = ensure(ctx, ctx->mout, m * rows * sizeof(float))) return s;
+    out = static_cast<float*>(ctx->mout.p);
+    out_stride = rows;
+  }
+  GemmArgs g{};
+  g.w = w;
+  g.actv = act.v;
+  g.acts = act.s;
+  g.bias = bias;
+  g.residual = p->activation_kind == GOSSMX_ACT_RESIDUAL_Q8 ? 1 : 0;
+  g.plain_expert = (int)p->expert;
+  g.plain_m = (int)m;
+  g.out = out;
+  g.out_stride = out_stride;
+  g.err = ctx->err;
+  g.bias_expert_stride = 0;  // this problem's single bias vector
+  {
+    OpScope scope(ctx, GOSSMX_OP_MATMUL);
+    HIP_TRY(launch_gemm(kPlain, g, (int)((m + kChunk - 1) / kChunk), ctx->stream), "matmul launch");
+  }
+  if (p->memory == GOSSMX_MEM_HOST) {
+    HIP_TRY(hipMemcpy2DAsync(p->output, p->output_stride * sizeof(float), out, rows * sizeof(float),
+                             rows * sizeof(float), m, hipMemcpyDeviceToHost, ctx->stream),
+            "D2H output");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  }
+  return GOSSMX_OK;
+}
+
+// --- MoE block -------------------------------------------------------------
+
+int gossmx_layer_create(gossmx_ctx* ctx, const gossmx_moe_config* cfg, const uint16_t* router_weight_bf16,
+                        const float* router_bias, const gossmx_weights* gate_up, const float* gate_up_bias,
+                        const gossmx_weights* down, const float* down_bias, gossmx_layer** out) {
+  if (!ctx || !cfg || !router_weight_bf16 || !router_bias || !gate_up || !gate_up_bias || !down || !down_bias || !out)
+    return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+  const size_t E = cfg->experts, H = cfg->hidden, I = cfg->intermediate, K = cfg->top_k;
+  if (E == 0 || E > (size_t)kMaxExperts || K == 0 || K > (size_t)kMaxTopK || K > E || H == 0 || I == 0 ||
+      H % kBlock || I % kBlock)
+    return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "invalid MoE config E=%zu H=%zu I=%zu K=%zu", E, H, I, K);
+  if (gate_up->t.experts != E || gate_up->t.rows != 2 * I || gate_up->t.blocks != H / kBlock ||
+      down->t.experts != E || down->t.rows != H || down->t.blocks != I / kBlock)
+    return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "expert tensors do not match [%zu, %zu, %zu] / [%zu, %zu, %zu]", E, 2 * I,
+                H / kBlock, E, H, I / kBlock);
+  if (int s = set_device(ctx->device)) return s;
+  auto* L = new gossmx_layer();
+  L->cfg = *cfg;
+  L->gate_up = gate_up;
+  L->down = down;
+  hipError_t e = hipMalloc(&L->router_w, E * H * 2);
+  if (e == hipSuccess) e = hipMalloc(&L->router_b, E * 4);
+  if (e == hipSuccess) e = hipMalloc(&L->gate_up_bias, E * 2 * I * 4);
+  if (e == hipSuccess) e = hipMalloc(&L->down_bias, E * H * 4);
+  if (e == hipSuccess) e = hipMemcpy(L->router_w, router_weight_bf16, E * H * 2, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(L->router_b, router_bias, E * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(L->gate_up_bias, gate_up_bias, E * 2 * I * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(L->down_bias, down_bias, E * H * 4, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    gossmx_layer_destroy(L);
+    return hip_fail(e, "layer upload");
+  }
+  *out = L;
+  return GOSSMX_OK;
+}
+
+void gossmx_layer_destroy(gossmx_layer* L) {
+  if (!L) return;
+  if (L->router_w) hipFree(L->router_w);
+  if (L->router_b) hipFree(L->router_b);
+  if (L->gate_up_bias) hipFree(L->gate_up_bias);
+  if (L->down_bias) hipFree(L->down_bias);
+  delete L;
+}
+
+int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_io* io) {
+  if (!ctx || !L || !io || !io->x || !io->output) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+  if (io->memory != GOSSMX_MEM_HOST && io->memory != GOSSMX_MEM_DEVICE)
+    return fail(GOSSMX_ERR_INVALID_ARGUMENT, "unknown memory kind %d", io->memory);
+  if (io->m == 0) return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "empty MoE batch");
+  const size_t m = io->m, E = L->cfg.experts, H = L->cfg.hidden, I = L->cfg.intermediate, K = L->cfg.top_k;
+  const size_t R = m * K, B1 = H / kBlock, B2 = I / kBlock;
+  if (m > (size_t)(INT32_MAX / 8) / std::max<size_t>(H, E)) return fail(GOSSMX_ERR_UNSUPPORTED, "batch too large");
+  if (ctx->fault_armed) {
+    ctx->fault_armed = false;
+    return fail(GOSSMX_ERR_INJECTED_FAULT, "injected fault before launch");
+  }
+  if (int s = set_device(ctx->device)) return s;
+  const bool host = io->memory == GOSSMX_MEM_HOST;
+  const size_t max_work = (R + kChunk - 1) / kChunk + std::min(E, R);
+
+  int s = GOSSMX_OK;
+  if ((s = ensure(ctx, ctx->logits, m * E * 4)) || (s = ensure(ctx, ctx->selected, R * 4)) ||
+      (s = ensure(ctx, ctx->weights, R * 4)) || (s = ensure(ctx, ctx->act1v, m * B1 * 2 * kBlock * 2)) ||
+      (s = ensure(ctx, ctx->act1s, m * B1 * 8)) || (s = ensure(ctx, ctx->bucket, (E + 1) * 4)) ||
+      (s = ensure(ctx, ctx->route_tok, R * 4)) || (s = ensure(ctx, ctx->route_slot, R * 4)) ||
+      (s = ensure(ctx, ctx->work, (2 * max_work + 1) * 4)) || (s = ensure(ctx, ctx->act2v, R * B2 * 2 * kBlock * 2)) ||
+      (s = ensure(ctx, ctx->act2s, R * B2 * 8)) || (s = ensure(ctx, ctx->y, R * H * 2)))
+    return s;
+  const uint16_t* x = io->x;
+  const float* injected = io->injected_logits;
+  float* output = io->output;
+  float* trace = io->trace_down;
+  float* logits = (!host && io->router_logits) ? io->router_logits : static_cast<float*>(ctx->logits.p);
+  if (host) {
+    if ((s = ensure(ctx, ctx->x, m * H * 2)) || (s = ensure(ctx, ctx->out, m * H * 4))) return s;
+    HIP_TRY(hipMemcpyAsync(ctx->x.p, io->x, m * H * 2, hipMemcpyHostToDevice, ctx->stream), "H2D x");
+    x = static_cast<const uint16_t*>(ctx->x.p);
+    if (injected) {
+      if ((s = ensure(ctx, ctx->injected, m * E * 4))) return s;
+      HIP_TRY(hipMemcpyAsync(ctx->injected.p, io->injected_logits, m * E * 4, hipMemcpyHostToDevice, ctx->stream),
+              "H2D logits");
+      injected = static_cast<const float*>(ctx->injected.p);
+    }
+    output = static_cast<float*>(ctx->out.p);
+    if (trace) {
+      if ((s = ensure(ctx, ctx->trace, R * H * 4))) return s;
+      trace = static_cast<float*>(ctx->trace.p);
+    }
+  }
+  int* selected = static_cast<int*>(ctx->selected.p);
+  float* weights = static_cast<float*>(ctx->weights.p);
+  int* bucket = static_cast<int*>(ctx->bucket.p);
+  int* work = static_cast<int*>(ctx->work.p);
+  int* n_work = work + 2 * max_work;
+  ActBuffers act1{static_cast<_Float16*>(ctx->act1v.p), static_cast<float*>(ctx->act1s.p)};
+
+  RouteArgs ra{};
+  ra.x = x;
+  ra.router_w = L->router_w;
+  ra.router_b = L->router_b;
+  ra.injected = injected;
+  ra.m = (int)m;
+  ra.hidden = (int)H;
+  ra.experts = (int)E;
+  ra.top_k = (int)K;
+  ra.logits = logits;
+  ra.selected = selected;
+  ra.weights = weights;
+  ra.act = act1;
+  ra.err = ctx->err;
+  {
+    OpScope sc(ctx, GOSSMX_OP_ROUTER_ROUTING);
+    HIP_TRY(launch_route(ra, ctx->stream), "route launch");
+  }
+  DispatchArgs da{};
+  da.selected = selected;
+  da.routes = (int)R;
+  da.top_k = (int)K;
+  da.experts = (int)E;
+  da.bucket_off = bucket;
+  da.route_tok = static_cast<int*>(ctx->route_tok.p);
+  da.route_slot = static_cast<int*>(ctx->route_slot.p);
+  da.work = work;
+  da.n_work = n_work;
+  {
+    OpScope sc(ctx, GOSSMX_OP_DISPATCH);
+    HIP_TRY(launch_dispatch(da, ctx->stream), "dispatch launch");
+  }
+  GemmArgs g{};
+  g.w = L->gate_up->t;
+  g.actv = act1.v;
+  g.acts = act1.s;
+  g.bias = L->gate_up_bias;
+  g.bias_expert_stride = 2 * I;
+  g.residual = 1;
+  g.work = work;
+  g.n_work = n_work;
+  g.bucket_off = bucket;
+  g.route_tok = da.route_tok;
+  g.route_slot = da.route_slot;
+  g.actv_next = static_cast<_Float16*>(ctx->act2v.p);
+  g.acts_next = static_cast<float*>(ctx->act2s.p);
+  g.alpha = L->cfg.alpha;
+  g.limit = L->cfg.limit;
+  g.err = ctx->err;
+  {
+    OpScope sc(ctx, GOSSMX_OP_GATE_UP);
+    HIP_TRY(launch_gemm(kGateUp, g, (int)max_work, ctx->stream), "gate_up launch");
+  }
+  GemmArgs d = g;
+  d.w = L->down->t;
+  d.actv = g.actv_next;
+  d.acts = g.acts_next;
+  d.bias = L->down_bias;
+  d.bias_expert_stride = H;
+  d.y = static_cast<uint16_t*>(ctx->y.p);
+  {
+    OpScope sc(ctx, GOSSMX_OP_DOWN);
+    HIP_TRY(launch_gemm(kDown, d, (int)max_work, ctx->stream), "down launch");
+  }
+  {
+    OpScope sc(ctx, GOSSMX_OP_WEIGHTING);
+    HIP_TRY(launch_combine(d.y, weights, (int)m, (int)K, (int)H, output, trace, ctx->stream), "combine launch");
+  }
+
+  if (host) {
+    if ((s = check_device_errors(ctx))) return s;
+    HIP_TRY(hipMemcpyAsync(io->output, output, m * H * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H output");
+    if (io->router_logits)
+      HIP_TRY(hipMemcpyAsync(io->router_logits, logits, m * E * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H logits");
+    if (io->selected)
+      HIP_TRY(hipMemcpyAsync(io->selected, selected, R * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H selected");
+    if (io->routing_weights)
+      HIP_TRY(hipMemcpyAsync(io->routing_weights, weights, R * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H weights");
+    if (io->route_order)
+      HIP_TRY(hipMemcpyAsync(io->route_order, da.route_slot, R * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H order");
+    if (io->trace_down)
+      HIP_TRY(hipMemcpyAsync(io->trace_down, trace, R * H * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H trace");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  } else {
+    if (io->selected)
+      HIP_TRY(hipMemcpyAsync(io->selected, selected, R * 4, hipMemcpyDeviceToDevice, ctx->stream), "D2D selected");
+    if (io->routing_weights)
+      HIP_TRY(hipMemcpyAsync(io->routing_weights, weights, R * 4, hipMemcpyDeviceToDevice, ctx->stream), "D2D weights");
+    if (io->route_order)
+      HIP_TRY(hipMemcpyAsync(io->route_order, da.route_slot, R * 4, hipMemcpyDeviceToDevice, ctx->stream), "D2D order");
+  }
+  return GOSSMX_OK;
+}
+
+// --- profiling, fault hook, self-test -------------------------------------------
+
+int gossmx_profile_enable(gossmx_ctx* ctx, int enabled) {
+  if (!ctx) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context");
+  ctx->profiling = enabled != 0;
+  return GOSSMX_OK;
+}
+
+int gossmx_profile_read(gossmx_ctx* ctx, gossmx_profile_record* out, size_t capacity, size_t* written) {
+  if (!ctx || !out || !written) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+  if (int s = fold_profile(ctx)) return s;
+  size_t n = std::min<size_t>(capacity, GOSSMX_OP_COUNT);
+  for (size_t i = 0; i < n; ++i) {
+    out[i].op = (int)i;
+    out[i].launches = ctx->op_launches[i];
+    out[i].total_ms = ctx->op_ms[i];
+  }
+  *written = n;
+  return GOSSMX_OK;
+}
+
+int gossmx_profile_reset(gossmx_ctx* ctx) {
+  if (!ctx) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context");
+  if (int s = fold_profile(ctx)) return s;
+  for (int i = 0; i < GOSSMX_OP_COUNT; ++i) {
+    ctx->op_ms[i] = 0.0;
+    ctx->op_launches[i] = 0;
+  }
+  return GOSSMX_OK;
+}
+
+int gossmx_inject_fault(gossmx_ctx* ctx, int armed) {
+  if (!ctx) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context");
+  ctx->fault_armed = armed != 0;
+  return GOSSMX_OK;
+}
+
+// Checks the lane layouts of the FP4 conversion and the 16x16x32 f16 MFMA on
+// this device against what the GEMM assumes.
+int gossmx_selftest(gossmx_ctx* ctx) {
+  if (!ctx) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context");
+  if (int s = set_device(ctx->device)) return s;
+  float* dev = nullptr;
+  HIP_TRY(hipMalloc(&dev, (8 + 256) * sizeof(float)), "hipMalloc(selftest)");
+  float host[8 + 256];
+  hipError_t e = launch_selftest(dev, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(host, dev, sizeof host, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  hipFree(dev);
+  if (e != hipSuccess) return hip_fail(e, "selftest");
+  const float codes[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+  for (int i = 0; i < 8; ++i)
+    if (host[i] != codes[i])
+      return fail(GOSSMX_ERR_UNSUPPORTED, "fp4 conversion element %d is %g, expected %g", i, host[i], codes[i]);
+  for (int lane = 0; lane < 64; ++lane)
+    for (int r = 0; r < 4; ++r) {
+      const float want = (float)(10 * (4 * (lane / 16) + r) + lane % 16);
+      if (host[8 + 4 * lane + r] != want)
+        return fail(GOSSMX_ERR_UNSUPPORTED, "mfma lane %d reg %d is %g, expected %g", lane, r, host[8 + 4 * lane + r],
+                    want);
+    }
+  return GOSSMX_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,111 @@
+// Internal declarations shared by the gfx950 kernels (gossmx_kernels.hip) and
+// the C ABI host code (gossmx_api.hip). Not part of the public interface.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstddef>
+#include <cstdint>
+
+namespace gossmx {
+
+constexpr int kBlock = 32;      // values per MXFP4 / Q8 block (QUANT_BLOCK_SIZE)
+constexpr int kRecord = 17;     // E8M0 byte + 16 packed nibble bytes per (row, block)
+constexpr int kTileRows = 16;   // rows per MFMA tile (one wave)
+constexpr int kWgRows = 64;     // rows per work-group (four waves)
+constexpr int kChunk = 64;      // activation rows per work item
+constexpr int kMaxExperts = 128;
+constexpr int kMaxTopK = 8;
+
+// Device error flags (sticky until the host reads them).
+constexpr int kErrNonFiniteLogits = 1;
+constexpr int kErrNonFiniteInput = 2;
+
+// Resident layout v3 of one [experts][rows][blocks] MXFP4 tensor.
+//  tiles = ceil(rows / 16). Per expert and tile t:
+//   nibble plane: 16 * blocks * 16 bytes at t * 256 * blocks. Block group
+//     q (blocks 4q .. 4q+nb-1, nb = min(4, blocks - 4q)) starts at q * 1024;
+//     lane L = 16 * g + n (g = K slice 0..3, n = row in tile) owns nb * 4
+//     bytes at L * nb * 4, one dword per block: packed bytes 4g..4g+3 of the
+//     canonical record, i.e. codes 8g..8g+7 (low nibble = even code).
+//   scale plane: 16 * blocks bytes at t * 16 * blocks; group q at q * 64,
+//     byte (n, j) at n * nb + j.
+//  Padding rows (rows..16*tiles-1) hold zero codes and scale 127.
+struct TiledWeights {
+  uint8_t* nib = nullptr;
+  uint8_t* scl = nullptr;
+  size_t experts = 0, rows = 0, blocks = 0, tiles = 0;
+  size_t nib_stride = 0;  // bytes per expert in the nibble plane
+  size_t scl_stride = 0;  // bytes per expert in the scale plane
+};
+
+// Activation operand of the expert GEMM, one row per token or route:
+//  actv [row][block][part 0 = primary, 1 = residual][32] f16 (the Q8 codes,
+//  exact in f16), acts [row][block][2] f32 (primary scale, residual scale).
+struct ActBuffers {
+  _Float16* v = nullptr;
+  float* s = nullptr;
+};
+
+enum GemmMode { kPlain = 0, kGateUp = 1, kDown = 2 };
+
+struct GemmArgs {
+  TiledWeights w;
+  const _Float16* actv;
+  const float* acts;
+  const float* bias;     // bias of expert e at bias + e * bias_expert_stride, or null
+  size_t bias_expert_stride;
+  int residual;          // 1 = residual-Q8 activations, 0 = Q8 (primary only)
+  // work items
+  int plain_expert, plain_m;          // kPlain
+  const int* work;                    // [n][2] (expert, chunk start)   (gate_up/down)
+  const int* n_work;
+  const int* bucket_off;              // [experts + 1]
+  const int* route_tok;               // grouped route -> source row
+  const int* route_slot;              // grouped route -> row * top_k + rank
+  // outputs
+  float* out; size_t out_stride;      // kPlain
+  _Float16* actv_next; float* acts_next;  // kGateUp: down-projection input per grouped route
+  float alpha, limit;                 // kGateUp
+  uint16_t* y;                        // kDown: [m * top_k][rows] bf16
+  int* err;
+};
+
+struct RouteArgs {
+  const uint16_t* x;        // [m][hidden] bf16
+  const uint16_t* router_w; // [experts][hidden]
+  const float* router_b;    // [experts]
+  const float* injected;    // [m][experts] or null
+  int m, hidden, experts, top_k;
+  float* logits;            // [m][experts]
+  int* selected;            // [m][top_k]
+  float* weights;           // [m][top_k]
+  ActBuffers act;           // gate_up input per token
+  int* err;
+};
+
+struct DispatchArgs {
+  const int* selected;  // [m * top_k]
+  int routes, top_k, experts;
+  int* bucket_off;      // [experts + 1]
+  int* route_tok;       // [routes]
+  int* route_slot;      // [routes]
+  int* work;            // [max_work][2]
+  int* n_work;
+};
+
+// Launchers (gossmx_kernels.hip). All are asynchronous on `stream`.
+hipError_t launch_route(const RouteArgs& a, hipStream_t stream);
+hipError_t launch_dispatch(const DispatchArgs& a, hipStream_t stream);
+hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream);
+hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int top_k, int hidden, float* out,
+                          float* trace_down, hipStream_t stream);
+hipError_t launch_prep_records(const uint8_t* records, int kind, size_t m, size_t blocks, size_t row_stride,
+                               ActBuffers act, int* err, hipStream_t stream);
+hipError_t launch_repack(const uint8_t* src, int layout, TiledWeights w, hipStream_t stream);
+hipError_t launch_generate(uint64_t seed, uint64_t stream_id, TiledWeights w, hipStream_t stream);
+hipError_t launch_export(TiledWeights w, uint8_t* dst, hipStream_t stream);
+hipError_t launch_fill_tiled_padding(TiledWeights w, hipStream_t stream);
+hipError_t launch_clear_ints(int* p, size_t n, hipStream_t stream);
+hipError_t launch_selftest(float* out, hipStream_t stream);
+
+}  // namespace gossmx

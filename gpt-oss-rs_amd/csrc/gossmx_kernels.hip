@@ -1,0 +1,733 @@
+// gfx950 kernels of the GPT-OSS MXFP4 mixture-of-experts block.
+//
+// Exactness contract (crates/gpt-oss-cpu-kernels and cpu_runner.rs of
+// gpt-oss-rs v0.1.0): every integer FP4 x Q8 block dot is exact, and every
+// float chain keeps the reference's operation order, so the outputs are
+// bit-identical to the scalar CPU path. Build with -ffp-contract=off: no
+// multiply-add below may be fused unless written as fma() on purpose.
+//
+// Expert GEMM: v_mfma_f32_16x16x32_f16 with K = 32 = one MXFP4 block. The B
+// operand is the weight tile converted from FP4 by v_cvt_scalef32_pk_f16_fp4
+// (E2M1 values are exact in f16); the A operand holds the Q8 codes as f16
+// (exact). Each product is exact in f32 and every partial sum is a multiple of
+// 0.5 below 2^15, so the MFMA returns p / 2 exactly, where p is the reference's
+// doubled-LUT integer dot (lib.rs:1067-1098). The reference term
+// (p * (0.5 * e8m0)) * act_scale equals ((p / 2) * e8m0) * act_scale bit for
+// bit: the first product is the same real number rounded once.
+#include "gossmx_internal.h"
+
+#include <cmath>
+
+namespace gossmx {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Scalar helpers.
+
+// bf16::from_f32 of half 2.7.1 (round to nearest even, NaN quieted), used by
+// fp32_to_bf16_roundtrip, cpu_runner.rs:3740-3744.
+__device__ __forceinline__ uint16_t bf16_bits(float f) {
+  const uint32_t x = __float_as_uint(f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x0040u);
+  const uint32_t round_bit = 0x8000u;
+  if ((x & round_bit) != 0 && (x & (3u * round_bit - 1u)) != 0) return (uint16_t)((x >> 16) + 1u);
+  return (uint16_t)(x >> 16);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ float bf16r(float f) { return bf16_to_f32(bf16_bits(f)); }
+
+// e8m0_scale, lib.rs:957-963: 0x00 -> 2^-127, 0xff -> NaN, else 2^(s-127).
+__device__ __forceinline__ float e8m0(uint32_t s) {
+  return s == 0 ? __uint_as_float(0x00400000u) : (s == 0xffu ? __uint_as_float(0x7fc00000u) : __uint_as_float(s << 23));
+}
+
+// expf with the exact results of the host's glibc 2.35 expf, which is what
+// Rust's f32::exp calls on x86_64 Linux (softmax cpu_runner.rs:3784-3795,
+// gpt_oss_swiglu :3797-3826). Algorithm of glibc sysdeps/ieee754/flt-32/e_expf.c
+// (Szabolcs Nagy, ARM optimized-routines): x * 32/ln2 split by the 0x1.8p52
+// shift into k and r, a 32-entry table of 2^(i/32), and a cubic in r, all in
+// double with fused multiply-adds as the FMA build of glibc evaluates it.
+// Table entries: bits of 2^(i/32) rounded to double, minus i << 47.
+__constant__ uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+__device__ float expf_glibc(float x) {
+  const uint32_t ux = __float_as_uint(x);
+  const uint32_t abstop = (ux >> 20) & 0x7ffu;
+  if (abstop >= 0x42bu) {  // |x| >= 88 (top 12 bits of 88.0f), inf or NaN
+    if (ux == 0xff800000u) return 0.0f;
+    if (abstop >= 0x7f8u) return x + x;
+    if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);
+    if (x < -0x1.9fe368p6f) return 0.0f;
+  }
+  const double inv_ln2_n = 0x1.71547652b82fep+0 * 32;
+  const double shift = 0x1.8p+52;
+  const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
+  const double c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
+  const double c2 = 0x1.62e42ff0c52d6p-1 / 32;
+  const double xd = (double)x;
+  double kd = fma(inv_ln2_n, xd, shift);
+  const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+  kd -= shift;
+  const double r = fma(inv_ln2_n, xd, -kd);
+  const uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+  const double s = __longlong_as_double((long long)t);
+  const double z = fma(c0, r, c1);
+  const double r2 = r * r;
+  double y = fma(c2, r, 1.0);
+  y = fma(z, r2, y);
+  y = y * s;
+  return (float)y;
+}
+
+// gpt_oss_swiglu for one (gate, up) pair, cpu_runner.rs:3797-3826: gate =
+// min(g, limit) (NaN-ignoring like f32::min), up = clamp(u, -limit, limit)
+// (NaN kept), then bf16 after every tensor operation.
+__device__ float swiglu_one(float g, float u, float alpha, float limit) {
+  const float gate = fminf(g, limit);
+  float up = u;
+  if (up < -limit) up = -limit;
+  if (up > limit) up = limit;
+  const float scaled = bf16r(gate * alpha);
+  const float sig = bf16r(1.0f / (1.0f + expf_glibc(-scaled)));
+  const float glu = bf16r(gate * sig);
+  const float lin = bf16r(up + 1.0f);
+  return bf16r(glu * lin);
+}
+
+// quantize_q8_block (lib.rs:1051-1065) for the 32 values held by a 32-lane
+// half wave (lane l32 holds value l32): scale = max|v| / 127, inverse =
+// 1 / scale (0 when scale is 0), q = clamp(round_half_away(v * inverse)).
+// max is order-free, so the butterfly gives the reference's fold.
+__device__ __forceinline__ void q8_half_wave(float v, float& q, float& scale) {
+  float mx = fabsf(v);
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  scale = mx / 127.0f;
+  const float inv = scale == 0.0f ? 0.0f : 1.0f / scale;
+  q = fminf(fmaxf(roundf(v * inv), -127.0f), 127.0f);
+}
+
+// quantize_residual_q8 (lib.rs:382-409) of one block held by a half wave;
+// writes the f16 codes and the two scales of (row, blk) into `act`.
+__device__ __forceinline__ void residual_q8_store(float v, int l32, size_t row, int blocks, int blk, ActBuffers act) {
+  float q, s;
+  q8_half_wave(v, q, s);
+  const float r = v - q * s;
+  float rq, rs;
+  q8_half_wave(r, rq, rs);
+  _Float16* dst = act.v + ((row * blocks + blk) * 2) * kBlock;
+  dst[l32] = (_Float16)q;
+  dst[kBlock + l32] = (_Float16)rq;
+  if (l32 == 0) {
+    float2 sc;
+    sc.x = s;
+    sc.y = rs;
+    reinterpret_cast<float2*>(act.s)[row * blocks + blk] = sc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Router projection, top-k, routing softmax and the gate_up input quantization,
+// one work-group per row (moe_batch routing loop, cpu_runner.rs:2808-2854).
+
+__device__ __forceinline__ bool route_better(float va, int ia, float vb, int ib) {
+  return va > vb || (va == vb && ia < ib);  // stable_top_k order, cpu_runner.rs:3768-3778
+}
+
+__global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
+  const int r = blockIdx.x;
+  const int E = a.experts, H = a.hidden, K = a.top_k;
+  const uint16_t* x = a.x + (size_t)r * H;
+  __shared__ float s_chain[kMaxExperts * 16];
+  __shared__ float s_logit[kMaxExperts];
+  __shared__ int s_sel[kMaxTopK];
+
+  if (a.injected == nullptr) {
+    // scalar_bf16_dot (lib.rs:1007-1029): 16 reduction lanes, lane j sums
+    // w[i] * x[i] for i = j mod 16 in increasing i, multiply then add.
+    for (int c = threadIdx.x; c < E * 16; c += blockDim.x) {
+      const int e = c >> 4, l = c & 15;
+      const uint16_t* w = a.router_w + (size_t)e * H;
+      float acc = 0.0f;
+      for (int i = l; i < H; i += 16) acc = acc + bf16_to_f32(w[i]) * bf16_to_f32(x[i]);
+      s_chain[c] = acc;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+      float s = s_chain[e * 16];
+      for (int l = 1; l < 16; ++l) s = s + s_chain[e * 16 + l];
+      s_logit[e] = bf16r(s + a.router_b[e]);  // += bias (cpu_runner.rs:2781-2783), bf16 (:2829)
+    }
+  } else {
+    for (int e = threadIdx.x; e < E; e += blockDim.x) s_logit[e] = bf16r(a.injected[(size_t)r * E + e]);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    const float v = s_logit[e];
+    if (!isfinite(v)) atomicOr(a.err, kErrNonFiniteLogits);
+    if (a.logits) a.logits[(size_t)r * E + e] = v;
+  }
+
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    // Each lane owns experts lane and lane + 64; K rounds of a wave argmax.
+    // NaN logits (already flagged as an error) rank as -inf so that every
+    // round still returns a valid expert index.
+    bool taken0 = false, taken1 = false;
+    float v0 = lane < E ? s_logit[lane] : -INFINITY;
+    float v1 = lane + 64 < E ? s_logit[lane + 64] : -INFINITY;
+    if (isnan(v0)) v0 = -INFINITY;
+    if (isnan(v1)) v1 = -INFINITY;
+    for (int k = 0; k < K; ++k) {
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+      if (lane < E && !taken0) { bv = v0; bi = lane; }
+      if (lane + 64 < E && !taken1 && route_better(v1, lane + 64, bv, bi)) { bv = v1; bi = lane + 64; }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (route_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+      }
+      if (bi < 0 || bi >= E) bi = 0;
+      if (bi == lane) taken0 = true;
+      if (bi == lane + 64) taken1 = true;
+      if (lane == 0) s_sel[k] = bi;
+    }
+    if (lane == 0) {
+      // softmax over the selected logits in rank order (cpu_runner.rs:3784-3795),
+      // then bf16 (:2840-2843).
+      float mx = -INFINITY;
+      for (int k = 0; k < K; ++k) mx = fmaxf(mx, s_logit[s_sel[k]]);
+      float ex[kMaxTopK];
+      float sum = 0.0f;
+      for (int k = 0; k < K; ++k) {
+        ex[k] = expf_glibc(s_logit[s_sel[k]] - mx);
+        sum = sum + ex[k];
+      }
+      for (int k = 0; k < K; ++k) {
+        a.selected[(size_t)r * K + k] = s_sel[k];
+        a.weights[(size_t)r * K + k] = bf16r(ex[k] / sum);
+      }
+    }
+  }
+
+  // quantize_residual_q8 of the row for gate_up (cpu_runner.rs:3224-3231):
+  // one half wave per 32-value block.
+  const int hw = threadIdx.x >> 5, l32 = threadIdx.x & 31;
+  const int blocks = H / kBlock;
+  for (int b = hw; b < blocks; b += blockDim.x / 32) {
+    const float v = bf16_to_f32(x[b * kBlock + l32]);
+    if (!isfinite(v)) atomicOr(a.err, kErrNonFiniteInput);
+    residual_q8_store(v, l32, (size_t)r, blocks, b, a.act);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Stable grouping of routes by expert (stable_group_routes,
+// cpu_runner.rs:3780-3782): route i = row * top_k + rank goes to
+// bucket_off[e] + #{j < i : expert(j) == e}. One work-group of 1024 threads;
+// in-wave ranks come from one ballot per expert.
+
+__global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
+  const int E = a.experts, R = a.routes;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ int s_tot[kMaxExperts];
+  __shared__ int s_off[kMaxExperts];
+  __shared__ int s_run[kMaxExperts];
+  __shared__ int s_wcnt[16][kMaxExperts];
+  for (int e = tid; e < E; e += 1024) { s_tot[e] = 0; s_run[e] = 0; }
+  __syncthreads();
+  for (int i = tid; i < R; i += 1024) atomicAdd(&s_tot[a.selected[i]], 1);
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0, n = 0;
+    for (int e = 0; e < E; ++e) {
+      s_off[e] = acc;
+      a.bucket_off[e] = acc;
+      for (int s = 0; s < s_tot[e]; s += kChunk) {
+        a.work[2 * n] = e;
+        a.work[2 * n + 1] = s;
+        ++n;
+      }
+      acc += s_tot[e];
+    }
+    a.bucket_off[E] = acc;
+    *a.n_work = n;
+  }
+  __syncthreads();
+  for (int base = 0; base < R; base += 1024) {
+    const int i = base + tid;
+    const int e = i < R ? a.selected[i] : -1;
+    const unsigned long long lt = (1ull << lane) - 1ull;
+    int rank = 0;
+    for (int ee = 0; ee < E; ++ee) {
+      const unsigned long long m = __ballot(e == ee);
+      if (e == ee) rank = __popcll(m & lt);
+      if (lane == 0) s_wcnt[wave][ee] = __popcll(m);
+    }
+    __syncthreads();
+    if (e >= 0) {
+      int pos = s_off[e] + s_run[e] + rank;
+      for (int w = 0; w < wave; ++w) pos += s_wcnt[w][e];
+      a.route_tok[pos] = i / a.top_k;
+      a.route_slot[pos] = i;
+    }
+    __syncthreads();
+    for (int ee = tid; ee < E; ee += 1024) {
+      int add = 0;
+      for (int w = 0; w < 16; ++w) add += s_wcnt[w][ee];
+      s_run[ee] += add;
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Expert GEMM on the resident v3 layout. One work-group = 4 waves = 64 weight
+// rows (one 16-row tile per wave) x one work item (<= 64 activation rows).
+// Each lane owns one weight row (lane % 16) and two activation rows per group
+// of 8, and runs the reference's per-row float chain in order:
+//   total = bias; for each block: total += (p * ws) * ps; total += (r * ws) * rs
+// (mxfp4_residual_q8_gemv_rows lib.rs:673-696, scalar_matmul_range
+// matmul.rs:529-578).
+
+__device__ __forceinline__ half8 fp4x8_to_half8(uint32_t w) {
+  const half2v h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0);
+  const half2v h1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1);
+  const half2v h2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2);
+  const half2v h3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3);
+  half8 b;
+  b[0] = h0[0]; b[1] = h0[1]; b[2] = h1[0]; b[3] = h1[1];
+  b[4] = h2[0]; b[5] = h2[1]; b[6] = h3[0]; b[7] = h3[1];
+  return b;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nl = lane & 15, G = lane >> 4;
+  int expert, start, count, route_base = 0;
+  if (MODE == kPlain) {
+    expert = a.plain_expert;
+    start = blockIdx.y * kChunk;
+    count = min(kChunk, a.plain_m - start);
+  } else {
+    const int wi = blockIdx.y;
+    if (wi >= *a.n_work) return;  // uniform over the work-group
+    expert = a.work[2 * wi];
+    start = a.work[2 * wi + 1];
+    route_base = a.bucket_off[expert];
+    count = min(kChunk, a.bucket_off[expert + 1] - route_base - start);
+  }
+  __shared__ int s_row[kChunk];
+  if (threadIdx.x < kChunk) {
+    const int c = threadIdx.x;
+    int r = -1;
+    if (c < count) {
+      if (MODE == kPlain) r = start + c;
+      else if (MODE == kGateUp) r = a.route_tok[route_base + start + c];
+      else r = route_base + start + c;
+    }
+    s_row[c] = r;
+  }
+  __syncthreads();
+
+  const int rows = (int)a.w.rows, B = (int)a.w.blocks;
+  const int tile = blockIdx.x * 4 + wave;
+  const bool tile_ok = tile < (int)a.w.tiles;
+  const int row = tile * kTileRows + nl;
+  const int n_tg = (count + 7) >> 3;
+
+  float b0 = 0.0f;
+  if (a.bias != nullptr && tile_ok && row < rows) b0 = a.bias[(size_t)expert * a.bias_expert_stride + row];
+  b0 = b0 + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
+  float tot[8][2];
+#pragma unroll
+  for (int tg = 0; tg < 8; ++tg) { tot[tg][0] = b0; tot[tg][1] = b0; }
+
+  if (tile_ok) {
+    const uint8_t* nib = a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)tile * 256 * B;
+    const uint8_t* scl = a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)tile * 16 * B;
+    int arow[8], erow0[8], erow1[8];
+#pragma unroll
+    for (int tg = 0; tg < 8; ++tg) {
+      arow[tg] = s_row[tg * 8 + (nl >> 1)];
+      erow0[tg] = s_row[tg * 8 + 2 * G];
+      erow1[tg] = s_row[tg * 8 + 2 * G + 1];
+    }
+    const int part = nl & 1;
+    const float2* acts = reinterpret_cast<const float2*>(a.acts);
+    const int nq = (B + 3) >> 2;
+    for (int q = 0; q < nq; ++q) {
+      const int nb = min(4, B - 4 * q);
+      uint32_t wv[4] = {0u, 0u, 0u, 0u};
+      uint32_t sv = 0u;
+      const uint8_t* gn = nib + (size_t)q * 1024;
+      const uint8_t* gs = scl + (size_t)q * 64;
+      if (nb == 4) {
+        const uint4 v = *reinterpret_cast<const uint4*>(gn + lane * 16);
+        wv[0] = v.x; wv[1] = v.y; wv[2] = v.z; wv[3] = v.w;
+        sv = *reinterpret_cast<const uint32_t*>(gs + nl * 4);
+      } else {
+        for (int j = 0; j < nb; ++j) {
+          wv[j] = *reinterpret_cast<const uint32_t*>(gn + lane * nb * 4 + j * 4);
+          sv |= (uint32_t)gs[nl * nb + j] << (8 * j);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (j < nb) {
+          const int b = 4 * q + j;
+          const half8 bop = fp4x8_to_half8(wv[j]);
+          const float e8 = e8m0((sv >> (8 * j)) & 0xffu);
+#pragma unroll
+          for (int tg = 0; tg < 8; ++tg) {
+            if (tg < n_tg) {
+              half8 aop = {0, 0, 0, 0, 0, 0, 0, 0};
+              if (arow[tg] >= 0)
+                aop = *reinterpret_cast<const half8*>(a.actv + (((size_t)arow[tg] * B + b) * 2 + part) * kBlock + G * 8);
+              const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+              const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, zero, 0, 0, 0);
+              float2 s0 = {0.0f, 0.0f}, s1 = {0.0f, 0.0f};
+              if (erow0[tg] >= 0) s0 = acts[(size_t)erow0[tg] * B + b];
+              if (erow1[tg] >= 0) s1 = acts[(size_t)erow1[tg] * B + b];
+              tot[tg][0] = tot[tg][0] + (d[0] * e8) * s0.x;
+              if (a.residual) tot[tg][0] = tot[tg][0] + (d[1] * e8) * s0.y;
+              tot[tg][1] = tot[tg][1] + (d[2] * e8) * s1.x;
+              if (a.residual) tot[tg][1] = tot[tg][1] + (d[3] * e8) * s1.y;
+            }
+          }
+        }
+      }
+    }
+  }
+
+  if (MODE == kPlain) {
+    if (tile_ok && row < rows) {
+#pragma unroll
+      for (int tg = 0; tg < 8; ++tg)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int c = tg * 8 + 2 * G + t;
+          if (c < count) a.out[(size_t)(start + c) * a.out_stride + row] = tot[tg][t];
+        }
+    }
+  } else if (MODE == kDown) {
+    if (tile_ok && row < rows) {
+#pragma unroll
+      for (int tg = 0; tg < 8; ++tg)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int c = tg * 8 + 2 * G + t;
+          if (c < count) {
+            const int slot = a.route_slot[route_base + start + c];
+            a.y[(size_t)slot * rows + row] = bf16_bits(tot[tg][t]);  // bf16 (cpu_runner.rs:2945-2947)
+          }
+        }
+    }
+  } else {
+    // gate_up epilogue: bf16 (cpu_runner.rs:2905), SwiGLU over (even, odd)
+    // rows (:2907-2919), then the down input's residual-Q8 block: the 64
+    // rows of this work-group make one 32-value block (cpu_runner.rs:3224-3231).
+    __shared__ float s_act[kChunk][kBlock + 1];
+#pragma unroll
+    for (int tg = 0; tg < 8; ++tg) {
+      if (tg < n_tg) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const float gu = bf16r(tot[tg][t]);
+          const float other = __shfl_xor(gu, 1);
+          const int c = tg * 8 + 2 * G + t;
+          if ((nl & 1) == 0 && c < count) s_act[c][wave * 8 + (nl >> 1)] = swiglu_one(gu, other, a.alpha, a.limit);
+        }
+      }
+    }
+    __syncthreads();
+    const int hw = threadIdx.x >> 5, l32 = threadIdx.x & 31;
+    const int blocks_next = rows / kWgRows;
+    for (int c = hw; c < count; c += 8) {
+      const float v = s_act[c][l32];
+      if (!isfinite(v)) atomicOr(a.err, kErrNonFiniteInput);
+      ActBuffers nx;
+      nx.v = a.actv_next;
+      nx.s = a.acts_next;
+      residual_q8_store(v, l32, (size_t)(route_base + start + c), blocks_next, blockIdx.x, nx);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Weighted combine by source row and rank (cpu_runner.rs:2959-2999):
+// out = 0; out += y_rank * w_rank in rank order; then bf16.
+
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* y, const float* w, int top_k, int hidden,
+                                                     float* out, float* trace) {
+  const int r = blockIdx.y;
+  const int h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h >= hidden) return;
+  float acc = 0.0f;
+  for (int k = 0; k < top_k; ++k) {
+    const size_t slot = (size_t)r * top_k + k;
+    const float v = bf16_to_f32(y[slot * hidden + h]);
+    acc = acc + v * w[slot];
+    if (trace) trace[slot * hidden + h] = v;
+  }
+  out[(size_t)r * hidden + h] = bf16r(acc);
+}
+
+// ---------------------------------------------------------------------------
+// Reference activation records -> GEMM operand. Q8Block {f32 scale; i8[32]}
+// is 36 bytes, ResidualQ8Block {primary; residual} 72 bytes (lib.rs:732-742).
+
+__global__ __launch_bounds__(256) void prep_records_kernel(const uint8_t* rec, int kind, int m, int blocks,
+                                                          size_t row_stride, ActBuffers act) {
+  const int hw = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+  const int l32 = threadIdx.x & 31;
+  if (hw >= m * blocks) return;
+  const int r = hw / blocks, b = hw % blocks;
+  const size_t rsz = kind == 2 ? 72 : 36;
+  const uint8_t* p = rec + ((size_t)r * row_stride + b) * rsz;
+  const float ps = *reinterpret_cast<const float*>(p);
+  const int8_t pq = (int8_t)p[4 + l32];
+  float rs = 0.0f;
+  int8_t rq = 0;
+  if (kind == 2) {
+    rs = *reinterpret_cast<const float*>(p + 36);
+    rq = (int8_t)p[40 + l32];
+  }
+  _Float16* dst = act.v + (((size_t)r * blocks + b) * 2) * kBlock;
+  dst[l32] = (_Float16)(float)pq;
+  dst[kBlock + l32] = (_Float16)(float)rq;
+  if (l32 == 0) {
+    float2 sc;
+    sc.x = ps;
+    sc.y = rs;
+    reinterpret_cast<float2*>(act.s)[(size_t)r * blocks + b] = sc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Layout conversion into the resident v3 layout.
+
+__device__ __forceinline__ void v3_offsets(const TiledWeights& w, size_t e, size_t row, size_t b, size_t g,
+                                           size_t* nib_off, size_t* scl_off) {
+  const size_t B = w.blocks, t = row / kTileRows, n = row % kTileRows, q = b / 4, j = b % 4;
+  const size_t nb = B - 4 * q < 4 ? B - 4 * q : 4;
+  *nib_off = e * w.nib_stride + t * 256 * B + q * 1024 + (g * 16 + n) * nb * 4 + j * 4;
+  *scl_off = e * w.scl_stride + t * 16 * B + q * 64 + n * nb + j;
+}
+
+// Mxfp4MatrixView::block (lib.rs:810-851) for canonical v1 and x8 v2 data of
+// one expert: fills the 16 adjacent-packed bytes and the scale byte.
+__device__ void view_block(const uint8_t* data, int layout, size_t rows, size_t blocks, size_t row, size_t b,
+                           uint8_t packed[16], uint8_t* scale) {
+  if (layout == 1) {
+    const uint8_t* p = data + (row * blocks + b) * kRecord;
+    *scale = p[0];
+    for (int i = 0; i < 16; ++i) packed[i] = p[1 + i];
+    return;
+  }
+  const size_t complete = rows / 8 * 8;
+  if (row < complete) {
+    const size_t group = row / 8, lane = row % 8;
+    const uint8_t* x8 = data + (group * blocks + b) * 136;
+    uint8_t split[16];
+    for (int i = 0; i < 16; ++i) split[i] = x8[8 + (i / 8) * 64 + lane * 8 + i % 8];
+    *scale = x8[lane];
+    // mxfp4_split_to_adjacent (lib.rs:919-928): split byte i = code(i) | code(i+16) << 4.
+    for (int i = 0; i < 16; ++i) {
+      const int c0 = 2 * i, c1 = 2 * i + 1;
+      const uint8_t lo = c0 < 16 ? (split[c0] & 0x0f) : (split[c0 - 16] >> 4);
+      const uint8_t hi = c1 < 16 ? (split[c1] & 0x0f) : (split[c1 - 16] >> 4);
+      packed[i] = (uint8_t)(lo | (hi << 4));
+    }
+    return;
+  }
+  const uint8_t* p = data + (rows / 8) * blocks * 136 + ((row - complete) * blocks + b) * kRecord;
+  *scale = p[0];
+  for (int i = 0; i < 16; ++i) packed[i] = p[1 + i];
+}
+
+__device__ __forceinline__ void store_v3(const TiledWeights& w, size_t e, size_t row, size_t b, const uint8_t packed[16],
+                                         uint8_t scale) {
+  for (size_t g = 0; g < 4; ++g) {
+    size_t no, so;
+    v3_offsets(w, e, row, b, g, &no, &so);
+    const uint32_t d = (uint32_t)packed[4 * g] | ((uint32_t)packed[4 * g + 1] << 8) |
+                       ((uint32_t)packed[4 * g + 2] << 16) | ((uint32_t)packed[4 * g + 3] << 24);
+    *reinterpret_cast<uint32_t*>(w.nib + no) = d;
+    if (g == 0) w.scl[so] = scale;
+  }
+}
+
+__global__ void repack_kernel(const uint8_t* src, int layout, TiledWeights w) {
+  const size_t per_expert = w.rows * w.blocks;
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= w.experts * per_expert) return;
+  const size_t e = i / per_expert, rb = i % per_expert, row = rb / w.blocks, b = rb % w.blocks;
+  uint8_t packed[16], scale;
+  view_block(src + e * per_expert * kRecord, layout, w.rows, w.blocks, row, b, packed, &scale);
+  store_v3(w, e, row, b, packed, scale);
+}
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  uint64_t z = x + 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+__device__ __forceinline__ uint64_t stream_hash(uint64_t seed, uint64_t stream, uint64_t index) {
+  return splitmix64(splitmix64(seed ^ (stream * 0xD1B54A32D192ED03ull)) + index);
+}
+
+__global__ void generate_kernel(uint64_t seed, uint64_t stream, TiledWeights w) {
+  const size_t per_expert = w.rows * w.blocks;
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= w.experts * per_expert) return;
+  const size_t e = i / per_expert, rb = i % per_expert, row = rb / w.blocks, b = rb % w.blocks;
+  const uint64_t h0 = stream_hash(seed, stream, 2 * i), h1 = stream_hash(seed, stream, 2 * i + 1);
+  uint8_t packed[16];
+  for (int j = 0; j < 8; ++j) packed[j] = (uint8_t)(h0 >> (8 * j));
+  for (int j = 0; j < 8; ++j) packed[8 + j] = (uint8_t)(h1 >> (8 * j));
+  store_v3(w, e, row, b, packed, (uint8_t)(119 + (h1 >> 61) % 5));
+}
+
+__global__ void export_kernel(TiledWeights w, uint8_t* dst) {
+  const size_t per_expert = w.rows * w.blocks;
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= w.experts * per_expert) return;
+  const size_t e = i / per_expert, rb = i % per_expert, row = rb / w.blocks, b = rb % w.blocks;
+  uint8_t* p = dst + i * kRecord;
+  for (size_t g = 0; g < 4; ++g) {
+    size_t no, so;
+    v3_offsets(w, e, row, b, g, &no, &so);
+    const uint32_t d = *reinterpret_cast<const uint32_t*>(w.nib + no);
+    for (int k = 0; k < 4; ++k) p[1 + 4 * g + k] = (uint8_t)(d >> (8 * k));
+    if (g == 0) p[0] = w.scl[so];
+  }
+}
+
+// Padding rows of the last tile: zero codes, scale 127.
+__global__ void fill_padding_kernel(TiledWeights w) {
+  const size_t pad_rows = w.tiles * kTileRows - w.rows;
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= w.experts * pad_rows * w.blocks) return;
+  const size_t e = i / (pad_rows * w.blocks), rb = i % (pad_rows * w.blocks);
+  const size_t row = w.rows + rb / w.blocks, b = rb % w.blocks;
+  const uint8_t zero[16] = {0};
+  store_v3(w, e, row, b, zero, 127);
+}
+
+__global__ void clear_ints_kernel(int* p, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// Lane-layout self-test of the two gfx950 builtins the GEMM relies on.
+// out[0..7]: v_cvt_scalef32_pk_f16_fp4 of codes 0..7 (bytes 0x10 0x32 0x54 0x76).
+// out[8 + 4 * lane + r]: D of a 16x16x32 f16 MFMA with A[i][k] = (k == i) and
+// B[k][j] = 10 k + j, expected 10 * (4 * (lane / 16) + r) + lane % 16.
+__global__ void selftest_kernel(float* out) {
+  const int lane = threadIdx.x;
+  const half8 w = fp4x8_to_half8(0x76543210u);
+  if (lane == 0)
+    for (int i = 0; i < 8; ++i) out[i] = (float)w[i];
+  half8 av, bv;
+  for (int e = 0; e < 8; ++e) {
+    const int k = 8 * (lane >> 4) + e;
+    av[e] = (_Float16)((k == (lane & 15)) ? 1.0f : 0.0f);
+    bv[e] = (_Float16)(float)(10 * k + (lane & 15));
+  }
+  const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, zero, 0, 0, 0);
+  for (int r = 0; r < 4; ++r) out[8 + 4 * lane + r] = d[r];
+}
+
+// ---------------------------------------------------------------------------
+// Launchers.
+
+static inline unsigned grid1d(size_t n, unsigned block) { return (unsigned)((n + block - 1) / block); }
+
+hipError_t launch_route(const RouteArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL(route_kernel, dim3(a.m), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_dispatch(const DispatchArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream) {
+  const dim3 grid((unsigned)((a.w.tiles + 3) / 4), (unsigned)grid_work);
+  switch (mode) {
+    case kPlain: hipLaunchKernelGGL(gemm_kernel<kPlain>, grid, dim3(256), 0, stream, a); break;
+    case kGateUp: hipLaunchKernelGGL(gemm_kernel<kGateUp>, grid, dim3(256), 0, stream, a); break;
+    case kDown: hipLaunchKernelGGL(gemm_kernel<kDown>, grid, dim3(256), 0, stream, a); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int top_k, int hidden, float* out,
+                          float* trace_down, hipStream_t stream) {
+  hipLaunchKernelGGL(combine_kernel, dim3(grid1d(hidden, 256), m), dim3(256), 0, stream, y, weights, top_k, hidden,
+                     out, trace_down);
+  return hipGetLastError();
+}
+
+hipError_t launch_prep_records(const uint8_t* records, int kind, size_t m, size_t blocks, size_t row_stride,
+                               ActBuffers act, int* /*err*/, hipStream_t stream) {
+  hipLaunchKernelGGL(prep_records_kernel, dim3(grid1d(m * blocks * 32, 256)), dim3(256), 0, stream, records, kind,
+                     (int)m, (int)blocks, row_stride, act);
+  return hipGetLastError();
+}
+
+hipError_t launch_repack(const uint8_t* src, int layout, TiledWeights w, hipStream_t stream) {
+  hipLaunchKernelGGL(repack_kernel, dim3(grid1d(w.experts * w.rows * w.blocks, 256)), dim3(256), 0, stream, src,
+                     layout, w);
+  return hipGetLastError();
+}
+
+hipError_t launch_generate(uint64_t seed, uint64_t stream_id, TiledWeights w, hipStream_t stream) {
+  hipLaunchKernelGGL(generate_kernel, dim3(grid1d(w.experts * w.rows * w.blocks, 256)), dim3(256), 0, stream, seed,
+                     stream_id, w);
+  return hipGetLastError();
+}
+
+hipError_t launch_export(TiledWeights w, uint8_t* dst, hipStream_t stream) {
+  hipLaunchKernelGGL(export_kernel, dim3(grid1d(w.experts * w.rows * w.blocks, 256)), dim3(256), 0, stream, w, dst);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_tiled_padding(TiledWeights w, hipStream_t stream) {
+  const size_t n = w.experts * (w.tiles * kTileRows - w.rows) * w.blocks;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_padding_kernel, dim3(grid1d(n, 256)), dim3(256), 0, stream, w);
+  return hipGetLastError();
+}
+
+hipError_t launch_clear_ints(int* p, size_t n, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(clear_ints_kernel, dim3(grid1d(n, 256)), dim3(256), 0, stream, p, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_selftest(float* out, hipStream_t stream) {
+  hipLaunchKernelGGL(selftest_kernel, dim3(1), dim3(64), 0, stream, out);
+  return hipGetLastError();
+}
+
+}  // namespace gossmx

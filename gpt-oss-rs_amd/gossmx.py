@@ -1,0 +1,391 @@
+"""Host-side mirror of gpt-oss-rs's MXFP4 MoE interfaces over libgossmx.so.
+
+`mxfp4_matmul` mirrors `Kernels::mxfp4_matmul` with a residual-Q8 or Q8
+`Mxfp4MatmulProblem` (crates/gpt-oss-cpu-kernels/src/matmul.rs:297-414), and
+`MoeLayer.moe_batch` mirrors `CpuModel::moe_batch`
+(crates/gpt-oss-model-runner/src/cpu_runner.rs:2794-3013), returning one
+`MoeStep` per input row like `CpuMoeStep` (:569-575). Errors raise
+`GossmxError` carrying the `KernelError`-like status code.
+
+The HIP library is required: importing works anywhere, but every call that
+needs the library raises if libgossmx.so is missing; there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libgossmx.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "gossmx.h")
+
+OK = 0
+ERR_INVALID_ARGUMENT = 1
+ERR_UNSUPPORTED = 2
+ERR_INVALID_DIMENSIONS = 3
+ERR_NON_FINITE_INPUT = 4
+ERR_UNAVAILABLE_BACKEND = 5
+ERR_DEVICE = 6
+ERR_OUT_OF_MEMORY = 7
+ERR_NON_FINITE_LOGITS = 8
+ERR_INJECTED_FAULT = 9
+
+LAYOUT_CANONICAL_V1 = 1
+LAYOUT_X8_SPLIT_V2 = 2
+ACT_Q8 = 1
+ACT_RESIDUAL_Q8 = 2
+MEM_HOST = 0
+MEM_DEVICE = 1
+
+OPS = ("router_routing", "dispatch", "gate_up", "down", "weighting", "matmul")
+
+# The reference's activation records (lib.rs:732-742), 36 and 72 bytes.
+Q8_DTYPE = np.dtype([("scale", "<f4"), ("values", "i1", (32,))])
+RQ8_DTYPE = np.dtype([("primary", Q8_DTYPE), ("residual", Q8_DTYPE)])
+
+
+class GossmxError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"gossmx status {status}: {message}")
+        self.status = status
+        self.message = message
+
+
+class MatmulProblem(C.Structure):
+    _fields_ = [
+        ("weights", C.c_void_p), ("expert", C.c_size_t), ("activation_kind", C.c_int),
+        ("activations", C.c_void_p), ("activations_len", C.c_size_t), ("m", C.c_size_t),
+        ("blocks_per_row", C.c_size_t), ("row_stride", C.c_size_t), ("bias", C.c_void_p),
+        ("bias_len", C.c_size_t), ("output", C.c_void_p), ("output_len", C.c_size_t),
+        ("output_stride", C.c_size_t), ("memory", C.c_int),
+    ]
+
+
+class MoeConfig(C.Structure):
+    _fields_ = [("experts", C.c_size_t), ("hidden", C.c_size_t), ("intermediate", C.c_size_t),
+                ("top_k", C.c_size_t), ("alpha", C.c_float), ("limit", C.c_float)]
+
+
+class MoeIo(C.Structure):
+    _fields_ = [("x", C.c_void_p), ("m", C.c_size_t), ("injected_logits", C.c_void_p),
+                ("router_logits", C.c_void_p), ("selected", C.c_void_p), ("routing_weights", C.c_void_p),
+                ("output", C.c_void_p), ("route_order", C.c_void_p), ("trace_down", C.c_void_p),
+                ("memory", C.c_int)]
+
+
+class ProfileRecord(C.Structure):
+    _fields_ = [("op", C.c_int), ("launches", C.c_uint64), ("total_ms", C.c_double)]
+
+
+_lib = None
+
+
+def header_symbols() -> list[str]:
+    """Every function the public header declares."""
+    with open(HEADER) as fh:
+        text = fh.read()
+    return sorted(set(re.findall(r"\b(gossmx_[a-z0-9_]+)\s*\(", text)))
+
+
+def load():
+    """Loads libgossmx.so; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise GossmxError(ERR_UNAVAILABLE_BACKEND, f"{LIB_PATH} is not built (run gpt-oss-rs_amd/build.py)")
+    L = C.CDLL(LIB_PATH)
+    vp, sz, i32, u64 = C.c_void_p, C.c_size_t, C.c_int, C.c_uint64
+    pp = C.POINTER(C.c_void_p)
+    sig = {
+        "gossmx_last_error": (C.c_char_p, []),
+        "gossmx_version": (i32, []),
+        "gossmx_device_count": (i32, [C.POINTER(C.c_int)]),
+        "gossmx_ctx_create": (i32, [i32, vp, pp]),
+        "gossmx_ctx_destroy": (None, [vp]),
+        "gossmx_ctx_set_stream": (i32, [vp, vp]),
+        "gossmx_ctx_stream": (vp, [vp]),
+        "gossmx_synchronize": (i32, [vp]),
+        "gossmx_malloc": (i32, [vp, sz, pp]),
+        "gossmx_free": (i32, [vp, vp]),
+        "gossmx_memcpy_h2d": (i32, [vp, vp, vp, sz]),
+        "gossmx_memcpy_d2h": (i32, [vp, vp, vp, sz]),
+        "gossmx_weights_upload": (i32, [vp, vp, sz, sz, sz, sz, i32, pp]),
+        "gossmx_weights_generate": (i32, [vp, u64, u64, sz, sz, sz, pp]),
+        "gossmx_weights_export": (i32, [vp, vp, vp, sz]),
+        "gossmx_weights_shape": (i32, [vp, C.POINTER(sz), C.POINTER(sz), C.POINTER(sz)]),
+        "gossmx_weights_device_bytes": (sz, [vp]),
+        "gossmx_weights_destroy": (None, [vp]),
+        "gossmx_mxfp4_matmul": (i32, [vp, C.POINTER(MatmulProblem)]),
+        "gossmx_mxfp4_matmul_check": (i32, [C.POINTER(MatmulProblem), sz, sz, sz]),
+        "gossmx_layer_create": (i32, [vp, C.POINTER(MoeConfig), vp, vp, vp, vp, vp, vp, pp]),
+        "gossmx_layer_destroy": (None, [vp]),
+        "gossmx_moe_forward": (i32, [vp, vp, C.POINTER(MoeIo)]),
+        "gossmx_profile_enable": (i32, [vp, i32]),
+        "gossmx_profile_read": (i32, [vp, C.POINTER(ProfileRecord), sz, C.POINTER(sz)]),
+        "gossmx_profile_reset": (i32, [vp]),
+        "gossmx_inject_fault": (i32, [vp, i32]),
+        "gossmx_selftest": (i32, [vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(status: int):
+    if status != OK:
+        raise GossmxError(status, load().gossmx_last_error().decode())
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    if isinstance(a, int):
+        return a
+    if hasattr(a, "data_ptr"):  # torch tensor on the device
+        return a.data_ptr()
+    return a.ctypes.data_as(C.c_void_p).value
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    _check(load().gossmx_device_count(C.byref(n)))
+    return n.value
+
+
+class Context:
+    """One device and one in-order stream (CpuExecutionContext analogue)."""
+
+    def __init__(self, device: int = 0, stream: int | None = None):
+        self._h = C.c_void_p()
+        _check(load().gossmx_ctx_create(device, stream, C.byref(self._h)))
+        self.device = device
+
+    @property
+    def handle(self):
+        return self._h
+
+    @property
+    def stream(self) -> int:
+        return load().gossmx_ctx_stream(self._h)
+
+    def set_stream(self, stream: int):
+        _check(load().gossmx_ctx_set_stream(self._h, stream))
+
+    def synchronize(self):
+        _check(load().gossmx_synchronize(self._h))
+
+    def selftest(self):
+        _check(load().gossmx_selftest(self._h))
+
+    def inject_fault(self, armed: bool = True):
+        _check(load().gossmx_inject_fault(self._h, 1 if armed else 0))
+
+    def profile(self, enabled: bool = True):
+        _check(load().gossmx_profile_enable(self._h, 1 if enabled else 0))
+
+    def profile_reset(self):
+        _check(load().gossmx_profile_reset(self._h))
+
+    def profile_read(self) -> dict:
+        recs = (ProfileRecord * len(OPS))()
+        n = C.c_size_t(0)
+        _check(load().gossmx_profile_read(self._h, recs, len(OPS), C.byref(n)))
+        return {OPS[r.op]: {"launches": int(r.launches), "total_ms": float(r.total_ms)} for r in recs[:n.value]}
+
+    def close(self):
+        if self._h:
+            load().gossmx_ctx_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+class Weights:
+    """Resident MXFP4 tensor [experts][rows][blocks] in the GPU layout."""
+
+    def __init__(self, ctx: Context, handle: C.c_void_p):
+        self.ctx = ctx
+        self._h = handle
+        e, r, b = C.c_size_t(), C.c_size_t(), C.c_size_t()
+        _check(load().gossmx_weights_shape(handle, C.byref(e), C.byref(r), C.byref(b)))
+        self.experts, self.rows, self.blocks = e.value, r.value, b.value
+
+    @classmethod
+    def upload(cls, ctx: Context, data: np.ndarray, experts: int, rows: int, blocks: int,
+               layout: int = LAYOUT_CANONICAL_V1) -> "Weights":
+        data = np.ascontiguousarray(data, dtype=np.uint8)
+        h = C.c_void_p()
+        _check(load().gossmx_weights_upload(ctx.handle, _ptr(data), data.size, experts, rows, blocks, layout,
+                                            C.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def generate(cls, ctx: Context, seed: int, stream: int, experts: int, rows: int, blocks: int) -> "Weights":
+        h = C.c_void_p()
+        _check(load().gossmx_weights_generate(ctx.handle, seed, stream, experts, rows, blocks, C.byref(h)))
+        return cls(ctx, h)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def device_bytes(self) -> int:
+        return load().gossmx_weights_device_bytes(self._h)
+
+    def export_canonical(self) -> np.ndarray:
+        out = np.zeros(self.experts * self.rows * self.blocks * 17, np.uint8)
+        _check(load().gossmx_weights_export(self.ctx.handle, self._h, _ptr(out), out.size))
+        return out
+
+    def close(self):
+        if self._h:
+            load().gossmx_weights_destroy(self._h)
+            self._h = C.c_void_p()
+
+
+def _problem(weights, expert, activations, m, bias, output, output_stride, kind, row_stride, memory,
+             activations_len=None, output_len=None, blocks_per_row=None):
+    p = MatmulProblem()
+    p.weights = weights.handle.value if isinstance(weights, Weights) else None
+    p.expert = expert
+    p.activation_kind = kind
+    p.activations = _ptr(activations)
+    p.activations_len = activations_len if activations_len is not None else int(np.asarray(activations).size)
+    p.m = m
+    p.blocks_per_row = weights.blocks if blocks_per_row is None else blocks_per_row
+    p.row_stride = row_stride
+    p.bias = _ptr(bias)
+    p.bias_len = 0 if bias is None else (bias.numel() if hasattr(bias, "numel") else int(np.asarray(bias).size))
+    p.output = _ptr(output)
+    p.output_len = output_len if output_len is not None else (output.numel() if hasattr(output, "numel")
+                                                             else int(np.asarray(output).size))
+    p.output_stride = output_stride
+    p.memory = memory
+    return p
+
+
+def mxfp4_matmul(ctx: Context, weights: Weights, expert: int, activations: np.ndarray, m: int,
+                 bias: np.ndarray | None, output: np.ndarray, output_stride: int | None = None,
+                 kind: int = ACT_RESIDUAL_Q8, row_stride: int | None = None, blocks_per_row: int | None = None):
+    """Kernels::mxfp4_matmul on host arrays (matmul.rs:398-414). `activations`
+    are Q8_DTYPE or RQ8_DTYPE records; columns output_stride > rows of each
+    output row are left untouched."""
+    output_stride = weights.rows if output_stride is None else output_stride
+    row_stride = weights.blocks if row_stride is None else row_stride
+    p = _problem(weights, expert, activations, m, bias, output, output_stride, kind, row_stride, MEM_HOST,
+                 blocks_per_row=blocks_per_row)
+    _check(load().gossmx_mxfp4_matmul(ctx.handle, C.byref(p)))
+    return output
+
+
+def mxfp4_matmul_device(ctx: Context, weights: Weights, expert: int, activations, activations_len: int, m: int,
+                        bias, output, output_len: int, output_stride: int, kind: int = ACT_RESIDUAL_Q8,
+                        row_stride: int | None = None):
+    """Same on device pointers (ints or torch tensors); asynchronous."""
+    row_stride = weights.blocks if row_stride is None else row_stride
+    p = _problem(weights, expert, activations, m, bias, output, output_stride, kind, row_stride, MEM_DEVICE,
+                 activations_len=activations_len, output_len=output_len)
+    _check(load().gossmx_mxfp4_matmul(ctx.handle, C.byref(p)))
+
+
+def matmul_check(rows: int, blocks: int, experts: int, activations_len: int, m: int, blocks_per_row: int,
+                 row_stride: int, bias_len: int | None, output_len: int, output_stride: int,
+                 kind: int = ACT_RESIDUAL_Q8, expert: int = 0) -> int:
+    """Status of the problem validation alone (no device needed)."""
+    p = MatmulProblem()
+    p.weights = None
+    p.expert = expert
+    p.activation_kind = kind
+    p.activations = 1  # non-null placeholder, never dereferenced
+    p.activations_len = activations_len
+    p.m = m
+    p.blocks_per_row = blocks_per_row
+    p.row_stride = row_stride
+    p.bias = None if bias_len is None else 1
+    p.bias_len = 0 if bias_len is None else bias_len
+    p.output = 1
+    p.output_len = output_len
+    p.output_stride = output_stride
+    p.memory = MEM_HOST
+    return load().gossmx_mxfp4_matmul_check(C.byref(p), rows, blocks, experts)
+
+
+@dataclass
+class MoeStep:
+    """CpuMoeStep (cpu_runner.rs:569-575)."""
+    router_logits: np.ndarray
+    selected_experts: np.ndarray
+    routing_weights: np.ndarray
+    output: np.ndarray
+
+
+class MoeLayer:
+    """One GPT-OSS MoE layer resident on the device."""
+
+    def __init__(self, ctx: Context, experts: int, hidden: int, intermediate: int, top_k: int,
+                 router_weight: np.ndarray, router_bias: np.ndarray, gate_up: Weights, gate_up_bias: np.ndarray,
+                 down: Weights, down_bias: np.ndarray, alpha: float = 1.702, limit: float = 7.0):
+        self.ctx = ctx
+        self.experts, self.hidden, self.intermediate, self.top_k = experts, hidden, intermediate, top_k
+        cfg = MoeConfig(experts, hidden, intermediate, top_k, alpha, limit)
+        rw = np.ascontiguousarray(router_weight, dtype=np.uint16)
+        rb = np.ascontiguousarray(router_bias, dtype=np.float32)
+        gb = np.ascontiguousarray(gate_up_bias, dtype=np.float32)
+        db = np.ascontiguousarray(down_bias, dtype=np.float32)
+        self._h = C.c_void_p()
+        _check(load().gossmx_layer_create(ctx.handle, C.byref(cfg), _ptr(rw), _ptr(rb), gate_up.handle, _ptr(gb),
+                                          down.handle, _ptr(db), C.byref(self._h)))
+        self.gate_up, self.down = gate_up, down
+
+    def forward(self, x_bf16: np.ndarray, injected_logits: np.ndarray | None = None, trace: bool = False) -> dict:
+        """All outputs as arrays: router_logits, selected, routing_weights,
+        output, route_order (+ trace_down)."""
+        x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+        m = x.shape[0]
+        E, K, H = self.experts, self.top_k, self.hidden
+        res = {
+            "router_logits": np.zeros((m, E), np.float32),
+            "selected": np.zeros((m, K), np.uint32),
+            "routing_weights": np.zeros((m, K), np.float32),
+            "output": np.zeros((m, H), np.float32),
+            "route_order": np.zeros(m * K, np.uint32),
+        }
+        if trace:
+            res["trace_down"] = np.zeros((m, K, H), np.float32)
+        inj = None if injected_logits is None else np.ascontiguousarray(injected_logits, dtype=np.float32)
+        io = MoeIo(_ptr(x), m, _ptr(inj), _ptr(res["router_logits"]), _ptr(res["selected"]),
+                   _ptr(res["routing_weights"]), _ptr(res["output"]), _ptr(res["route_order"]),
+                   _ptr(res.get("trace_down")), MEM_HOST)
+        _check(load().gossmx_moe_forward(self.ctx.handle, self._h, C.byref(io)))
+        return res
+
+    def forward_device(self, x, m: int, output, injected_logits=None, router_logits=None, selected=None,
+                       routing_weights=None, route_order=None):
+        """Asynchronous forward on device pointers (ints or torch tensors);
+        device-side errors surface at the next Context.synchronize()."""
+        io = MoeIo(_ptr(x), m, _ptr(injected_logits), _ptr(router_logits), _ptr(selected), _ptr(routing_weights),
+                   _ptr(output), _ptr(route_order), None, MEM_DEVICE)
+        _check(load().gossmx_moe_forward(self.ctx.handle, self._h, C.byref(io)))
+
+    def moe_batch(self, inputs: np.ndarray, injected_logits: np.ndarray | None = None) -> list[MoeStep]:
+        """CpuModel::moe_batch: one MoeStep per input row."""
+        r = self.forward(inputs, injected_logits)
+        return [MoeStep(r["router_logits"][i], r["selected"][i].astype(np.int64), r["routing_weights"][i],
+                        r["output"][i]) for i in range(r["output"].shape[0])]
+
+    def close(self):
+        if self._h:
+            load().gossmx_layer_destroy(self._h)
+            self._h = C.c_void_p()

@@ -1,0 +1,221 @@
+/*
+ * gossmx: MI355X (gfx950) MXFP4 mixture-of-experts block for GPT-OSS.
+ *
+ * C ABI of libgossmx.so. Plain pointers and sizes only. Every entry point
+ * returns a gossmx_status; the message of the last failure on the calling
+ * thread is available from gossmx_last_error().
+ *
+ * Reference interfaces replaced (paths relative to gpt-oss-rs v0.1.0):
+ *   - gossmx_mxfp4_matmul       <- Kernels::mxfp4_matmul(backend, Mxfp4MatmulProblem, scratch)
+ *                                  crates/gpt-oss-cpu-kernels/src/matmul.rs:398-414, problem
+ *                                  constructors and validation matmul.rs:297-369
+ *   - gossmx_moe_forward        <- CpuModel::moe_batch(layer, idx, inputs, capture, ...)
+ *                                  crates/gpt-oss-model-runner/src/cpu_runner.rs:2794-3013
+ *   - gossmx_weights_upload     <- CpuRepackCache::open_or_create + RepackedMxfp4::expert_view
+ *                                  crates/gpt-oss-model-runner/src/cpu_repack.rs:149-216,302-318
+ *                                  (the resident copy is a new GPU layout, see below)
+ *   - gossmx_layer_create       <- load_layer (router/gate_up/down tensors and biases)
+ *                                  crates/gpt-oss-model-runner/src/cpu_runner.rs:3526-3671
+ *   - gossmx_status codes       <- KernelError variants, crates/gpt-oss-cpu-kernels/src/lib.rs:138-157,
+ *                                  and the non-finite router ModelError, cpu_runner.rs:2829-2834
+ *   - gossmx_profile_*          <- CpuExecutionProfiler records, cpu_profile.rs:30-51
+ *   - gossmx_inject_fault       <- CpuExecutionFailurePoint test hook, cpu_runner.rs:478-483
+ *
+ * Weight layouts accepted on upload (Mxfp4WeightLayout, lib.rs:70-90):
+ *   GOSSMX_LAYOUT_CANONICAL_V1 : per (row, block) 17 bytes = E8M0 scale byte, then
+ *                                16 bytes with code(2j) | code(2j+1) << 4.
+ *   GOSSMX_LAYOUT_X8_SPLIT_V2  : complete 8-row groups of 136-byte records, rows % 8
+ *                                tail canonical (lib.rs:810-851, cpu_repack.rs:437-480).
+ * Resident layout (GOSSMX_LAYOUT_GPU_TILED_V3, device only): 16-row tiles; a nibble
+ * plane where each 64-lane wave loads one contiguous 1 KiB segment per 4 K-blocks,
+ * and a separate E8M0 scale plane. Same 17 bytes per (row, block).
+ *
+ * Threading: a context owns one HIP stream and is used by one thread at a time
+ * (like CpuExecutionContext, cpu_runner.rs:868-876). Calls are asynchronous on that
+ * stream unless they return host data; gossmx_synchronize() waits.
+ */
+#ifndef GOSSMX_H
+#define GOSSMX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum gossmx_status {
+  GOSSMX_OK = 0,
+  GOSSMX_ERR_INVALID_ARGUMENT = 1,    /* null pointer or unknown enum value */
+  GOSSMX_ERR_UNSUPPORTED = 2,         /* shape this build does not handle */
+  GOSSMX_ERR_INVALID_DIMENSIONS = 3,  /* KernelError::InvalidDimensions */
+  GOSSMX_ERR_NON_FINITE_INPUT = 4,    /* KernelError::NonFiniteInput */
+  GOSSMX_ERR_UNAVAILABLE_BACKEND = 5, /* KernelError::UnavailableMatmulBackend (no gfx950 device) */
+  GOSSMX_ERR_DEVICE = 6,              /* HIP runtime error */
+  GOSSMX_ERR_OUT_OF_MEMORY = 7,
+  GOSSMX_ERR_NON_FINITE_LOGITS = 8,   /* "CPU router produced non-finite logits" */
+  GOSSMX_ERR_INJECTED_FAULT = 9       /* gossmx_inject_fault test hook fired */
+} gossmx_status;
+
+enum {
+  GOSSMX_LAYOUT_CANONICAL_V1 = 1,
+  GOSSMX_LAYOUT_X8_SPLIT_V2 = 2,
+  GOSSMX_LAYOUT_GPU_TILED_V3 = 3
+};
+
+enum { GOSSMX_ACT_Q8 = 1, GOSSMX_ACT_RESIDUAL_Q8 = 2 };
+
+/* Where the caller's activation/bias/output pointers live. */
+enum { GOSSMX_MEM_HOST = 0, GOSSMX_MEM_DEVICE = 1 };
+
+typedef struct gossmx_ctx gossmx_ctx;
+typedef struct gossmx_weights gossmx_weights;
+typedef struct gossmx_layer gossmx_layer;
+
+/* Last failure message of the calling thread ("" when none). */
+const char* gossmx_last_error(void);
+/* Library/ABI version: major * 10000 + minor * 100 + patch. */
+int gossmx_version(void);
+/* Number of visible gfx950 devices (0 on a host without one). */
+int gossmx_device_count(int* count);
+
+/* Context: one device, one in-order HIP stream. `stream` may be NULL (the
+ * context creates its own) or a caller hipStream_t (not destroyed by us). */
+int gossmx_ctx_create(int device, void* stream, gossmx_ctx** out);
+void gossmx_ctx_destroy(gossmx_ctx* ctx);
+int gossmx_ctx_set_stream(gossmx_ctx* ctx, void* stream);
+void* gossmx_ctx_stream(gossmx_ctx* ctx);
+int gossmx_synchronize(gossmx_ctx* ctx);
+
+/* Device memory helpers (so non-PyTorch callers can stage device buffers). */
+int gossmx_malloc(gossmx_ctx* ctx, size_t bytes, void** out);
+int gossmx_free(gossmx_ctx* ctx, void* ptr);
+int gossmx_memcpy_h2d(gossmx_ctx* ctx, void* dst, const void* src, size_t bytes);
+int gossmx_memcpy_d2h(gossmx_ctx* ctx, void* dst, const void* src, size_t bytes);
+
+/* Resident MXFP4 weights [experts][rows][blocks] (17 B per row-block).
+ * `data` is host memory in `layout` (canonical v1 or x8 v2), `len` must be
+ * experts * rows * blocks * 17 bytes, each expert laid out independently as
+ * RepackedMxfp4::expert_view yields it. Repacked on the device to v3. */
+int gossmx_weights_upload(gossmx_ctx* ctx, const uint8_t* data, size_t len, size_t experts, size_t rows,
+                          size_t blocks, int layout, gossmx_weights** out);
+/* Synthetic weights generated on the device: record i = (expert*rows+row)*blocks+block
+ * takes two 64-bit counter hashes h0 = H(seed, stream, 2i), h1 = H(seed, stream, 2i+1)
+ * (SplitMix64 based); scale byte = 119 + (h1 >> 61) % 5, packed bytes = h0 then h1
+ * little-endian. Equal to the canonical tensor a host generator of the same rule makes. */
+int gossmx_weights_generate(gossmx_ctx* ctx, uint64_t seed, uint64_t stream, size_t experts, size_t rows,
+                            size_t blocks, gossmx_weights** out);
+/* Copy the resident weights back to host memory in layout v1 (canonical). */
+int gossmx_weights_export(gossmx_ctx* ctx, const gossmx_weights* w, uint8_t* out, size_t len);
+int gossmx_weights_shape(const gossmx_weights* w, size_t* experts, size_t* rows, size_t* blocks);
+size_t gossmx_weights_device_bytes(const gossmx_weights* w);
+void gossmx_weights_destroy(gossmx_weights* w);
+
+/* Kernel boundary: C[m, n] = A[m, K] . W[expert][n, K]^T + bias[n] for n < rows,
+ * written at output[i * output_stride + n]; columns rows..output_stride-1 of each
+ * output row are never written. Activations are the reference's records:
+ * Q8Block {f32 scale; i8 values[32]} (36 B) or ResidualQ8Block {Q8Block primary;
+ * Q8Block residual} (72 B), row i at activations + i * row_stride records
+ * (ResidualQ8MatrixView, lib.rs). The float accumulation per output is the
+ * reference's: total = bias; per block in order total += (p * 0.5 * e8m0) * ps
+ * (then the residual term), bit-identical to scalar_matmul_range
+ * (matmul.rs:529-578). Validation failures return before any output write. */
+typedef struct gossmx_matmul_problem {
+  const gossmx_weights* weights;
+  size_t expert;
+  int activation_kind;     /* GOSSMX_ACT_Q8 or GOSSMX_ACT_RESIDUAL_Q8 */
+  const void* activations; /* records, see above */
+  size_t activations_len;  /* in records */
+  size_t m;                /* activation rows */
+  size_t blocks_per_row;   /* must equal the weights' blocks */
+  size_t row_stride;       /* in records, >= blocks_per_row */
+  const float* bias;       /* nullable, bias_len == rows */
+  size_t bias_len;
+  float* output;
+  size_t output_len;       /* in floats, >= (m - 1) * output_stride + rows */
+  size_t output_stride;    /* >= rows */
+  int memory;              /* GOSSMX_MEM_HOST or GOSSMX_MEM_DEVICE for activations/bias/output */
+} gossmx_matmul_problem;
+
+int gossmx_mxfp4_matmul(gossmx_ctx* ctx, const gossmx_matmul_problem* problem);
+/* The validation gossmx_mxfp4_matmul runs first, against a weights shape, with
+ * no device access (Mxfp4MatmulProblem::new, matmul.rs:339-369). */
+int gossmx_mxfp4_matmul_check(const gossmx_matmul_problem* problem, size_t rows, size_t blocks, size_t experts);
+
+/* MoE layer (GPT-OSS): router [experts][hidden] bf16 + f32 bias, gate_up
+ * [experts][2*intermediate][hidden/32] with gate/up rows interleaved even/odd
+ * and f32 bias [experts][2*intermediate], down [experts][hidden][intermediate/32]
+ * and f32 bias [experts][hidden]. Host arrays are copied; weights are borrowed
+ * (they must outlive the layer). */
+typedef struct gossmx_moe_config {
+  size_t experts;      /* num_local_experts, <= 128 */
+  size_t hidden;       /* hidden_size, multiple of 32 */
+  size_t intermediate; /* intermediate_size, multiple of 32 */
+  size_t top_k;        /* num_experts_per_tok, 1..8 and <= experts */
+  float alpha;         /* 1.702 */
+  float limit;         /* swiglu_limit, 7.0 */
+} gossmx_moe_config;
+
+int gossmx_layer_create(gossmx_ctx* ctx, const gossmx_moe_config* config, const uint16_t* router_weight_bf16,
+                        const float* router_bias, const gossmx_weights* gate_up, const float* gate_up_bias,
+                        const gossmx_weights* down, const float* down_bias, gossmx_layer** out);
+void gossmx_layer_destroy(gossmx_layer* layer);
+
+/* One MoE block over m rows (CpuMoeStep per row, cpu_runner.rs:569-575).
+ * Required: x [m][hidden] bf16 and output [m][hidden] f32 (bf16-rounded values).
+ * Optional (nullable): injected_logits [m][experts] replaces the router
+ * projection output before its bf16 round trip; router_logits [m][experts];
+ * selected [m][top_k]; routing_weights [m][top_k]; route_order [m*top_k] receives
+ * row * top_k + rank in the grouped (expert, row, rank) order; trace_down
+ * [m][top_k][hidden] receives each rank's bf16-rounded down projection.
+ * All pointers are host or device memory as `memory` says. */
+typedef struct gossmx_moe_io {
+  const uint16_t* x;
+  size_t m;
+  const float* injected_logits;
+  float* router_logits;
+  uint32_t* selected;
+  float* routing_weights;
+  float* output;
+  uint32_t* route_order;
+  float* trace_down;
+  int memory;
+} gossmx_moe_io;
+
+int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* layer, const gossmx_moe_io* io);
+
+/* Profiling with hipEvents on the context stream, in the reference's operation
+ * vocabulary (CpuProfileOperation, cpu_profile.rs:30-51). */
+enum {
+  GOSSMX_OP_ROUTER_ROUTING = 0,     /* RouterProjection + Routing + ResidualQ8Preparation */
+  GOSSMX_OP_DISPATCH = 1,           /* stable_group_routes + bucket gather */
+  GOSSMX_OP_GATE_UP = 2,            /* GateUpProjection + SwiGlu + the down input quantization */
+  GOSSMX_OP_DOWN = 3,               /* DownProjection */
+  GOSSMX_OP_WEIGHTING = 4,          /* ExpertWeightingAccumulation */
+  GOSSMX_OP_MATMUL = 5,             /* gossmx_mxfp4_matmul kernel */
+  GOSSMX_OP_COUNT = 6
+};
+typedef struct gossmx_profile_record {
+  int op;
+  uint64_t launches;
+  double total_ms;
+} gossmx_profile_record;
+int gossmx_profile_enable(gossmx_ctx* ctx, int enabled);
+/* Synchronizes, folds pending events into totals, writes GOSSMX_OP_COUNT records. */
+int gossmx_profile_read(gossmx_ctx* ctx, gossmx_profile_record* out, size_t capacity, size_t* written);
+int gossmx_profile_reset(gossmx_ctx* ctx);
+
+/* Test hook: the next gossmx_moe_forward / gossmx_mxfp4_matmul on this context
+ * fails with GOSSMX_ERR_INJECTED_FAULT before launching anything (outputs untouched). */
+int gossmx_inject_fault(gossmx_ctx* ctx, int armed);
+
+/* Device self-test of the lane layouts the GEMM relies on (FP4 -> f16
+ * conversion order, 16x16x32 MFMA operand/result layout). No counterpart in
+ * the reference; GOSSMX_ERR_UNSUPPORTED with a message on mismatch. */
+int gossmx_selftest(gossmx_ctx* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GOSSMX_H */

@@ -1,0 +1,186 @@
+"""GPU parity of the MoE block (gossmx_moe_forward) against the oracle's
+moe_batch (cpu_runner.rs:2794-3013): router logits, expert indices, routing
+order, routing weights and output, all bit-exact; plus error paths and the
+full-size properties (row independence) at the benchmark shapes."""
+import numpy as np
+import pytest
+
+import gossmx as G
+import oracle as O
+import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = G.Context(0)
+    yield c
+    c.close()
+
+
+def gpu_layer(ctx, host: O.MoeLayerHost):
+    E, H, I = host.experts, host.hidden, host.intermediate
+    gu = G.Weights.upload(ctx, host.gate_up, E, 2 * I, H // 32)
+    dn = G.Weights.upload(ctx, host.down, E, H, I // 32)
+    return G.MoeLayer(ctx, E, H, I, host.top_k, host.router_weight, host.router_bias, gu, host.gate_up_bias, dn,
+                      host.down_bias, host.alpha, host.limit)
+
+
+def close(layer):
+    layer.close()
+    layer.gate_up.close()
+    layer.down.close()
+
+
+def assert_moe_equal(got, want):
+    for key in ("router_logits", "routing_weights", "output"):
+        g = np.ascontiguousarray(got[key], np.float32).view(np.uint32)
+        w = np.ascontiguousarray(want[key], np.float32).view(np.uint32)
+        bad = np.argwhere(g != w)
+        assert bad.size == 0, f"{key}: {len(bad)} mismatches, first {bad[:3].tolist()}"
+    assert (got["selected"] == want["selected"]).all(), "expert indices differ"
+    assert (got["route_order"] == want["route_order"]).all(), "routing order differs"
+
+
+@pytest.mark.parametrize("experts,hidden,inter,top_k,m", [(3, 64, 32, 2, 2), (4, 96, 64, 2, 5), (8, 128, 96, 4, 17),
+                                                           (32, 256, 128, 4, 70)])
+def test_small_layers_bit_exact(ctx, experts, hidden, inter, top_k, m):
+    host = O.synthetic_layer(11, 0, experts=experts, hidden=hidden, intermediate=inter, top_k=top_k)
+    x = O.gen_hidden(11, 100, m, hidden)
+    want = O.moe_batch(host, x, trace=True)
+    assert want["status"] == O.OK
+    layer = gpu_layer(ctx, host)
+    got = layer.forward(x, trace=True)
+    assert_moe_equal(got, want)
+    assert (got["trace_down"].view(np.uint32) == want["down"].view(np.uint32)).all()
+    close(layer)
+
+
+@pytest.fixture(scope="module")
+def layer20b(ctx):
+    host = O.synthetic_layer(2024, 0)
+    layer = gpu_layer(ctx, host)
+    yield host, layer
+    close(layer)
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_20b_shape_decode_bit_exact(layer20b, m):
+    host, layer = layer20b
+    x = O.gen_hidden(2024, 200 + m, m, 2880)
+    want = O.moe_batch(host, x)
+    assert want["status"] == O.OK
+    assert_moe_equal(layer.forward(x), want)
+
+
+def test_20b_shape_zipf_batch64_rows_match(layer20b):
+    """Batch 64 with injected Zipf(1.1) logits; the oracle checks a sample of
+    rows (each row's result depends only on that row)."""
+    host, layer = layer20b
+    rng = np.random.default_rng(64)
+    x = synth.hidden_rows(rng, 64)
+    logits = synth.zipf_logits(rng, 64, 32)
+    got = layer.forward(x, injected_logits=logits)
+    rows = [0, 17, 63]
+    want = O.moe_batch(host, x[rows], injected_logits=logits[rows])
+    for key in ("router_logits", "routing_weights", "output", "selected"):
+        assert (np.ascontiguousarray(got[key][rows]).view(np.uint32)
+                == np.ascontiguousarray(want[key]).view(np.uint32)).all(), key
+    # The full grouped order is the stable sort of all routes by expert.
+    sel = got["selected"].ravel()
+    order = np.argsort(sel, kind="stable")
+    assert (got["route_order"] == order).all()
+
+
+def test_prefill_2048_rows_match_and_group(layer20b):
+    host, layer = layer20b
+    rng = np.random.default_rng(2048)
+    x = synth.hidden_rows(rng, 2048)
+    got = layer.forward(x)
+    sel = got["selected"].ravel()
+    assert (got["route_order"] == np.argsort(sel, kind="stable")).all()
+    counts = np.bincount(sel, minlength=32)
+    assert counts.sum() == 2048 * 4 and counts.max() > 64  # several chunks per expert
+    rows = [0, 1, 1023, 2047]
+    want = O.moe_batch(host, x[rows])
+    for key in ("router_logits", "routing_weights", "output", "selected"):
+        assert (np.ascontiguousarray(got[key][rows]).view(np.uint32)
+                == np.ascontiguousarray(want[key]).view(np.uint32)).all(), key
+
+
+def test_all_experts_selected(ctx):
+    host = O.synthetic_layer(5, 0, experts=4, hidden=64, intermediate=64, top_k=4)
+    x = O.gen_hidden(5, 1, 9, 64)
+    want = O.moe_batch(host, x)
+    layer = gpu_layer(ctx, host)
+    assert_moe_equal(layer.forward(x), want)
+    close(layer)
+
+
+def test_tied_logits_route_to_lower_index(ctx):
+    host = O.synthetic_layer(6, 0, experts=8, hidden=64, intermediate=32, top_k=4)
+    x = O.gen_hidden(6, 1, 3, 64)
+    logits = np.zeros((3, 8), np.float32)
+    logits[0, [1, 5, 6]] = 1.0
+    logits[1] = -0.0
+    logits[2, 7] = 2.0
+    logits[2, 3] = 2.0
+    want = O.moe_batch(host, x, injected_logits=logits)
+    layer = gpu_layer(ctx, host)
+    got = layer.forward(x, injected_logits=logits)
+    assert_moe_equal(got, want)
+    assert got["selected"][0].tolist() == [1, 5, 6, 0]
+    assert got["selected"][1].tolist() == [0, 1, 2, 3]
+    close(layer)
+
+
+def test_non_finite_logits_and_inputs_fail(ctx):
+    host = O.synthetic_layer(7, 0, experts=4, hidden=64, intermediate=32, top_k=2)
+    layer = gpu_layer(ctx, host)
+    x = O.gen_hidden(7, 1, 2, 64)
+    logits = np.zeros((2, 4), np.float32)
+    logits[1, 2] = np.inf
+    with pytest.raises(G.GossmxError) as e:
+        layer.forward(x, injected_logits=logits)
+    assert e.value.status == G.ERR_NON_FINITE_LOGITS
+    assert O.moe_batch(host, x, injected_logits=logits)["status"] == O.NON_FINITE_LOGITS
+    bad = x.copy()
+    bad[0, 5] = 0x7F80  # +inf bf16: the router logits become non-finite first
+    with pytest.raises(G.GossmxError) as e:
+        layer.forward(bad)
+    assert e.value.status == G.ERR_NON_FINITE_LOGITS
+    with pytest.raises(G.GossmxError) as e:  # injected finite logits: the quantizer rejects the input
+        layer.forward(bad, injected_logits=np.zeros((2, 4), np.float32))
+    assert e.value.status == G.ERR_NON_FINITE_INPUT
+    # the context recovers
+    want = O.moe_batch(host, x)
+    assert_moe_equal(layer.forward(x), want)
+    close(layer)
+
+
+def test_injected_fault_leaves_outputs_untouched(ctx):
+    host = O.synthetic_layer(8, 0, experts=4, hidden=64, intermediate=32, top_k=2)
+    layer = gpu_layer(ctx, host)
+    x = O.gen_hidden(8, 1, 2, 64)
+    ctx.inject_fault(True)
+    with pytest.raises(G.GossmxError) as e:
+        layer.forward(x)
+    assert e.value.status == G.ERR_INJECTED_FAULT
+    assert_moe_equal(layer.forward(x), O.moe_batch(host, x))
+    close(layer)
+
+
+def test_profiler_counts_every_stage(ctx):
+    host = O.synthetic_layer(9, 0, experts=4, hidden=64, intermediate=32, top_k=2)
+    layer = gpu_layer(ctx, host)
+    x = O.gen_hidden(9, 1, 4, 64)
+    ctx.profile(True)
+    ctx.profile_reset()
+    for _ in range(3):
+        layer.forward(x)
+    rec = ctx.profile_read()
+    ctx.profile(False)
+    for op in ("router_routing", "dispatch", "gate_up", "down", "weighting"):
+        assert rec[op]["launches"] == 3 and rec[op]["total_ms"] > 0.0
+    close(layer)
