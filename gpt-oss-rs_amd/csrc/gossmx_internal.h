@@ -11,7 +11,7 @@ namespace gossmx {
 constexpr int kBlock = 32;      // values per MXFP4 / Q8 block (QUANT_BLOCK_SIZE)
 constexpr int kRecord = 17;     // E8M0 byte + 16 packed nibble bytes per (row, block)
 constexpr int kTileRows = 16;   // rows per MFMA tile (one wave)
-constexpr int kWgRows = 64;     // rows per work-group (four waves)
+constexpr int kWgRows = 64;     // gate_up rows (32 gate/up pairs) per 32-value block of the down input
 constexpr int kChunk = 64;      // activation rows per work item
 constexpr int kMaxExperts = 128;
 constexpr int kMaxTopK = 8;

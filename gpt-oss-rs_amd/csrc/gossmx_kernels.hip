@@ -296,13 +296,21 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Expert GEMM on the resident v3 layout. One work-group = 4 waves = 64 weight
-// rows (one 16-row tile per wave) x one work item (<= 64 activation rows).
-// Each lane owns one weight row (lane % 16) and two activation rows per group
-// of 8, and runs the reference's per-row float chain in order:
+// Expert GEMM on the resident v3 layout. One work-group = kWaves waves, one
+// 16-row weight tile per wave (128 rows), times one work item (<= 64
+// activation rows). Each lane owns one weight row (lane % 16) and two
+// activation rows per group of 8, and runs the reference's per-row float
+// chain in order:
 //   total = bias; for each block: total += (p * ws) * ps; total += (r * ws) * rs
 // (mxfp4_residual_q8_gemv_rows lib.rs:673-696, scalar_matmul_range
 // matmul.rs:529-578).
+//
+// Streaming: K is walked in groups of 4 blocks. Each wave keeps the weights of
+// the next kPrefetch groups in flight in registers (one 16-byte load per lane
+// per group, a 1 KiB contiguous segment per wave). The work item's activations
+// for a group (f16 codes and scales) are staged through LDS once per
+// work-group: loaded from global memory into registers one group ahead, then
+// written to LDS between two barriers, so all waves share one L2 read.
 
 __device__ __forceinline__ half8 fp4x8_to_half8(uint32_t w) {
   const half2v h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0);
@@ -315,9 +323,51 @@ __device__ __forceinline__ half8 fp4x8_to_half8(uint32_t w) {
   return b;
 }
 
+constexpr int kWaves = 8;                  // waves per GEMM work-group
+constexpr int kGemmThreads = 64 * kWaves;  // 512
+constexpr int kGemmRows = 16 * kWaves;     // weight rows per work-group
+constexpr int kPrefetch = 3;               // weight groups in flight per wave
+// Activation staging: per group, count * nb rows of 128 bytes (8 chunks of 16 B).
+constexpr int kStageChunks = (kChunk * 4 * 8 + kGemmThreads - 1) / kGemmThreads;  // 4 per thread
+
+struct WeightGroup {
+  uint4 v;
+  uint32_t s;
+};
+
+__device__ __forceinline__ WeightGroup load_weight_group(const uint8_t* nib, const uint8_t* scl, int q, int B,
+                                                         int lane, int nl) {
+  WeightGroup g;
+  g.v = make_uint4(0u, 0u, 0u, 0u);
+  g.s = 0u;
+  const int nq = (B + 3) >> 2;
+  if (q >= nq) return g;
+  const int nb = min(4, B - 4 * q);
+  const uint8_t* gn = nib + (size_t)q * 1024;
+  const uint8_t* gs = scl + (size_t)q * 64;
+  if (nb == 4) {
+    g.v = *reinterpret_cast<const uint4*>(gn + lane * 16);
+    g.s = *reinterpret_cast<const uint32_t*>(gs + nl * 4);
+  } else {  // last group of a K that is not a multiple of 4 blocks: nb = 1..3
+    const uint32_t* gw = reinterpret_cast<const uint32_t*>(gn + lane * nb * 4);
+    g.v.x = gw[0];
+    g.s = gs[nl * nb];
+    if (nb > 1) {
+      g.v.y = gw[1];
+      g.s |= (uint32_t)gs[nl * nb + 1] << 8;
+    }
+    if (nb > 2) {
+      g.v.z = gw[2];
+      g.s |= (uint32_t)gs[nl * nb + 2] << 16;
+    }
+  }
+  return g;
+}
+
 template <int MODE>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
   const int nl = lane & 15, G = lane >> 4;
   int expert, start, count, route_base = 0;
   if (MODE == kPlain) {
@@ -332,21 +382,25 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     route_base = a.bucket_off[expert];
     count = min(kChunk, a.bucket_off[expert + 1] - route_base - start);
   }
+  // LDS: activation codes [4 blocks][64 rows][2 parts][32] f16 and scales
+  // [4][64] float2 for the current group; reused as SwiGLU staging afterwards.
+  __shared__ __align__(16) _Float16 s_actv[4 * kChunk * 2 * kBlock];
+  __shared__ __align__(16) float2 s_acts[4 * kChunk];
   __shared__ int s_row[kChunk];
-  if (threadIdx.x < kChunk) {
-    const int c = threadIdx.x;
+  if (tid < kChunk) {
     int r = -1;
-    if (c < count) {
-      if (MODE == kPlain) r = start + c;
-      else if (MODE == kGateUp) r = a.route_tok[route_base + start + c];
-      else r = route_base + start + c;
+    if (tid < count) {
+      if (MODE == kPlain) r = start + tid;
+      else if (MODE == kGateUp) r = a.route_tok[route_base + start + tid];
+      else r = route_base + start + tid;
     }
-    s_row[c] = r;
+    s_row[tid] = r;
   }
   __syncthreads();
 
   const int rows = (int)a.w.rows, B = (int)a.w.blocks;
-  const int tile = blockIdx.x * 4 + wave;
+  const int nq = (B + 3) >> 2;
+  const int tile = blockIdx.x * kWaves + wave;
   const bool tile_ok = tile < (int)a.w.tiles;
   const int row = tile * kTileRows + nl;
   const int n_tg = (count + 7) >> 3;
@@ -358,56 +412,91 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 #pragma unroll
   for (int tg = 0; tg < 8; ++tg) { tot[tg][0] = b0; tot[tg][1] = b0; }
 
-  if (tile_ok) {
-    const uint8_t* nib = a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)tile * 256 * B;
-    const uint8_t* scl = a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)tile * 16 * B;
-    int arow[8], erow0[8], erow1[8];
+  const int safe_tile = tile_ok ? tile : 0;
+  const uint8_t* nib = a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)safe_tile * 256 * B;
+  const uint8_t* scl = a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)safe_tile * 16 * B;
+  WeightGroup wg[kPrefetch];
 #pragma unroll
-    for (int tg = 0; tg < 8; ++tg) {
-      arow[tg] = s_row[tg * 8 + (nl >> 1)];
-      erow0[tg] = s_row[tg * 8 + 2 * G];
-      erow1[tg] = s_row[tg * 8 + 2 * G + 1];
-    }
-    const int part = nl & 1;
-    const float2* acts = reinterpret_cast<const float2*>(a.acts);
-    const int nq = (B + 3) >> 2;
-    for (int q = 0; q < nq; ++q) {
+  for (int p = 0; p < kPrefetch; ++p) wg[p] = load_weight_group(nib, scl, tile_ok ? p : nq, B, lane, nl);
+
+  // Activation staging registers for one group: kStageChunks (4) 16-byte
+  // pieces per thread, unrolled by hand so that they stay in VGPRs.
+  static_assert(kStageChunks == 4, "staging is unrolled for 4 pieces per thread");
+  uint4 st0 = make_uint4(0u, 0u, 0u, 0u), st1 = st0, st2 = st0, st3 = st0;
+  float2 stage_s = make_float2(0.0f, 0.0f);
+  const uint4* gactv = reinterpret_cast<const uint4*>(a.actv);
+  const float2* gacts = reinterpret_cast<const float2*>(a.acts);
+  uint4* lds_actv = reinterpret_cast<uint4*>(s_actv);
+  const int per_block = count * 8;  // 16-byte pieces per block of the group
+#define GOSSMX_STAGE_PIECE_LOAD(REG, I, QQ, ITEMS)                                       \
+  {                                                                                      \
+    const int c = tid + (I) * kGemmThreads;                                              \
+    if (c < (ITEMS)) {                                                                   \
+      const int j = c / per_block, rem = c - j * per_block;                              \
+      REG = gactv[((size_t)s_row[rem >> 3] * B + 4 * (QQ) + j) * 8 + (rem & 7)];         \
+    }                                                                                    \
+  }
+#define GOSSMX_STAGE_PIECE_STORE(REG, I, ITEMS)                                          \
+  {                                                                                      \
+    const int c = tid + (I) * kGemmThreads;                                              \
+    if (c < (ITEMS)) {                                                                   \
+      const int j = c / per_block, rem = c - j * per_block;                              \
+      lds_actv[(j * kChunk + (rem >> 3)) * 8 + (rem & 7)] = REG;                          \
+    }                                                                                    \
+  }
+#define GOSSMX_STAGE_LOAD(QQ)                                                            \
+  do {                                                                                   \
+    const int nb_ = min(4, B - 4 * (QQ));                                                \
+    const int items_ = per_block * nb_;                                                  \
+    GOSSMX_STAGE_PIECE_LOAD(st0, 0, QQ, items_)                                          \
+    GOSSMX_STAGE_PIECE_LOAD(st1, 1, QQ, items_)                                          \
+    GOSSMX_STAGE_PIECE_LOAD(st2, 2, QQ, items_)                                          \
+    GOSSMX_STAGE_PIECE_LOAD(st3, 3, QQ, items_)                                          \
+    if (tid < count * nb_) stage_s = gacts[(size_t)s_row[tid % count] * B + 4 * (QQ) + tid / count]; \
+  } while (0)
+#define GOSSMX_STAGE_STORE(QQ)                                                           \
+  do {                                                                                   \
+    const int nb_ = min(4, B - 4 * (QQ));                                                \
+    const int items_ = per_block * nb_;                                                  \
+    GOSSMX_STAGE_PIECE_STORE(st0, 0, items_)                                             \
+    GOSSMX_STAGE_PIECE_STORE(st1, 1, items_)                                             \
+    GOSSMX_STAGE_PIECE_STORE(st2, 2, items_)                                             \
+    GOSSMX_STAGE_PIECE_STORE(st3, 3, items_)                                             \
+    if (tid < count * nb_) s_acts[(tid / count) * kChunk + tid % count] = stage_s;        \
+  } while (0)
+
+  GOSSMX_STAGE_LOAD(0);
+  const int part = nl & 1;
+  const int a_tok = nl >> 1;  // token within a group of 8 for the A operand
+  for (int q = 0; q < nq; ++q) {
+    __syncthreads();  // every wave is done reading the previous group
+    GOSSMX_STAGE_STORE(q);
+    __syncthreads();
+    if (q + 1 < nq) GOSSMX_STAGE_LOAD(q + 1);
+    const WeightGroup cur = wg[0];
+#pragma unroll
+    for (int p = 0; p + 1 < kPrefetch; ++p) wg[p] = wg[p + 1];
+    wg[kPrefetch - 1] = load_weight_group(nib, scl, tile_ok ? q + kPrefetch : nq, B, lane, nl);
+    if (tile_ok) {
       const int nb = min(4, B - 4 * q);
-      uint32_t wv[4] = {0u, 0u, 0u, 0u};
-      uint32_t sv = 0u;
-      const uint8_t* gn = nib + (size_t)q * 1024;
-      const uint8_t* gs = scl + (size_t)q * 64;
-      if (nb == 4) {
-        const uint4 v = *reinterpret_cast<const uint4*>(gn + lane * 16);
-        wv[0] = v.x; wv[1] = v.y; wv[2] = v.z; wv[3] = v.w;
-        sv = *reinterpret_cast<const uint32_t*>(gs + nl * 4);
-      } else {
-        for (int j = 0; j < nb; ++j) {
-          wv[j] = *reinterpret_cast<const uint32_t*>(gn + lane * nb * 4 + j * 4);
-          sv |= (uint32_t)gs[nl * nb + j] << (8 * j);
-        }
-      }
+      const uint32_t wv[4] = {cur.v.x, cur.v.y, cur.v.z, cur.v.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         if (j < nb) {
-          const int b = 4 * q + j;
           const half8 bop = fp4x8_to_half8(wv[j]);
-          const float e8 = e8m0((sv >> (8 * j)) & 0xffu);
+          const float e8 = e8m0((cur.s >> (8 * j)) & 0xffu);
 #pragma unroll
           for (int tg = 0; tg < 8; ++tg) {
             if (tg < n_tg) {
-              half8 aop = {0, 0, 0, 0, 0, 0, 0, 0};
-              if (arow[tg] >= 0)
-                aop = *reinterpret_cast<const half8*>(a.actv + (((size_t)arow[tg] * B + b) * 2 + part) * kBlock + G * 8);
+              const half8 aop =
+                  *reinterpret_cast<const half8*>(s_actv + ((j * kChunk + tg * 8 + a_tok) * 2 + part) * kBlock + G * 8);
               const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
               const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, zero, 0, 0, 0);
-              float2 s0 = {0.0f, 0.0f}, s1 = {0.0f, 0.0f};
-              if (erow0[tg] >= 0) s0 = acts[(size_t)erow0[tg] * B + b];
-              if (erow1[tg] >= 0) s1 = acts[(size_t)erow1[tg] * B + b];
-              tot[tg][0] = tot[tg][0] + (d[0] * e8) * s0.x;
-              if (a.residual) tot[tg][0] = tot[tg][0] + (d[1] * e8) * s0.y;
-              tot[tg][1] = tot[tg][1] + (d[2] * e8) * s1.x;
-              if (a.residual) tot[tg][1] = tot[tg][1] + (d[3] * e8) * s1.y;
+              const float4 s = *reinterpret_cast<const float4*>(&s_acts[j * kChunk + tg * 8 + 2 * G]);
+              tot[tg][0] = tot[tg][0] + (d[0] * e8) * s.x;
+              if (a.residual) tot[tg][0] = tot[tg][0] + (d[1] * e8) * s.y;
+              tot[tg][1] = tot[tg][1] + (d[2] * e8) * s.z;
+              if (a.residual) tot[tg][1] = tot[tg][1] + (d[3] * e8) * s.w;
             }
           }
         }
@@ -440,9 +529,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     }
   } else {
     // gate_up epilogue: bf16 (cpu_runner.rs:2905), SwiGLU over (even, odd)
-    // rows (:2907-2919), then the down input's residual-Q8 block: the 64
-    // rows of this work-group make one 32-value block (cpu_runner.rs:3224-3231).
-    __shared__ float s_act[kChunk][kBlock + 1];
+    // rows (:2907-2919), then the down input's residual-Q8 blocks: the 128
+    // rows of this work-group make two 32-value blocks (cpu_runner.rs:3224-3231).
+    // The SwiGLU values reuse the activation LDS as [64 rows][64 values].
+    __syncthreads();
+    float* s_act = reinterpret_cast<float*>(s_actv);
+    constexpr int kActStride = kGemmRows / 2 + 1;
 #pragma unroll
     for (int tg = 0; tg < 8; ++tg) {
       if (tg < n_tg) {
@@ -451,20 +543,24 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
           const float gu = bf16r(tot[tg][t]);
           const float other = __shfl_xor(gu, 1);
           const int c = tg * 8 + 2 * G + t;
-          if ((nl & 1) == 0 && c < count) s_act[c][wave * 8 + (nl >> 1)] = swiglu_one(gu, other, a.alpha, a.limit);
+          if ((nl & 1) == 0 && c < count)
+            s_act[c * kActStride + wave * 8 + (nl >> 1)] = swiglu_one(gu, other, a.alpha, a.limit);
         }
       }
     }
     __syncthreads();
-    const int hw = threadIdx.x >> 5, l32 = threadIdx.x & 31;
+    const int hw = tid >> 5, l32 = tid & 31;
     const int blocks_next = rows / kWgRows;
-    for (int c = hw; c < count; c += 8) {
-      const float v = s_act[c][l32];
+    constexpr int kBlocksPerWg = kGemmRows / 64;
+    for (int item = hw; item < count * kBlocksPerWg; item += kGemmThreads / 32) {
+      const int c = item / kBlocksPerWg, h = item % kBlocksPerWg;
+      if (blockIdx.x * kBlocksPerWg + h >= blocks_next) continue;  // uniform per half wave
+      const float v = s_act[c * kActStride + h * kBlock + l32];
       if (!isfinite(v)) atomicOr(a.err, kErrNonFiniteInput);
       ActBuffers nx;
       nx.v = a.actv_next;
       nx.s = a.acts_next;
-      residual_q8_store(v, l32, (size_t)(route_base + start + c), blocks_next, blockIdx.x, nx);
+      residual_q8_store(v, l32, (size_t)(route_base + start + c), blocks_next, blockIdx.x * kBlocksPerWg + h, nx);
     }
   }
 }
@@ -672,11 +768,11 @@ hipError_t launch_dispatch(const DispatchArgs& a, hipStream_t stream) {
 }
 
 hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream) {
-  const dim3 grid((unsigned)((a.w.tiles + 3) / 4), (unsigned)grid_work);
+  const dim3 grid((unsigned)((a.w.tiles + kWaves - 1) / kWaves), (unsigned)grid_work);
   switch (mode) {
-    case kPlain: hipLaunchKernelGGL(gemm_kernel<kPlain>, grid, dim3(256), 0, stream, a); break;
-    case kGateUp: hipLaunchKernelGGL(gemm_kernel<kGateUp>, grid, dim3(256), 0, stream, a); break;
-    case kDown: hipLaunchKernelGGL(gemm_kernel<kDown>, grid, dim3(256), 0, stream, a); break;
+    case kPlain: hipLaunchKernelGGL(gemm_kernel<kPlain>, grid, dim3(kGemmThreads), 0, stream, a); break;
+    case kGateUp: hipLaunchKernelGGL(gemm_kernel<kGateUp>, grid, dim3(kGemmThreads), 0, stream, a); break;
+    case kDown: hipLaunchKernelGGL(gemm_kernel<kDown>, grid, dim3(kGemmThreads), 0, stream, a); break;
   }
   return hipGetLastError();
 }
