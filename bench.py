@@ -103,7 +103,18 @@ def main() -> int:
     ap.add_argument("--zipf", type=float, default=1.1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run a device-to-device copy of this many MiB (calibrates HBM byte counters)")
     args = ap.parse_args()
+    if args.copy_probe_mib:
+        import torch
+
+        src = torch.empty(args.copy_probe_mib << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": args.copy_probe_mib << 20}))
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the single-GPU MoE block only; multi-GPU runs are not part of this build "
               "(expert-parallel sharding is a design note, not an implementation)", file=sys.stderr)

@@ -186,8 +186,8 @@ int alloc_tiled(gossmx_ctx* ctx, size_t experts, size_t rows, size_t blocks, gos
   w->ctx = ctx;
   w->device = ctx->device;
   w->t = make_tiled(experts, rows, blocks);
-  hipError_t e = hipMalloc(&w->t.nib, experts * w->t.nib_stride);
-  if (e == hipSuccess) e = hipMalloc(&w->t.scl, experts * w->t.scl_stride);
+  hipError_t e = hipMalloc(&w->t.nib, experts * w->t.nib_stride + kPlaneSlack);
+  if (e == hipSuccess) e = hipMalloc(&w->t.scl, experts * w->t.scl_stride + kPlaneSlack);
   if (e != hipSuccess) {
     if (w->t.nib) hipFree(w->t.nib);
     delete w;
@@ -225,7 +225,7 @@ int validate_problem(const gossmx_matmul_problem* p, size_t rows, size_t blocks,
       (m - 1) * p->output_stride + rows > p->output_len || (p->bias && p->bias_len != rows))
     return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "invalid MXFP4 matmul: M=%zu, N=%zu, K=%zu, output_stride=%zu", m, rows,
                 blocks * kBlock, p->output_stride);
-  if (m > (size_t)INT32_MAX / 2 || rows > (size_t)INT32_MAX / 2)
+  if (m > (size_t)INT32_MAX / 2 || rows > (size_t)INT32_MAX / 2 || m * blocks * 8 >= (size_t)INT32_MAX)
     return fail(GOSSMX_ERR_UNSUPPORTED, "matrix too large for this build");
   return GOSSMX_OK;
 }
@@ -726,8 +726,8 @@ int gossmx_selftest(gossmx_ctx* ctx) {
   if (!ctx) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context");
   if (int s = set_device(ctx->device)) return s;
   float* dev = nullptr;
-  HIP_TRY(hipMalloc(&dev, (8 + 256) * sizeof(float)), "hipMalloc(selftest)");
-  float host[8 + 256];
+  HIP_TRY(hipMalloc(&dev, (8 + 256 + 8) * sizeof(float)), "hipMalloc(selftest)");
+  float host[8 + 256 + 8];
   hipError_t e = launch_selftest(dev, ctx->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(host, dev, sizeof host, hipMemcpyDeviceToHost, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
@@ -737,6 +737,10 @@ int gossmx_selftest(gossmx_ctx* ctx) {
   for (int i = 0; i < 8; ++i)
     if (host[i] != codes[i])
       return fail(GOSSMX_ERR_UNSUPPORTED, "fp4 conversion element %d is %g, expected %g", i, host[i], codes[i]);
+  for (int i = 0; i < 8; ++i)
+    if (host[264 + i] != codes[i] * 0.0625f)
+      return fail(GOSSMX_ERR_UNSUPPORTED, "scaled fp4 conversion element %d is %g, expected %g", i, host[264 + i],
+                  codes[i] * 0.0625f);
   for (int lane = 0; lane < 64; ++lane)
     for (int r = 0; r < 4; ++r) {
       const float want = (float)(10 * (4 * (lane / 16) + r) + lane % 16);

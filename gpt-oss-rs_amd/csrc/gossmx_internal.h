@@ -38,6 +38,10 @@ struct TiledWeights {
   size_t scl_stride = 0;  // bytes per expert in the scale plane
 };
 
+// Extra bytes allocated after each plane: the GEMM reads whole 4-block groups
+// (and dword-granular tails) of the last tile unconditionally.
+constexpr size_t kPlaneSlack = 2048;
+
 // Activation operand of the expert GEMM, one row per token or route:
 //  actv [row][block][part 0 = primary, 1 = residual][32] f16 (the Q8 codes,
 //  exact in f16), acts [row][block][2] f32 (primary scale, residual scale).

@@ -331,40 +331,112 @@ constexpr int kPrefetch = 3;               // weight groups in flight per wave
 constexpr int kStageChunks = (kChunk * 4 * 8 + kGemmThreads - 1) / kGemmThreads;  // 4 per thread
 
 struct WeightGroup {
-  uint4 v;
-  uint32_t s;
+  uint4 v;     // one dword of nibbles per block (codes 8g..8g+7 of this lane's row)
+  uint32_t s;  // E8M0 bytes of this lane's row for the group's blocks
 };
 
-__device__ __forceinline__ WeightGroup load_weight_group(const uint8_t* nib, const uint8_t* scl, int q, int B,
-                                                         int lane, int nl) {
+// Loads of a full 4-block group q. Unconditional (no branch around a load),
+// so the compiler's load counters stay exact and the prefetched groups stay
+// in flight; callers clamp q to a full group of a valid tile.
+__device__ __forceinline__ WeightGroup load_full_group(const uint8_t* nib, const uint8_t* scl, int q, int lane,
+                                                       int nl) {
   WeightGroup g;
-  g.v = make_uint4(0u, 0u, 0u, 0u);
-  g.s = 0u;
-  const int nq = (B + 3) >> 2;
-  if (q >= nq) return g;
-  const int nb = min(4, B - 4 * q);
-  const uint8_t* gn = nib + (size_t)q * 1024;
-  const uint8_t* gs = scl + (size_t)q * 64;
-  if (nb == 4) {
-    g.v = *reinterpret_cast<const uint4*>(gn + lane * 16);
-    g.s = *reinterpret_cast<const uint32_t*>(gs + nl * 4);
-  } else {  // last group of a K that is not a multiple of 4 blocks: nb = 1..3
-    const uint32_t* gw = reinterpret_cast<const uint32_t*>(gn + lane * nb * 4);
-    g.v.x = gw[0];
-    g.s = gs[nl * nb];
-    if (nb > 1) {
-      g.v.y = gw[1];
-      g.s |= (uint32_t)gs[nl * nb + 1] << 8;
-    }
-    if (nb > 2) {
-      g.v.z = gw[2];
-      g.s |= (uint32_t)gs[nl * nb + 2] << 16;
-    }
-  }
+  g.v = *reinterpret_cast<const uint4*>(nib + (size_t)q * 1024 + lane * 16);
+  g.s = *reinterpret_cast<const uint32_t*>(scl + (size_t)q * 64 + nl * 4);
   return g;
 }
 
-template <int MODE>
+// Loads of the last group when K is not a multiple of 4 blocks (rem = 1..3
+// blocks): dwords at lane * rem * 4 and bytes at nl * rem. Reads past the
+// group stay inside the allocation slack (kPlaneSlack).
+__device__ __forceinline__ WeightGroup load_tail_group(const uint8_t* nib, const uint8_t* scl, int q, int rem,
+                                                       int lane, int nl) {
+  const uint32_t* gw = reinterpret_cast<const uint32_t*>(nib + (size_t)q * 1024 + lane * rem * 4);
+  const uint8_t* gs = scl + (size_t)q * 64 + nl * rem;
+  WeightGroup g;
+  g.v = make_uint4(gw[0], gw[1], gw[2], 0u);
+  g.s = (uint32_t)gs[0] | ((uint32_t)gs[1] << 8) | ((uint32_t)gs[2] << 16);
+  return g;
+}
+
+// E8M0 bytes whose scaled E2M1 values are exact f16 normals: 0.5 * 2^(s-127)
+// >= 2^-14 and 6 * 2^(s-127) <= 65504.
+constexpr uint32_t kFastScaleLo = 114, kFastScaleHi = 139;
+
+// One block j of the current group against every token group: the MFMAs and
+// the ordered chain updates. SCALED: the weight operand already carries the
+// E8M0 scale (exact), so the MFMA returns (p / 2) * e8m0 and a term is
+// d * act_scale; otherwise a term is (d * e8m0) * act_scale. Both are the
+// reference's (p * (0.5 * e8m0)) * act_scale rounded once.
+template <bool RESIDUAL, bool SCALED>
+__device__ __forceinline__ void block_update(float (&tot)[8][2], const _Float16* s_actv, const float2* s_acts,
+                                             const half8 bop, const float e8, const int j, const int n_tg,
+                                             const int a_off, const int G) {
+#pragma unroll
+  for (int tg = 0; tg < 8; ++tg) {
+    if (tg < n_tg) {
+      const half8 aop = *reinterpret_cast<const half8*>(s_actv + (j * kChunk + tg * 8) * 2 * kBlock + a_off);
+      const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+      const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, zero, 0, 0, 0);
+      const float4 sc = *reinterpret_cast<const float4*>(&s_acts[j * kChunk + tg * 8 + 2 * G]);
+      if (SCALED) {
+        tot[tg][0] = tot[tg][0] + d[0] * sc.x;
+        if (RESIDUAL) tot[tg][0] = tot[tg][0] + d[1] * sc.y;
+        tot[tg][1] = tot[tg][1] + d[2] * sc.z;
+        if (RESIDUAL) tot[tg][1] = tot[tg][1] + d[3] * sc.w;
+      } else {
+        tot[tg][0] = tot[tg][0] + (d[0] * e8) * sc.x;
+        if (RESIDUAL) tot[tg][0] = tot[tg][0] + (d[1] * e8) * sc.y;
+        tot[tg][1] = tot[tg][1] + (d[2] * e8) * sc.z;
+        if (RESIDUAL) tot[tg][1] = tot[tg][1] + (d[3] * e8) * sc.w;
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ half8 fp4x8_to_half8_scaled(uint32_t w, float scale) {
+  const half2v h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 0);
+  const half2v h1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 1);
+  const half2v h2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 2);
+  const half2v h3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 3);
+  half8 b;
+  b[0] = h0[0]; b[1] = h0[1]; b[2] = h1[0]; b[3] = h1[1];
+  b[4] = h2[0]; b[5] = h2[1]; b[6] = h3[0]; b[7] = h3[1];
+  return b;
+}
+
+// All blocks of one K group for this wave's tile.
+template <bool RESIDUAL>
+__device__ __forceinline__ void group_update(float (&tot)[8][2], const _Float16* s_actv, const float2* s_acts,
+                                             const WeightGroup cur, const int nb, const int n_tg, const int a_off,
+                                             const int G) {
+  const uint32_t wv[4] = {cur.v.x, cur.v.y, cur.v.z, cur.v.w};
+  bool in_range = true;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t s = (cur.s >> (8 * j)) & 0xffu;
+    if (j < nb) in_range = in_range && (s - kFastScaleLo) <= (kFastScaleHi - kFastScaleLo);
+  }
+  if (__all(in_range)) {  // wave-uniform
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j < nb) {
+        const float e8 = __uint_as_float(((cur.s >> (8 * j)) & 0xffu) << 23);
+        block_update<RESIDUAL, true>(tot, s_actv, s_acts, fp4x8_to_half8_scaled(wv[j], e8), 0.0f, j, n_tg, a_off, G);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j < nb) {
+        const float e8 = e8m0((cur.s >> (8 * j)) & 0xffu);
+        block_update<RESIDUAL, false>(tot, s_actv, s_acts, fp4x8_to_half8(wv[j]), e8, j, n_tg, a_off, G);
+      }
+    }
+  }
+}
+
+template <int MODE, bool RESIDUAL>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -412,97 +484,91 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
 #pragma unroll
   for (int tg = 0; tg < 8; ++tg) { tot[tg][0] = b0; tot[tg][1] = b0; }
 
+  // Waves past the last tile read tile 0 and discard it.
   const int safe_tile = tile_ok ? tile : 0;
   const uint8_t* nib = a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)safe_tile * 256 * B;
   const uint8_t* scl = a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)safe_tile * 16 * B;
+  const int nqf = B >> 2, rem = B & 3;
+  const int last_full = nqf > 0 ? nqf - 1 : 0;
+  const WeightGroup tail = load_tail_group(nib, scl, nqf, rem > 0 ? rem : 1, lane, nl);
   WeightGroup wg[kPrefetch];
 #pragma unroll
-  for (int p = 0; p < kPrefetch; ++p) wg[p] = load_weight_group(nib, scl, tile_ok ? p : nq, B, lane, nl);
+  for (int p = 0; p < kPrefetch; ++p) wg[p] = load_full_group(nib, scl, min(p, last_full), lane, nl);
 
-  // Activation staging registers for one group: kStageChunks (4) 16-byte
-  // pieces per thread, unrolled by hand so that they stay in VGPRs.
+  // Activation staging: each thread moves up to kStageChunks 16-byte pieces
+  // and one scale pair per group. The piece -> (block j, row t, piece) map is
+  // the same for every group, so it is computed once here.
   static_assert(kStageChunks == 4, "staging is unrolled for 4 pieces per thread");
-  uint4 st0 = make_uint4(0u, 0u, 0u, 0u), st1 = st0, st2 = st0, st3 = st0;
-  float2 stage_s = make_float2(0.0f, 0.0f);
+  const int per_block = count * 8;
   const uint4* gactv = reinterpret_cast<const uint4*>(a.actv);
   const float2* gacts = reinterpret_cast<const float2*>(a.acts);
   uint4* lds_actv = reinterpret_cast<uint4*>(s_actv);
-  const int per_block = count * 8;  // 16-byte pieces per block of the group
-#define GOSSMX_STAGE_PIECE_LOAD(REG, I, QQ, ITEMS)                                       \
-  {                                                                                      \
-    const int c = tid + (I) * kGemmThreads;                                              \
-    if (c < (ITEMS)) {                                                                   \
-      const int j = c / per_block, rem = c - j * per_block;                              \
-      REG = gactv[((size_t)s_row[rem >> 3] * B + 4 * (QQ) + j) * 8 + (rem & 7)];         \
-    }                                                                                    \
+  int pj[4], pbase[4], plds[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c_raw = tid + i * kGemmThreads;
+    const int c = min(c_raw, 4 * per_block - 1);
+    const int j = c / per_block, rr = c - j * per_block;
+    pj[i] = c_raw < 4 * per_block ? j : 4;  // 4 = never stored
+    pbase[i] = s_row[rr >> 3] * B * 8 + (rr & 7);
+    plds[i] = (j * kChunk + (rr >> 3)) * 8 + (rr & 7);
   }
-#define GOSSMX_STAGE_PIECE_STORE(REG, I, ITEMS)                                          \
-  {                                                                                      \
-    const int c = tid + (I) * kGemmThreads;                                              \
-    if (c < (ITEMS)) {                                                                   \
-      const int j = c / per_block, rem = c - j * per_block;                              \
-      lds_actv[(j * kChunk + (rem >> 3)) * 8 + (rem & 7)] = REG;                          \
-    }                                                                                    \
+  const int cs = min(tid, 4 * count - 1);
+  const int sj_raw = cs / count, st = cs - sj_raw * count;
+  const int sj = tid < 4 * count ? sj_raw : 4;
+  const int sbase = s_row[st] * B;
+  const int slds = sj_raw * kChunk + st;
+  uint4 st0, st1, st2, st3;
+  float2 stage_s;
+#define GOSSMX_STAGE_LOAD(QQ)                                                             \
+  {                                                                                       \
+    const int qq_ = (QQ), nbq_ = min(4, B - 4 * qq_);                                    \
+    st0 = gactv[pbase[0] + (4 * qq_ + min(pj[0], nbq_ - 1)) * 8];                         \
+    st1 = gactv[pbase[1] + (4 * qq_ + min(pj[1], nbq_ - 1)) * 8];                         \
+    st2 = gactv[pbase[2] + (4 * qq_ + min(pj[2], nbq_ - 1)) * 8];                         \
+    st3 = gactv[pbase[3] + (4 * qq_ + min(pj[3], nbq_ - 1)) * 8];                         \
+    stage_s = gacts[sbase + 4 * qq_ + min(sj_raw, nbq_ - 1)];                             \
   }
-#define GOSSMX_STAGE_LOAD(QQ)                                                            \
-  do {                                                                                   \
-    const int nb_ = min(4, B - 4 * (QQ));                                                \
-    const int items_ = per_block * nb_;                                                  \
-    GOSSMX_STAGE_PIECE_LOAD(st0, 0, QQ, items_)                                          \
-    GOSSMX_STAGE_PIECE_LOAD(st1, 1, QQ, items_)                                          \
-    GOSSMX_STAGE_PIECE_LOAD(st2, 2, QQ, items_)                                          \
-    GOSSMX_STAGE_PIECE_LOAD(st3, 3, QQ, items_)                                          \
-    if (tid < count * nb_) stage_s = gacts[(size_t)s_row[tid % count] * B + 4 * (QQ) + tid / count]; \
-  } while (0)
-#define GOSSMX_STAGE_STORE(QQ)                                                           \
-  do {                                                                                   \
-    const int nb_ = min(4, B - 4 * (QQ));                                                \
-    const int items_ = per_block * nb_;                                                  \
-    GOSSMX_STAGE_PIECE_STORE(st0, 0, items_)                                             \
-    GOSSMX_STAGE_PIECE_STORE(st1, 1, items_)                                             \
-    GOSSMX_STAGE_PIECE_STORE(st2, 2, items_)                                             \
-    GOSSMX_STAGE_PIECE_STORE(st3, 3, items_)                                             \
-    if (tid < count * nb_) s_acts[(tid / count) * kChunk + tid % count] = stage_s;        \
-  } while (0)
+#define GOSSMX_STAGE_STORE(QQ)                                                            \
+  {                                                                                       \
+    const int nbq_ = min(4, B - 4 * (QQ));                                               \
+    if (pj[0] < nbq_) lds_actv[plds[0]] = st0;                                            \
+    if (pj[1] < nbq_) lds_actv[plds[1]] = st1;                                            \
+    if (pj[2] < nbq_) lds_actv[plds[2]] = st2;                                            \
+    if (pj[3] < nbq_) lds_actv[plds[3]] = st3;                                            \
+    if (sj < nbq_) s_acts[slds] = stage_s;                                                \
+  }
 
   GOSSMX_STAGE_LOAD(0);
-  const int part = nl & 1;
-  const int a_tok = nl >> 1;  // token within a group of 8 for the A operand
-  for (int q = 0; q < nq; ++q) {
-    __syncthreads();  // every wave is done reading the previous group
-    GOSSMX_STAGE_STORE(q);
-    __syncthreads();
-    if (q + 1 < nq) GOSSMX_STAGE_LOAD(q + 1);
-    const WeightGroup cur = wg[0];
-#pragma unroll
-    for (int p = 0; p + 1 < kPrefetch; ++p) wg[p] = wg[p + 1];
-    wg[kPrefetch - 1] = load_weight_group(nib, scl, tile_ok ? q + kPrefetch : nq, B, lane, nl);
-    if (tile_ok) {
-      const int nb = min(4, B - 4 * q);
-      const uint32_t wv[4] = {cur.v.x, cur.v.y, cur.v.z, cur.v.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (j < nb) {
-          const half8 bop = fp4x8_to_half8(wv[j]);
-          const float e8 = e8m0((cur.s >> (8 * j)) & 0xffu);
-#pragma unroll
-          for (int tg = 0; tg < 8; ++tg) {
-            if (tg < n_tg) {
-              const half8 aop =
-                  *reinterpret_cast<const half8*>(s_actv + ((j * kChunk + tg * 8 + a_tok) * 2 + part) * kBlock + G * 8);
-              const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-              const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, zero, 0, 0, 0);
-              const float4 s = *reinterpret_cast<const float4*>(&s_acts[j * kChunk + tg * 8 + 2 * G]);
-              tot[tg][0] = tot[tg][0] + (d[0] * e8) * s.x;
-              if (a.residual) tot[tg][0] = tot[tg][0] + (d[1] * e8) * s.y;
-              tot[tg][1] = tot[tg][1] + (d[2] * e8) * s.z;
-              if (a.residual) tot[tg][1] = tot[tg][1] + (d[3] * e8) * s.w;
-            }
-          }
-        }
-      }
-    }
+  const int a_off = ((nl >> 1) * 2 + (nl & 1)) * kBlock + G * 8;  // this lane's A operand in a token group
+
+  // One K group: stage its activations into LDS, start the next group's
+  // staging loads, run the MFMAs and the ordered float chain, then refill
+  // this ring slot with group q + kPrefetch. Iterations past the last group
+  // only keep the barriers and loads in step (no compute, nothing stored).
+#define GOSSMX_GROUP(QV, SLOT)                                                            \
+  {                                                                                       \
+    const int q = (QV);                                                                   \
+    __syncthreads(); /* every wave is done reading the previous group */                 \
+    GOSSMX_STAGE_STORE(q);                                                                \
+    __syncthreads();                                                                      \
+    GOSSMX_STAGE_LOAD(min(q + 1, nq - 1));                                                \
+    const WeightGroup cur = q < nqf ? SLOT : tail;                                        \
+    if (tile_ok && q < nq)                                                                \
+      group_update<RESIDUAL>(tot, s_actv, s_acts, cur, min(4, B - 4 * q), n_tg, a_off, G); \
+    /* refill after the last use of the slot, so the load lands in the same registers */ \
+    SLOT = load_full_group(nib, scl, min(q + kPrefetch, last_full), lane, nl);            \
   }
+  static_assert(kPrefetch == 3, "the K loop is unrolled by the prefetch depth");
+  const int nq_pad = (nq + 2) / 3 * 3;
+  for (int q0 = 0; q0 < nq_pad; q0 += 3) {
+    GOSSMX_GROUP(q0, wg[0])
+    GOSSMX_GROUP(q0 + 1, wg[1])
+    GOSSMX_GROUP(q0 + 2, wg[2])
+  }
+#undef GOSSMX_GROUP
+#undef GOSSMX_STAGE_LOAD
+#undef GOSSMX_STAGE_STORE
 
   if (MODE == kPlain) {
     if (tile_ok && row < rows) {
@@ -736,6 +802,7 @@ __global__ void clear_ints_kernel(int* p, size_t n) {
 // out[0..7]: v_cvt_scalef32_pk_f16_fp4 of codes 0..7 (bytes 0x10 0x32 0x54 0x76).
 // out[8 + 4 * lane + r]: D of a 16x16x32 f16 MFMA with A[i][k] = (k == i) and
 // B[k][j] = 10 k + j, expected 10 * (4 * (lane / 16) + r) + lane % 16.
+// out[264..271]: codes 0..7 converted with scale 2^-4.
 __global__ void selftest_kernel(float* out) {
   const int lane = threadIdx.x;
   const half8 w = fp4x8_to_half8(0x76543210u);
@@ -750,6 +817,10 @@ __global__ void selftest_kernel(float* out) {
   const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
   const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, zero, 0, 0, 0);
   for (int r = 0; r < 4; ++r) out[8 + 4 * lane + r] = d[r];
+  // out[264..271]: the scaled conversion with E8M0 byte 123 (2^-4).
+  const half8 ws = fp4x8_to_half8_scaled(0x76543210u, __uint_as_float(123u << 23));
+  if (lane == 0)
+    for (int i = 0; i < 8; ++i) out[264 + i] = (float)ws[i];
 }
 
 // ---------------------------------------------------------------------------
@@ -769,10 +840,16 @@ hipError_t launch_dispatch(const DispatchArgs& a, hipStream_t stream) {
 
 hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream) {
   const dim3 grid((unsigned)((a.w.tiles + kWaves - 1) / kWaves), (unsigned)grid_work);
-  switch (mode) {
-    case kPlain: hipLaunchKernelGGL(gemm_kernel<kPlain>, grid, dim3(kGemmThreads), 0, stream, a); break;
-    case kGateUp: hipLaunchKernelGGL(gemm_kernel<kGateUp>, grid, dim3(kGemmThreads), 0, stream, a); break;
-    case kDown: hipLaunchKernelGGL(gemm_kernel<kDown>, grid, dim3(kGemmThreads), 0, stream, a); break;
+  const dim3 block(kGemmThreads);
+  if (a.residual) {
+    switch (mode) {
+      case kPlain: hipLaunchKernelGGL((gemm_kernel<kPlain, true>), grid, block, 0, stream, a); break;
+      case kGateUp: hipLaunchKernelGGL((gemm_kernel<kGateUp, true>), grid, block, 0, stream, a); break;
+      case kDown: hipLaunchKernelGGL((gemm_kernel<kDown, true>), grid, block, 0, stream, a); break;
+    }
+  } else {
+    if (mode != kPlain) return hipErrorInvalidValue;  // the MoE block always runs residual-Q8
+    hipLaunchKernelGGL((gemm_kernel<kPlain, false>), grid, block, 0, stream, a);
   }
   return hipGetLastError();
 }
