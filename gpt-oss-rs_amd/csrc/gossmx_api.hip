@@ -173,7 +173,7 @@ TiledWeights make_tiled(size_t experts, size_t rows, size_t blocks) {
   t.blocks = blocks;
   t.tiles = (rows + kTileRows - 1) / kTileRows;
   t.nib_stride = t.tiles * 256 * blocks;
-  t.scl_stride = t.tiles * 16 * blocks;
+  t.scl_stride = t.tiles * 64 * ((blocks + 3) / 4);
   return t;
 }
 
@@ -449,8 +449,8 @@ int gossmx_mxfp4_matmul(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
     HIP_TRY(hipMemcpyAsync(ctx->rec.p, rec, rec_count * rsz, hipMemcpyHostToDevice, ctx->stream), "H2D activations");
     rec = static_cast<const uint8_t*>(ctx->rec.p);
   }
-  if (int s = ensure(ctx, ctx->act1v, m * B * 2 * kBlock * sizeof(_Float16))) return s;
-  if (int s = ensure(ctx, ctx->act1s, m * B * 2 * sizeof(float))) return s;
+  if (int s = ensure(ctx, ctx->act1v, m * B * 2 * kBlock * sizeof(_Float16) + kActSlack)) return s;
+  if (int s = ensure(ctx, ctx->act1s, m * B * 2 * sizeof(float) + kActSlack)) return s;
   ActBuffers act{static_cast<_Float16*>(ctx->act1v.p), static_cast<float*>(ctx->act1s.p)};
   HIP_TRY(launch_prep_records(rec, p->activation_kind, m, B, p->row_stride, act, ctx->err, ctx->stream),
           "prepare activations");
@@ -555,11 +555,12 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
 
   int s = GOSSMX_OK;
   if ((s = ensure(ctx, ctx->logits, m * E * 4)) || (s = ensure(ctx, ctx->selected, R * 4)) ||
-      (s = ensure(ctx, ctx->weights, R * 4)) || (s = ensure(ctx, ctx->act1v, m * B1 * 2 * kBlock * 2)) ||
-      (s = ensure(ctx, ctx->act1s, m * B1 * 8)) || (s = ensure(ctx, ctx->bucket, (E + 1) * 4)) ||
+      (s = ensure(ctx, ctx->weights, R * 4)) || (s = ensure(ctx, ctx->act1v, m * B1 * 2 * kBlock * 2 + kActSlack)) ||
+      (s = ensure(ctx, ctx->act1s, m * B1 * 8 + kActSlack)) || (s = ensure(ctx, ctx->bucket, (E + 1) * 4)) ||
       (s = ensure(ctx, ctx->route_tok, R * 4)) || (s = ensure(ctx, ctx->route_slot, R * 4)) ||
-      (s = ensure(ctx, ctx->work, (2 * max_work + 1) * 4)) || (s = ensure(ctx, ctx->act2v, R * B2 * 2 * kBlock * 2)) ||
-      (s = ensure(ctx, ctx->act2s, R * B2 * 8)) || (s = ensure(ctx, ctx->y, R * H * 2)))
+      (s = ensure(ctx, ctx->work, (2 * max_work + 1) * 4)) ||
+      (s = ensure(ctx, ctx->act2v, R * B2 * 2 * kBlock * 2 + kActSlack)) ||
+      (s = ensure(ctx, ctx->act2s, R * B2 * 8 + kActSlack)) || (s = ensure(ctx, ctx->y, R * H * 2)))
     return s;
   const uint16_t* x = io->x;
   const float* injected = io->injected_logits;

@@ -12,7 +12,7 @@ constexpr int kBlock = 32;      // values per MXFP4 / Q8 block (QUANT_BLOCK_SIZE
 constexpr int kRecord = 17;     // E8M0 byte + 16 packed nibble bytes per (row, block)
 constexpr int kTileRows = 16;   // rows per MFMA tile (one wave)
 constexpr int kWgRows = 64;     // gate_up rows (32 gate/up pairs) per 32-value block of the down input
-constexpr int kChunk = 64;      // activation rows per work item
+constexpr int kChunk = 48;      // activation rows per work item
 constexpr int kMaxExperts = 128;
 constexpr int kMaxTopK = 8;
 
@@ -27,8 +27,9 @@ constexpr int kErrNonFiniteInput = 2;
 //     lane L = 16 * g + n (g = K slice 0..3, n = row in tile) owns nb * 4
 //     bytes at L * nb * 4, one dword per block: packed bytes 4g..4g+3 of the
 //     canonical record, i.e. codes 8g..8g+7 (low nibble = even code).
-//   scale plane: 16 * blocks bytes at t * 16 * blocks; group q at q * 64,
-//     byte (n, j) at n * nb + j.
+//   scale plane: 64 * ceil(blocks / 4) bytes at t * 64 * ceil(blocks / 4);
+//     group q at q * 64, byte (n, j) at n * 4 + j (a partial last group is
+//     padded to 4 bytes per row so every group is one aligned dword per row).
 //  Padding rows (rows..16*tiles-1) hold zero codes and scale 127.
 struct TiledWeights {
   uint8_t* nib = nullptr;
@@ -41,6 +42,9 @@ struct TiledWeights {
 // Extra bytes allocated after each plane: the GEMM reads whole 4-block groups
 // (and dword-granular tails) of the last tile unconditionally.
 constexpr size_t kPlaneSlack = 2048;
+// Extra bytes after each activation operand buffer: the GEMM's staging reads
+// a last partial K group as whole 4-block groups (up to 3 blocks past a row).
+constexpr size_t kActSlack = 1024;
 
 // Activation operand of the expert GEMM, one row per token or route:
 //  actv [row][block][part 0 = primary, 1 = residual][32] f16 (the Q8 codes,

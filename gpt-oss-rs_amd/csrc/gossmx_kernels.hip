@@ -324,11 +324,18 @@ __device__ __forceinline__ half8 fp4x8_to_half8(uint32_t w) {
 }
 
 constexpr int kWaves = 8;                  // waves per GEMM work-group
+constexpr int kSlotBytes = 4 * kChunk * 2 * kBlock * 2;  // f16 codes of one K group in LDS
+constexpr int kCodeDma = 4 * kChunk * 8 / (64 * kWaves);  // 16-byte DMA instructions per wave per group
+static_assert(4 * kChunk * 8 == kCodeDma * 64 * kWaves, "code DMA covers a slot exactly");
+static_assert(4 * kChunk * 2 <= 64 * kWaves, "one 4-byte DMA per wave covers a group's scales");
+constexpr int kSclSlot = 64 * kWaves / 2;                  // float2 written by one group's scale DMA
+// s_waitcnt immediate: vmcnt = kCodeDma + 1 (D(q+1)) + 2 + 2 (W(q+1), W(q+2)),
+// expcnt and lgkmcnt not waited on (7, 15).
+constexpr int kWaitVm = kCodeDma + 1 + 4;
+constexpr int kWaitDmaGroup = (kWaitVm & 15) | ((kWaitVm >> 4) << 14) | (7 << 4) | (15 << 8);
 constexpr int kGemmThreads = 64 * kWaves;  // 512
 constexpr int kGemmRows = 16 * kWaves;     // weight rows per work-group
 constexpr int kPrefetch = 3;               // weight groups in flight per wave
-// Activation staging: per group, count * nb rows of 128 bytes (8 chunks of 16 B).
-constexpr int kStageChunks = (kChunk * 4 * 8 + kGemmThreads - 1) / kGemmThreads;  // 4 per thread
 
 struct WeightGroup {
   uint4 v;     // one dword of nibbles per block (codes 8g..8g+7 of this lane's row)
@@ -347,52 +354,21 @@ __device__ __forceinline__ WeightGroup load_full_group(const uint8_t* nib, const
 }
 
 // Loads of the last group when K is not a multiple of 4 blocks (rem = 1..3
-// blocks): dwords at lane * rem * 4 and bytes at nl * rem. Reads past the
-// group stay inside the allocation slack (kPlaneSlack).
+// blocks): dwords at lane * rem * 4 of the compact nibble group, and the
+// row's (padded) scale dword. Reads past the group stay inside the
+// allocation slack (kPlaneSlack).
 __device__ __forceinline__ WeightGroup load_tail_group(const uint8_t* nib, const uint8_t* scl, int q, int rem,
                                                        int lane, int nl) {
   const uint32_t* gw = reinterpret_cast<const uint32_t*>(nib + (size_t)q * 1024 + lane * rem * 4);
-  const uint8_t* gs = scl + (size_t)q * 64 + nl * rem;
   WeightGroup g;
   g.v = make_uint4(gw[0], gw[1], gw[2], 0u);
-  g.s = (uint32_t)gs[0] | ((uint32_t)gs[1] << 8) | ((uint32_t)gs[2] << 16);
+  g.s = *reinterpret_cast<const uint32_t*>(scl + (size_t)q * 64 + nl * 4);
   return g;
 }
 
 // E8M0 bytes whose scaled E2M1 values are exact f16 normals: 0.5 * 2^(s-127)
 // >= 2^-14 and 6 * 2^(s-127) <= 65504.
 constexpr uint32_t kFastScaleLo = 114, kFastScaleHi = 139;
-
-// One block j of the current group against every token group: the MFMAs and
-// the ordered chain updates. SCALED: the weight operand already carries the
-// E8M0 scale (exact), so the MFMA returns (p / 2) * e8m0 and a term is
-// d * act_scale; otherwise a term is (d * e8m0) * act_scale. Both are the
-// reference's (p * (0.5 * e8m0)) * act_scale rounded once.
-template <bool RESIDUAL, bool SCALED>
-__device__ __forceinline__ void block_update(float (&tot)[8][2], const _Float16* s_actv, const float2* s_acts,
-                                             const half8 bop, const float e8, const int j, const int n_tg,
-                                             const int a_off, const int G) {
-#pragma unroll
-  for (int tg = 0; tg < 8; ++tg) {
-    if (tg < n_tg) {
-      const half8 aop = *reinterpret_cast<const half8*>(s_actv + (j * kChunk + tg * 8) * 2 * kBlock + a_off);
-      const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-      const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, zero, 0, 0, 0);
-      const float4 sc = *reinterpret_cast<const float4*>(&s_acts[j * kChunk + tg * 8 + 2 * G]);
-      if (SCALED) {
-        tot[tg][0] = tot[tg][0] + d[0] * sc.x;
-        if (RESIDUAL) tot[tg][0] = tot[tg][0] + d[1] * sc.y;
-        tot[tg][1] = tot[tg][1] + d[2] * sc.z;
-        if (RESIDUAL) tot[tg][1] = tot[tg][1] + d[3] * sc.w;
-      } else {
-        tot[tg][0] = tot[tg][0] + (d[0] * e8) * sc.x;
-        if (RESIDUAL) tot[tg][0] = tot[tg][0] + (d[1] * e8) * sc.y;
-        tot[tg][1] = tot[tg][1] + (d[2] * e8) * sc.z;
-        if (RESIDUAL) tot[tg][1] = tot[tg][1] + (d[3] * e8) * sc.w;
-      }
-    }
-  }
-}
 
 __device__ __forceinline__ half8 fp4x8_to_half8_scaled(uint32_t w, float scale) {
   const half2v h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 0);
@@ -405,11 +381,52 @@ __device__ __forceinline__ half8 fp4x8_to_half8_scaled(uint32_t w, float scale) 
   return b;
 }
 
-// All blocks of one K group for this wave's tile.
-template <bool RESIDUAL>
-__device__ __forceinline__ void group_update(float (&tot)[8][2], const _Float16* s_actv, const float2* s_acts,
-                                             const WeightGroup cur, const int nb, const int n_tg, const int a_off,
+// e8m0_scale without branches (lib.rs:957-963).
+__device__ __forceinline__ float e8m0_select(uint32_t s) {
+  const float normal = __uint_as_float(s << 23);
+  const float v = s == 0u ? __uint_as_float(0x00400000u) : normal;
+  return s == 0xffu ? __uint_as_float(0x7fc00000u) : v;
+}
+
+// LDS slot layout of one K group (written by DMA, read as MFMA A operands):
+// for block j and token group tg, 1 KiB = [k-slice g (4)][vector i (16)][16 B]
+// with vector i = 2 * (row within the group) + part (0 primary, 1 residual),
+// so lane (g, i) of a wave reads the 16 bytes at lane * 16 (conflict-free).
+__device__ __forceinline__ int slot_chunk(int j, int tg) { return j * (kChunk / 8) + tg; }
+
+// One block j of the current group against NTG token groups: the MFMAs and
+// the ordered chain updates. SCALED: the weight operand already carries the
+// E8M0 scale (exact), so the MFMA returns (p / 2) * e8m0 and a term is
+// d * act_scale; otherwise a term is (d * e8m0) * act_scale. Both are the
+// reference's (p * (0.5 * e8m0)) * act_scale rounded once.
+template <bool RESIDUAL, bool SCALED, int NTG>
+__device__ __forceinline__ void block_update(float (&tot)[kChunk / 8][2], const char* codes, const float2* scl,
+                                             const half8 bop, const float e8, const int j, const int lane,
                                              const int G) {
+#pragma unroll
+  for (int tg = 0; tg < NTG; ++tg) {
+    const half8 aop = *reinterpret_cast<const half8*>(codes + slot_chunk(j, tg) * 1024 + lane * 16);
+    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, zero, 0, 0, 0);
+    const float4 sc = *reinterpret_cast<const float4*>(&scl[j * kChunk + tg * 8 + 2 * G]);
+    if (SCALED) {
+      tot[tg][0] = tot[tg][0] + d[0] * sc.x;
+      if (RESIDUAL) tot[tg][0] = tot[tg][0] + d[1] * sc.y;
+      tot[tg][1] = tot[tg][1] + d[2] * sc.z;
+      if (RESIDUAL) tot[tg][1] = tot[tg][1] + d[3] * sc.w;
+    } else {
+      tot[tg][0] = tot[tg][0] + (d[0] * e8) * sc.x;
+      if (RESIDUAL) tot[tg][0] = tot[tg][0] + (d[1] * e8) * sc.y;
+      tot[tg][1] = tot[tg][1] + (d[2] * e8) * sc.z;
+      if (RESIDUAL) tot[tg][1] = tot[tg][1] + (d[3] * e8) * sc.w;
+    }
+  }
+}
+
+// All blocks of one K group for this wave's tile.
+template <bool RESIDUAL, int NTG>
+__device__ __forceinline__ void group_update(float (&tot)[kChunk / 8][2], const char* codes, const float2* scl,
+                                             const WeightGroup cur, const int nb, const int lane, const int G) {
   const uint32_t wv[4] = {cur.v.x, cur.v.y, cur.v.z, cur.v.w};
   bool in_range = true;
 #pragma unroll
@@ -422,22 +439,98 @@ __device__ __forceinline__ void group_update(float (&tot)[8][2], const _Float16*
     for (int j = 0; j < 4; ++j) {
       if (j < nb) {
         const float e8 = __uint_as_float(((cur.s >> (8 * j)) & 0xffu) << 23);
-        block_update<RESIDUAL, true>(tot, s_actv, s_acts, fp4x8_to_half8_scaled(wv[j], e8), 0.0f, j, n_tg, a_off, G);
+        block_update<RESIDUAL, true, NTG>(tot, codes, scl, fp4x8_to_half8_scaled(wv[j], e8), 0.0f, j, lane, G);
       }
     }
   } else {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j < nb) {
-        const float e8 = e8m0((cur.s >> (8 * j)) & 0xffu);
-        block_update<RESIDUAL, false>(tot, s_actv, s_acts, fp4x8_to_half8(wv[j]), e8, j, n_tg, a_off, G);
-      }
+    // Rare: a scale outside the exact-f16 range (including the 0x00 and 0xff
+    // encodings). Kept compact; same bits through the unscaled operand.
+#pragma unroll 1
+    for (int j = 0; j < nb; ++j) {
+      const uint32_t w = j == 0 ? wv[0] : (j == 1 ? wv[1] : (j == 2 ? wv[2] : wv[3]));
+      const float e8 = e8m0_select((cur.s >> (8 * j)) & 0xffu);
+      block_update<RESIDUAL, false, NTG>(tot, codes, scl, fp4x8_to_half8(w), e8, j, lane, G);
     }
   }
 }
 
+// Loop-invariant state of the K loop.
+struct KLoop {
+  const uint8_t* nib;
+  const uint8_t* scl;
+  WeightGroup tail;
+  int nq, nqf, last_full, B, wave, lane, nl, G;
+  bool tile_ok;
+  // DMA lane map (see gemm_kernel)
+  const char* gcodes;
+  const char* gscl;
+  int coff[kCodeDma];  // byte offset of this lane's code piece in group 0, or -1: nothing to move
+  int soff;            // same for the scale dword
+};
+
+// Issues the DMA of group qq (clamped to the last group) into one ring slot.
+__device__ __forceinline__ void issue_dma(const KLoop& k, int qq_raw, char* codes, float2* scl) {
+  const int qq = min(qq_raw, k.nq - 1);
+  const int gstep = qq * 4 * 128;  // 4 blocks of 128 B per activation row
+#pragma unroll
+  for (int i = 0; i < kCodeDma; ++i) {
+    const char* src = k.coff[i] >= 0 ? k.gcodes + (k.coff[i] + gstep) : k.gcodes;
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)(codes + (i * kWaves + k.wave) * 1024),
+                                     16, 0, 0);
+  }
+  const char* ssrc = k.soff >= 0 ? k.gscl + (k.soff + qq * 4 * 8) : k.gscl;
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)ssrc,
+                                   (__attribute__((address_space(3))) void*)((char*)scl + k.wave * 256), 4, 0, 0);
+}
+
+// The K loop for NTG token groups. Vector-memory issue order per wave, fixed
+// so that one immediate wait covers every group:
+//   prologue W(0) D(0) W(1) D(1) W(2); iteration q: wait(D(q)) barrier
+//   D(q+2) compute(q) W(q+3).
+// After D(q) come W(q+1), D(q+1), W(q+2) = kWaitVm instructions.
+template <bool RESIDUAL, int NTG>
+__device__ __forceinline__ void k_loop(const KLoop& k, float (&tot)[kChunk / 8][2], char* c0, char* c1, char* c2,
+                                       float2* s0, float2* s1, float2* s2) {
+  WeightGroup wg0, wg1, wg2;
+  __builtin_amdgcn_sched_barrier(0);
+  wg0 = load_full_group(k.nib, k.scl, min(0, k.last_full), k.lane, k.nl);
+  __builtin_amdgcn_sched_barrier(0);
+  issue_dma(k, 0, c0, s0);
+  __builtin_amdgcn_sched_barrier(0);
+  wg1 = load_full_group(k.nib, k.scl, min(1, k.last_full), k.lane, k.nl);
+  __builtin_amdgcn_sched_barrier(0);
+  issue_dma(k, 1, c1, s1);
+  __builtin_amdgcn_sched_barrier(0);
+  wg2 = load_full_group(k.nib, k.scl, min(2, k.last_full), k.lane, k.nl);
+  __builtin_amdgcn_sched_barrier(0);
+#define GOSSMX_GROUP(QV, SLOT, CODES, SCL, NCODES, NSCL)                                            \
+  {                                                                                                 \
+    const int q = (QV);                                                                             \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    __builtin_amdgcn_s_waitcnt(kWaitDmaGroup); /* this wave's DMA for group q has landed */        \
+    __builtin_amdgcn_s_barrier();              /* ... and every other wave's; slot of q-1 is free */ \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    issue_dma(k, q + 2, NCODES, NSCL);                                                              \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    const WeightGroup cur = q < k.nqf ? SLOT : k.tail;                                              \
+    if (k.tile_ok && q < k.nq)                                                                      \
+      group_update<RESIDUAL, NTG>(tot, CODES, SCL, cur, min(4, k.B - 4 * q), k.lane, k.G);          \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    SLOT = load_full_group(k.nib, k.scl, min(q + 3, k.last_full), k.lane, k.nl);                    \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+  }
+  const int nq_pad = (k.nq + 2) / 3 * 3;
+  for (int q0 = 0; q0 < nq_pad; q0 += 3) {
+    GOSSMX_GROUP(q0, wg0, c0, s0, c2, s2)
+    GOSSMX_GROUP(q0 + 1, wg1, c1, s1, c0, s0)
+    GOSSMX_GROUP(q0 + 2, wg2, c2, s2, c1, s1)
+  }
+#undef GOSSMX_GROUP
+}
+
 template <int MODE, bool RESIDUAL>
-__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int nl = lane & 15, G = lane >> 4;
@@ -454,10 +547,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
     route_base = a.bucket_off[expert];
     count = min(kChunk, a.bucket_off[expert + 1] - route_base - start);
   }
-  // LDS: activation codes [4 blocks][64 rows][2 parts][32] f16 and scales
-  // [4][64] float2 for the current group; reused as SwiGLU staging afterwards.
-  __shared__ __align__(16) _Float16 s_actv[4 * kChunk * 2 * kBlock];
-  __shared__ __align__(16) float2 s_acts[4 * kChunk];
+  // LDS ring of three K groups, filled by global->LDS DMA two groups ahead.
+  __shared__ __align__(16) char s_codes0[kSlotBytes], s_codes1[kSlotBytes], s_codes2[kSlotBytes];
+  // A scale DMA writes 64 dwords per wave: kSclSlot float2 per slot, of which
+  // the first 4 * kChunk ([block][row]) hold data.
+  __shared__ __align__(16) float2 s_scl0[kSclSlot], s_scl1[kSclSlot], s_scl2[kSclSlot];
   __shared__ int s_row[kChunk];
   if (tid < kChunk) {
     int r = -1;
@@ -471,109 +565,77 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
   __syncthreads();
 
   const int rows = (int)a.w.rows, B = (int)a.w.blocks;
-  const int nq = (B + 3) >> 2;
   const int tile = blockIdx.x * kWaves + wave;
-  const bool tile_ok = tile < (int)a.w.tiles;
   const int row = tile * kTileRows + nl;
   const int n_tg = (count + 7) >> 3;
 
-  float b0 = 0.0f;
-  if (a.bias != nullptr && tile_ok && row < rows) b0 = a.bias[(size_t)expert * a.bias_expert_stride + row];
-  b0 = b0 + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
-  float tot[8][2];
-#pragma unroll
-  for (int tg = 0; tg < 8; ++tg) { tot[tg][0] = b0; tot[tg][1] = b0; }
-
+  KLoop k;
+  k.B = B;
+  k.nq = (B + 3) >> 2;
+  k.nqf = B >> 2;
+  k.last_full = k.nqf > 0 ? k.nqf - 1 : 0;
+  k.wave = wave;
+  k.lane = lane;
+  k.nl = nl;
+  k.G = G;
+  k.tile_ok = tile < (int)a.w.tiles;
   // Waves past the last tile read tile 0 and discard it.
-  const int safe_tile = tile_ok ? tile : 0;
-  const uint8_t* nib = a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)safe_tile * 256 * B;
-  const uint8_t* scl = a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)safe_tile * 16 * B;
-  const int nqf = B >> 2, rem = B & 3;
-  const int last_full = nqf > 0 ? nqf - 1 : 0;
-  const WeightGroup tail = load_tail_group(nib, scl, nqf, rem > 0 ? rem : 1, lane, nl);
-  WeightGroup wg[kPrefetch];
+  const int safe_tile = k.tile_ok ? tile : 0;
+  k.nib = a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)safe_tile * 256 * B;
+  k.scl = a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)safe_tile * 64 * k.nq;
+  k.tail = load_tail_group(k.nib, k.scl, k.nqf, (B & 3) > 0 ? (B & 3) : 1, lane, nl);
+
+  float b0 = 0.0f;
+  if (a.bias != nullptr && k.tile_ok && row < rows) b0 = a.bias[(size_t)expert * a.bias_expert_stride + row];
+  b0 = b0 + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
+  float tot[kChunk / 8][2];
 #pragma unroll
-  for (int p = 0; p < kPrefetch; ++p) wg[p] = load_full_group(nib, scl, min(p, last_full), lane, nl);
+  for (int tg = 0; tg < kChunk / 8; ++tg) { tot[tg][0] = b0; tot[tg][1] = b0; }
 
-  // Activation staging: each thread moves up to kStageChunks 16-byte pieces
-  // and one scale pair per group. The piece -> (block j, row t, piece) map is
-  // the same for every group, so it is computed once here.
-  static_assert(kStageChunks == 4, "staging is unrolled for 4 pieces per thread");
-  const int per_block = count * 8;
-  const uint4* gactv = reinterpret_cast<const uint4*>(a.actv);
-  const float2* gacts = reinterpret_cast<const float2*>(a.acts);
-  uint4* lds_actv = reinterpret_cast<uint4*>(s_actv);
-  int pj[4], pbase[4], plds[4];
+  // DMA lane map, the same for every group. Code instruction i of this wave
+  // fills slot bytes c * 16 with c = (i * kWaves + wave) * 64 + lane, i.e.
+  // block j, token group tg, k-slice g, vector v (row tg*8 + v/2, part v%2)
+  // in the slot layout above; its source is piece (part, g) of the row's
+  // 128-byte block record. Scale dword d = wave * 64 + lane holds half d % 2
+  // of (block d / (2 kChunk), row (d / 2) % kChunk). Lanes with nothing to
+  // move read the buffer base (valid memory) into slot bytes no row uses, so
+  // every wave issues the same instructions. Reads of a last partial group
+  // run up to 3 blocks past a row, inside the buffers' slack.
+  k.gcodes = reinterpret_cast<const char*>(a.actv);
+  k.gscl = reinterpret_cast<const char*>(a.acts);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c_raw = tid + i * kGemmThreads;
-    const int c = min(c_raw, 4 * per_block - 1);
-    const int j = c / per_block, rr = c - j * per_block;
-    pj[i] = c_raw < 4 * per_block ? j : 4;  // 4 = never stored
-    pbase[i] = s_row[rr >> 3] * B * 8 + (rr & 7);
-    plds[i] = (j * kChunk + (rr >> 3)) * 8 + (rr & 7);
+  for (int i = 0; i < kCodeDma; ++i) {
+    const int c = (i * kWaves + wave) * 64 + lane;
+    const int j = c / (kChunk * 8), r = c % (kChunk * 8);
+    const int tg = r >> 6, g = (r >> 4) & 3, v = r & 15;
+    const int t = tg * 8 + (v >> 1), part = v & 1;
+    k.coff[i] = t < count ? ((s_row[t] * B + j) * 8 + part * 4 + g) * 16 : -1;
   }
-  const int cs = min(tid, 4 * count - 1);
-  const int sj_raw = cs / count, st = cs - sj_raw * count;
-  const int sj = tid < 4 * count ? sj_raw : 4;
-  const int sbase = s_row[st] * B;
-  const int slds = sj_raw * kChunk + st;
-  uint4 st0, st1, st2, st3;
-  float2 stage_s;
-#define GOSSMX_STAGE_LOAD(QQ)                                                             \
-  {                                                                                       \
-    const int qq_ = (QQ), nbq_ = min(4, B - 4 * qq_);                                    \
-    st0 = gactv[pbase[0] + (4 * qq_ + min(pj[0], nbq_ - 1)) * 8];                         \
-    st1 = gactv[pbase[1] + (4 * qq_ + min(pj[1], nbq_ - 1)) * 8];                         \
-    st2 = gactv[pbase[2] + (4 * qq_ + min(pj[2], nbq_ - 1)) * 8];                         \
-    st3 = gactv[pbase[3] + (4 * qq_ + min(pj[3], nbq_ - 1)) * 8];                         \
-    stage_s = gacts[sbase + 4 * qq_ + min(sj_raw, nbq_ - 1)];                             \
-  }
-#define GOSSMX_STAGE_STORE(QQ)                                                            \
-  {                                                                                       \
-    const int nbq_ = min(4, B - 4 * (QQ));                                               \
-    if (pj[0] < nbq_) lds_actv[plds[0]] = st0;                                            \
-    if (pj[1] < nbq_) lds_actv[plds[1]] = st1;                                            \
-    if (pj[2] < nbq_) lds_actv[plds[2]] = st2;                                            \
-    if (pj[3] < nbq_) lds_actv[plds[3]] = st3;                                            \
-    if (sj < nbq_) s_acts[slds] = stage_s;                                                \
+  {
+    const int d = wave * 64 + lane;
+    const int j = d / (kChunk * 2), t = (d >> 1) % kChunk;
+    k.soff = (d < 4 * kChunk * 2 && t < count) ? ((s_row[t] * B + j) * 2 + (d & 1)) * 4 : -1;
   }
 
-  GOSSMX_STAGE_LOAD(0);
-  const int a_off = ((nl >> 1) * 2 + (nl & 1)) * kBlock + G * 8;  // this lane's A operand in a token group
+  switch (n_tg) {
+    case 1: k_loop<RESIDUAL, 1>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2); break;
+    case 2: k_loop<RESIDUAL, 2>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2); break;
+    case 3: k_loop<RESIDUAL, 3>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2); break;
+    case 4: k_loop<RESIDUAL, 4>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2); break;
+    default: k_loop<RESIDUAL, 6>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2); break;
+  }
+  // Drain the trailing DMA into the ring before the LDS is reused or the
+  // work-group ends.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  const bool tile_ok = k.tile_ok;
+  float* s_act = reinterpret_cast<float*>(s_codes0);
 
-  // One K group: stage its activations into LDS, start the next group's
-  // staging loads, run the MFMAs and the ordered float chain, then refill
-  // this ring slot with group q + kPrefetch. Iterations past the last group
-  // only keep the barriers and loads in step (no compute, nothing stored).
-#define GOSSMX_GROUP(QV, SLOT)                                                            \
-  {                                                                                       \
-    const int q = (QV);                                                                   \
-    __syncthreads(); /* every wave is done reading the previous group */                 \
-    GOSSMX_STAGE_STORE(q);                                                                \
-    __syncthreads();                                                                      \
-    GOSSMX_STAGE_LOAD(min(q + 1, nq - 1));                                                \
-    const WeightGroup cur = q < nqf ? SLOT : tail;                                        \
-    if (tile_ok && q < nq)                                                                \
-      group_update<RESIDUAL>(tot, s_actv, s_acts, cur, min(4, B - 4 * q), n_tg, a_off, G); \
-    /* refill after the last use of the slot, so the load lands in the same registers */ \
-    SLOT = load_full_group(nib, scl, min(q + kPrefetch, last_full), lane, nl);            \
-  }
-  static_assert(kPrefetch == 3, "the K loop is unrolled by the prefetch depth");
-  const int nq_pad = (nq + 2) / 3 * 3;
-  for (int q0 = 0; q0 < nq_pad; q0 += 3) {
-    GOSSMX_GROUP(q0, wg[0])
-    GOSSMX_GROUP(q0 + 1, wg[1])
-    GOSSMX_GROUP(q0 + 2, wg[2])
-  }
-#undef GOSSMX_GROUP
-#undef GOSSMX_STAGE_LOAD
-#undef GOSSMX_STAGE_STORE
 
   if (MODE == kPlain) {
     if (tile_ok && row < rows) {
 #pragma unroll
-      for (int tg = 0; tg < 8; ++tg)
+      for (int tg = 0; tg < kChunk / 8; ++tg)
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const int c = tg * 8 + 2 * G + t;
@@ -583,7 +645,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
   } else if (MODE == kDown) {
     if (tile_ok && row < rows) {
 #pragma unroll
-      for (int tg = 0; tg < 8; ++tg)
+      for (int tg = 0; tg < kChunk / 8; ++tg)
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const int c = tg * 8 + 2 * G + t;
@@ -597,12 +659,10 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
     // gate_up epilogue: bf16 (cpu_runner.rs:2905), SwiGLU over (even, odd)
     // rows (:2907-2919), then the down input's residual-Q8 blocks: the 128
     // rows of this work-group make two 32-value blocks (cpu_runner.rs:3224-3231).
-    // The SwiGLU values reuse the activation LDS as [64 rows][64 values].
-    __syncthreads();
-    float* s_act = reinterpret_cast<float*>(s_actv);
+    // The SwiGLU values reuse the first LDS slot as [kChunk rows][64 values].
     constexpr int kActStride = kGemmRows / 2 + 1;
 #pragma unroll
-    for (int tg = 0; tg < 8; ++tg) {
+    for (int tg = 0; tg < kChunk / 8; ++tg) {
       if (tg < n_tg) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -689,7 +749,7 @@ __device__ __forceinline__ void v3_offsets(const TiledWeights& w, size_t e, size
   const size_t B = w.blocks, t = row / kTileRows, n = row % kTileRows, q = b / 4, j = b % 4;
   const size_t nb = B - 4 * q < 4 ? B - 4 * q : 4;
   *nib_off = e * w.nib_stride + t * 256 * B + q * 1024 + (g * 16 + n) * nb * 4 + j * 4;
-  *scl_off = e * w.scl_stride + t * 16 * B + q * 64 + n * nb + j;
+  *scl_off = e * w.scl_stride + t * 64 * ((B + 3) / 4) + q * 64 + n * 4 + j;
 }
 
 // Mxfp4MatrixView::block (lib.rs:810-851) for canonical v1 and x8 v2 data of
