@@ -4,6 +4,7 @@
 #include "gossmx_internal.h"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -55,6 +56,7 @@ struct gossmx_ctx {
   hipStream_t stream = nullptr;
   bool own_stream = false;
   int* err = nullptr;  // device error flags
+  uint16_t* sig_tab = nullptr;  // SwiGLU sigmoid table (built at context creation)
   bool fault_armed = false;
   bool profiling = false;
   std::vector<ProfileMark> marks;
@@ -275,6 +277,8 @@ int gossmx_ctx_create(int device, void* stream, gossmx_ctx** out) {
   }
   hipError_t e = hipMalloc(&ctx->err, 16);
   if (e == hipSuccess) e = launch_clear_ints(ctx->err, 4, ctx->stream);
+  if (e == hipSuccess) e = hipMalloc(&ctx->sig_tab, 65536 * sizeof(uint16_t));
+  if (e == hipSuccess) e = launch_build_sigmoid_table(ctx->sig_tab, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) {
     gossmx_ctx_destroy(ctx);
@@ -299,6 +303,7 @@ void gossmx_ctx_destroy(gossmx_ctx* ctx) {
   for (DevBuf* b : bufs)
     if (b->p) hipFree(b->p);
   if (ctx->err) hipFree(ctx->err);
+  if (ctx->sig_tab) hipFree(ctx->sig_tab);
   if (ctx->own_stream && ctx->stream) hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -638,6 +643,7 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   g.acts_next = static_cast<float*>(ctx->act2s.p);
   g.alpha = L->cfg.alpha;
   g.limit = L->cfg.limit;
+  g.sig_tab = ctx->sig_tab;
   g.err = ctx->err;
   {
     OpScope sc(ctx, GOSSMX_OP_GATE_UP);
@@ -749,6 +755,26 @@ int gossmx_selftest(gossmx_ctx* ctx) {
         return fail(GOSSMX_ERR_UNSUPPORTED, "mfma lane %d reg %d is %g, expected %g", lane, r, host[8 + 4 * lane + r],
                     want);
     }
+  // The device SwiGLU sigmoid table against the host libm expf on all 65,536
+  // bf16 inputs (the reference's f32::exp is the host expf).
+  std::vector<uint16_t> tab(65536);
+  HIP_TRY(hipMemcpyAsync(tab.data(), ctx->sig_tab, 65536 * sizeof(uint16_t), hipMemcpyDeviceToHost, ctx->stream),
+          "D2H sigmoid table");
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  for (uint32_t i = 0; i < 65536u; ++i) {
+    uint32_t xb = i << 16;
+    float x;
+    std::memcpy(&x, &xb, 4);
+    const float y = 1.0f / (1.0f + expf(-x));
+    uint32_t yb;
+    std::memcpy(&yb, &y, 4);
+    uint16_t want;
+    if ((yb & 0x7fffffffu) > 0x7f800000u) want = (uint16_t)((yb >> 16) | 0x40u);
+    else if ((yb & 0x8000u) && (yb & 0x17fffu)) want = (uint16_t)((yb >> 16) + 1u);
+    else want = (uint16_t)(yb >> 16);
+    if (tab[i] != want)
+      return fail(GOSSMX_ERR_UNSUPPORTED, "sigmoid table entry %#06x is %#06x, host expf gives %#06x", i, tab[i], want);
+  }
   return GOSSMX_OK;
 }
 

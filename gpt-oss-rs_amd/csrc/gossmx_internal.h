@@ -74,6 +74,7 @@ struct GemmArgs {
   float* out; size_t out_stride;      // kPlain
   _Float16* actv_next; float* acts_next;  // kGateUp: down-projection input per grouped route
   float alpha, limit;                 // kGateUp
+  const uint16_t* sig_tab;            // kGateUp: SwiGLU sigmoid per bf16 input (65,536 entries)
   uint16_t* y;                        // kDown: [m * top_k][rows] bf16
   int* err;
 };
@@ -114,6 +115,7 @@ hipError_t launch_generate(uint64_t seed, uint64_t stream_id, TiledWeights w, hi
 hipError_t launch_export(TiledWeights w, uint8_t* dst, hipStream_t stream);
 hipError_t launch_fill_tiled_padding(TiledWeights w, hipStream_t stream);
 hipError_t launch_clear_ints(int* p, size_t n, hipStream_t stream);
+hipError_t launch_build_sigmoid_table(uint16_t* tab, hipStream_t stream);
 hipError_t launch_selftest(float* out, hipStream_t stream);
 
 }  // namespace gossmx

@@ -91,19 +91,32 @@ __device__ float expf_glibc(float x) {
   return (float)y;
 }
 
+// The SwiGLU sigmoid bf16(1 / (1 + expf(-s))) of gpt_oss_swiglu
+// (cpu_runner.rs:3819-3820) for every bf16 value s = bits << 16.
+__device__ __forceinline__ uint16_t sigmoid_bf16(uint32_t bits) {
+  const float scaled = bf16_to_f32((uint16_t)bits);
+  return bf16_bits(1.0f / (1.0f + expf_glibc(-scaled)));
+}
+
 // gpt_oss_swiglu for one (gate, up) pair, cpu_runner.rs:3797-3826: gate =
 // min(g, limit) (NaN-ignoring like f32::min), up = clamp(u, -limit, limit)
-// (NaN kept), then bf16 after every tensor operation.
-__device__ float swiglu_one(float g, float u, float alpha, float limit) {
+// (NaN kept), then bf16 after every tensor operation. The sigmoid's input is
+// a bf16 value, so it is read from `sig_tab`, the 65,536 values of
+// sigmoid_bf16 computed by the same code (build_sigmoid_table).
+__device__ __forceinline__ float swiglu_one(float g, float u, float alpha, float limit, const uint16_t* sig_tab) {
   const float gate = fminf(g, limit);
   float up = u;
   if (up < -limit) up = -limit;
   if (up > limit) up = limit;
-  const float scaled = bf16r(gate * alpha);
-  const float sig = bf16r(1.0f / (1.0f + expf_glibc(-scaled)));
+  const float sig = bf16_to_f32(sig_tab[bf16_bits(gate * alpha)]);
   const float glu = bf16r(gate * sig);
   const float lin = bf16r(up + 1.0f);
   return bf16r(glu * lin);
+}
+
+__global__ void build_sigmoid_table_kernel(uint16_t* tab) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < 65536u) tab[i] = sigmoid_bf16(i);
 }
 
 // quantize_q8_block (lib.rs:1051-1065) for the 32 values held by a 32-lane
@@ -661,17 +674,19 @@ __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
     // rows of this work-group make two 32-value blocks (cpu_runner.rs:3224-3231).
     // The SwiGLU values reuse the first LDS slot as [kChunk rows][64 values].
     constexpr int kActStride = kGemmRows / 2 + 1;
+    // Lane pairs (even = gate row, odd = up row) hold both values for tokens
+    // t0 = 2G and t1 = 2G + 1; the even lane finishes t0 and the odd lane t1.
+    const bool odd = (nl & 1) != 0;
 #pragma unroll
     for (int tg = 0; tg < kChunk / 8; ++tg) {
       if (tg < n_tg) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const float gu = bf16r(tot[tg][t]);
-          const float other = __shfl_xor(gu, 1);
-          const int c = tg * 8 + 2 * G + t;
-          if ((nl & 1) == 0 && c < count)
-            s_act[c * kActStride + wave * 8 + (nl >> 1)] = swiglu_one(gu, other, a.alpha, a.limit);
-        }
+        const float own0 = bf16r(tot[tg][0]), own1 = bf16r(tot[tg][1]);
+        const float recv = __shfl_xor(odd ? own0 : own1, 1);
+        const float gate = odd ? recv : own0;
+        const float up = odd ? own1 : recv;
+        const int c = tg * 8 + 2 * G + (odd ? 1 : 0);
+        if (c < count)
+          s_act[c * kActStride + wave * 8 + (nl >> 1)] = swiglu_one(gate, up, a.alpha, a.limit, a.sig_tab);
       }
     }
     __syncthreads();
@@ -955,6 +970,11 @@ hipError_t launch_fill_tiled_padding(TiledWeights w, hipStream_t stream) {
 hipError_t launch_clear_ints(int* p, size_t n, hipStream_t stream) {
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(clear_ints_kernel, dim3(grid1d(n, 256)), dim3(256), 0, stream, p, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_build_sigmoid_table(uint16_t* tab, hipStream_t stream) {
+  hipLaunchKernelGGL(build_sigmoid_table_kernel, dim3(256), dim3(256), 0, stream, tab);
   return hipGetLastError();
 }
 
