@@ -57,6 +57,10 @@ struct gossmx_ctx {
   bool own_stream = false;
   int* err = nullptr;  // device error flags
   uint16_t* sig_tab = nullptr;  // SwiGLU sigmoid table (built at context creation)
+  // Second in-order stream (default priority) for the small-bucket GEMMs,
+  // joined back to `stream` with events.
+  hipStream_t side = nullptr;
+  hipEvent_t ev_dispatched = nullptr, ev_small_gate_up = nullptr, ev_small_down = nullptr;
   bool fault_armed = false;
   bool profiling = false;
   std::vector<ProfileMark> marks;
@@ -277,6 +281,10 @@ int gossmx_ctx_create(int device, void* stream, gossmx_ctx** out) {
   }
   hipError_t e = hipMalloc(&ctx->err, 16);
   if (e == hipSuccess) e = launch_clear_ints(ctx->err, 4, ctx->stream);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ev_dispatched, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ev_small_gate_up, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ev_small_down, hipEventDisableTiming);
   if (e == hipSuccess) e = hipMalloc(&ctx->sig_tab, 65536 * sizeof(uint16_t));
   if (e == hipSuccess) e = launch_build_sigmoid_table(ctx->sig_tab, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
@@ -302,6 +310,11 @@ void gossmx_ctx_destroy(gossmx_ctx* ctx) {
                     &ctx->act2s, &ctx->y, &ctx->out, &ctx->trace, &ctx->rec, &ctx->bias, &ctx->mout};
   for (DevBuf* b : bufs)
     if (b->p) hipFree(b->p);
+  if (ctx->side) hipStreamSynchronize(ctx->side);
+  if (ctx->ev_dispatched) hipEventDestroy(ctx->ev_dispatched);
+  if (ctx->ev_small_gate_up) hipEventDestroy(ctx->ev_small_gate_up);
+  if (ctx->ev_small_down) hipEventDestroy(ctx->ev_small_down);
+  if (ctx->side) hipStreamDestroy(ctx->side);
   if (ctx->err) hipFree(ctx->err);
   if (ctx->sig_tab) hipFree(ctx->sig_tab);
   if (ctx->own_stream && ctx->stream) hipStreamDestroy(ctx->stream);
@@ -563,7 +576,7 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
       (s = ensure(ctx, ctx->weights, R * 4)) || (s = ensure(ctx, ctx->act1v, m * B1 * 2 * kBlock * 2 + kActSlack)) ||
       (s = ensure(ctx, ctx->act1s, m * B1 * 8 + kActSlack)) || (s = ensure(ctx, ctx->bucket, (E + 1) * 4)) ||
       (s = ensure(ctx, ctx->route_tok, R * 4)) || (s = ensure(ctx, ctx->route_slot, R * 4)) ||
-      (s = ensure(ctx, ctx->work, (2 * max_work + 1) * 4)) ||
+      (s = ensure(ctx, ctx->work, (2 * max_work + 1 + 2 * E + 1) * 4)) ||
       (s = ensure(ctx, ctx->act2v, R * B2 * 2 * kBlock * 2 + kActSlack)) ||
       (s = ensure(ctx, ctx->act2s, R * B2 * 8 + kActSlack)) || (s = ensure(ctx, ctx->y, R * H * 2)))
     return s;
@@ -593,6 +606,11 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   int* bucket = static_cast<int*>(ctx->bucket.p);
   int* work = static_cast<int*>(ctx->work.p);
   int* n_work = work + 2 * max_work;
+  int* work_small = n_work + 1;
+  int* n_work_small = work_small + 2 * E;
+  const size_t max_small = std::min(E, R);
+  // Buckets of <= kSmallRows rows use the small-bucket kernel.
+  const bool small = true;
   ActBuffers act1{static_cast<_Float16*>(ctx->act1v.p), static_cast<float*>(ctx->act1s.p)};
 
   RouteArgs ra{};
@@ -623,10 +641,14 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   da.route_slot = static_cast<int*>(ctx->route_slot.p);
   da.work = work;
   da.n_work = n_work;
+  da.work_small = work_small;
+  da.n_work_small = n_work_small;
+  da.small_enabled = small ? 1 : 0;
   {
     OpScope sc(ctx, GOSSMX_OP_DISPATCH);
     HIP_TRY(launch_dispatch(da, ctx->stream), "dispatch launch");
   }
+  if (small) HIP_TRY(hipEventRecord(ctx->ev_dispatched, ctx->stream), "event record");
   GemmArgs g{};
   g.w = L->gate_up->t;
   g.actv = act1.v;
@@ -636,6 +658,8 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   g.residual = 1;
   g.work = work;
   g.n_work = n_work;
+  g.work_small = work_small;
+  g.n_work_small = n_work_small;
   g.bucket_off = bucket;
   g.route_tok = da.route_tok;
   g.route_slot = da.route_slot;
@@ -645,10 +669,6 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   g.limit = L->cfg.limit;
   g.sig_tab = ctx->sig_tab;
   g.err = ctx->err;
-  {
-    OpScope sc(ctx, GOSSMX_OP_GATE_UP);
-    HIP_TRY(launch_gemm(kGateUp, g, (int)max_work, ctx->stream), "gate_up launch");
-  }
   GemmArgs d = g;
   d.w = L->down->t;
   d.actv = g.actv_next;
@@ -656,9 +676,25 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   d.bias = L->down_bias;
   d.bias_expert_stride = H;
   d.y = static_cast<uint16_t*>(ctx->y.p);
+  if (small) {
+    // Small buckets on the side stream: gate_up then down of the same experts
+    // (their down inputs come only from their own gate_up), overlapping the
+    // large-bucket GEMMs on the main stream.
+    HIP_TRY(hipStreamWaitEvent(ctx->side, ctx->ev_dispatched, 0), "stream wait");
+    HIP_TRY(launch_gemm_small(kGateUp, g, (int)max_small, ctx->side), "gate_up small launch");
+    HIP_TRY(hipEventRecord(ctx->ev_small_gate_up, ctx->side), "event record");
+    HIP_TRY(launch_gemm_small(kDown, d, (int)max_small, ctx->side), "down small launch");
+    HIP_TRY(hipEventRecord(ctx->ev_small_down, ctx->side), "event record");
+  }
+  {
+    OpScope sc(ctx, GOSSMX_OP_GATE_UP);
+    HIP_TRY(launch_gemm(kGateUp, g, (int)max_work, ctx->stream), "gate_up launch");
+    if (small) HIP_TRY(hipStreamWaitEvent(ctx->stream, ctx->ev_small_gate_up, 0), "stream wait");
+  }
   {
     OpScope sc(ctx, GOSSMX_OP_DOWN);
     HIP_TRY(launch_gemm(kDown, d, (int)max_work, ctx->stream), "down launch");
+    if (small) HIP_TRY(hipStreamWaitEvent(ctx->stream, ctx->ev_small_down, 0), "stream wait");
   }
   {
     OpScope sc(ctx, GOSSMX_OP_WEIGHTING);

@@ -15,6 +15,7 @@ constexpr int kWgRows = 64;     // gate_up rows (32 gate/up pairs) per 32-value 
 constexpr int kChunk = 48;      // activation rows per work item
 constexpr int kMaxExperts = 128;
 constexpr int kMaxTopK = 8;
+constexpr int kSmallRows = 4;        // buckets of at most this many rows use the small-bucket GEMM
 
 // Device error flags (sticky until the host reads them).
 constexpr int kErrNonFiniteLogits = 1;
@@ -67,6 +68,8 @@ struct GemmArgs {
   int plain_expert, plain_m;          // kPlain
   const int* work;                    // [n][2] (expert, chunk start)   (gate_up/down)
   const int* n_work;
+  const int* work_small;              // [n][2] (expert, 0): buckets for the small-bucket kernel
+  const int* n_work_small;
   const int* bucket_off;              // [experts + 1]
   const int* route_tok;               // grouped route -> source row
   const int* route_slot;              // grouped route -> row * top_k + rank
@@ -100,12 +103,18 @@ struct DispatchArgs {
   int* route_slot;      // [routes]
   int* work;            // [max_work][2]
   int* n_work;
+  int* work_small;      // [experts][2]
+  int* n_work_small;
+  int small_enabled;    // 1: buckets of <= kSmallRows rows go to work_small
 };
 
 // Launchers (gossmx_kernels.hip). All are asynchronous on `stream`.
 hipError_t launch_route(const RouteArgs& a, hipStream_t stream);
 hipError_t launch_dispatch(const DispatchArgs& a, hipStream_t stream);
 hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream);
+// Small-bucket variant (work_small items; residual-Q8, gate_up or down).
+hipError_t launch_gemm_small(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream);
+
 hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int top_k, int hidden, float* out,
                           float* trace_down, hipStream_t stream);
 hipError_t launch_prep_records(const uint8_t* records, int kind, size_t m, size_t blocks, size_t row_stride,

@@ -266,19 +266,53 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
   for (int i = tid; i < R; i += 1024) atomicAdd(&s_tot[a.selected[i]], 1);
   __syncthreads();
   if (tid == 0) {
-    int acc = 0, n = 0;
+    // Work items: buckets of at most kSmallRows rows go to the small-bucket
+    // kernel (when enabled), larger ones are cut into kChunk-row chunks.
+    int acc = 0, ns = 0;
     for (int e = 0; e < E; ++e) {
       s_off[e] = acc;
       a.bucket_off[e] = acc;
-      for (int s = 0; s < s_tot[e]; s += kChunk) {
-        a.work[2 * n] = e;
-        a.work[2 * n + 1] = s;
-        ++n;
+      const int c = s_tot[e];
+      if (a.small_enabled && c > 0 && c <= kSmallRows) {
+        a.work_small[2 * ns] = e;
+        a.work_small[2 * ns + 1] = 0;
+        ++ns;
       }
-      acc += s_tot[e];
+      acc += c;
     }
     a.bucket_off[E] = acc;
-    *a.n_work = n;
+    *a.n_work_small = ns;
+  }
+  __syncthreads();
+  // Large buckets: chunks in descending row count, so the heaviest work items
+  // are dispatched first and the grid's last wave is light. All chunks of an
+  // expert but the last hold kChunk rows; full chunks come first (expert
+  // order), then the partial last chunks by size (ties by expert).
+  for (int e = tid; e < E; e += 1024) {
+    const int c = s_tot[e];
+    const bool large = c > 0 && !(a.small_enabled && c <= kSmallRows);
+    const int full = large ? c / kChunk : 0, part = large ? c % kChunk : 0;
+    int full_before = 0, full_total = 0, part_before = 0, parts = 0;
+    for (int f = 0; f < E; ++f) {
+      const int cf = s_tot[f];
+      const bool lf = cf > 0 && !(a.small_enabled && cf <= kSmallRows);
+      const int ff = lf ? cf / kChunk : 0, pf = lf ? cf % kChunk : 0;
+      full_total += ff;
+      if (f < e) full_before += ff;
+      if (pf > 0) {
+        ++parts;
+        if (pf > part || (pf == part && f < e)) ++part_before;
+      }
+    }
+    for (int i = 0; i < full; ++i) {
+      a.work[2 * (full_before + i)] = e;
+      a.work[2 * (full_before + i) + 1] = i * kChunk;
+    }
+    if (part > 0) {
+      a.work[2 * (full_total + part_before)] = e;
+      a.work[2 * (full_total + part_before) + 1] = full * kChunk;
+    }
+    if (e == 0) *a.n_work = full_total + parts;
   }
   __syncthreads();
   for (int base = 0; base < R; base += 1024) {
@@ -467,6 +501,80 @@ __device__ __forceinline__ void group_update(float (&tot)[kChunk / 8][2], const 
   }
 }
 
+// Shared GEMM epilogue: plain f32 stores, the down projection's bf16 rows,
+// or gate_up's SwiGLU and down-input quantization. `s_act` is LDS scratch of
+// at least count * (kGemmRows / 2 + 1) floats, free for reuse.
+template <int MODE, int NT>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const float (&tot)[NT][2], const int n_tg,
+                                              const int count, const int start, const int route_base, const int row,
+                                              const bool tile_ok, float* s_act) {
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int nl = lane & 15, G = lane >> 4;
+  const int rows = (int)a.w.rows;
+
+
+  if (MODE == kPlain) {
+    if (tile_ok && row < rows) {
+#pragma unroll
+      for (int tg = 0; tg < NT; ++tg)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int c = tg * 8 + 2 * G + t;
+          if (c < count) a.out[(size_t)(start + c) * a.out_stride + row] = tot[tg][t];
+        }
+    }
+  } else if (MODE == kDown) {
+    if (tile_ok && row < rows) {
+#pragma unroll
+      for (int tg = 0; tg < NT; ++tg)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int c = tg * 8 + 2 * G + t;
+          if (c < count) {
+            const int slot = a.route_slot[route_base + start + c];
+            a.y[(size_t)slot * rows + row] = bf16_bits(tot[tg][t]);  // bf16 (cpu_runner.rs:2945-2947)
+          }
+        }
+    }
+  } else {
+    // gate_up epilogue: bf16 (cpu_runner.rs:2905), SwiGLU over (even, odd)
+    // rows (:2907-2919), then the down input's residual-Q8 blocks: the 128
+    // rows of this work-group make two 32-value blocks (cpu_runner.rs:3224-3231).
+    // The SwiGLU values reuse the first LDS slot as [kChunk rows][64 values].
+    constexpr int kActStride = kGemmRows / 2 + 1;
+    // Lane pairs (even = gate row, odd = up row) hold both values for tokens
+    // t0 = 2G and t1 = 2G + 1; the even lane finishes t0 and the odd lane t1.
+    const bool odd = (nl & 1) != 0;
+#pragma unroll
+    for (int tg = 0; tg < NT; ++tg) {
+      if (tg < n_tg) {
+        const float own0 = bf16r(tot[tg][0]), own1 = bf16r(tot[tg][1]);
+        const float recv = __shfl_xor(odd ? own0 : own1, 1);
+        const float gate = odd ? recv : own0;
+        const float up = odd ? own1 : recv;
+        const int c = tg * 8 + 2 * G + (odd ? 1 : 0);
+        if (c < count)
+          s_act[c * kActStride + wave * 8 + (nl >> 1)] = swiglu_one(gate, up, a.alpha, a.limit, a.sig_tab);
+      }
+    }
+    __syncthreads();
+    const int hw = tid >> 5, l32 = tid & 31;
+    const int blocks_next = rows / kWgRows;
+    constexpr int kBlocksPerWg = kGemmRows / 64;
+    for (int item = hw; item < count * kBlocksPerWg; item += kGemmThreads / 32) {
+      const int c = item / kBlocksPerWg, h = item % kBlocksPerWg;
+      if (blockIdx.x * kBlocksPerWg + h >= blocks_next) continue;  // uniform per half wave
+      const float v = s_act[c * kActStride + h * kBlock + l32];
+      if (!isfinite(v)) atomicOr(a.err, kErrNonFiniteInput);
+      ActBuffers nx;
+      nx.v = a.actv_next;
+      nx.s = a.acts_next;
+      residual_q8_store(v, l32, (size_t)(route_base + start + c), blocks_next, blockIdx.x * kBlocksPerWg + h, nx);
+    }
+  }
+}
+
 // Loop-invariant state of the K loop.
 struct KLoop {
   const uint8_t* nib;
@@ -641,69 +749,208 @@ __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
   // work-group ends.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  const bool tile_ok = k.tile_ok;
-  float* s_act = reinterpret_cast<float*>(s_codes0);
+  gemm_epilogue<MODE, kChunk / 8>(a, tot, n_tg, count, start, route_base, row, k.tile_ok,
+                                  reinterpret_cast<float*>(s_codes0));
+}
 
+// ---------------------------------------------------------------------------
+// Small-bucket expert GEMM: work items of at most kSmallRows (16) activation
+// rows, most of the experts at decode batch 64 under Zipf routing. The item's
+// activations are staged into LDS for a whole phase of K (all 90 blocks for
+// <= 4 rows, 48 blocks for <= 8, 24 blocks for <= 16), so the K loop inside a
+// phase has no barriers and no activation traffic: each wave streams its
+// 16-row weight tile through a kSmallRing-deep register ring that continues
+// across phases. Same operands, chain order and epilogue as gemm_kernel.
+//
+// Per-block LDS layouts (V vectors = 2 parts x token slots):
+//   V = 8  (<= 4 rows):  512 B = [k-slice g][vector v < 8][16 B]; MFMA rows
+//                         8..15 repeat rows 0..7 (unused results).
+//   V = 16 (<= 8 rows):  1 KiB = [g][v < 16][16 B]
+//   V = 32 (<= 16 rows): 2 KiB = two 1 KiB token groups of the V = 16 form.
+// Scales: [block][token slot] float2, V / 2 slots per block, plus an 8-entry
+// tail (lanes of unused token slots read past a block).
+constexpr int kSmallRing = 3;
+constexpr int kSmallCodeBytes = 48 * 1024;
+constexpr int kSmallSclEntries = 384 + 8;
+constexpr int kSmallStage = 6;  // 16-byte staging pieces per thread per phase (max over layouts)
 
-  if (MODE == kPlain) {
-    if (tile_ok && row < rows) {
+template <int V>
+struct SmallLayout {
+  static constexpr int kNT = V <= 16 ? 1 : 2;           // MFMA token groups
+  static constexpr int kBlockBytes = V * 64;            // LDS bytes per block
+  static constexpr int kSlots = V / 2;                  // token slots per block
+  static constexpr int kPhaseBlocks = kSmallCodeBytes / kBlockBytes;  // 96, 48, 24
+  static_assert(kPhaseBlocks % 12 == 0, "phases are whole multiples of the 3-deep, 4-block ring");
+  static_assert(kPhaseBlocks * kSlots + 8 <= kSmallSclEntries, "scale LDS");
+  static_assert(16 * 24 * 8 <= kSmallStage * kGemmThreads, "staging pieces");
+};
+
+template <int V, bool RESIDUAL, bool SCALED>
+__device__ __forceinline__ void small_block(float (&tot)[2][2], const char* codes, const float2* scl, const half8 bop,
+                                            const float e8, const int jl, const int lane, const int nl,
+                                            const int G) {
+  using L = SmallLayout<V>;
 #pragma unroll
-      for (int tg = 0; tg < kChunk / 8; ++tg)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int c = tg * 8 + 2 * G + t;
-          if (c < count) a.out[(size_t)(start + c) * a.out_stride + row] = tot[tg][t];
-        }
-    }
-  } else if (MODE == kDown) {
-    if (tile_ok && row < rows) {
-#pragma unroll
-      for (int tg = 0; tg < kChunk / 8; ++tg)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int c = tg * 8 + 2 * G + t;
-          if (c < count) {
-            const int slot = a.route_slot[route_base + start + c];
-            a.y[(size_t)slot * rows + row] = bf16_bits(tot[tg][t]);  // bf16 (cpu_runner.rs:2945-2947)
-          }
-        }
-    }
-  } else {
-    // gate_up epilogue: bf16 (cpu_runner.rs:2905), SwiGLU over (even, odd)
-    // rows (:2907-2919), then the down input's residual-Q8 blocks: the 128
-    // rows of this work-group make two 32-value blocks (cpu_runner.rs:3224-3231).
-    // The SwiGLU values reuse the first LDS slot as [kChunk rows][64 values].
-    constexpr int kActStride = kGemmRows / 2 + 1;
-    // Lane pairs (even = gate row, odd = up row) hold both values for tokens
-    // t0 = 2G and t1 = 2G + 1; the even lane finishes t0 and the odd lane t1.
-    const bool odd = (nl & 1) != 0;
-#pragma unroll
-    for (int tg = 0; tg < kChunk / 8; ++tg) {
-      if (tg < n_tg) {
-        const float own0 = bf16r(tot[tg][0]), own1 = bf16r(tot[tg][1]);
-        const float recv = __shfl_xor(odd ? own0 : own1, 1);
-        const float gate = odd ? recv : own0;
-        const float up = odd ? own1 : recv;
-        const int c = tg * 8 + 2 * G + (odd ? 1 : 0);
-        if (c < count)
-          s_act[c * kActStride + wave * 8 + (nl >> 1)] = swiglu_one(gate, up, a.alpha, a.limit, a.sig_tab);
-      }
-    }
-    __syncthreads();
-    const int hw = tid >> 5, l32 = tid & 31;
-    const int blocks_next = rows / kWgRows;
-    constexpr int kBlocksPerWg = kGemmRows / 64;
-    for (int item = hw; item < count * kBlocksPerWg; item += kGemmThreads / 32) {
-      const int c = item / kBlocksPerWg, h = item % kBlocksPerWg;
-      if (blockIdx.x * kBlocksPerWg + h >= blocks_next) continue;  // uniform per half wave
-      const float v = s_act[c * kActStride + h * kBlock + l32];
-      if (!isfinite(v)) atomicOr(a.err, kErrNonFiniteInput);
-      ActBuffers nx;
-      nx.v = a.actv_next;
-      nx.s = a.acts_next;
-      residual_q8_store(v, l32, (size_t)(route_base + start + c), blocks_next, blockIdx.x * kBlocksPerWg + h, nx);
+  for (int tg = 0; tg < L::kNT; ++tg) {
+    const int a_off = V == 8 ? (G * 8 + (nl & 7)) * 16 : tg * 1024 + lane * 16;
+    const half8 aop = *reinterpret_cast<const half8*>(codes + jl * L::kBlockBytes + a_off);
+    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, zero, 0, 0, 0);
+    const float4 sc = *reinterpret_cast<const float4*>(&scl[jl * L::kSlots + tg * 8 + 2 * G]);
+    if (SCALED) {
+      tot[tg][0] = tot[tg][0] + d[0] * sc.x;
+      if (RESIDUAL) tot[tg][0] = tot[tg][0] + d[1] * sc.y;
+      tot[tg][1] = tot[tg][1] + d[2] * sc.z;
+      if (RESIDUAL) tot[tg][1] = tot[tg][1] + d[3] * sc.w;
+    } else {
+      tot[tg][0] = tot[tg][0] + (d[0] * e8) * sc.x;
+      if (RESIDUAL) tot[tg][0] = tot[tg][0] + (d[1] * e8) * sc.y;
+      tot[tg][1] = tot[tg][1] + (d[2] * e8) * sc.z;
+      if (RESIDUAL) tot[tg][1] = tot[tg][1] + (d[3] * e8) * sc.w;
     }
   }
+}
+
+// One 4-block weight group whose first block is phase-local block jl0.
+template <int V, bool RESIDUAL>
+__device__ __forceinline__ void small_group(float (&tot)[2][2], const char* codes, const float2* scl,
+                                            const WeightGroup cur, const int jl0, const int nb, const int lane,
+                                            const int nl, const int G) {
+  const uint32_t wv[4] = {cur.v.x, cur.v.y, cur.v.z, cur.v.w};
+  bool in_range = true;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t s = (cur.s >> (8 * j)) & 0xffu;
+    if (j < nb) in_range = in_range && (s - kFastScaleLo) <= (kFastScaleHi - kFastScaleLo);
+  }
+  if (__all(in_range)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j < nb) {
+        const float e8 = __uint_as_float(((cur.s >> (8 * j)) & 0xffu) << 23);
+        small_block<V, RESIDUAL, true>(tot, codes, scl, fp4x8_to_half8_scaled(wv[j], e8), 0.0f, jl0 + j, lane, nl, G);
+      }
+    }
+  } else {
+#pragma unroll 1
+    for (int j = 0; j < nb; ++j) {
+      const uint32_t w = j == 0 ? wv[0] : (j == 1 ? wv[1] : (j == 2 ? wv[2] : wv[3]));
+      const float e8 = e8m0_select((cur.s >> (8 * j)) & 0xffu);
+      small_block<V, RESIDUAL, false>(tot, codes, scl, fp4x8_to_half8(w), e8, jl0 + j, lane, nl, G);
+    }
+  }
+}
+
+// Stages blocks [k0, k0 + nbk) of every row into LDS (loads unconditional,
+// clamped to valid indices; stores only for real pieces).
+template <int V>
+__device__ __forceinline__ void small_stage(char* codes, float2* scl, const uint4* gactv, const float2* gacts,
+                                            const int* s_row, const int count, const int B, const int k0,
+                                            const int nbk, const int tid) {
+  using L = SmallLayout<V>;
+  const int per_row = nbk * 8, pieces = count * per_row;
+  uint4 st[kSmallStage];
+#pragma unroll
+  for (int i = 0; i < kSmallStage; ++i) {
+    const int c = min(tid + i * kGemmThreads, pieces - 1);
+    const int t = c / per_row, rem = c - t * per_row;
+    st[i] = gactv[((size_t)s_row[t] * B + k0) * 8 + rem];
+  }
+  const int sc = min(tid, count * nbk - 1);
+  const int stt = sc / nbk, stj = sc - stt * nbk;
+  const float2 sv = gacts[(size_t)s_row[stt] * B + k0 + stj];
+#pragma unroll
+  for (int i = 0; i < kSmallStage; ++i) {
+    const int c = tid + i * kGemmThreads;
+    if (c < pieces) {
+      const int t = c / per_row, rem = c - t * per_row;
+      const int j = rem >> 3, p = rem & 7, part = p >> 2, g = p & 3;  // piece p of the block's 128-byte record
+      const int off = V == 8 ? j * 512 + (g * 8 + 2 * t + part) * 16
+                             : j * L::kBlockBytes + (t >> 3) * 1024 + (g * 16 + 2 * (t & 7) + part) * 16;
+      *reinterpret_cast<uint4*>(codes + off) = st[i];
+    }
+  }
+  if (tid < count * nbk) scl[stj * L::kSlots + stt] = sv;
+}
+
+template <int V, bool RESIDUAL>
+__device__ __forceinline__ void small_k_loop(float (&tot)[2][2], char* codes, float2* scl, const int* s_row,
+                                             const GemmArgs& a, const uint8_t* nib, const uint8_t* wscl,
+                                             const int count, const int B, const int tid, const int lane,
+                                             const int nl, const int G) {
+  using L = SmallLayout<V>;
+  const int nqf = B >> 2, last_full = nqf > 0 ? nqf - 1 : 0;
+  const uint4* gactv = reinterpret_cast<const uint4*>(a.actv);
+  const float2* gacts = reinterpret_cast<const float2*>(a.acts);
+  const WeightGroup tail = load_tail_group(nib, wscl, nqf, (B & 3) > 0 ? (B & 3) : 1, lane, nl);
+  WeightGroup r0 = load_full_group(nib, wscl, min(0, last_full), lane, nl);
+  WeightGroup r1 = load_full_group(nib, wscl, min(1, last_full), lane, nl);
+  WeightGroup r2 = load_full_group(nib, wscl, min(2, last_full), lane, nl);
+  const int phases = (B + L::kPhaseBlocks - 1) / L::kPhaseBlocks;
+  for (int ph = 0; ph < phases; ++ph) {
+    const int k0 = ph * L::kPhaseBlocks, nbk = min(L::kPhaseBlocks, B - k0);
+    if (ph > 0) __syncthreads();  // every wave is done with the previous phase
+    small_stage<V>(codes, scl, gactv, gacts, s_row, count, B, k0, nbk, tid);
+    __syncthreads();
+    const int q_begin = k0 >> 2, q_end = (k0 + nbk + 3) >> 2;
+#define GOSSMX_SMALL_GROUP(QQ, SLOT)                                                                   \
+  {                                                                                                    \
+    const int q = (QQ);                                                                                \
+    if (q < q_end) {                                                                                   \
+      const bool full = q < nqf;                                                                       \
+      small_group<V, RESIDUAL>(tot, codes, scl, full ? SLOT : tail, 4 * q - k0, full ? 4 : (B & 3), lane, \
+                               nl, G);                                                                 \
+    }                                                                                                  \
+    SLOT = load_full_group(nib, wscl, min(q + kSmallRing, last_full), lane, nl); /* after last use */  \
+  }
+    for (int q0 = q_begin; q0 < q_begin + L::kPhaseBlocks / 4; q0 += 3) {
+      GOSSMX_SMALL_GROUP(q0, r0)
+      GOSSMX_SMALL_GROUP(q0 + 1, r1)
+      GOSSMX_SMALL_GROUP(q0 + 2, r2)
+    }
+#undef GOSSMX_SMALL_GROUP
+  }
+}
+
+template <int MODE, bool RESIDUAL>
+__global__ __launch_bounds__(kGemmThreads, 6) void gemm_small_kernel(GemmArgs a) {
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int nl = lane & 15, G = lane >> 4;
+  const int wi = blockIdx.y;
+  if (wi >= *a.n_work_small) return;  // uniform over the work-group
+  const int expert = a.work_small[2 * wi];
+  const int route_base = a.bucket_off[expert];
+  const int count = a.bucket_off[expert + 1] - route_base;  // 1..kSmallRows
+  __shared__ __align__(16) char s_codes[kSmallCodeBytes];
+  __shared__ __align__(16) float2 s_scl[kSmallSclEntries];
+  __shared__ int s_row[kSmallRows];
+  if (tid < kSmallRows) {
+    int r = -1;
+    if (tid < count) r = MODE == kGateUp ? a.route_tok[route_base + tid] : route_base + tid;
+    s_row[tid] = r;
+  }
+  __syncthreads();
+
+  const int rows = (int)a.w.rows, B = (int)a.w.blocks;
+  const int nq = (B + 3) >> 2;
+  const int tile = blockIdx.x * kWaves + wave;
+  const bool tile_ok = tile < (int)a.w.tiles;
+  const int row = tile * kTileRows + nl;
+  const int safe_tile = tile_ok ? tile : 0;
+  const uint8_t* nib = a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)safe_tile * 256 * B;
+  const uint8_t* wscl = a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)safe_tile * 64 * nq;
+
+  float b0 = 0.0f;
+  if (a.bias != nullptr && tile_ok && row < rows) b0 = a.bias[(size_t)expert * a.bias_expert_stride + row];
+  b0 = b0 + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
+  float tot[2][2] = {{b0, b0}, {b0, b0}};
+  if (count <= 4) small_k_loop<8, RESIDUAL>(tot, s_codes, s_scl, s_row, a, nib, wscl, count, B, tid, lane, nl, G);
+  else if (count <= 8) small_k_loop<16, RESIDUAL>(tot, s_codes, s_scl, s_row, a, nib, wscl, count, B, tid, lane, nl, G);
+  else small_k_loop<32, RESIDUAL>(tot, s_codes, s_scl, s_row, a, nib, wscl, count, B, tid, lane, nl, G);
+  __syncthreads();  // the activation LDS is reused by the epilogue
+  gemm_epilogue<MODE, 2>(a, tot, count <= 8 ? 1 : 2, count, 0, route_base, row, tile_ok,
+                         reinterpret_cast<float*>(s_codes));
 }
 
 // ---------------------------------------------------------------------------
@@ -926,6 +1173,15 @@ hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int grid_work, hipStrea
     if (mode != kPlain) return hipErrorInvalidValue;  // the MoE block always runs residual-Q8
     hipLaunchKernelGGL((gemm_kernel<kPlain, false>), grid, block, 0, stream, a);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_small(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream) {
+  if (!a.residual || mode == kPlain) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((a.w.tiles + kWaves - 1) / kWaves), (unsigned)grid_work);
+  const dim3 block(kGemmThreads);
+  if (mode == kGateUp) hipLaunchKernelGGL((gemm_small_kernel<kGateUp, true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((gemm_small_kernel<kDown, true>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 
