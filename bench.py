@@ -102,6 +102,8 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--zipf", type=float, default=1.1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", dest="graph", action="store_false",
+                    help="time eager launches instead of the captured HIP graph of the step")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a device-to-device copy of this many MiB (calibrates HBM byte counters)")
@@ -134,24 +136,41 @@ def main() -> int:
         for st in state:
             st["moe"].forward_device(x_dev, args.batch, st["out_dev"], injected_logits=st["logits_dev"])
 
-    with torch.cuda.stream(stream):
-        for _ in range(args.warmup):
-            step()
-        ctx.synchronize()
-        torch.cuda.synchronize()
-        ctx.profile(True)
-        ctx.profile_reset()
+    def timed(fn) -> float:
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         start.record(stream)
         for _ in range(args.steps):
-            step()
+            fn()
         end.record(stream)
         torch.cuda.synchronize()
         ctx.synchronize()  # raises if a device-side check failed
-        ms_total = start.elapsed_time(end)
+        return start.elapsed_time(end)
+
+    graph = None
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            step()
+        ctx.synchronize()
+        # Eager pass with the library's hipEvent profiler on the kernels' stream:
+        # per-kernel durations for the roofline and the stage breakdown.
+        ctx.profile(True)
+        ctx.profile_reset()
+        ms_eager = timed(step)
         prof = ctx.profile_read()
         ctx.profile(False)
+        if args.graph:
+            # The same 24-layer step captured once as a HIP graph and replayed:
+            # identical kernels and arguments, without per-launch gaps.
+            ctx.capture_begin()
+            step()
+            graph = ctx.capture_end()
+            for _ in range(args.warmup):
+                graph.launch()
+            ctx.synchronize()
+            ms_total = timed(graph.launch)
+        else:
+            ms_total = ms_eager
 
     ms_step = ms_total / args.steps
     layer_tokens = args.batch * args.layers
@@ -198,9 +217,13 @@ def main() -> int:
             "avg_launch_ms": gu_avg_ms, "bytes_per_launch": gu_bytes_per_launch,
         },
         "stage_ms_per_step": {k: v["total_ms"] / args.steps for k, v in prof.items() if v["launches"]},
+        "launch": "hip-graph" if args.graph else "eager",
+        "eager_ms_per_step": ms_eager / args.steps,
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(x, state[0], out0, args.cpu_threads)
+    if graph is not None:
+        graph.close()
     for st in state:
         st["moe"].close()
         st["gu"].close()

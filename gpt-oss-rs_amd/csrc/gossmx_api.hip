@@ -60,6 +60,7 @@ struct gossmx_ctx {
   // Second in-order stream (default priority) for the small-bucket GEMMs,
   // joined back to `stream` with events.
   hipStream_t side = nullptr;
+  bool capturing = false;
   hipEvent_t ev_dispatched = nullptr, ev_small_gate_up = nullptr, ev_small_down = nullptr;
   bool fault_armed = false;
   bool profiling = false;
@@ -78,6 +79,12 @@ struct gossmx_weights {
   TiledWeights t;
 };
 
+struct gossmx_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  int device = 0;
+};
+
 struct gossmx_layer {
   gossmx_moe_config cfg;
   const gossmx_weights* gate_up = nullptr;
@@ -92,6 +99,8 @@ namespace {
 
 int ensure(gossmx_ctx* ctx, DevBuf& b, size_t bytes) {
   if (bytes <= b.cap) return GOSSMX_OK;
+  if (ctx->capturing)
+    return fail(GOSSMX_ERR_UNSUPPORTED, "scratch would grow during graph capture; run the same shapes eagerly first");
   if (b.p) {
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     HIP_TRY(hipFree(b.p), "hipFree");
@@ -121,7 +130,7 @@ struct OpScope {
   int op;
   hipEvent_t start = nullptr;
   OpScope(gossmx_ctx* c, int o) : ctx(c), op(o) {
-    if (ctx->profiling) {
+    if (ctx->profiling && !ctx->capturing) {
       start = take_event(ctx);
       if (start) hipEventRecord(start, ctx->stream);
     }
@@ -453,6 +462,8 @@ int gossmx_mxfp4_matmul(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
   if (!p || !p->weights) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null problem or weights");
   const TiledWeights& w = p->weights->t;
   if (int s = validate_problem(p, w.rows, w.blocks, w.experts)) return s;
+  if (ctx->capturing && p->memory == GOSSMX_MEM_HOST)
+    return fail(GOSSMX_ERR_UNSUPPORTED, "host-memory calls cannot be captured");
   if (ctx->fault_armed) {
     ctx->fault_armed = false;
     return fail(GOSSMX_ERR_INJECTED_FAULT, "injected fault before launch");
@@ -560,6 +571,8 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   if (io->memory != GOSSMX_MEM_HOST && io->memory != GOSSMX_MEM_DEVICE)
     return fail(GOSSMX_ERR_INVALID_ARGUMENT, "unknown memory kind %d", io->memory);
   if (io->m == 0) return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "empty MoE batch");
+  if (ctx->capturing && io->memory == GOSSMX_MEM_HOST)
+    return fail(GOSSMX_ERR_UNSUPPORTED, "host-memory calls cannot be captured");
   const size_t m = io->m, E = L->cfg.experts, H = L->cfg.hidden, I = L->cfg.intermediate, K = L->cfg.top_k;
   const size_t R = m * K, B1 = H / kBlock, B2 = I / kBlock;
   if (m > (size_t)(INT32_MAX / 8) / std::max<size_t>(H, E)) return fail(GOSSMX_ERR_UNSUPPORTED, "batch too large");
@@ -755,6 +768,50 @@ int gossmx_profile_reset(gossmx_ctx* ctx) {
     ctx->op_launches[i] = 0;
   }
   return GOSSMX_OK;
+}
+
+int gossmx_capture_begin(gossmx_ctx* ctx) {
+  if (!ctx) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context");
+  if (ctx->capturing) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "already capturing");
+  if (int s = set_device(ctx->device)) return s;
+  if (int s = fold_profile(ctx)) return s;
+  HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  ctx->capturing = true;
+  return GOSSMX_OK;
+}
+
+int gossmx_capture_end(gossmx_ctx* ctx, gossmx_graph** out) {
+  if (!ctx || !out) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+  if (!ctx->capturing) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "not capturing");
+  ctx->capturing = false;
+  hipGraph_t graph = nullptr;
+  HIP_TRY(hipStreamEndCapture(ctx->stream, &graph), "hipStreamEndCapture");
+  auto* g = new gossmx_graph();
+  g->graph = graph;
+  g->device = ctx->device;
+  hipError_t e = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    gossmx_graph_destroy(g);
+    return hip_fail(e, "hipGraphInstantiate");
+  }
+  *out = g;
+  return GOSSMX_OK;
+}
+
+int gossmx_graph_launch(gossmx_ctx* ctx, const gossmx_graph* g) {
+  if (!ctx || !g || !g->exec) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+  if (ctx->capturing) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "cannot launch a graph while capturing");
+  if (int s = set_device(ctx->device)) return s;
+  HIP_TRY(hipGraphLaunch(g->exec, ctx->stream), "hipGraphLaunch");
+  return GOSSMX_OK;
+}
+
+void gossmx_graph_destroy(gossmx_graph* g) {
+  if (!g) return;
+  hipSetDevice(g->device);
+  if (g->exec) hipGraphExecDestroy(g->exec);
+  if (g->graph) hipGraphDestroy(g->graph);
+  delete g;
 }
 
 int gossmx_inject_fault(gossmx_ctx* ctx, int armed) {

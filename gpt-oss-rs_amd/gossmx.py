@@ -129,6 +129,10 @@ def load():
         "gossmx_profile_read": (i32, [vp, C.POINTER(ProfileRecord), sz, C.POINTER(sz)]),
         "gossmx_profile_reset": (i32, [vp]),
         "gossmx_inject_fault": (i32, [vp, i32]),
+        "gossmx_capture_begin": (i32, [vp]),
+        "gossmx_capture_end": (i32, [vp, pp]),
+        "gossmx_graph_launch": (i32, [vp, vp]),
+        "gossmx_graph_destroy": (None, [vp]),
         "gossmx_selftest": (i32, [vp]),
     }
     for name, (res, args) in sig.items():
@@ -200,6 +204,29 @@ class Context:
         _check(load().gossmx_profile_read(self._h, recs, len(OPS), C.byref(n)))
         return {OPS[r.op]: {"launches": int(r.launches), "total_ms": float(r.total_ms)} for r in recs[:n.value]}
 
+    def capture_begin(self):
+        _check(load().gossmx_capture_begin(self._h))
+
+    def capture_end(self) -> "Graph":
+        h = C.c_void_p()
+        _check(load().gossmx_capture_end(self._h, C.byref(h)))
+        return Graph(self, h)
+
+    def malloc(self, nbytes: int) -> int:
+        p = C.c_void_p()
+        _check(load().gossmx_malloc(self._h, nbytes, C.byref(p)))
+        return p.value
+
+    def free(self, ptr: int):
+        _check(load().gossmx_free(self._h, ptr))
+
+    def h2d(self, dst: int, src: np.ndarray):
+        src = np.ascontiguousarray(src)
+        _check(load().gossmx_memcpy_h2d(self._h, dst, _ptr(src), src.nbytes))
+
+    def d2h(self, dst: np.ndarray, src: int):
+        _check(load().gossmx_memcpy_d2h(self._h, _ptr(dst), src, dst.nbytes))
+
     def close(self):
         if self._h:
             load().gossmx_ctx_destroy(self._h)
@@ -210,6 +237,22 @@ class Context:
 
     def __exit__(self, *exc):
         self.close()
+
+
+class Graph:
+    """A recorded sequence of device-memory calls (gossmx_capture_*)."""
+
+    def __init__(self, ctx: Context, handle: C.c_void_p):
+        self.ctx = ctx
+        self._h = handle
+
+    def launch(self):
+        _check(load().gossmx_graph_launch(self.ctx.handle, self._h))
+
+    def close(self):
+        if self._h:
+            load().gossmx_graph_destroy(self._h)
+            self._h = C.c_void_p()
 
 
 class Weights:

@@ -205,6 +205,20 @@ int gossmx_profile_enable(gossmx_ctx* ctx, int enabled);
 int gossmx_profile_read(gossmx_ctx* ctx, gossmx_profile_record* out, size_t capacity, size_t* written);
 int gossmx_profile_reset(gossmx_ctx* ctx);
 
+/* HIP-graph capture of a sequence of calls on this context (no counterpart in
+ * the reference; it removes the per-kernel launch gaps of a multi-layer step).
+ * Between begin and end, gossmx_moe_forward / gossmx_mxfp4_matmul calls with
+ * GOSSMX_MEM_DEVICE pointers are recorded, not run; host-memory calls and
+ * profiling are refused, and scratch buffers must already be large enough
+ * (run the same shapes once eagerly first). A graph replays on the context's
+ * stream with the pointers it was recorded with; device-side checks surface at
+ * gossmx_synchronize as usual. */
+typedef struct gossmx_graph gossmx_graph;
+int gossmx_capture_begin(gossmx_ctx* ctx);
+int gossmx_capture_end(gossmx_ctx* ctx, gossmx_graph** out);
+int gossmx_graph_launch(gossmx_ctx* ctx, const gossmx_graph* graph);
+void gossmx_graph_destroy(gossmx_graph* graph);
+
 /* Test hook: the next gossmx_moe_forward / gossmx_mxfp4_matmul on this context
  * fails with GOSSMX_ERR_INJECTED_FAULT before launching anything (outputs untouched). */
 int gossmx_inject_fault(gossmx_ctx* ctx, int armed);
