@@ -57,11 +57,7 @@ struct gossmx_ctx {
   bool own_stream = false;
   int* err = nullptr;  // device error flags
   uint16_t* sig_tab = nullptr;  // SwiGLU sigmoid table (built at context creation)
-  // Second in-order stream (default priority) for the small-bucket GEMMs,
-  // joined back to `stream` with events.
-  hipStream_t side = nullptr;
   bool capturing = false;
-  hipEvent_t ev_dispatched = nullptr, ev_small_gate_up = nullptr, ev_small_down = nullptr;
   bool fault_armed = false;
   bool profiling = false;
   std::vector<ProfileMark> marks;
@@ -201,19 +197,20 @@ int alloc_tiled(gossmx_ctx* ctx, size_t experts, size_t rows, size_t blocks, gos
   w->ctx = ctx;
   w->device = ctx->device;
   w->t = make_tiled(experts, rows, blocks);
+  if (w->t.nib_stride > (size_t)INT32_MAX - kPlaneSlack || w->t.scl_stride > (size_t)INT32_MAX - kPlaneSlack) {
+    delete w;
+    return fail(GOSSMX_ERR_UNSUPPORTED, "expert of %zu x %zu blocks too large for this build", rows, blocks);
+  }
   hipError_t e = hipMalloc(&w->t.nib, experts * w->t.nib_stride + kPlaneSlack);
   if (e == hipSuccess) e = hipMalloc(&w->t.scl, experts * w->t.scl_stride + kPlaneSlack);
+  if (e == hipSuccess) e = hipMalloc(&w->t.fast, experts * w->t.tiles);
+  if (e == hipSuccess) e = launch_fill_tiled_padding(w->t, ctx->stream);
   if (e != hipSuccess) {
     if (w->t.nib) hipFree(w->t.nib);
+    if (w->t.scl) hipFree(w->t.scl);
+    if (w->t.fast) hipFree(w->t.fast);
     delete w;
-    return hip_fail(e, "hipMalloc(weights)");
-  }
-  hipError_t f = launch_fill_tiled_padding(w->t, ctx->stream);
-  if (f != hipSuccess) {
-    hipFree(w->t.nib);
-    hipFree(w->t.scl);
-    delete w;
-    return hip_fail(f, "padding fill");
+    return hip_fail(e, "weights allocation");
   }
   *out = w;
   return GOSSMX_OK;
@@ -240,7 +237,9 @@ int validate_problem(const gossmx_matmul_problem* p, size_t rows, size_t blocks,
       (m - 1) * p->output_stride + rows > p->output_len || (p->bias && p->bias_len != rows))
     return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "invalid MXFP4 matmul: M=%zu, N=%zu, K=%zu, output_stride=%zu", m, rows,
                 blocks * kBlock, p->output_stride);
-  if (m > (size_t)INT32_MAX / 2 || rows > (size_t)INT32_MAX / 2 || m * blocks * 8 >= (size_t)INT32_MAX)
+  // The GEMM addresses the activation operand with 32-bit byte offsets.
+  if (m > (size_t)INT32_MAX / 2 || rows > (size_t)INT32_MAX / 2 ||
+      m * blocks * 2 * kBlock * sizeof(_Float16) >= (size_t)INT32_MAX - kActSlack)
     return fail(GOSSMX_ERR_UNSUPPORTED, "matrix too large for this build");
   return GOSSMX_OK;
 }
@@ -290,10 +289,6 @@ int gossmx_ctx_create(int device, void* stream, gossmx_ctx** out) {
   }
   hipError_t e = hipMalloc(&ctx->err, 16);
   if (e == hipSuccess) e = launch_clear_ints(ctx->err, 4, ctx->stream);
-  if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking);
-  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ev_dispatched, hipEventDisableTiming);
-  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ev_small_gate_up, hipEventDisableTiming);
-  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ev_small_down, hipEventDisableTiming);
   if (e == hipSuccess) e = hipMalloc(&ctx->sig_tab, 65536 * sizeof(uint16_t));
   if (e == hipSuccess) e = launch_build_sigmoid_table(ctx->sig_tab, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
@@ -319,11 +314,6 @@ void gossmx_ctx_destroy(gossmx_ctx* ctx) {
                     &ctx->act2s, &ctx->y, &ctx->out, &ctx->trace, &ctx->rec, &ctx->bias, &ctx->mout};
   for (DevBuf* b : bufs)
     if (b->p) hipFree(b->p);
-  if (ctx->side) hipStreamSynchronize(ctx->side);
-  if (ctx->ev_dispatched) hipEventDestroy(ctx->ev_dispatched);
-  if (ctx->ev_small_gate_up) hipEventDestroy(ctx->ev_small_gate_up);
-  if (ctx->ev_small_down) hipEventDestroy(ctx->ev_small_down);
-  if (ctx->side) hipStreamDestroy(ctx->side);
   if (ctx->err) hipFree(ctx->err);
   if (ctx->sig_tab) hipFree(ctx->sig_tab);
   if (ctx->own_stream && ctx->stream) hipStreamDestroy(ctx->stream);
@@ -391,6 +381,7 @@ int gossmx_weights_upload(gossmx_ctx* ctx, const uint8_t* data, size_t len, size
   hipError_t e = hipMalloc(&staging, len);
   if (e == hipSuccess) e = hipMemcpyAsync(staging, data, len, hipMemcpyHostToDevice, ctx->stream);
   if (e == hipSuccess) e = launch_repack(static_cast<const uint8_t*>(staging), layout, w->t, ctx->stream);
+  if (e == hipSuccess) e = launch_tile_flags(w->t, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   if (staging) hipFree(staging);
   if (e != hipSuccess) {
@@ -406,6 +397,7 @@ int gossmx_weights_generate(gossmx_ctx* ctx, uint64_t seed, uint64_t stream, siz
   gossmx_weights* w = nullptr;
   if (int s = alloc_tiled(ctx, experts, rows, blocks, &w)) return s;
   hipError_t e = launch_generate(seed, stream, w->t, ctx->stream);
+  if (e == hipSuccess) e = launch_tile_flags(w->t, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) {
     gossmx_weights_destroy(w);
@@ -448,6 +440,7 @@ void gossmx_weights_destroy(gossmx_weights* w) {
   if (w->ctx && w->ctx->stream) hipStreamSynchronize(w->ctx->stream);
   if (w->t.nib) hipFree(w->t.nib);
   if (w->t.scl) hipFree(w->t.scl);
+  if (w->t.fast) hipFree(w->t.fast);
   delete w;
 }
 
@@ -575,7 +568,9 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
     return fail(GOSSMX_ERR_UNSUPPORTED, "host-memory calls cannot be captured");
   const size_t m = io->m, E = L->cfg.experts, H = L->cfg.hidden, I = L->cfg.intermediate, K = L->cfg.top_k;
   const size_t R = m * K, B1 = H / kBlock, B2 = I / kBlock;
-  if (m > (size_t)(INT32_MAX / 8) / std::max<size_t>(H, E)) return fail(GOSSMX_ERR_UNSUPPORTED, "batch too large");
+  if (m > (size_t)(INT32_MAX / 8) / std::max<size_t>(H, E) ||
+      R * std::max(B1, B2) * 2 * kBlock * sizeof(_Float16) >= (size_t)INT32_MAX - kActSlack)
+    return fail(GOSSMX_ERR_UNSUPPORTED, "batch too large for this build");
   if (ctx->fault_armed) {
     ctx->fault_armed = false;
     return fail(GOSSMX_ERR_INJECTED_FAULT, "injected fault before launch");
@@ -589,7 +584,7 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
       (s = ensure(ctx, ctx->weights, R * 4)) || (s = ensure(ctx, ctx->act1v, m * B1 * 2 * kBlock * 2 + kActSlack)) ||
       (s = ensure(ctx, ctx->act1s, m * B1 * 8 + kActSlack)) || (s = ensure(ctx, ctx->bucket, (E + 1) * 4)) ||
       (s = ensure(ctx, ctx->route_tok, R * 4)) || (s = ensure(ctx, ctx->route_slot, R * 4)) ||
-      (s = ensure(ctx, ctx->work, (2 * max_work + 1 + 2 * E + 1) * 4)) ||
+      (s = ensure(ctx, ctx->work, (2 * max_work + 1) * 4)) ||
       (s = ensure(ctx, ctx->act2v, R * B2 * 2 * kBlock * 2 + kActSlack)) ||
       (s = ensure(ctx, ctx->act2s, R * B2 * 8 + kActSlack)) || (s = ensure(ctx, ctx->y, R * H * 2)))
     return s;
@@ -619,11 +614,6 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   int* bucket = static_cast<int*>(ctx->bucket.p);
   int* work = static_cast<int*>(ctx->work.p);
   int* n_work = work + 2 * max_work;
-  int* work_small = n_work + 1;
-  int* n_work_small = work_small + 2 * E;
-  const size_t max_small = std::min(E, R);
-  // Buckets of <= kSmallRows rows use the small-bucket kernel.
-  const bool small = true;
   ActBuffers act1{static_cast<_Float16*>(ctx->act1v.p), static_cast<float*>(ctx->act1s.p)};
 
   RouteArgs ra{};
@@ -654,14 +644,10 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   da.route_slot = static_cast<int*>(ctx->route_slot.p);
   da.work = work;
   da.n_work = n_work;
-  da.work_small = work_small;
-  da.n_work_small = n_work_small;
-  da.small_enabled = small ? 1 : 0;
   {
     OpScope sc(ctx, GOSSMX_OP_DISPATCH);
     HIP_TRY(launch_dispatch(da, ctx->stream), "dispatch launch");
   }
-  if (small) HIP_TRY(hipEventRecord(ctx->ev_dispatched, ctx->stream), "event record");
   GemmArgs g{};
   g.w = L->gate_up->t;
   g.actv = act1.v;
@@ -671,8 +657,6 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   g.residual = 1;
   g.work = work;
   g.n_work = n_work;
-  g.work_small = work_small;
-  g.n_work_small = n_work_small;
   g.bucket_off = bucket;
   g.route_tok = da.route_tok;
   g.route_slot = da.route_slot;
@@ -689,25 +673,13 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   d.bias = L->down_bias;
   d.bias_expert_stride = H;
   d.y = static_cast<uint16_t*>(ctx->y.p);
-  if (small) {
-    // Small buckets on the side stream: gate_up then down of the same experts
-    // (their down inputs come only from their own gate_up), overlapping the
-    // large-bucket GEMMs on the main stream.
-    HIP_TRY(hipStreamWaitEvent(ctx->side, ctx->ev_dispatched, 0), "stream wait");
-    HIP_TRY(launch_gemm_small(kGateUp, g, (int)max_small, ctx->side), "gate_up small launch");
-    HIP_TRY(hipEventRecord(ctx->ev_small_gate_up, ctx->side), "event record");
-    HIP_TRY(launch_gemm_small(kDown, d, (int)max_small, ctx->side), "down small launch");
-    HIP_TRY(hipEventRecord(ctx->ev_small_down, ctx->side), "event record");
-  }
   {
     OpScope sc(ctx, GOSSMX_OP_GATE_UP);
     HIP_TRY(launch_gemm(kGateUp, g, (int)max_work, ctx->stream), "gate_up launch");
-    if (small) HIP_TRY(hipStreamWaitEvent(ctx->stream, ctx->ev_small_gate_up, 0), "stream wait");
   }
   {
     OpScope sc(ctx, GOSSMX_OP_DOWN);
     HIP_TRY(launch_gemm(kDown, d, (int)max_work, ctx->stream), "down launch");
-    if (small) HIP_TRY(hipStreamWaitEvent(ctx->stream, ctx->ev_small_down, 0), "stream wait");
   }
   {
     OpScope sc(ctx, GOSSMX_OP_WEIGHTING);

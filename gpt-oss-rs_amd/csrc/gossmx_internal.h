@@ -12,10 +12,9 @@ constexpr int kBlock = 32;      // values per MXFP4 / Q8 block (QUANT_BLOCK_SIZE
 constexpr int kRecord = 17;     // E8M0 byte + 16 packed nibble bytes per (row, block)
 constexpr int kTileRows = 16;   // rows per MFMA tile (one wave)
 constexpr int kWgRows = 64;     // gate_up rows (32 gate/up pairs) per 32-value block of the down input
-constexpr int kChunk = 48;      // activation rows per work item
+constexpr int kChunk = 16;      // activation rows per GEMM work item
 constexpr int kMaxExperts = 128;
 constexpr int kMaxTopK = 8;
-constexpr int kSmallRows = 4;        // buckets of at most this many rows use the small-bucket GEMM
 
 // Device error flags (sticky until the host reads them).
 constexpr int kErrNonFiniteLogits = 1;
@@ -38,13 +37,16 @@ struct TiledWeights {
   size_t experts = 0, rows = 0, blocks = 0, tiles = 0;
   size_t nib_stride = 0;  // bytes per expert in the nibble plane
   size_t scl_stride = 0;  // bytes per expert in the scale plane
+  // [experts][tiles]: 1 when every scale byte of the tile is in the exact
+  // scaled-conversion range (see tile_flags_kernel); set after every write.
+  uint8_t* fast = nullptr;
 };
 
 // Extra bytes allocated after each plane: the GEMM reads whole 4-block groups
 // (and dword-granular tails) of the last tile unconditionally.
 constexpr size_t kPlaneSlack = 2048;
 // Extra bytes after each activation operand buffer: the GEMM's staging reads
-// a last partial K group as whole 4-block groups (up to 3 blocks past a row).
+// a last partial K step as a whole 8-block step (up to 7 blocks past a row).
 constexpr size_t kActSlack = 1024;
 
 // Activation operand of the expert GEMM, one row per token or route:
@@ -68,8 +70,6 @@ struct GemmArgs {
   int plain_expert, plain_m;          // kPlain
   const int* work;                    // [n][2] (expert, chunk start)   (gate_up/down)
   const int* n_work;
-  const int* work_small;              // [n][2] (expert, 0): buckets for the small-bucket kernel
-  const int* n_work_small;
   const int* bucket_off;              // [experts + 1]
   const int* route_tok;               // grouped route -> source row
   const int* route_slot;              // grouped route -> row * top_k + rank
@@ -101,19 +101,15 @@ struct DispatchArgs {
   int* bucket_off;      // [experts + 1]
   int* route_tok;       // [routes]
   int* route_slot;      // [routes]
-  int* work;            // [max_work][2]
+  int* work;            // [max_work][2] (expert, first row of the chunk)
   int* n_work;
-  int* work_small;      // [experts][2]
-  int* n_work_small;
-  int small_enabled;    // 1: buckets of <= kSmallRows rows go to work_small
 };
 
 // Launchers (gossmx_kernels.hip). All are asynchronous on `stream`.
 hipError_t launch_route(const RouteArgs& a, hipStream_t stream);
 hipError_t launch_dispatch(const DispatchArgs& a, hipStream_t stream);
 hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream);
-// Small-bucket variant (work_small items; residual-Q8, gate_up or down).
-hipError_t launch_gemm_small(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream);
+hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream);
 
 hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int top_k, int hidden, float* out,
                           float* trace_down, hipStream_t stream);

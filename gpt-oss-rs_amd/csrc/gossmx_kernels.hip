@@ -152,17 +152,33 @@ __device__ __forceinline__ void residual_q8_store(float v, int l32, size_t row, 
 }
 
 // ---------------------------------------------------------------------------
-// Router projection, top-k, routing softmax and the gate_up input quantization,
-// one work-group per row (moe_batch routing loop, cpu_runner.rs:2808-2854).
+// Router projection, top-k and routing softmax (blockIdx.y == 0), and the
+// gate_up input quantization (blockIdx.y >= 1: 8 blocks of 32 values per
+// work-group, one per half wave), for row blockIdx.x (moe_batch routing
+// loop, cpu_runner.rs:2808-2854; quantize_residual_q8 of the row,
+// cpu_runner.rs:3224-3231).
 
 __device__ __forceinline__ bool route_better(float va, int ia, float vb, int ib) {
   return va > vb || (va == vb && ia < ib);  // stable_top_k order, cpu_runner.rs:3768-3778
 }
 
+constexpr int kRouteQuantBlocks = 8;  // quantized blocks per work-group (256 threads)
+
 __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   const int r = blockIdx.x;
   const int E = a.experts, H = a.hidden, K = a.top_k;
   const uint16_t* x = a.x + (size_t)r * H;
+  if (blockIdx.y > 0) {
+    const int hw = threadIdx.x >> 5, l32 = threadIdx.x & 31;
+    const int blocks = H / kBlock;
+    const int b = (blockIdx.y - 1) * kRouteQuantBlocks + hw;
+    if (b < blocks) {  // uniform per half wave
+      const float v = bf16_to_f32(x[b * kBlock + l32]);
+      if (!isfinite(v)) atomicOr(a.err, kErrNonFiniteInput);
+      residual_q8_store(v, l32, (size_t)r, blocks, b, a.act);
+    }
+    return;
+  }
   __shared__ float s_chain[kMaxExperts * 16];
   __shared__ float s_logit[kMaxExperts];
   __shared__ int s_sel[kMaxTopK];
@@ -236,94 +252,91 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
       }
     }
   }
-
-  // quantize_residual_q8 of the row for gate_up (cpu_runner.rs:3224-3231):
-  // one half wave per 32-value block.
-  const int hw = threadIdx.x >> 5, l32 = threadIdx.x & 31;
-  const int blocks = H / kBlock;
-  for (int b = hw; b < blocks; b += blockDim.x / 32) {
-    const float v = bf16_to_f32(x[b * kBlock + l32]);
-    if (!isfinite(v)) atomicOr(a.err, kErrNonFiniteInput);
-    residual_q8_store(v, l32, (size_t)r, blocks, b, a.act);
-  }
 }
 
 // ---------------------------------------------------------------------------
 // Stable grouping of routes by expert (stable_group_routes,
 // cpu_runner.rs:3780-3782): route i = row * top_k + rank goes to
 // bucket_off[e] + #{j < i : expert(j) == e}. One work-group of 1024 threads;
-// in-wave ranks come from one ballot per expert.
+// in-wave ranks come from one ballot per expert present in the wave.
+//
+// Work items: every bucket is cut into kChunk-row chunks. Full chunks come
+// first (expert order), then the partial last chunks by descending size
+// (ties by expert), so the heaviest work items start first.
 
 __global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
   const int E = a.experts, R = a.routes;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   __shared__ int s_tot[kMaxExperts];
   __shared__ int s_off[kMaxExperts];
+  __shared__ int s_part[kMaxExperts];
   __shared__ int s_run[kMaxExperts];
+  __shared__ int s_scan[4];
   __shared__ int s_wcnt[16][kMaxExperts];
-  for (int e = tid; e < E; e += 1024) { s_tot[e] = 0; s_run[e] = 0; }
+  for (int e = tid; e < kMaxExperts; e += 1024) { s_tot[e] = 0; s_run[e] = 0; }
   __syncthreads();
   for (int i = tid; i < R; i += 1024) atomicAdd(&s_tot[a.selected[i]], 1);
   __syncthreads();
-  if (tid == 0) {
-    // Work items: buckets of at most kSmallRows rows go to the small-bucket
-    // kernel (when enabled), larger ones are cut into kChunk-row chunks.
-    int acc = 0, ns = 0;
-    for (int e = 0; e < E; ++e) {
-      s_off[e] = acc;
-      a.bucket_off[e] = acc;
-      const int c = s_tot[e];
-      if (a.small_enabled && c > 0 && c <= kSmallRows) {
-        a.work_small[2 * ns] = e;
-        a.work_small[2 * ns + 1] = 0;
-        ++ns;
-      }
-      acc += c;
+  // Waves 0 and 1: lane = expert (kMaxExperts = 128). Inclusive scans of the
+  // row counts and of the full-chunk counts, then the carry of wave 0.
+  int c = 0, full = 0, sc = 0, sf = 0;
+  if (wave < 2) {
+    c = tid < E ? s_tot[tid] : 0;
+    full = c / kChunk;
+    s_part[tid] = c % kChunk;
+    sc = c;
+    sf = full;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(sc, o), v = __shfl_up(sf, o);
+      if (lane >= o) { sc += u; sf += v; }
     }
-    a.bucket_off[E] = acc;
-    *a.n_work_small = ns;
+    if (lane == 63) { s_scan[2 * wave] = sc; s_scan[2 * wave + 1] = sf; }
   }
   __syncthreads();
-  // Large buckets: chunks in descending row count, so the heaviest work items
-  // are dispatched first and the grid's last wave is light. All chunks of an
-  // expert but the last hold kChunk rows; full chunks come first (expert
-  // order), then the partial last chunks by size (ties by expert).
-  for (int e = tid; e < E; e += 1024) {
-    const int c = s_tot[e];
-    const bool large = c > 0 && !(a.small_enabled && c <= kSmallRows);
-    const int full = large ? c / kChunk : 0, part = large ? c % kChunk : 0;
-    int full_before = 0, full_total = 0, part_before = 0, parts = 0;
-    for (int f = 0; f < E; ++f) {
-      const int cf = s_tot[f];
-      const bool lf = cf > 0 && !(a.small_enabled && cf <= kSmallRows);
-      const int ff = lf ? cf / kChunk : 0, pf = lf ? cf % kChunk : 0;
-      full_total += ff;
-      if (f < e) full_before += ff;
-      if (pf > 0) {
-        ++parts;
-        if (pf > part || (pf == part && f < e)) ++part_before;
+  if (wave < 2) {
+    if (wave == 1) { sc += s_scan[0]; sf += s_scan[1]; }
+    const int total_full = s_scan[1] + s_scan[3];
+    const int off = sc - c, full_before = sf - full;
+    if (tid < E) {
+      s_off[tid] = off;
+      a.bucket_off[tid] = off;
+      for (int i = 0; i < full; ++i) {
+        a.work[2 * (full_before + i)] = tid;
+        a.work[2 * (full_before + i) + 1] = i * kChunk;
+      }
+      const int part = s_part[tid];
+      int parts = 0, before = 0;
+      for (int f = 0; f < E; ++f) {
+        const int pf = s_part[f];
+        parts += pf > 0;
+        before += pf > part || (pf == part && f < tid);
+      }
+      if (part > 0) {
+        a.work[2 * (total_full + before)] = tid;
+        a.work[2 * (total_full + before) + 1] = full * kChunk;
+      }
+      if (tid == 0) {
+        *a.n_work = total_full + parts;
+        a.bucket_off[E] = s_scan[0] + s_scan[2];
       }
     }
-    for (int i = 0; i < full; ++i) {
-      a.work[2 * (full_before + i)] = e;
-      a.work[2 * (full_before + i) + 1] = i * kChunk;
-    }
-    if (part > 0) {
-      a.work[2 * (full_total + part_before)] = e;
-      a.work[2 * (full_total + part_before) + 1] = full * kChunk;
-    }
-    if (e == 0) *a.n_work = full_total + parts;
   }
   __syncthreads();
+  const unsigned long long lt = (1ull << lane) - 1ull;
   for (int base = 0; base < R; base += 1024) {
     const int i = base + tid;
     const int e = i < R ? a.selected[i] : -1;
-    const unsigned long long lt = (1ull << lane) - 1ull;
+    for (int ee = lane; ee < E; ee += 64) s_wcnt[wave][ee] = 0;
     int rank = 0;
-    for (int ee = 0; ee < E; ++ee) {
+    unsigned long long pending = __ballot(e >= 0);
+    while (pending) {
+      const int leader = __ffsll((long long)pending) - 1;
+      const int ee = __shfl(e, leader);
       const unsigned long long m = __ballot(e == ee);
       if (e == ee) rank = __popcll(m & lt);
       if (lane == 0) s_wcnt[wave][ee] = __popcll(m);
+      pending &= ~m;
     }
     __syncthreads();
     if (e >= 0) {
@@ -344,20 +357,22 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
 
 // ---------------------------------------------------------------------------
 // Expert GEMM on the resident v3 layout. One work-group = kWaves waves, one
-// 16-row weight tile per wave (128 rows), times one work item (<= 64
-// activation rows). Each lane owns one weight row (lane % 16) and two
+// 16-row weight tile per wave (kGemmRows rows), times one work item of at most
+// kChunk activation rows. Each lane owns one weight row (lane % 16) and two
 // activation rows per group of 8, and runs the reference's per-row float
 // chain in order:
 //   total = bias; for each block: total += (p * ws) * ps; total += (r * ws) * rs
 // (mxfp4_residual_q8_gemv_rows lib.rs:673-696, scalar_matmul_range
 // matmul.rs:529-578).
 //
-// Streaming: K is walked in groups of 4 blocks. Each wave keeps the weights of
-// the next kPrefetch groups in flight in registers (one 16-byte load per lane
-// per group, a 1 KiB contiguous segment per wave). The work item's activations
-// for a group (f16 codes and scales) are staged through LDS once per
-// work-group: loaded from global memory into registers one group ahead, then
-// written to LDS between two barriers, so all waves share one L2 read.
+// Pipeline: K advances in steps of kStep = 8 blocks, two 4-block groups of
+// the v3 layout. Each wave keeps its tile's nibbles (2 KiB per step, one
+// 16-byte load per lane and group) and scale dwords three steps deep in a
+// register ring. The step's activations (f16 codes and scales) move from
+// global memory into a ring of three LDS slots by DMA (buffer_load ... lds)
+// two steps ahead, published by one barrier per step. Every wave issues the
+// same vector-memory instructions in the same order, so one s_waitcnt
+// immediate covers every step, and all per-step addressing is scalar.
 
 __device__ __forceinline__ half8 fp4x8_to_half8(uint32_t w) {
   const half2v h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0);
@@ -368,49 +383,6 @@ __device__ __forceinline__ half8 fp4x8_to_half8(uint32_t w) {
   b[0] = h0[0]; b[1] = h0[1]; b[2] = h1[0]; b[3] = h1[1];
   b[4] = h2[0]; b[5] = h2[1]; b[6] = h3[0]; b[7] = h3[1];
   return b;
-}
-
-constexpr int kWaves = 8;                  // waves per GEMM work-group
-constexpr int kSlotBytes = 4 * kChunk * 2 * kBlock * 2;  // f16 codes of one K group in LDS
-constexpr int kCodeDma = 4 * kChunk * 8 / (64 * kWaves);  // 16-byte DMA instructions per wave per group
-static_assert(4 * kChunk * 8 == kCodeDma * 64 * kWaves, "code DMA covers a slot exactly");
-static_assert(4 * kChunk * 2 <= 64 * kWaves, "one 4-byte DMA per wave covers a group's scales");
-constexpr int kSclSlot = 64 * kWaves / 2;                  // float2 written by one group's scale DMA
-// s_waitcnt immediate: vmcnt = kCodeDma + 1 (D(q+1)) + 2 + 2 (W(q+1), W(q+2)),
-// expcnt and lgkmcnt not waited on (7, 15).
-constexpr int kWaitVm = kCodeDma + 1 + 4;
-constexpr int kWaitDmaGroup = (kWaitVm & 15) | ((kWaitVm >> 4) << 14) | (7 << 4) | (15 << 8);
-constexpr int kGemmThreads = 64 * kWaves;  // 512
-constexpr int kGemmRows = 16 * kWaves;     // weight rows per work-group
-constexpr int kPrefetch = 3;               // weight groups in flight per wave
-
-struct WeightGroup {
-  uint4 v;     // one dword of nibbles per block (codes 8g..8g+7 of this lane's row)
-  uint32_t s;  // E8M0 bytes of this lane's row for the group's blocks
-};
-
-// Loads of a full 4-block group q. Unconditional (no branch around a load),
-// so the compiler's load counters stay exact and the prefetched groups stay
-// in flight; callers clamp q to a full group of a valid tile.
-__device__ __forceinline__ WeightGroup load_full_group(const uint8_t* nib, const uint8_t* scl, int q, int lane,
-                                                       int nl) {
-  WeightGroup g;
-  g.v = *reinterpret_cast<const uint4*>(nib + (size_t)q * 1024 + lane * 16);
-  g.s = *reinterpret_cast<const uint32_t*>(scl + (size_t)q * 64 + nl * 4);
-  return g;
-}
-
-// Loads of the last group when K is not a multiple of 4 blocks (rem = 1..3
-// blocks): dwords at lane * rem * 4 of the compact nibble group, and the
-// row's (padded) scale dword. Reads past the group stay inside the
-// allocation slack (kPlaneSlack).
-__device__ __forceinline__ WeightGroup load_tail_group(const uint8_t* nib, const uint8_t* scl, int q, int rem,
-                                                       int lane, int nl) {
-  const uint32_t* gw = reinterpret_cast<const uint32_t*>(nib + (size_t)q * 1024 + lane * rem * 4);
-  WeightGroup g;
-  g.v = make_uint4(gw[0], gw[1], gw[2], 0u);
-  g.s = *reinterpret_cast<const uint32_t*>(scl + (size_t)q * 64 + nl * 4);
-  return g;
 }
 
 // E8M0 bytes whose scaled E2M1 values are exact f16 normals: 0.5 * 2^(s-127)
@@ -435,19 +407,55 @@ __device__ __forceinline__ float e8m0_select(uint32_t s) {
   return s == 0xffu ? __uint_as_float(0x7fc00000u) : v;
 }
 
-// LDS slot layout of one K group (written by DMA, read as MFMA A operands):
-// for block j and token group tg, 1 KiB = [k-slice g (4)][vector i (16)][16 B]
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+constexpr int kWaves = 8;                   // waves per GEMM work-group
+constexpr int kGemmThreads = 64 * kWaves;   // 512
+constexpr int kGemmRows = 16 * kWaves;      // weight rows per work-group
+constexpr int kNtg = kChunk / 8;            // MFMA token groups per work item
+constexpr int kStep = 8;                    // K blocks per pipeline step
+constexpr int kSlotBytes = kStep * kChunk * 2 * kBlock * 2;  // f16 codes of one step in LDS
+constexpr int kCodeDma = kSlotBytes / (16 * kGemmThreads);   // 16-byte DMA per lane per step
+constexpr int kSclSlot = 64 * kWaves;       // floats written by one step's scale DMA (a dword per lane)
+static_assert(kSlotBytes == kCodeDma * 16 * kGemmThreads, "code DMA covers a slot exactly");
+static_assert(kStep * kChunk * 2 <= kSclSlot, "one dword DMA per lane covers a step's scales");
+static_assert(kChunk % 8 == 0 && kStep == 8, "token groups of 8, steps of two 4-block groups");
+// Vector-memory instructions per wave and step: weights 2 x (nibbles, scale
+// dword); activations kCodeDma code pieces + 1 scale dword.
+constexpr int kLoadsW = 4;
+constexpr int kLoadsD = kCodeDma + 1;
+// s_waitcnt immediate for "the DMA of step q has landed": issued after it are
+// W(q+1), D(q+1), W(q+2) (see k_loop). expcnt and lgkmcnt are not waited on.
+constexpr int kWaitVm = 2 * kLoadsW + kLoadsD;
+static_assert(kWaitVm < 64, "vmcnt field");
+constexpr int kWaitDma = (kWaitVm & 15) | ((kWaitVm >> 4) << 14) | (7 << 4) | (15 << 8);
+constexpr int kBufferFlags = 0x00020000;    // raw 32-bit buffer resource, gfx9 family
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, kBufferFlags);
+}
+
+// One step of a wave's weights: nibble groups 2q and 2q+1 and their scale dwords.
+struct WStep {
+  u32x4 v0, v1;
+  uint32_t s0, s1;
+};
+
+// LDS slot layout of one step (written by DMA, read as MFMA A operands): for
+// block j and token group tg, 1 KiB = [k-slice g (4)][vector i (16)][16 B]
 // with vector i = 2 * (row within the group) + part (0 primary, 1 residual),
 // so lane (g, i) of a wave reads the 16 bytes at lane * 16 (conflict-free).
-__device__ __forceinline__ int slot_chunk(int j, int tg) { return j * (kChunk / 8) + tg; }
+// Scales: float2 (primary, residual) at [j][row].
+__device__ __forceinline__ int slot_chunk(int j, int tg) { return j * kNtg + tg; }
 
-// One block j of the current group against NTG token groups: the MFMAs and
+// One block j of the current step against NTG token groups: the MFMAs and
 // the ordered chain updates. SCALED: the weight operand already carries the
 // E8M0 scale (exact), so the MFMA returns (p / 2) * e8m0 and a term is
 // d * act_scale; otherwise a term is (d * e8m0) * act_scale. Both are the
 // reference's (p * (0.5 * e8m0)) * act_scale rounded once.
 template <bool RESIDUAL, bool SCALED, int NTG>
-__device__ __forceinline__ void block_update(float (&tot)[kChunk / 8][2], const char* codes, const float2* scl,
+__device__ __forceinline__ void block_update(float (&tot)[kNtg][2], const char* codes, const float2* scl,
                                              const half8 bop, const float e8, const int j, const int lane,
                                              const int G) {
 #pragma unroll
@@ -470,33 +478,25 @@ __device__ __forceinline__ void block_update(float (&tot)[kChunk / 8][2], const 
   }
 }
 
-// All blocks of one K group for this wave's tile.
-template <bool RESIDUAL, int NTG>
-__device__ __forceinline__ void group_update(float (&tot)[kChunk / 8][2], const char* codes, const float2* scl,
-                                             const WeightGroup cur, const int nb, const int lane, const int G) {
-  const uint32_t wv[4] = {cur.v.x, cur.v.y, cur.v.z, cur.v.w};
-  bool in_range = true;
+// The first nb blocks of one 4-block group (nibble dwords v, scale bytes s)
+// at step-relative block jb. FAST: every scale of the tile is in
+// [kFastScaleLo, kFastScaleHi] (checked when the weights were stored), so the
+// conversion applies the scale exactly; otherwise the scale multiplies the
+// MFMA result, with the reference's 0x00 and 0xff encodings.
+template <bool RESIDUAL, int NTG, bool FAST>
+__device__ __forceinline__ void group_update(float (&tot)[kNtg][2], const char* codes, const float2* scl,
+                                             const u32x4 v, const uint32_t s, const int jb, const int nb,
+                                             const int lane, const int G) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const uint32_t s = (cur.s >> (8 * j)) & 0xffu;
-    if (j < nb) in_range = in_range && (s - kFastScaleLo) <= (kFastScaleHi - kFastScaleLo);
-  }
-  if (__all(in_range)) {  // wave-uniform
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j < nb) {
-        const float e8 = __uint_as_float(((cur.s >> (8 * j)) & 0xffu) << 23);
-        block_update<RESIDUAL, true, NTG>(tot, codes, scl, fp4x8_to_half8_scaled(wv[j], e8), 0.0f, j, lane, G);
+    if (j < nb) {
+      const uint32_t sb = (s >> (8 * j)) & 0xffu;
+      if (FAST) {
+        const float e8 = __uint_as_float(sb << 23);
+        block_update<RESIDUAL, true, NTG>(tot, codes, scl, fp4x8_to_half8_scaled(v[j], e8), 0.0f, jb + j, lane, G);
+      } else {
+        block_update<RESIDUAL, false, NTG>(tot, codes, scl, fp4x8_to_half8(v[j]), e8m0_select(sb), jb + j, lane, G);
       }
-    }
-  } else {
-    // Rare: a scale outside the exact-f16 range (including the 0x00 and 0xff
-    // encodings). Kept compact; same bits through the unscaled operand.
-#pragma unroll 1
-    for (int j = 0; j < nb; ++j) {
-      const uint32_t w = j == 0 ? wv[0] : (j == 1 ? wv[1] : (j == 2 ? wv[2] : wv[3]));
-      const float e8 = e8m0_select((cur.s >> (8 * j)) & 0xffu);
-      block_update<RESIDUAL, false, NTG>(tot, codes, scl, fp4x8_to_half8(w), e8, j, lane, G);
     }
   }
 }
@@ -512,7 +512,6 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const float (&t
   const int wave = tid >> 6, lane = tid & 63;
   const int nl = lane & 15, G = lane >> 4;
   const int rows = (int)a.w.rows;
-
 
   if (MODE == kPlain) {
     if (tile_ok && row < rows) {
@@ -539,9 +538,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const float (&t
     }
   } else {
     // gate_up epilogue: bf16 (cpu_runner.rs:2905), SwiGLU over (even, odd)
-    // rows (:2907-2919), then the down input's residual-Q8 blocks: the 128
-    // rows of this work-group make two 32-value blocks (cpu_runner.rs:3224-3231).
-    // The SwiGLU values reuse the first LDS slot as [kChunk rows][64 values].
+    // rows (:2907-2919), then the down input's residual-Q8 blocks: the
+    // kGemmRows rows of this work-group make kGemmRows / 64 blocks of 32
+    // values (cpu_runner.rs:3224-3231). The SwiGLU values reuse an LDS slot
+    // as [kChunk rows][kGemmRows / 2 values].
     constexpr int kActStride = kGemmRows / 2 + 1;
     // Lane pairs (even = gate row, odd = up row) hold both values for tokens
     // t0 = 2G and t1 = 2G + 1; the even lane finishes t0 and the odd lane t1.
@@ -575,85 +575,113 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const float (&t
   }
 }
 
-// Loop-invariant state of the K loop.
+// Loop-invariant state of the K loop. All members but the DMA and weight
+// lane offsets are wave-uniform (scalar registers).
 struct KLoop {
-  const uint8_t* nib;
-  const uint8_t* scl;
-  WeightGroup tail;
-  int nq, nqf, last_full, B, wave, lane, nl, G;
+  __amdgpu_buffer_rsrc_t nib, scl;   // this wave's tile of the nibble and scale planes
+  __amdgpu_buffer_rsrc_t codes, scales;  // the activation operand buffers
+  u32x4 tail_v;                      // the partial last 4-block group (B % 4 blocks), if any
+  uint32_t tail_s;
+  int B, nsteps, nfull4, last_full, wave, lane, G;
   bool tile_ok;
-  // DMA lane map (see gemm_kernel)
-  const char* gcodes;
-  const char* gscl;
-  int coff[kCodeDma];  // byte offset of this lane's code piece in group 0, or -1: nothing to move
-  int soff;            // same for the scale dword
+  int vl, vs;                        // weight lane offsets: nibbles lane * 16, scales (lane % 16) * 4
+  int voff[kCodeDma];                // DMA source of this lane's code pieces in step 0
+  int soff;                          // DMA source of this lane's scale dword in step 0
 };
 
-// Issues the DMA of group qq (clamped to the last group) into one ring slot.
-__device__ __forceinline__ void issue_dma(const KLoop& k, int qq_raw, char* codes, float2* scl) {
-  const int qq = min(qq_raw, k.nq - 1);
-  const int gstep = qq * 4 * 128;  // 4 blocks of 128 B per activation row
-#pragma unroll
-  for (int i = 0; i < kCodeDma; ++i) {
-    const char* src = k.coff[i] >= 0 ? k.gcodes + (k.coff[i] + gstep) : k.gcodes;
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                     (__attribute__((address_space(3))) void*)(codes + (i * kWaves + k.wave) * 1024),
-                                     16, 0, 0);
-  }
-  const char* ssrc = k.soff >= 0 ? k.gscl + (k.soff + qq * 4 * 8) : k.gscl;
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)ssrc,
-                                   (__attribute__((address_space(3))) void*)((char*)scl + k.wave * 256), 4, 0, 0);
+// Weights of step q (4-block groups 2q, 2q+1, clamped to the last full group:
+// loads past the end are issued anyway so that every step has the same
+// instruction count, and their data is never used).
+__device__ __forceinline__ WStep load_wstep(const KLoop& k, int q) {
+  const int g0 = min(2 * q, k.last_full), g1 = min(2 * q + 1, k.last_full);
+  WStep w;
+  w.v0 = __builtin_amdgcn_raw_buffer_load_b128(k.nib, k.vl, g0 * 1024, 0);
+  w.s0 = __builtin_amdgcn_raw_buffer_load_b32(k.scl, k.vs, g0 * 64, 0);
+  w.v1 = __builtin_amdgcn_raw_buffer_load_b128(k.nib, k.vl, g1 * 1024, 0);
+  w.s1 = __builtin_amdgcn_raw_buffer_load_b32(k.scl, k.vs, g1 * 64, 0);
+  return w;
 }
 
-// The K loop for NTG token groups. Vector-memory issue order per wave, fixed
-// so that one immediate wait covers every group:
-//   prologue W(0) D(0) W(1) D(1) W(2); iteration q: wait(D(q)) barrier
+// The DMA of step q (clamped to the last step) into one ring slot.
+__device__ __forceinline__ void issue_dma(const KLoop& k, int q_raw, char* codes, float* scl) {
+  const int q = min(q_raw, k.nsteps - 1);
+#pragma unroll
+  for (int i = 0; i < kCodeDma; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(k.codes, (lds_ptr)(codes + (i * kWaves + k.wave) * 1024), 16, k.voff[i],
+                                             q * (kStep * 2 * kBlock * 2), 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(k.scales, (lds_ptr)(reinterpret_cast<char*>(scl) + k.wave * 256), 4,
+                                           k.soff, q * (kStep * 8), 0, 0);
+}
+
+// Compute of step q (q < nsteps).
+template <bool RESIDUAL, int NTG, bool FAST>
+__device__ __forceinline__ void step_update(const KLoop& k, float (&tot)[kNtg][2], const char* codes,
+                                            const float* scl, const WStep& w, const int q) {
+  const float2* s2 = reinterpret_cast<const float2*>(scl);
+  if (8 * q + 8 <= k.B) {
+    group_update<RESIDUAL, NTG, FAST>(tot, codes, s2, w.v0, w.s0, 0, 4, k.lane, k.G);
+    group_update<RESIDUAL, NTG, FAST>(tot, codes, s2, w.v1, w.s1, 4, 4, k.lane, k.G);
+  } else {
+    // Last step: groups 2q and 2q+1, each full, partial (the tail) or absent.
+    const int a0 = 2 * q, a1 = 2 * q + 1;
+    const int nb0 = min(4, k.B - 4 * a0), nb1 = min(4, k.B - 4 * a1);
+    const bool full0 = a0 < k.nfull4, full1 = a1 < k.nfull4;
+    group_update<RESIDUAL, NTG, FAST>(tot, codes, s2, full0 ? w.v0 : k.tail_v, full0 ? w.s0 : k.tail_s, 0, nb0,
+                                      k.lane, k.G);
+    if (nb1 > 0)
+      group_update<RESIDUAL, NTG, FAST>(tot, codes, s2, full1 ? w.v1 : k.tail_v, full1 ? w.s1 : k.tail_s, 4, nb1,
+                                        k.lane, k.G);
+  }
+}
+
+// The K loop. Vector-memory issue order per wave, fixed so that one
+// immediate wait covers every step:
+//   prologue W(0) D(0) W(1) D(1) W(2); step q: wait(D(q)) barrier
 //   D(q+2) compute(q) W(q+3).
-// After D(q) come W(q+1), D(q+1), W(q+2) = kWaitVm instructions.
-template <bool RESIDUAL, int NTG>
-__device__ __forceinline__ void k_loop(const KLoop& k, float (&tot)[kChunk / 8][2], char* c0, char* c1, char* c2,
-                                       float2* s0, float2* s1, float2* s2) {
-  WeightGroup wg0, wg1, wg2;
+// After D(q) come W(q+1), D(q+1), W(q+2) = kWaitVm instructions, and W(q)
+// was issued before D(q), so the wait also covers the weights of step q.
+template <bool RESIDUAL, int NTG, bool FAST>
+__device__ __forceinline__ void k_loop(const KLoop& k, float (&tot)[kNtg][2], char* c0, char* c1, char* c2, float* s0,
+                                       float* s1, float* s2) {
+  WStep w0, w1, w2;
   __builtin_amdgcn_sched_barrier(0);
-  wg0 = load_full_group(k.nib, k.scl, min(0, k.last_full), k.lane, k.nl);
+  w0 = load_wstep(k, 0);
   __builtin_amdgcn_sched_barrier(0);
   issue_dma(k, 0, c0, s0);
   __builtin_amdgcn_sched_barrier(0);
-  wg1 = load_full_group(k.nib, k.scl, min(1, k.last_full), k.lane, k.nl);
+  w1 = load_wstep(k, 1);
   __builtin_amdgcn_sched_barrier(0);
   issue_dma(k, 1, c1, s1);
   __builtin_amdgcn_sched_barrier(0);
-  wg2 = load_full_group(k.nib, k.scl, min(2, k.last_full), k.lane, k.nl);
+  w2 = load_wstep(k, 2);
   __builtin_amdgcn_sched_barrier(0);
-#define GOSSMX_GROUP(QV, SLOT, CODES, SCL, NCODES, NSCL)                                            \
-  {                                                                                                 \
-    const int q = (QV);                                                                             \
-    __builtin_amdgcn_sched_barrier(0);                                                              \
-    __builtin_amdgcn_s_waitcnt(kWaitDmaGroup); /* this wave's DMA for group q has landed */        \
-    __builtin_amdgcn_s_barrier();              /* ... and every other wave's; slot of q-1 is free */ \
-    __builtin_amdgcn_sched_barrier(0);                                                              \
-    issue_dma(k, q + 2, NCODES, NSCL);                                                              \
-    __builtin_amdgcn_sched_barrier(0);                                                              \
-    const WeightGroup cur = q < k.nqf ? SLOT : k.tail;                                              \
-    if (k.tile_ok && q < k.nq)                                                                      \
-      group_update<RESIDUAL, NTG>(tot, CODES, SCL, cur, min(4, k.B - 4 * q), k.lane, k.G);          \
-    __builtin_amdgcn_sched_barrier(0);                                                              \
-    SLOT = load_full_group(k.nib, k.scl, min(q + 3, k.last_full), k.lane, k.nl);                    \
-    __builtin_amdgcn_sched_barrier(0);                                                              \
+#define GOSSMX_STEP(QV, SLOT, CODES, SCL, NCODES, NSCL)                                              \
+  {                                                                                                  \
+    const int q = (QV);                                                                              \
+    __builtin_amdgcn_sched_barrier(0);                                                               \
+    __builtin_amdgcn_s_waitcnt(kWaitDma); /* this wave's DMA for step q has landed */               \
+    __builtin_amdgcn_s_barrier();         /* ... and every other wave's; the slot of q-1 is free */  \
+    __builtin_amdgcn_sched_barrier(0);                                                               \
+    issue_dma(k, q + 2, NCODES, NSCL);                                                               \
+    __builtin_amdgcn_sched_barrier(0);                                                               \
+    if (k.tile_ok && q < k.nsteps) step_update<RESIDUAL, NTG, FAST>(k, tot, CODES, SCL, SLOT, q);    \
+    __builtin_amdgcn_sched_barrier(0);                                                               \
+    SLOT = load_wstep(k, q + 3);                                                                     \
+    __builtin_amdgcn_sched_barrier(0);                                                               \
   }
-  const int nq_pad = (k.nq + 2) / 3 * 3;
-  for (int q0 = 0; q0 < nq_pad; q0 += 3) {
-    GOSSMX_GROUP(q0, wg0, c0, s0, c2, s2)
-    GOSSMX_GROUP(q0 + 1, wg1, c1, s1, c0, s0)
-    GOSSMX_GROUP(q0 + 2, wg2, c2, s2, c1, s1)
+  const int n_pad = (k.nsteps + 2) / 3 * 3;
+  for (int q0 = 0; q0 < n_pad; q0 += 3) {
+    GOSSMX_STEP(q0, w0, c0, s0, c2, s2)
+    GOSSMX_STEP(q0 + 1, w1, c1, s1, c0, s0)
+    GOSSMX_STEP(q0 + 2, w2, c2, s2, c1, s1)
   }
-#undef GOSSMX_GROUP
+#undef GOSSMX_STEP
 }
 
 template <int MODE, bool RESIDUAL>
 __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int nl = lane & 15, G = lane >> 4;
   int expert, start, count, route_base = 0;
   if (MODE == kPlain) {
@@ -668,11 +696,9 @@ __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
     route_base = a.bucket_off[expert];
     count = min(kChunk, a.bucket_off[expert + 1] - route_base - start);
   }
-  // LDS ring of three K groups, filled by global->LDS DMA two groups ahead.
+  // LDS ring of three steps, filled by DMA two steps ahead.
   __shared__ __align__(16) char s_codes0[kSlotBytes], s_codes1[kSlotBytes], s_codes2[kSlotBytes];
-  // A scale DMA writes 64 dwords per wave: kSclSlot float2 per slot, of which
-  // the first 4 * kChunk ([block][row]) hold data.
-  __shared__ __align__(16) float2 s_scl0[kSclSlot], s_scl1[kSclSlot], s_scl2[kSclSlot];
+  __shared__ __align__(16) float s_scl0[kSclSlot], s_scl1[kSclSlot], s_scl2[kSclSlot];
   __shared__ int s_row[kChunk];
   if (tid < kChunk) {
     int r = -1;
@@ -689,268 +715,97 @@ __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
   const int tile = blockIdx.x * kWaves + wave;
   const int row = tile * kTileRows + nl;
   const int n_tg = (count + 7) >> 3;
+  const int nq4 = (B + 3) >> 2;
 
   KLoop k;
   k.B = B;
-  k.nq = (B + 3) >> 2;
-  k.nqf = B >> 2;
-  k.last_full = k.nqf > 0 ? k.nqf - 1 : 0;
+  k.nsteps = (B + kStep - 1) / kStep;
+  k.nfull4 = B >> 2;
+  k.last_full = k.nfull4 > 0 ? k.nfull4 - 1 : 0;
   k.wave = wave;
   k.lane = lane;
-  k.nl = nl;
   k.G = G;
   k.tile_ok = tile < (int)a.w.tiles;
-  // Waves past the last tile read tile 0 and discard it.
+  // Waves past the last tile stream tile 0 and discard it.
   const int safe_tile = k.tile_ok ? tile : 0;
-  k.nib = a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)safe_tile * 256 * B;
-  k.scl = a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)safe_tile * 64 * k.nq;
-  k.tail = load_tail_group(k.nib, k.scl, k.nqf, (B & 3) > 0 ? (B & 3) : 1, lane, nl);
+  const uint8_t* nib = a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)safe_tile * 256 * B;
+  const uint8_t* scl = a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)safe_tile * 64 * nq4;
+  k.nib = buffer_rsrc(nib);
+  k.scl = buffer_rsrc(scl);
+  k.vl = lane * 16;
+  k.vs = nl * 4;
+  {
+    // The partial last group (B % 4 = rem blocks): dwords at lane * rem * 4 of
+    // the compact group, and the row's padded scale dword. Reads past the
+    // group stay inside the plane slack.
+    const int rem = (B & 3) > 0 ? (B & 3) : 1;
+    const uint32_t* gw = reinterpret_cast<const uint32_t*>(nib + (size_t)k.nfull4 * 1024 + lane * rem * 4);
+    k.tail_v = u32x4{gw[0], gw[1], gw[2], 0u};
+    k.tail_s = *reinterpret_cast<const uint32_t*>(scl + (size_t)k.nfull4 * 64 + nl * 4);
+  }
+  const bool fast = !k.tile_ok || a.w.fast[(size_t)expert * a.w.tiles + tile] != 0;
 
   float b0 = 0.0f;
   if (a.bias != nullptr && k.tile_ok && row < rows) b0 = a.bias[(size_t)expert * a.bias_expert_stride + row];
   b0 = b0 + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
-  float tot[kChunk / 8][2];
+  float tot[kNtg][2];
 #pragma unroll
-  for (int tg = 0; tg < kChunk / 8; ++tg) { tot[tg][0] = b0; tot[tg][1] = b0; }
+  for (int tg = 0; tg < kNtg; ++tg) { tot[tg][0] = b0; tot[tg][1] = b0; }
 
-  // DMA lane map, the same for every group. Code instruction i of this wave
-  // fills slot bytes c * 16 with c = (i * kWaves + wave) * 64 + lane, i.e.
-  // block j, token group tg, k-slice g, vector v (row tg*8 + v/2, part v%2)
-  // in the slot layout above; its source is piece (part, g) of the row's
-  // 128-byte block record. Scale dword d = wave * 64 + lane holds half d % 2
-  // of (block d / (2 kChunk), row (d / 2) % kChunk). Lanes with nothing to
-  // move read the buffer base (valid memory) into slot bytes no row uses, so
-  // every wave issues the same instructions. Reads of a last partial group
-  // run up to 3 blocks past a row, inside the buffers' slack.
-  k.gcodes = reinterpret_cast<const char*>(a.actv);
-  k.gscl = reinterpret_cast<const char*>(a.acts);
+  // DMA lane map, the same for every step. Code piece i of this wave fills
+  // slot bytes c * 16 with c = (i * kWaves + wave) * 64 + lane, i.e. block j,
+  // token group tg, k-slice g, vector v (row tg*8 + v/2, part v%2) in the
+  // slot layout above; its source is piece (part, g) of the row's 128-byte
+  // block record. Scale dword d = wave * 64 + lane holds half d % 2 of
+  // (block d / (2 kChunk), row (d / 2) % kChunk). Lanes with nothing to move
+  // read the start of the buffer (valid memory) into slot bytes no row uses.
+  // A last partial step reads up to 7 blocks past a row, inside the
+  // buffers' slack.
+  k.codes = buffer_rsrc(a.actv);
+  k.scales = buffer_rsrc(a.acts);
 #pragma unroll
   for (int i = 0; i < kCodeDma; ++i) {
     const int c = (i * kWaves + wave) * 64 + lane;
-    const int j = c / (kChunk * 8), r = c % (kChunk * 8);
-    const int tg = r >> 6, g = (r >> 4) & 3, v = r & 15;
+    const int ch = c >> 6, p = c & 63;
+    const int j = ch / kNtg, tg = ch % kNtg, g = p >> 4, v = p & 15;
     const int t = tg * 8 + (v >> 1), part = v & 1;
-    k.coff[i] = t < count ? ((s_row[t] * B + j) * 8 + part * 4 + g) * 16 : -1;
+    k.voff[i] = t < count ? ((s_row[t] * B + j) * 8 + part * 4 + g) * 16 : 0;
   }
   {
     const int d = wave * 64 + lane;
     const int j = d / (kChunk * 2), t = (d >> 1) % kChunk;
-    k.soff = (d < 4 * kChunk * 2 && t < count) ? ((s_row[t] * B + j) * 2 + (d & 1)) * 4 : -1;
+    k.soff = (d < kStep * kChunk * 2 && t < count) ? ((s_row[t] * B + j) * 2 + (d & 1)) * 4 : 0;
   }
 
-  switch (n_tg) {
-    case 1: k_loop<RESIDUAL, 1>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2); break;
-    case 2: k_loop<RESIDUAL, 2>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2); break;
-    case 3: k_loop<RESIDUAL, 3>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2); break;
-    case 4: k_loop<RESIDUAL, 4>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2); break;
-    default: k_loop<RESIDUAL, 6>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2); break;
+  if (n_tg == 1) {
+    if (fast) k_loop<RESIDUAL, 1, true>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2);
+    else k_loop<RESIDUAL, 1, false>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2);
+  } else {
+    if (fast) k_loop<RESIDUAL, kNtg, true>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2);
+    else k_loop<RESIDUAL, kNtg, false>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2);
   }
   // Drain the trailing DMA into the ring before the LDS is reused or the
   // work-group ends.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  gemm_epilogue<MODE, kChunk / 8>(a, tot, n_tg, count, start, route_base, row, k.tile_ok,
-                                  reinterpret_cast<float*>(s_codes0));
+  gemm_epilogue<MODE, kNtg>(a, tot, n_tg, count, start, route_base, row, k.tile_ok,
+                            reinterpret_cast<float*>(s_codes0));
 }
 
-// ---------------------------------------------------------------------------
-// Small-bucket expert GEMM: work items of at most kSmallRows (16) activation
-// rows, most of the experts at decode batch 64 under Zipf routing. The item's
-// activations are staged into LDS for a whole phase of K (all 90 blocks for
-// <= 4 rows, 48 blocks for <= 8, 24 blocks for <= 16), so the K loop inside a
-// phase has no barriers and no activation traffic: each wave streams its
-// 16-row weight tile through a kSmallRing-deep register ring that continues
-// across phases. Same operands, chain order and epilogue as gemm_kernel.
-//
-// Per-block LDS layouts (V vectors = 2 parts x token slots):
-//   V = 8  (<= 4 rows):  512 B = [k-slice g][vector v < 8][16 B]; MFMA rows
-//                         8..15 repeat rows 0..7 (unused results).
-//   V = 16 (<= 8 rows):  1 KiB = [g][v < 16][16 B]
-//   V = 32 (<= 16 rows): 2 KiB = two 1 KiB token groups of the V = 16 form.
-// Scales: [block][token slot] float2, V / 2 slots per block, plus an 8-entry
-// tail (lanes of unused token slots read past a block).
-constexpr int kSmallRing = 3;
-constexpr int kSmallCodeBytes = 48 * 1024;
-constexpr int kSmallSclEntries = 384 + 8;
-constexpr int kSmallStage = 6;  // 16-byte staging pieces per thread per phase (max over layouts)
-
-template <int V>
-struct SmallLayout {
-  static constexpr int kNT = V <= 16 ? 1 : 2;           // MFMA token groups
-  static constexpr int kBlockBytes = V * 64;            // LDS bytes per block
-  static constexpr int kSlots = V / 2;                  // token slots per block
-  static constexpr int kPhaseBlocks = kSmallCodeBytes / kBlockBytes;  // 96, 48, 24
-  static_assert(kPhaseBlocks % 12 == 0, "phases are whole multiples of the 3-deep, 4-block ring");
-  static_assert(kPhaseBlocks * kSlots + 8 <= kSmallSclEntries, "scale LDS");
-  static_assert(16 * 24 * 8 <= kSmallStage * kGemmThreads, "staging pieces");
-};
-
-template <int V, bool RESIDUAL, bool SCALED>
-__device__ __forceinline__ void small_block(float (&tot)[2][2], const char* codes, const float2* scl, const half8 bop,
-                                            const float e8, const int jl, const int lane, const int nl,
-                                            const int G) {
-  using L = SmallLayout<V>;
-#pragma unroll
-  for (int tg = 0; tg < L::kNT; ++tg) {
-    const int a_off = V == 8 ? (G * 8 + (nl & 7)) * 16 : tg * 1024 + lane * 16;
-    const half8 aop = *reinterpret_cast<const half8*>(codes + jl * L::kBlockBytes + a_off);
-    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, zero, 0, 0, 0);
-    const float4 sc = *reinterpret_cast<const float4*>(&scl[jl * L::kSlots + tg * 8 + 2 * G]);
-    if (SCALED) {
-      tot[tg][0] = tot[tg][0] + d[0] * sc.x;
-      if (RESIDUAL) tot[tg][0] = tot[tg][0] + d[1] * sc.y;
-      tot[tg][1] = tot[tg][1] + d[2] * sc.z;
-      if (RESIDUAL) tot[tg][1] = tot[tg][1] + d[3] * sc.w;
-    } else {
-      tot[tg][0] = tot[tg][0] + (d[0] * e8) * sc.x;
-      if (RESIDUAL) tot[tg][0] = tot[tg][0] + (d[1] * e8) * sc.y;
-      tot[tg][1] = tot[tg][1] + (d[2] * e8) * sc.z;
-      if (RESIDUAL) tot[tg][1] = tot[tg][1] + (d[3] * e8) * sc.w;
-    }
+// Exactness flag per (expert, tile): 1 when every E8M0 byte of the tile's
+// blocks lies in [kFastScaleLo, kFastScaleHi]. One work-group per tile.
+__global__ __launch_bounds__(256) void tile_flags_kernel(TiledWeights w) {
+  const size_t e = blockIdx.y, t = blockIdx.x;
+  const size_t nq = (w.blocks + 3) / 4;
+  const uint8_t* scl = w.scl + e * w.scl_stride + t * 64 * nq;
+  int bad = 0;
+  for (size_t i = threadIdx.x; i < kTileRows * w.blocks; i += blockDim.x) {
+    const size_t n = i / w.blocks, b = i % w.blocks;
+    const uint32_t s = scl[(b / 4) * 64 + n * 4 + (b % 4)];
+    bad |= (s - kFastScaleLo) > (kFastScaleHi - kFastScaleLo);
   }
-}
-
-// One 4-block weight group whose first block is phase-local block jl0.
-template <int V, bool RESIDUAL>
-__device__ __forceinline__ void small_group(float (&tot)[2][2], const char* codes, const float2* scl,
-                                            const WeightGroup cur, const int jl0, const int nb, const int lane,
-                                            const int nl, const int G) {
-  const uint32_t wv[4] = {cur.v.x, cur.v.y, cur.v.z, cur.v.w};
-  bool in_range = true;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t s = (cur.s >> (8 * j)) & 0xffu;
-    if (j < nb) in_range = in_range && (s - kFastScaleLo) <= (kFastScaleHi - kFastScaleLo);
-  }
-  if (__all(in_range)) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j < nb) {
-        const float e8 = __uint_as_float(((cur.s >> (8 * j)) & 0xffu) << 23);
-        small_block<V, RESIDUAL, true>(tot, codes, scl, fp4x8_to_half8_scaled(wv[j], e8), 0.0f, jl0 + j, lane, nl, G);
-      }
-    }
-  } else {
-#pragma unroll 1
-    for (int j = 0; j < nb; ++j) {
-      const uint32_t w = j == 0 ? wv[0] : (j == 1 ? wv[1] : (j == 2 ? wv[2] : wv[3]));
-      const float e8 = e8m0_select((cur.s >> (8 * j)) & 0xffu);
-      small_block<V, RESIDUAL, false>(tot, codes, scl, fp4x8_to_half8(w), e8, jl0 + j, lane, nl, G);
-    }
-  }
-}
-
-// Stages blocks [k0, k0 + nbk) of every row into LDS (loads unconditional,
-// clamped to valid indices; stores only for real pieces).
-template <int V>
-__device__ __forceinline__ void small_stage(char* codes, float2* scl, const uint4* gactv, const float2* gacts,
-                                            const int* s_row, const int count, const int B, const int k0,
-                                            const int nbk, const int tid) {
-  using L = SmallLayout<V>;
-  const int per_row = nbk * 8, pieces = count * per_row;
-  uint4 st[kSmallStage];
-#pragma unroll
-  for (int i = 0; i < kSmallStage; ++i) {
-    const int c = min(tid + i * kGemmThreads, pieces - 1);
-    const int t = c / per_row, rem = c - t * per_row;
-    st[i] = gactv[((size_t)s_row[t] * B + k0) * 8 + rem];
-  }
-  const int sc = min(tid, count * nbk - 1);
-  const int stt = sc / nbk, stj = sc - stt * nbk;
-  const float2 sv = gacts[(size_t)s_row[stt] * B + k0 + stj];
-#pragma unroll
-  for (int i = 0; i < kSmallStage; ++i) {
-    const int c = tid + i * kGemmThreads;
-    if (c < pieces) {
-      const int t = c / per_row, rem = c - t * per_row;
-      const int j = rem >> 3, p = rem & 7, part = p >> 2, g = p & 3;  // piece p of the block's 128-byte record
-      const int off = V == 8 ? j * 512 + (g * 8 + 2 * t + part) * 16
-                             : j * L::kBlockBytes + (t >> 3) * 1024 + (g * 16 + 2 * (t & 7) + part) * 16;
-      *reinterpret_cast<uint4*>(codes + off) = st[i];
-    }
-  }
-  if (tid < count * nbk) scl[stj * L::kSlots + stt] = sv;
-}
-
-template <int V, bool RESIDUAL>
-__device__ __forceinline__ void small_k_loop(float (&tot)[2][2], char* codes, float2* scl, const int* s_row,
-                                             const GemmArgs& a, const uint8_t* nib, const uint8_t* wscl,
-                                             const int count, const int B, const int tid, const int lane,
-                                             const int nl, const int G) {
-  using L = SmallLayout<V>;
-  const int nqf = B >> 2, last_full = nqf > 0 ? nqf - 1 : 0;
-  const uint4* gactv = reinterpret_cast<const uint4*>(a.actv);
-  const float2* gacts = reinterpret_cast<const float2*>(a.acts);
-  const WeightGroup tail = load_tail_group(nib, wscl, nqf, (B & 3) > 0 ? (B & 3) : 1, lane, nl);
-  WeightGroup r0 = load_full_group(nib, wscl, min(0, last_full), lane, nl);
-  WeightGroup r1 = load_full_group(nib, wscl, min(1, last_full), lane, nl);
-  WeightGroup r2 = load_full_group(nib, wscl, min(2, last_full), lane, nl);
-  const int phases = (B + L::kPhaseBlocks - 1) / L::kPhaseBlocks;
-  for (int ph = 0; ph < phases; ++ph) {
-    const int k0 = ph * L::kPhaseBlocks, nbk = min(L::kPhaseBlocks, B - k0);
-    if (ph > 0) __syncthreads();  // every wave is done with the previous phase
-    small_stage<V>(codes, scl, gactv, gacts, s_row, count, B, k0, nbk, tid);
-    __syncthreads();
-    const int q_begin = k0 >> 2, q_end = (k0 + nbk + 3) >> 2;
-#define GOSSMX_SMALL_GROUP(QQ, SLOT)                                                                   \
-  {                                                                                                    \
-    const int q = (QQ);                                                                                \
-    if (q < q_end) {                                                                                   \
-      const bool full = q < nqf;                                                                       \
-      small_group<V, RESIDUAL>(tot, codes, scl, full ? SLOT : tail, 4 * q - k0, full ? 4 : (B & 3), lane, \
-                               nl, G);                                                                 \
-    }                                                                                                  \
-    SLOT = load_full_group(nib, wscl, min(q + kSmallRing, last_full), lane, nl); /* after last use */  \
-  }
-    for (int q0 = q_begin; q0 < q_begin + L::kPhaseBlocks / 4; q0 += 3) {
-      GOSSMX_SMALL_GROUP(q0, r0)
-      GOSSMX_SMALL_GROUP(q0 + 1, r1)
-      GOSSMX_SMALL_GROUP(q0 + 2, r2)
-    }
-#undef GOSSMX_SMALL_GROUP
-  }
-}
-
-template <int MODE, bool RESIDUAL>
-__global__ __launch_bounds__(kGemmThreads, 6) void gemm_small_kernel(GemmArgs a) {
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int nl = lane & 15, G = lane >> 4;
-  const int wi = blockIdx.y;
-  if (wi >= *a.n_work_small) return;  // uniform over the work-group
-  const int expert = a.work_small[2 * wi];
-  const int route_base = a.bucket_off[expert];
-  const int count = a.bucket_off[expert + 1] - route_base;  // 1..kSmallRows
-  __shared__ __align__(16) char s_codes[kSmallCodeBytes];
-  __shared__ __align__(16) float2 s_scl[kSmallSclEntries];
-  __shared__ int s_row[kSmallRows];
-  if (tid < kSmallRows) {
-    int r = -1;
-    if (tid < count) r = MODE == kGateUp ? a.route_tok[route_base + tid] : route_base + tid;
-    s_row[tid] = r;
-  }
-  __syncthreads();
-
-  const int rows = (int)a.w.rows, B = (int)a.w.blocks;
-  const int nq = (B + 3) >> 2;
-  const int tile = blockIdx.x * kWaves + wave;
-  const bool tile_ok = tile < (int)a.w.tiles;
-  const int row = tile * kTileRows + nl;
-  const int safe_tile = tile_ok ? tile : 0;
-  const uint8_t* nib = a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)safe_tile * 256 * B;
-  const uint8_t* wscl = a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)safe_tile * 64 * nq;
-
-  float b0 = 0.0f;
-  if (a.bias != nullptr && tile_ok && row < rows) b0 = a.bias[(size_t)expert * a.bias_expert_stride + row];
-  b0 = b0 + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
-  float tot[2][2] = {{b0, b0}, {b0, b0}};
-  if (count <= 4) small_k_loop<8, RESIDUAL>(tot, s_codes, s_scl, s_row, a, nib, wscl, count, B, tid, lane, nl, G);
-  else if (count <= 8) small_k_loop<16, RESIDUAL>(tot, s_codes, s_scl, s_row, a, nib, wscl, count, B, tid, lane, nl, G);
-  else small_k_loop<32, RESIDUAL>(tot, s_codes, s_scl, s_row, a, nib, wscl, count, B, tid, lane, nl, G);
-  __syncthreads();  // the activation LDS is reused by the epilogue
-  gemm_epilogue<MODE, 2>(a, tot, count <= 8 ? 1 : 2, count, 0, route_base, row, tile_ok,
-                         reinterpret_cast<float*>(s_codes));
+  bad = __syncthreads_or(bad);
+  if (threadIdx.x == 0) w.fast[e * w.tiles + t] = bad ? 0 : 1;
 }
 
 // ---------------------------------------------------------------------------
@@ -1151,7 +1006,8 @@ __global__ void selftest_kernel(float* out) {
 static inline unsigned grid1d(size_t n, unsigned block) { return (unsigned)((n + block - 1) / block); }
 
 hipError_t launch_route(const RouteArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL(route_kernel, dim3(a.m), dim3(256), 0, stream, a);
+  const int quant_groups = (a.hidden / kBlock + kRouteQuantBlocks - 1) / kRouteQuantBlocks;
+  hipLaunchKernelGGL(route_kernel, dim3(a.m, 1 + quant_groups), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -1176,12 +1032,9 @@ hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int grid_work, hipStrea
   return hipGetLastError();
 }
 
-hipError_t launch_gemm_small(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream) {
-  if (!a.residual || mode == kPlain) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)((a.w.tiles + kWaves - 1) / kWaves), (unsigned)grid_work);
-  const dim3 block(kGemmThreads);
-  if (mode == kGateUp) hipLaunchKernelGGL((gemm_small_kernel<kGateUp, true>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((gemm_small_kernel<kDown, true>), grid, block, 0, stream, a);
+hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream) {
+  if (w.experts == 0 || w.tiles == 0) return hipSuccess;
+  hipLaunchKernelGGL(tile_flags_kernel, dim3((unsigned)w.tiles, (unsigned)w.experts), dim3(256), 0, stream, w);
   return hipGetLastError();
 }
 
