@@ -412,7 +412,9 @@ typedef __attribute__((address_space(3))) void* lds_ptr;
 
 constexpr int kWaves = 8;                   // waves per GEMM work-group
 constexpr int kGemmThreads = 64 * kWaves;   // 512
-constexpr int kGemmRows = 16 * kWaves;      // weight rows per work-group
+constexpr int kWaveTiles = 2;               // 16-row weight tiles per wave
+constexpr int kWgTiles = kWaves * kWaveTiles;
+constexpr int kGemmRows = kTileRows * kWgTiles;  // weight rows per work-group (256)
 constexpr int kNtg = kChunk / 8;            // MFMA token groups per work item
 constexpr int kStep = 8;                    // K blocks per pipeline step
 constexpr int kSlotBytes = kStep * kChunk * 2 * kBlock * 2;  // f16 codes of one step in LDS
@@ -421,9 +423,10 @@ constexpr int kSclSlot = 64 * kWaves;       // floats written by one step's scal
 static_assert(kSlotBytes == kCodeDma * 16 * kGemmThreads, "code DMA covers a slot exactly");
 static_assert(kStep * kChunk * 2 <= kSclSlot, "one dword DMA per lane covers a step's scales");
 static_assert(kChunk % 8 == 0 && kStep == 8, "token groups of 8, steps of two 4-block groups");
+static_assert(kGemmRows % 64 == 0, "a work-group's gate_up rows make whole 32-value down-input blocks");
 // Vector-memory instructions per wave and step: weights 2 x (nibbles, scale
-// dword); activations kCodeDma code pieces + 1 scale dword.
-constexpr int kLoadsW = 4;
+// dword) per tile; activations kCodeDma code pieces + 1 scale dword.
+constexpr int kLoadsW = 4 * kWaveTiles;
 constexpr int kLoadsD = kCodeDma + 1;
 // s_waitcnt immediate for "the DMA of step q has landed": issued after it are
 // W(q+1), D(q+1), W(q+2) (see k_loop). expcnt and lgkmcnt are not waited on.
@@ -436,11 +439,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base) 
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, kBufferFlags);
 }
 
-// One step of a wave's weights: nibble groups 2q and 2q+1 and their scale dwords.
+// One step of a wave's weights: per tile, nibble groups 2q and 2q+1 and their
+// scale dwords.
 struct WStep {
-  u32x4 v0, v1;
-  uint32_t s0, s1;
+  u32x4 v0[kWaveTiles], v1[kWaveTiles];
+  uint32_t s0[kWaveTiles], s1[kWaveTiles];
 };
+
+// Accumulators of one wave: [tile][token group][token of the lane's pair].
+typedef float Acc[kWaveTiles][kNtg][2];
 
 // LDS slot layout of one step (written by DMA, read as MFMA A operands): for
 // block j and token group tg, 1 KiB = [k-slice g (4)][vector i (16)][16 B]
@@ -449,115 +456,130 @@ struct WStep {
 // Scales: float2 (primary, residual) at [j][row].
 __device__ __forceinline__ int slot_chunk(int j, int tg) { return j * kNtg + tg; }
 
-// One block j of the current step against NTG token groups: the MFMAs and
-// the ordered chain updates. SCALED: the weight operand already carries the
-// E8M0 scale (exact), so the MFMA returns (p / 2) * e8m0 and a term is
-// d * act_scale; otherwise a term is (d * e8m0) * act_scale. Both are the
-// reference's (p * (0.5 * e8m0)) * act_scale rounded once.
+// One block j of the current step against NTG token groups and the wave's
+// tiles: one A operand and one scale read per token group feed an MFMA per
+// tile, then the ordered chain updates. SCALED: the weight operand already
+// carries the E8M0 scale (exact), so the MFMA returns (p / 2) * e8m0 and a
+// term is d * act_scale; otherwise a term is (d * e8m0) * act_scale. Both are
+// the reference's (p * (0.5 * e8m0)) * act_scale rounded once.
 template <bool RESIDUAL, bool SCALED, int NTG>
-__device__ __forceinline__ void block_update(float (&tot)[kNtg][2], const char* codes, const float2* scl,
-                                             const half8 bop, const float e8, const int j, const int lane,
-                                             const int G) {
+__device__ __forceinline__ void block_update(Acc& tot, const char* codes, const float2* scl,
+                                             const half8 (&bop)[kWaveTiles], const float (&e8)[kWaveTiles],
+                                             const int j, const int lane, const int G) {
+  const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int tg = 0; tg < NTG; ++tg) {
     const half8 aop = *reinterpret_cast<const half8*>(codes + slot_chunk(j, tg) * 1024 + lane * 16);
-    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, zero, 0, 0, 0);
     const float4 sc = *reinterpret_cast<const float4*>(&scl[j * kChunk + tg * 8 + 2 * G]);
-    if (SCALED) {
-      tot[tg][0] = tot[tg][0] + d[0] * sc.x;
-      if (RESIDUAL) tot[tg][0] = tot[tg][0] + d[1] * sc.y;
-      tot[tg][1] = tot[tg][1] + d[2] * sc.z;
-      if (RESIDUAL) tot[tg][1] = tot[tg][1] + d[3] * sc.w;
-    } else {
-      tot[tg][0] = tot[tg][0] + (d[0] * e8) * sc.x;
-      if (RESIDUAL) tot[tg][0] = tot[tg][0] + (d[1] * e8) * sc.y;
-      tot[tg][1] = tot[tg][1] + (d[2] * e8) * sc.z;
-      if (RESIDUAL) tot[tg][1] = tot[tg][1] + (d[3] * e8) * sc.w;
+    f32x4 d[kWaveTiles];
+#pragma unroll
+    for (int t = 0; t < kWaveTiles; ++t) d[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop[t], zero, 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < kWaveTiles; ++t) {
+      if (SCALED) {
+        tot[t][tg][0] = tot[t][tg][0] + d[t][0] * sc.x;
+        if (RESIDUAL) tot[t][tg][0] = tot[t][tg][0] + d[t][1] * sc.y;
+        tot[t][tg][1] = tot[t][tg][1] + d[t][2] * sc.z;
+        if (RESIDUAL) tot[t][tg][1] = tot[t][tg][1] + d[t][3] * sc.w;
+      } else {
+        tot[t][tg][0] = tot[t][tg][0] + (d[t][0] * e8[t]) * sc.x;
+        if (RESIDUAL) tot[t][tg][0] = tot[t][tg][0] + (d[t][1] * e8[t]) * sc.y;
+        tot[t][tg][1] = tot[t][tg][1] + (d[t][2] * e8[t]) * sc.z;
+        if (RESIDUAL) tot[t][tg][1] = tot[t][tg][1] + (d[t][3] * e8[t]) * sc.w;
+      }
     }
   }
 }
 
-// The first nb blocks of one 4-block group (nibble dwords v, scale bytes s)
-// at step-relative block jb. FAST: every scale of the tile is in
-// [kFastScaleLo, kFastScaleHi] (checked when the weights were stored), so the
-// conversion applies the scale exactly; otherwise the scale multiplies the
-// MFMA result, with the reference's 0x00 and 0xff encodings.
+// The first nb blocks of one 4-block group (per tile: nibble dwords v, scale
+// bytes s) at step-relative block jb. FAST: every scale of the wave's tiles is
+// in [kFastScaleLo, kFastScaleHi] (checked when the weights were stored), so
+// the conversion applies the scale exactly; otherwise the scale multiplies
+// the MFMA result, with the reference's 0x00 and 0xff encodings.
 template <bool RESIDUAL, int NTG, bool FAST>
-__device__ __forceinline__ void group_update(float (&tot)[kNtg][2], const char* codes, const float2* scl,
-                                             const u32x4 v, const uint32_t s, const int jb, const int nb,
-                                             const int lane, const int G) {
+__device__ __forceinline__ void group_update(Acc& tot, const char* codes, const float2* scl,
+                                             const u32x4 (&v)[kWaveTiles], const uint32_t (&s)[kWaveTiles],
+                                             const int jb, const int nb, const int lane, const int G) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     if (j < nb) {
-      const uint32_t sb = (s >> (8 * j)) & 0xffu;
-      if (FAST) {
-        const float e8 = __uint_as_float(sb << 23);
-        block_update<RESIDUAL, true, NTG>(tot, codes, scl, fp4x8_to_half8_scaled(v[j], e8), 0.0f, jb + j, lane, G);
-      } else {
-        block_update<RESIDUAL, false, NTG>(tot, codes, scl, fp4x8_to_half8(v[j]), e8m0_select(sb), jb + j, lane, G);
+      half8 bop[kWaveTiles];
+      float e8[kWaveTiles];
+#pragma unroll
+      for (int t = 0; t < kWaveTiles; ++t) {
+        const uint32_t sb = (s[t] >> (8 * j)) & 0xffu;
+        if (FAST) {
+          bop[t] = fp4x8_to_half8_scaled(v[t][j], __uint_as_float(sb << 23));
+          e8[t] = 0.0f;
+        } else {
+          bop[t] = fp4x8_to_half8(v[t][j]);
+          e8[t] = e8m0_select(sb);
+        }
       }
+      block_update<RESIDUAL, FAST, NTG>(tot, codes, scl, bop, e8, jb + j, lane, G);
     }
   }
 }
 
 // Shared GEMM epilogue: plain f32 stores, the down projection's bf16 rows,
 // or gate_up's SwiGLU and down-input quantization. `s_act` is LDS scratch of
-// at least count * (kGemmRows / 2 + 1) floats, free for reuse.
-template <int MODE, int NT>
-__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const float (&tot)[NT][2], const int n_tg,
-                                              const int count, const int start, const int route_base, const int row,
-                                              const bool tile_ok, float* s_act) {
+// at least count * (kGemmRows / 2 + 1) floats, free for reuse. Rows of tiles
+// past the end (row >= rows) are never stored.
+template <int MODE>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc& tot, const int n_tg, const int count,
+                                              const int start, const int route_base, const int tile0, float* s_act) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int nl = lane & 15, G = lane >> 4;
   const int rows = (int)a.w.rows;
 
-  if (MODE == kPlain) {
-    if (tile_ok && row < rows) {
+  if (MODE == kPlain || MODE == kDown) {
 #pragma unroll
-      for (int tg = 0; tg < NT; ++tg)
+    for (int t = 0; t < kWaveTiles; ++t) {
+      const int row = (tile0 + t) * kTileRows + nl;
+      if (row < rows) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int c = tg * 8 + 2 * G + t;
-          if (c < count) a.out[(size_t)(start + c) * a.out_stride + row] = tot[tg][t];
-        }
-    }
-  } else if (MODE == kDown) {
-    if (tile_ok && row < rows) {
+        for (int tg = 0; tg < kNtg; ++tg)
 #pragma unroll
-      for (int tg = 0; tg < NT; ++tg)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int c = tg * 8 + 2 * G + t;
-          if (c < count) {
-            const int slot = a.route_slot[route_base + start + c];
-            a.y[(size_t)slot * rows + row] = bf16_bits(tot[tg][t]);  // bf16 (cpu_runner.rs:2945-2947)
+          for (int u = 0; u < 2; ++u) {
+            const int c = tg * 8 + 2 * G + u;
+            if (c < count) {
+              if (MODE == kPlain) {
+                a.out[(size_t)(start + c) * a.out_stride + row] = tot[t][tg][u];
+              } else {
+                const int slot = a.route_slot[route_base + start + c];
+                a.y[(size_t)slot * rows + row] = bf16_bits(tot[t][tg][u]);  // bf16 (cpu_runner.rs:2945-2947)
+              }
+            }
           }
-        }
+      }
     }
   } else {
     // gate_up epilogue: bf16 (cpu_runner.rs:2905), SwiGLU over (even, odd)
     // rows (:2907-2919), then the down input's residual-Q8 blocks: the
     // kGemmRows rows of this work-group make kGemmRows / 64 blocks of 32
     // values (cpu_runner.rs:3224-3231). The SwiGLU values reuse an LDS slot
-    // as [kChunk rows][kGemmRows / 2 values].
+    // as [kChunk rows][kGemmRows / 2 values]; tile t of wave w holds values
+    // (w * kWaveTiles + t) * 8 .. + 7.
     constexpr int kActStride = kGemmRows / 2 + 1;
     // Lane pairs (even = gate row, odd = up row) hold both values for tokens
     // t0 = 2G and t1 = 2G + 1; the even lane finishes t0 and the odd lane t1.
     const bool odd = (nl & 1) != 0;
 #pragma unroll
-    for (int tg = 0; tg < NT; ++tg) {
-      if (tg < n_tg) {
-        const float own0 = bf16r(tot[tg][0]), own1 = bf16r(tot[tg][1]);
-        const float recv = __shfl_xor(odd ? own0 : own1, 1);
-        const float gate = odd ? recv : own0;
-        const float up = odd ? own1 : recv;
-        const int c = tg * 8 + 2 * G + (odd ? 1 : 0);
-        if (c < count)
-          s_act[c * kActStride + wave * 8 + (nl >> 1)] = swiglu_one(gate, up, a.alpha, a.limit, a.sig_tab);
+    for (int t = 0; t < kWaveTiles; ++t)
+#pragma unroll
+      for (int tg = 0; tg < kNtg; ++tg) {
+        if (tg < n_tg) {
+          const float own0 = bf16r(tot[t][tg][0]), own1 = bf16r(tot[t][tg][1]);
+          const float recv = __shfl_xor(odd ? own0 : own1, 1);
+          const float gate = odd ? recv : own0;
+          const float up = odd ? own1 : recv;
+          const int c = tg * 8 + 2 * G + (odd ? 1 : 0);
+          if (c < count)
+            s_act[c * kActStride + (wave * kWaveTiles + t) * 8 + (nl >> 1)] =
+                swiglu_one(gate, up, a.alpha, a.limit, a.sig_tab);
+        }
       }
-    }
     __syncthreads();
     const int hw = tid >> 5, l32 = tid & 31;
     const int blocks_next = rows / kWgRows;
@@ -578,27 +600,33 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const float (&t
 // Loop-invariant state of the K loop. All members but the DMA and weight
 // lane offsets are wave-uniform (scalar registers).
 struct KLoop {
-  __amdgpu_buffer_rsrc_t nib, scl;   // this wave's tile of the nibble and scale planes
+  __amdgpu_buffer_rsrc_t nib[kWaveTiles], scl[kWaveTiles];  // this wave's tiles of the nibble and scale planes
   __amdgpu_buffer_rsrc_t codes, scales;  // the activation operand buffers
-  u32x4 tail_v;                      // the partial last 4-block group (B % 4 blocks), if any
-  uint32_t tail_s;
-  int B, nsteps, nfull4, last_full, wave, lane, G;
-  bool tile_ok;
-  int vl, vs;                        // weight lane offsets: nibbles lane * 16, scales (lane % 16) * 4
+  int B, nsteps, nfull4, last_group, wave, lane, G;
+  bool wave_ok;                      // the wave's first tile exists
+  int vl, vl_tail, vs;               // weight lane offsets: nibbles lane * 16 (full group) or lane * (B % 4) * 4
+                                     // (the compact last group), scales (lane % 16) * 4
   int voff[kCodeDma];                // DMA source of this lane's code pieces in step 0
   int soff;                          // DMA source of this lane's scale dword in step 0
 };
 
-// Weights of step q (4-block groups 2q, 2q+1, clamped to the last full group:
+// Weights of step q (4-block groups 2q, 2q+1, clamped to the last group:
 // loads past the end are issued anyway so that every step has the same
-// instruction count, and their data is never used).
+// instruction count, and their data is never used). The compact last group
+// (B % 4 blocks) is read with its own lane offset; the 16 bytes a lane loads
+// there end at most 772 bytes into the group, inside the tile or the plane
+// slack, and the dwords past the group's blocks are never used.
 __device__ __forceinline__ WStep load_wstep(const KLoop& k, int q) {
-  const int g0 = min(2 * q, k.last_full), g1 = min(2 * q + 1, k.last_full);
+  const int g0 = min(2 * q, k.last_group), g1 = min(2 * q + 1, k.last_group);
+  const int o0 = g0 < k.nfull4 ? k.vl : k.vl_tail, o1 = g1 < k.nfull4 ? k.vl : k.vl_tail;
   WStep w;
-  w.v0 = __builtin_amdgcn_raw_buffer_load_b128(k.nib, k.vl, g0 * 1024, 0);
-  w.s0 = __builtin_amdgcn_raw_buffer_load_b32(k.scl, k.vs, g0 * 64, 0);
-  w.v1 = __builtin_amdgcn_raw_buffer_load_b128(k.nib, k.vl, g1 * 1024, 0);
-  w.s1 = __builtin_amdgcn_raw_buffer_load_b32(k.scl, k.vs, g1 * 64, 0);
+#pragma unroll
+  for (int t = 0; t < kWaveTiles; ++t) {
+    w.v0[t] = __builtin_amdgcn_raw_buffer_load_b128(k.nib[t], o0, g0 * 1024, 0);
+    w.s0[t] = __builtin_amdgcn_raw_buffer_load_b32(k.scl[t], k.vs, g0 * 64, 0);
+    w.v1[t] = __builtin_amdgcn_raw_buffer_load_b128(k.nib[t], o1, g1 * 1024, 0);
+    w.s1[t] = __builtin_amdgcn_raw_buffer_load_b32(k.scl[t], k.vs, g1 * 64, 0);
+  }
   return w;
 }
 
@@ -615,22 +643,17 @@ __device__ __forceinline__ void issue_dma(const KLoop& k, int q_raw, char* codes
 
 // Compute of step q (q < nsteps).
 template <bool RESIDUAL, int NTG, bool FAST>
-__device__ __forceinline__ void step_update(const KLoop& k, float (&tot)[kNtg][2], const char* codes,
-                                            const float* scl, const WStep& w, const int q) {
+__device__ __forceinline__ void step_update(const KLoop& k, Acc& tot, const char* codes, const float* scl,
+                                            const WStep& w, const int q) {
   const float2* s2 = reinterpret_cast<const float2*>(scl);
   if (8 * q + 8 <= k.B) {
     group_update<RESIDUAL, NTG, FAST>(tot, codes, s2, w.v0, w.s0, 0, 4, k.lane, k.G);
     group_update<RESIDUAL, NTG, FAST>(tot, codes, s2, w.v1, w.s1, 4, 4, k.lane, k.G);
   } else {
-    // Last step: groups 2q and 2q+1, each full, partial (the tail) or absent.
-    const int a0 = 2 * q, a1 = 2 * q + 1;
-    const int nb0 = min(4, k.B - 4 * a0), nb1 = min(4, k.B - 4 * a1);
-    const bool full0 = a0 < k.nfull4, full1 = a1 < k.nfull4;
-    group_update<RESIDUAL, NTG, FAST>(tot, codes, s2, full0 ? w.v0 : k.tail_v, full0 ? w.s0 : k.tail_s, 0, nb0,
-                                      k.lane, k.G);
-    if (nb1 > 0)
-      group_update<RESIDUAL, NTG, FAST>(tot, codes, s2, full1 ? w.v1 : k.tail_v, full1 ? w.s1 : k.tail_s, 4, nb1,
-                                        k.lane, k.G);
+    // Last step: groups 2q and 2q+1, each full, partial or absent.
+    const int nb0 = min(4, k.B - 8 * q), nb1 = min(4, k.B - 8 * q - 4);
+    group_update<RESIDUAL, NTG, FAST>(tot, codes, s2, w.v0, w.s0, 0, nb0, k.lane, k.G);
+    if (nb1 > 0) group_update<RESIDUAL, NTG, FAST>(tot, codes, s2, w.v1, w.s1, 4, nb1, k.lane, k.G);
   }
 }
 
@@ -641,8 +664,8 @@ __device__ __forceinline__ void step_update(const KLoop& k, float (&tot)[kNtg][2
 // After D(q) come W(q+1), D(q+1), W(q+2) = kWaitVm instructions, and W(q)
 // was issued before D(q), so the wait also covers the weights of step q.
 template <bool RESIDUAL, int NTG, bool FAST>
-__device__ __forceinline__ void k_loop(const KLoop& k, float (&tot)[kNtg][2], char* c0, char* c1, char* c2, float* s0,
-                                       float* s1, float* s2) {
+__device__ __forceinline__ void k_loop(const KLoop& k, Acc& tot, char* c0, char* c1, char* c2, float* s0, float* s1,
+                                       float* s2) {
   WStep w0, w1, w2;
   __builtin_amdgcn_sched_barrier(0);
   w0 = load_wstep(k, 0);
@@ -664,7 +687,7 @@ __device__ __forceinline__ void k_loop(const KLoop& k, float (&tot)[kNtg][2], ch
     __builtin_amdgcn_sched_barrier(0);                                                               \
     issue_dma(k, q + 2, NCODES, NSCL);                                                               \
     __builtin_amdgcn_sched_barrier(0);                                                               \
-    if (k.tile_ok && q < k.nsteps) step_update<RESIDUAL, NTG, FAST>(k, tot, CODES, SCL, SLOT, q);    \
+    if (k.wave_ok && q < k.nsteps) step_update<RESIDUAL, NTG, FAST>(k, tot, CODES, SCL, SLOT, q);    \
     __builtin_amdgcn_sched_barrier(0);                                                               \
     SLOT = load_wstep(k, q + 3);                                                                     \
     __builtin_amdgcn_sched_barrier(0);                                                               \
@@ -712,8 +735,7 @@ __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
   __syncthreads();
 
   const int rows = (int)a.w.rows, B = (int)a.w.blocks;
-  const int tile = blockIdx.x * kWaves + wave;
-  const int row = tile * kTileRows + nl;
+  const int tile0 = (blockIdx.x * kWaves + wave) * kWaveTiles;
   const int n_tg = (count + 7) >> 3;
   const int nq4 = (B + 3) >> 2;
 
@@ -721,36 +743,37 @@ __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
   k.B = B;
   k.nsteps = (B + kStep - 1) / kStep;
   k.nfull4 = B >> 2;
-  k.last_full = k.nfull4 > 0 ? k.nfull4 - 1 : 0;
+  k.last_group = nq4 - 1;
   k.wave = wave;
   k.lane = lane;
   k.G = G;
-  k.tile_ok = tile < (int)a.w.tiles;
-  // Waves past the last tile stream tile 0 and discard it.
-  const int safe_tile = k.tile_ok ? tile : 0;
-  const uint8_t* nib = a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)safe_tile * 256 * B;
-  const uint8_t* scl = a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)safe_tile * 64 * nq4;
-  k.nib = buffer_rsrc(nib);
-  k.scl = buffer_rsrc(scl);
+  k.wave_ok = tile0 < (int)a.w.tiles;
   k.vl = lane * 16;
+  k.vl_tail = lane * (B & 3) * 4;
   k.vs = nl * 4;
-  {
-    // The partial last group (B % 4 = rem blocks): dwords at lane * rem * 4 of
-    // the compact group, and the row's padded scale dword. Reads past the
-    // group stay inside the plane slack.
-    const int rem = (B & 3) > 0 ? (B & 3) : 1;
-    const uint32_t* gw = reinterpret_cast<const uint32_t*>(nib + (size_t)k.nfull4 * 1024 + lane * rem * 4);
-    k.tail_v = u32x4{gw[0], gw[1], gw[2], 0u};
-    k.tail_s = *reinterpret_cast<const uint32_t*>(scl + (size_t)k.nfull4 * 64 + nl * 4);
-  }
-  const bool fast = !k.tile_ok || a.w.fast[(size_t)expert * a.w.tiles + tile] != 0;
-
-  float b0 = 0.0f;
-  if (a.bias != nullptr && k.tile_ok && row < rows) b0 = a.bias[(size_t)expert * a.bias_expert_stride + row];
-  b0 = b0 + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
-  float tot[kNtg][2];
+  bool fast = true;
+  float b0[kWaveTiles];
 #pragma unroll
-  for (int tg = 0; tg < kNtg; ++tg) { tot[tg][0] = b0; tot[tg][1] = b0; }
+  for (int t = 0; t < kWaveTiles; ++t) {
+    const int tile = tile0 + t;
+    const bool ok = tile < (int)a.w.tiles;
+    // Tiles past the end stream tile 0 and discard it.
+    const int safe_tile = ok ? tile : 0;
+    const uint8_t* nib = a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)safe_tile * 256 * B;
+    const uint8_t* scl = a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)safe_tile * 64 * nq4;
+    k.nib[t] = buffer_rsrc(nib);
+    k.scl[t] = buffer_rsrc(scl);
+    fast = fast && (!ok || a.w.fast[(size_t)expert * a.w.tiles + tile] != 0);
+    const int row = tile * kTileRows + nl;
+    float bias = 0.0f;
+    if (a.bias != nullptr && ok && row < rows) bias = a.bias[(size_t)expert * a.bias_expert_stride + row];
+    b0[t] = bias + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
+  }
+  Acc tot;
+#pragma unroll
+  for (int t = 0; t < kWaveTiles; ++t)
+#pragma unroll
+    for (int tg = 0; tg < kNtg; ++tg) { tot[t][tg][0] = b0[t]; tot[t][tg][1] = b0[t]; }
 
   // DMA lane map, the same for every step. Code piece i of this wave fills
   // slot bytes c * 16 with c = (i * kWaves + wave) * 64 + lane, i.e. block j,
@@ -788,8 +811,7 @@ __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
   // work-group ends.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  gemm_epilogue<MODE, kNtg>(a, tot, n_tg, count, start, route_base, row, k.tile_ok,
-                            reinterpret_cast<float*>(s_codes0));
+  gemm_epilogue<MODE>(a, tot, n_tg, count, start, route_base, tile0, reinterpret_cast<float*>(s_codes0));
 }
 
 // Exactness flag per (expert, tile): 1 when every E8M0 byte of the tile's
@@ -1017,7 +1039,7 @@ hipError_t launch_dispatch(const DispatchArgs& a, hipStream_t stream) {
 }
 
 hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream) {
-  const dim3 grid((unsigned)((a.w.tiles + kWaves - 1) / kWaves), (unsigned)grid_work);
+  const dim3 grid((unsigned)((a.w.tiles + kWgTiles - 1) / kWgTiles), (unsigned)grid_work);
   const dim3 block(kGemmThreads);
   if (a.residual) {
     switch (mode) {
