@@ -630,10 +630,11 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   ra.weights = weights;
   ra.act = act1;
   ra.err = ctx->err;
-  {
-    OpScope sc(ctx, GOSSMX_OP_ROUTER_ROUTING);
-    HIP_TRY(launch_route(ra, ctx->stream), "route launch");
-  }
+  // Batches whose logits fit one work-group take the fused selection +
+  // dispatch kernel; the router projection (when the logits are not
+  // injected) stays a per-row kernel in front of it.
+  const bool fused = m * (E + 1) <= (size_t)kSelectLds && R <= (size_t)kSelectMaxRoutes && K <= (size_t)kSelectTopK;
+  ra.select = fused ? 0 : 1;
   DispatchArgs da{};
   da.selected = selected;
   da.routes = (int)R;
@@ -644,9 +645,18 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   da.route_slot = static_cast<int*>(ctx->route_slot.p);
   da.work = work;
   da.n_work = n_work;
+  if (!fused || injected == nullptr) {
+    OpScope sc(ctx, GOSSMX_OP_ROUTER_ROUTING);
+    HIP_TRY(launch_route(ra, ctx->stream), "route launch");
+  }
   {
+    // In the fused path this stage also holds top-k, softmax and (with
+    // injected logits) the gate_up input quantization.
     OpScope sc(ctx, GOSSMX_OP_DISPATCH);
-    HIP_TRY(launch_dispatch(da, ctx->stream), "dispatch launch");
+    if (fused)
+      HIP_TRY(launch_select_dispatch(ra, da, injected != nullptr ? 1 : 0, ctx->stream), "select/dispatch launch");
+    else
+      HIP_TRY(launch_dispatch(da, ctx->stream), "dispatch launch");
   }
   GemmArgs g{};
   g.w = L->gate_up->t;

@@ -93,6 +93,7 @@ struct RouteArgs {
   float* weights;           // [m][top_k]
   ActBuffers act;           // gate_up input per token
   int* err;
+  int select;               // 1: top-k and softmax per row here; 0: logits only (select_dispatch follows)
 };
 
 struct DispatchArgs {
@@ -105,9 +106,20 @@ struct DispatchArgs {
   int* n_work;
 };
 
+// Batches whose logits fit one work-group's LDS take the fused selection +
+// dispatch kernel (one launch; no global round trip between the two).
+constexpr int kSelectLds = 8448;        // m * (experts + 1) floats
+constexpr int kSelectMaxRoutes = 2048;  // m * top_k
+constexpr int kSelectTopK = 4;          // top_k (GPT-OSS routes to 4 experts)
+
 // Launchers (gossmx_kernels.hip). All are asynchronous on `stream`.
 hipError_t launch_route(const RouteArgs& a, hipStream_t stream);
 hipError_t launch_dispatch(const DispatchArgs& a, hipStream_t stream);
+// Work-group 0: top-k, softmax and dispatch of all rows from r.injected (bf16
+// rounded here) or from the logits r.logits computed by launch_route with
+// select = 0. quantize = 1 adds the gate_up input quantization work-groups
+// (when no launch_route ran).
+hipError_t launch_select_dispatch(const RouteArgs& r, const DispatchArgs& d, int quantize, hipStream_t stream);
 hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream);
 hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream);
 

@@ -62,7 +62,8 @@ __constant__ uint64_t kExp2Tab[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-__device__ float expf_glibc(float x) {
+// `tab` is kExp2Tab or a copy of it (e.g. in LDS).
+__device__ float expf_glibc(float x, const uint64_t* tab = kExp2Tab) {
   const uint32_t ux = __float_as_uint(x);
   const uint32_t abstop = (ux >> 20) & 0x7ffu;
   if (abstop >= 0x42bu) {  // |x| >= 88 (top 12 bits of 88.0f), inf or NaN
@@ -81,7 +82,7 @@ __device__ float expf_glibc(float x) {
   const uint64_t ki = (uint64_t)__double_as_longlong(kd);
   kd -= shift;
   const double r = fma(inv_ln2_n, xd, -kd);
-  const uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+  const uint64_t t = tab[ki % 32] + (ki << 47);
   const double s = __longlong_as_double((long long)t);
   const double z = fma(c0, r, c1);
   const double r2 = r * r;
@@ -152,10 +153,11 @@ __device__ __forceinline__ void residual_q8_store(float v, int l32, size_t row, 
 }
 
 // ---------------------------------------------------------------------------
-// Router projection, top-k and routing softmax (blockIdx.y == 0), and the
-// gate_up input quantization (blockIdx.y >= 1: 8 blocks of 32 values per
-// work-group, one per half wave), for row blockIdx.x (moe_batch routing
-// loop, cpu_runner.rs:2808-2854; quantize_residual_q8 of the row,
+// Router projection, top-k and routing softmax (blockIdx.y == 0; with
+// select = 0 only the bf16-rounded logits), and the gate_up input
+// quantization (blockIdx.y >= 1: 8 blocks of 32 values per work-group, one
+// per half wave), for row blockIdx.x (moe_batch routing loop,
+// cpu_runner.rs:2808-2854; quantize_residual_q8 of the row,
 // cpu_runner.rs:3224-3231).
 
 __device__ __forceinline__ bool route_better(float va, int ia, float vb, int ib) {
@@ -163,6 +165,53 @@ __device__ __forceinline__ bool route_better(float va, int ia, float vb, int ib)
 }
 
 constexpr int kRouteQuantBlocks = 8;  // quantized blocks per work-group (256 threads)
+
+// stable_top_k (cpu_runner.rs:3768-3778) and the routing softmax in rank
+// order (:3784-3795, then bf16 :2840-2843) of one row, by one wave. `lg` holds
+// the row's bf16-rounded logits and `s_k` is kMaxTopK ints of LDS owned by
+// the wave. Each lane owns experts lane and lane + 64; K rounds of a wave
+// argmax. NaN logits (already flagged as an error) rank as -inf so that every
+// round still returns a valid expert index. Writes sel[0..K) and w[0..K), and
+// sel_copy[0..K) when it is not null.
+__device__ __forceinline__ void select_row(const float* lg, int E, int K, int lane, int* s_k, int* sel, float* w,
+                                           int* sel_copy) {
+  bool taken0 = false, taken1 = false;
+  float v0 = lane < E ? lg[lane] : -INFINITY;
+  float v1 = lane + 64 < E ? lg[lane + 64] : -INFINITY;
+  if (isnan(v0)) v0 = -INFINITY;
+  if (isnan(v1)) v1 = -INFINITY;
+  for (int k = 0; k < K; ++k) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    if (lane < E && !taken0) { bv = v0; bi = lane; }
+    if (lane + 64 < E && !taken1 && route_better(v1, lane + 64, bv, bi)) { bv = v1; bi = lane + 64; }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      if (route_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    if (bi < 0 || bi >= E) bi = 0;
+    if (bi == lane) taken0 = true;
+    if (bi == lane + 64) taken1 = true;
+    if (lane == 0) s_k[k] = bi;
+  }
+  if (lane == 0) {
+    float mx = -INFINITY;
+    for (int k = 0; k < K; ++k) mx = fmaxf(mx, lg[s_k[k]]);
+    float ex[kMaxTopK];
+    float sum = 0.0f;
+    for (int k = 0; k < K; ++k) {
+      ex[k] = expf_glibc(lg[s_k[k]] - mx);
+      sum = sum + ex[k];
+    }
+    for (int k = 0; k < K; ++k) {
+      sel[k] = s_k[k];
+      w[k] = bf16r(ex[k] / sum);
+      if (sel_copy) sel_copy[k] = s_k[k];
+    }
+  }
+}
 
 __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   const int r = blockIdx.x;
@@ -209,49 +258,8 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
     if (a.logits) a.logits[(size_t)r * E + e] = v;
   }
 
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    // Each lane owns experts lane and lane + 64; K rounds of a wave argmax.
-    // NaN logits (already flagged as an error) rank as -inf so that every
-    // round still returns a valid expert index.
-    bool taken0 = false, taken1 = false;
-    float v0 = lane < E ? s_logit[lane] : -INFINITY;
-    float v1 = lane + 64 < E ? s_logit[lane + 64] : -INFINITY;
-    if (isnan(v0)) v0 = -INFINITY;
-    if (isnan(v1)) v1 = -INFINITY;
-    for (int k = 0; k < K; ++k) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
-      if (lane < E && !taken0) { bv = v0; bi = lane; }
-      if (lane + 64 < E && !taken1 && route_better(v1, lane + 64, bv, bi)) { bv = v1; bi = lane + 64; }
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) {
-        const float ov = __shfl_xor(bv, o);
-        const int oi = __shfl_xor(bi, o);
-        if (route_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-      }
-      if (bi < 0 || bi >= E) bi = 0;
-      if (bi == lane) taken0 = true;
-      if (bi == lane + 64) taken1 = true;
-      if (lane == 0) s_sel[k] = bi;
-    }
-    if (lane == 0) {
-      // softmax over the selected logits in rank order (cpu_runner.rs:3784-3795),
-      // then bf16 (:2840-2843).
-      float mx = -INFINITY;
-      for (int k = 0; k < K; ++k) mx = fmaxf(mx, s_logit[s_sel[k]]);
-      float ex[kMaxTopK];
-      float sum = 0.0f;
-      for (int k = 0; k < K; ++k) {
-        ex[k] = expf_glibc(s_logit[s_sel[k]] - mx);
-        sum = sum + ex[k];
-      }
-      for (int k = 0; k < K; ++k) {
-        a.selected[(size_t)r * K + k] = s_sel[k];
-        a.weights[(size_t)r * K + k] = bf16r(ex[k] / sum);
-      }
-    }
-  }
+  if (a.select && threadIdx.x < 64)
+    select_row(s_logit, E, K, threadIdx.x, s_sel, a.selected + (size_t)r * K, a.weights + (size_t)r * K, nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -264,7 +272,8 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
 // first (expert order), then the partial last chunks by descending size
 // (ties by expert), so the heaviest work items start first.
 
-__global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
+// `sel` is the selected experts in route order (global memory or LDS).
+__device__ __forceinline__ void dispatch_body(const DispatchArgs& a, const int* sel) {
   const int E = a.experts, R = a.routes;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   __shared__ int s_tot[kMaxExperts];
@@ -275,7 +284,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
   __shared__ int s_wcnt[16][kMaxExperts];
   for (int e = tid; e < kMaxExperts; e += 1024) { s_tot[e] = 0; s_run[e] = 0; }
   __syncthreads();
-  for (int i = tid; i < R; i += 1024) atomicAdd(&s_tot[a.selected[i]], 1);
+  for (int i = tid; i < R; i += 1024) atomicAdd(&s_tot[sel[i]], 1);
   __syncthreads();
   // Waves 0 and 1: lane = expert (kMaxExperts = 128). Inclusive scans of the
   // row counts and of the full-chunk counts, then the carry of wave 0.
@@ -326,7 +335,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
   const unsigned long long lt = (1ull << lane) - 1ull;
   for (int base = 0; base < R; base += 1024) {
     const int i = base + tid;
-    const int e = i < R ? a.selected[i] : -1;
+    const int e = i < R ? sel[i] : -1;
     for (int ee = lane; ee < E; ee += 64) s_wcnt[wave][ee] = 0;
     int rank = 0;
     unsigned long long pending = __ballot(e >= 0);
@@ -353,6 +362,155 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
     }
     __syncthreads();
   }
+}
+
+__global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) { dispatch_body(a, a.selected); }
+
+// stable_top_k order (route_better) as one unsigned 64-bit key per (logit,
+// expert) for the fused kernel: NaN ranks as -inf and -0.0 as +0.0 (they
+// compare equal as floats), the float bits are mapped to an order-preserving
+// unsigned word, and the low word is ~e so that equal logits favour the lower
+// index. A larger key is a better route; key 0 is below every real key.
+__device__ __forceinline__ uint64_t route_key(float v, int e) {
+  v = isnan(v) ? -INFINITY : v;
+  v = v + 0.0f;  // -0.0 -> +0.0
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)u << 32) | (uint64_t)(~(uint32_t)e);
+}
+__device__ __forceinline__ int route_key_expert(uint64_t key) { return key == 0 ? 0 : (int)(~(uint32_t)key); }
+
+// One step of a running top-K list of keys, sorted best first (slots k >= K
+// stay 0). A key enters at the first slot it beats; the slots it beats form a
+// suffix of the sorted list, so after all experts the list equals K rounds of
+// argmax (the order is strict: keys are distinct). Branch-free.
+template <int KMAX>
+__device__ __forceinline__ void topk_insert(uint64_t (&keys)[KMAX], const uint64_t key, const int K) {
+  bool beats[KMAX];
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) beats[k] = (k < K) & (key > keys[k]);
+#pragma unroll
+  for (int k = KMAX - 1; k >= 1; --k) keys[k] = beats[k - 1] ? keys[k - 1] : (beats[k] ? key : keys[k]);
+  keys[0] = beats[0] ? key : keys[0];
+}
+
+// stable_top_k and the routing softmax of one row by T lanes (T a power of two
+// dividing 64 and >= K, consecutive lanes): lane j scans experts j, j + T,
+// ..., then a butterfly over the T lanes merges the lists (the top K of a
+// strictly ordered set is unique, so the merged list is the sequential one).
+// Lanes j < K finish rank j of the softmax. `lg`: the row's logits in LDS;
+// `tab`: kExp2Tab. Every lane of the wave must call this (the shuffles);
+// has_row = false lanes carry empty lists and write nothing.
+template <int KMAX>
+__device__ __forceinline__ void select_row_lanes(const float* lg, bool has_row, int j, int T, int E, int K, int* sel,
+                                                 float* w, int* sel_copy, const uint64_t* tab) {
+  uint64_t keys[KMAX];
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) keys[k] = 0;
+  // Loops stay rolled: this code runs once per launch from a cold
+  // instruction cache, so its size costs more than its instruction count.
+  if (has_row) {
+#pragma unroll 1
+    for (int e = j; e < E; e += T) topk_insert<KMAX>(keys, route_key(lg[e], e), K);
+  }
+#pragma unroll 1
+  for (int o = 1; o < T; o <<= 1) {
+    uint64_t pk[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      const uint32_t lo = __shfl_xor((uint32_t)keys[k], o);
+      const uint32_t hi = __shfl_xor((uint32_t)(keys[k] >> 32), o);
+      pk[k] = ((uint64_t)hi << 32) | lo;
+    }
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) topk_insert<KMAX>(keys, pk[k], K);
+  }
+  // Softmax over the selected logits in rank order (select_row's float
+  // operations): lane j < K of the row holds rank j. Every lane computes the
+  // same max (fmaxf folded in rank order); lane j computes its exponential;
+  // the sum is folded in rank order from 0.0f by shuffles and broadcast.
+  const int rank = j < K ? j : 0;
+  uint64_t mine = keys[0];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    if (k < K) {
+      int ek = route_key_expert(keys[k]);
+      if (ek < 0 || ek >= E) ek = 0;
+      mx = fmaxf(mx, lg[ek]);
+    }
+    mine = k == rank ? keys[k] : mine;
+  }
+  int my_e = route_key_expert(mine);
+  if (my_e < 0 || my_e >= E) my_e = 0;
+  const float ex = expf_glibc(lg[my_e] - mx, tab);
+  const int row_lane0 = (threadIdx.x & 63) - j;
+  float sum = 0.0f;
+#pragma unroll 1
+  for (int k = 0; k < K; ++k) sum = sum + __shfl(ex, row_lane0 + k);
+  if (has_row && j < K) {
+    sel[j] = my_e;
+    w[j] = bf16r(ex / sum);
+    sel_copy[j] = my_e;
+  }
+}
+
+// Fused selection and dispatch for batches whose logits fit one work-group
+// (m * (experts + 1) <= kSelectLds floats): work-group 0 reads every row's
+// logits into LDS (injected ones are bf16-rounded here, as route_kernel does;
+// rows padded to experts + 1 floats so that lanes on consecutive rows hit
+// different banks), selects per row with one lane per row, and runs the
+// dispatch on the LDS copy of the selections. Work-groups 1.. quantize the
+// gate_up input when no route_kernel ran: kSelectQuantBlocks blocks of 32
+// values each, one per half wave.
+constexpr int kSelectQuantBlocks = 32;
+
+__global__ __launch_bounds__(1024) void select_dispatch_kernel(RouteArgs r, DispatchArgs d) {
+  const int tid = threadIdx.x;
+  if (blockIdx.x > 0) {
+    const int blocks = r.hidden / kBlock;
+    const int g = (blockIdx.x - 1) * kSelectQuantBlocks + (tid >> 5);
+    if (g < r.m * blocks) {  // uniform per half wave
+      const int row = g / blocks, b = g % blocks;
+      const float v = bf16_to_f32(r.x[(size_t)row * r.hidden + b * kBlock + (tid & 31)]);
+      if (!isfinite(v)) atomicOr(r.err, kErrNonFiniteInput);
+      residual_q8_store(v, tid & 31, (size_t)row, blocks, b, r.act);
+    }
+    return;
+  }
+  const int E = r.experts, K = r.top_k, M = r.m, stride = E + 1;
+  __shared__ float s_lg[kSelectLds];
+  __shared__ int s_sel[kSelectMaxRoutes];
+  __shared__ uint64_t s_tab[32];
+  if (tid < 32) s_tab[tid] = kExp2Tab[tid];
+  for (int i = tid; i < M * E; i += 1024) {
+    float v;
+    if (r.injected != nullptr) {
+      v = bf16r(r.injected[i]);
+      if (r.logits) r.logits[i] = v;
+    } else {
+      v = r.logits[i];
+    }
+    if (!isfinite(v)) atomicOr(r.err, kErrNonFiniteLogits);
+    s_lg[(i / E) * stride + i % E] = v;
+  }
+  __syncthreads();
+  // T lanes per row: the largest power of two <= 64 with T * M <= 1024 and T
+  // <= E / 4 (a few experts per lane), but at least top_k (<= 4).
+  int T = 64;
+  while (T > 1 && (T * M > 1024 || 4 * T > E)) T >>= 1;
+  while (T < K) T <<= 1;
+  const int rows_per_pass = 1024 / T;
+  for (int base = 0; base < M; base += rows_per_pass) {  // uniform
+    const int row = base + tid / T, j = tid % T;
+    const bool has_row = row < M;
+    const int rr = has_row ? row : 0;
+    float* const wr = r.weights + (size_t)rr * K;
+    int* const sr = r.selected + (size_t)rr * K;
+    select_row_lanes<kSelectTopK>(s_lg + rr * stride, has_row, j, T, E, K, sr, wr, s_sel + rr * K, s_tab);
+  }
+  __syncthreads();
+  dispatch_body(d, s_sel);
 }
 
 // ---------------------------------------------------------------------------
@@ -1035,6 +1193,16 @@ hipError_t launch_route(const RouteArgs& a, hipStream_t stream) {
 
 hipError_t launch_dispatch(const DispatchArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_select_dispatch(const RouteArgs& r, const DispatchArgs& d, int quantize, hipStream_t stream) {
+  if (r.m * (r.experts + 1) > kSelectLds || d.routes > kSelectMaxRoutes || r.top_k > kSelectTopK ||
+      r.experts > kMaxExperts)
+    return hipErrorInvalidValue;
+  const size_t qblocks = quantize ? (size_t)r.m * (r.hidden / kBlock) : 0;
+  const unsigned grid = 1u + (unsigned)((qblocks + kSelectQuantBlocks - 1) / kSelectQuantBlocks);
+  hipLaunchKernelGGL(select_dispatch_kernel, dim3(grid), dim3(1024), 0, stream, r, d);
   return hipGetLastError();
 }
 

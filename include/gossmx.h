@@ -185,7 +185,11 @@ typedef struct gossmx_moe_io {
 int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* layer, const gossmx_moe_io* io);
 
 /* Profiling with hipEvents on the context stream, in the reference's operation
- * vocabulary (CpuProfileOperation, cpu_profile.rs:30-51). */
+ * vocabulary (CpuProfileOperation, cpu_profile.rs:30-51). Batches with
+ * m * (experts + 1) <= 8448, m * top_k <= 2048 and top_k <= 4 run top-k, softmax and the
+ * grouping in one kernel, recorded as GOSSMX_OP_DISPATCH; GOSSMX_OP_ROUTER_ROUTING
+ * then holds the router projection and input quantization only, and has no
+ * launch when the logits are injected. */
 enum {
   GOSSMX_OP_ROUTER_ROUTING = 0,     /* RouterProjection + Routing + ResidualQ8Preparation */
   GOSSMX_OP_DISPATCH = 1,           /* stable_group_routes + bucket gather */

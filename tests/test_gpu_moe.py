@@ -109,6 +109,68 @@ def test_prefill_2048_rows_match_and_group(layer20b):
                 == np.ascontiguousarray(want[key]).view(np.uint32)).all(), key
 
 
+@pytest.mark.parametrize("experts,top_k,m,inject", [
+    (8, 6, 5, False),     # top_k > 4: per-row route kernel + dispatch kernel
+    (8, 6, 5, True),
+    (128, 4, 3, False),   # 128 experts, fused selection + dispatch
+    (128, 4, 3, True),
+    (128, 4, 80, True),   # m * (experts + 1) > 8448: route + dispatch kernels
+    (32, 4, 256, True),   # largest fused batch at 32 experts (256 * 33 = 8448)
+    (32, 4, 257, True),   # first batch past it
+    (32, 4, 257, False),
+])
+def test_routing_paths_bit_exact(ctx, experts, top_k, m, inject):
+    """Both routing implementations (one work-group selecting and grouping
+    every row, or a work-group per row then a grouping kernel) against the
+    oracle, with coarse injected logits so that ties occur."""
+    host = O.synthetic_layer(31, 0, experts=experts, hidden=64, intermediate=64, top_k=top_k)
+    x = O.gen_hidden(31, 300 + m, m, 64)
+    logits = None
+    if inject:
+        rng = np.random.default_rng(m)
+        logits = (np.round(rng.standard_normal((m, experts)) * 4.0) / 4.0).astype(np.float32)
+    want = O.moe_batch(host, x, injected_logits=logits)
+    assert want["status"] == O.OK
+    layer = gpu_layer(ctx, host)
+    assert_moe_equal(layer.forward(x, injected_logits=logits), want)
+    close(layer)
+
+
+@pytest.fixture(scope="module")
+def layer120b(ctx):
+    host = O.synthetic_layer(120, 0, experts=128)
+    layer = gpu_layer(ctx, host)
+    yield host, layer
+    close(layer)
+
+
+def test_120b_shape_decode_bit_exact(layer120b):
+    """configs[4] layer shape (128 experts, H = I = 2880), router computed."""
+    host, layer = layer120b
+    x = O.gen_hidden(120, 7, 2, 2880)
+    want = O.moe_batch(host, x)
+    assert want["status"] == O.OK
+    assert_moe_equal(layer.forward(x), want)
+
+
+def test_120b_shape_zipf_batch256_rows_match(layer120b):
+    """configs[4] decode: batch 256 with injected Zipf(1.2) logits over 128
+    experts; the oracle checks a sample of rows, and the grouped order is
+    the stable sort of all routes by expert."""
+    host, layer = layer120b
+    rng = np.random.default_rng(256)
+    x = synth.hidden_rows(rng, 256)
+    logits = synth.zipf_logits(rng, 256, 128, 4, 1.2)
+    got = layer.forward(x, injected_logits=logits)
+    rows = [0, 101, 255]
+    want = O.moe_batch(host, x[rows], injected_logits=logits[rows])
+    for key in ("router_logits", "routing_weights", "output", "selected"):
+        assert (np.ascontiguousarray(got[key][rows]).view(np.uint32)
+                == np.ascontiguousarray(want[key]).view(np.uint32)).all(), key
+    sel = got["selected"].ravel()
+    assert (got["route_order"] == np.argsort(sel, kind="stable")).all()
+
+
 def test_all_experts_selected(ctx):
     host = O.synthetic_layer(5, 0, experts=4, hidden=64, intermediate=64, top_k=4)
     x = O.gen_hidden(5, 1, 9, 64)
