@@ -4,15 +4,24 @@
 Default workload: GPT-OSS-20B-shape MoE decode at
 batch 64 over all 24 layers' expert weights resident in HBM (~10 GB MXFP4),
 32 experts, top-4, router logits injected so expert popularity follows
-Zipf(1.1). A step is one pass of the 64-token batch through the 24 MoE layers;
-`value` is layer-tokens/s (tokens through one MoE layer per second, the unit of
+Zipf(1.1). A step is one pass of the batch through every layer; `value` is
+layer-tokens/s (tokens through one MoE layer per second, the unit of
 BASELINE.md's CPU figures). Inputs and weights are resident before timing.
+
+`--config` selects the other measured workloads of the same metric:
+  0  decode of 1 token, router computed, rotating over 12 layer copies
+     (5 GB of weights, far beyond the 256 MB Infinity Cache);
+  2  prefill of 2048 tokens through one layer, near-uniform top-4
+     (MFMA roofline: 407.69 GFLOP per layer);
+  4  GPT-OSS-120B shape: 128 experts, all 36 layers resident (61 GB),
+     decode batch 256 with Zipf(1.2) routing.
 
 Prints one JSON line. The per-kernel roofline uses the library's hipEvent
 profiler on the stream the kernels run on; `cpu_baseline` times the oracle's
 faithful Auto lane (x8 AVX2 GEMV for single-row buckets, scalar matmul for
-multi-row buckets, one thread, as moe_batch runs it) on layer 0 of the same
-batch after checking that the GPU's layer-0 output is bit-identical to it.
+multi-row buckets, one thread, as moe_batch runs it) on a bounded sample of
+layer 0 of the same batch after checking that the GPU's rows are
+bit-identical to it.
 """
 from __future__ import annotations
 
@@ -32,9 +41,31 @@ import synth  # noqa: E402
 
 METRIC = "MoE-layer tokens/s + achieved HBM GB/s (% of peak), 20B shape bs=1/64"
 HBM_PEAK_GBPS = 8000.0
-GATE_UP_BYTES = 5760 * 90 * 17   # 8,812,800 B per expert
-DOWN_BYTES = 2880 * 90 * 17      # 4,406,400 B per expert
+F16_MFMA_PEAK_TFLOPS = 2500.0     # dense f16 MFMA, the instruction the expert GEMM issues
+HIDDEN = INTER = 2880
+BLOCKS = HIDDEN // 32
+GATE_UP_BYTES = 2 * INTER * BLOCKS * 17   # 8,812,800 B per expert
+DOWN_BYTES = HIDDEN * BLOCKS * 17         # 4,406,400 B per expert
 SEED = 20251201
+
+CONFIGS = {
+    0: {"batch": 1, "layers": 12, "experts": 32, "routing": "router", "zipf": None, "roofline": "hbm",
+        "workload": "configs[0]: GPT-OSS-20B-shape MoE decode, 1 token, router computed, rotating over {layers} "
+                    "layer copies resident (weights far beyond the 256 MB Infinity Cache), top-4 of 32 experts",
+        "sample_rows": 1},
+    1: {"batch": 64, "layers": 24, "experts": 32, "routing": "zipf", "zipf": 1.1, "roofline": "hbm",
+        "workload": "configs[1]: GPT-OSS-20B-shape MoE decode, batch {batch}, all {layers} layers resident, "
+                    "Zipf({zipf}) injected routing, top-4 of 32 experts",
+        "sample_rows": 64},
+    2: {"batch": 2048, "layers": 1, "experts": 32, "routing": "uniform", "zipf": None, "roofline": "mfma",
+        "workload": "configs[2]: GPT-OSS-20B-shape MoE prefill, {batch} tokens, {layers} layer, near-uniform "
+                    "injected routing, top-4 of 32 experts",
+        "sample_rows": 32},
+    4: {"batch": 256, "layers": 36, "experts": 128, "routing": "zipf", "zipf": 1.2, "roofline": "hbm",
+        "workload": "configs[4]: GPT-OSS-120B-shape MoE decode, batch {batch}, all {layers} layers resident, "
+                    "Zipf({zipf}) injected routing, top-4 of 128 experts",
+        "sample_rows": 32},
+}
 
 
 def stable_topk_sets(logits: np.ndarray, k: int) -> np.ndarray:
@@ -43,53 +74,65 @@ def stable_topk_sets(logits: np.ndarray, k: int) -> np.ndarray:
     return order[:, :k]
 
 
-def build_workload(ctx, layers: int, experts: int, m: int, zipf_s: float, rng):
+def build_workload(ctx, cfg: dict, rng):
     import torch
 
     dev = torch.device("cuda", 0)
+    m, E = cfg["batch"], cfg["experts"]
     x = synth.hidden_rows(rng, m)
     x_dev = torch.from_numpy(x.view(np.int16)).to(dev)
     state = []
-    for layer in range(layers):
-        gu = G.Weights.generate(ctx, SEED, 16 * layer + 4, experts, 5760, 90)
-        dn = G.Weights.generate(ctx, SEED, 16 * layer + 5, experts, 2880, 90)
-        p = synth.dense_layer_params(np.random.default_rng(SEED + layer), experts)
-        moe = G.MoeLayer(ctx, experts, 2880, 2880, 4, p["router_weight"], p["router_bias"], gu, p["gate_up_bias"],
+    for layer in range(cfg["layers"]):
+        gu = G.Weights.generate(ctx, SEED, 16 * layer + 4, E, 2 * INTER, BLOCKS)
+        dn = G.Weights.generate(ctx, SEED, 16 * layer + 5, E, HIDDEN, BLOCKS)
+        p = synth.dense_layer_params(np.random.default_rng(SEED + layer), E)
+        moe = G.MoeLayer(ctx, E, HIDDEN, INTER, 4, p["router_weight"], p["router_bias"], gu, p["gate_up_bias"],
                          dn, p["down_bias"])
-        logits = synth.zipf_logits(rng, m, experts, 4, zipf_s)
+        if cfg["routing"] == "zipf":
+            logits = synth.zipf_logits(rng, m, E, 4, cfg["zipf"])
+        elif cfg["routing"] == "uniform":
+            logits = synth.uniform_logits(rng, m, E)
+        else:
+            logits = None
         state.append({
             "moe": moe, "gu": gu, "dn": dn, "params": p, "logits": logits,
-            "logits_dev": torch.from_numpy(logits).to(dev),
-            "out_dev": torch.empty((m, 2880), dtype=torch.float32, device=dev),
-            "touched": len(np.unique(stable_topk_sets(logits, 4))),
+            "logits_dev": None if logits is None else torch.from_numpy(logits).to(dev),
+            "out_dev": torch.empty((m, HIDDEN), dtype=torch.float32, device=dev),
+            "sel_dev": torch.empty((m, 4), dtype=torch.int32, device=dev),
         })
     return x, x_dev, state
 
 
-def cpu_baseline(x, st0, layer_out_gpu, threads: int):
-    """Oracle lanes on layer 0 of the batch; checks GPU bits first."""
+def cpu_baseline(cfg: dict, x, st0, layer_out_gpu, threads: int):
+    """Oracle lanes on a bounded sample of layer 0's rows; checks GPU bits first."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
     p = st0["params"]
-    host = O.MoeLayerHost(p["router_weight"], p["router_bias"], O.gen_mxfp4(SEED, 4, 32, 5760, 90),
-                          p["gate_up_bias"], O.gen_mxfp4(SEED, 5, 32, 2880, 90), p["down_bias"], 32, 2880, 2880, 4)
-    m = x.shape[0]
+    E = cfg["experts"]
+    host = O.MoeLayerHost(p["router_weight"], p["router_bias"], O.gen_mxfp4(SEED, 4, E, 2 * INTER, BLOCKS),
+                          p["gate_up_bias"], O.gen_mxfp4(SEED, 5, E, HIDDEN, BLOCKS), p["down_bias"], E, HIDDEN,
+                          INTER, 4)
+    n = min(cfg["sample_rows"], x.shape[0])
+    rows = np.linspace(0, x.shape[0] - 1, n).astype(np.int64) if n < x.shape[0] else np.arange(n)
+    xs = x[rows]
+    inj = None if st0["logits"] is None else st0["logits"][rows]
     t0 = time.perf_counter()
-    ref = O.moe_batch(host, x, injected_logits=st0["logits"], auto_lane=True, threads=1)
+    ref = O.moe_batch(host, xs, injected_logits=inj, auto_lane=True, threads=1)
     t_auto = time.perf_counter() - t0
     assert ref["status"] == O.OK
-    same = bool((ref["output"].view(np.uint32) == layer_out_gpu.view(np.uint32)).all())
+    same = bool((ref["output"].view(np.uint32) == layer_out_gpu[rows].view(np.uint32)).all())
     t0 = time.perf_counter()
-    ref_mt = O.moe_batch(host, x, injected_logits=st0["logits"], auto_lane=True, threads=threads)
+    ref_mt = O.moe_batch(host, xs, injected_logits=inj, auto_lane=True, threads=threads)
     t_all = time.perf_counter() - t0
     same_mt = bool((ref_mt["output"].view(np.uint32) == ref["output"].view(np.uint32)).all())
+    whole = "the whole batch" if n == x.shape[0] else f"{n} evenly spaced rows of the {x.shape[0]}-token batch"
     return {
-        "value": m / t_auto, "unit": "layer-tokens/s", "cores": 1, "kind": "port",
-        "sample": f"layer 0 of the batch ({m} tokens, {4 * m} routes), oracle Auto lane (x8 AVX2 GEMV at M=1, "
+        "value": n / t_auto, "unit": "layer-tokens/s", "cores": 1, "kind": "port",
+        "sample": f"layer 0, {whole} ({n} tokens, {4 * n} routes), oracle Auto lane (x8 AVX2 GEMV at M=1, "
                   f"scalar matmul for M>1 buckets, cpu_runner.rs:3409-3416), {t_auto:.1f} s",
         "gpu_bits_equal": same,
-        "all_cores": {"value": m / t_all, "cores": threads, "seconds": round(t_all, 2), "bits_equal": same_mt},
+        "all_cores": {"value": n / t_all, "cores": threads, "seconds": round(t_all, 2), "bits_equal": same_mt},
     }
 
 
@@ -98,9 +141,11 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--layers", type=int, default=24)
-    ap.add_argument("--batch", type=int, default=64)
-    ap.add_argument("--zipf", type=float, default=1.1)
+    ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS),
+                    help="BASELINE.json configs[] index of the workload (default 1)")
+    ap.add_argument("--layers", type=int, default=None, help="override the config's layer count")
+    ap.add_argument("--batch", type=int, default=None, help="override the config's batch")
+    ap.add_argument("--zipf", type=float, default=None, help="override the config's Zipf exponent")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", dest="graph", action="store_false",
                     help="time eager launches instead of the captured HIP graph of the step")
@@ -121,6 +166,11 @@ def main() -> int:
         print("bench.py measures the single-GPU MoE block only; multi-GPU runs are not part of this build "
               "(expert-parallel sharding is a design note, not an implementation)", file=sys.stderr)
         return 2
+    cfg = dict(CONFIGS[args.config])
+    for key in ("layers", "batch", "zipf"):
+        if getattr(args, key) is not None:
+            cfg[key] = getattr(args, key)
+    m, E, L = cfg["batch"], cfg["experts"], cfg["layers"]
 
     import torch
 
@@ -129,12 +179,12 @@ def main() -> int:
     rng = np.random.default_rng(SEED)
     ctx = G.Context(0, stream=stream.cuda_stream)
     ctx.selftest()
-    x, x_dev, state = build_workload(ctx, args.layers, 32, args.batch, args.zipf, rng)
+    x, x_dev, state = build_workload(ctx, cfg, rng)
     torch.cuda.synchronize()
 
     def step():
         for st in state:
-            st["moe"].forward_device(x_dev, args.batch, st["out_dev"], injected_logits=st["logits_dev"])
+            st["moe"].forward_device(x_dev, m, st["out_dev"], injected_logits=st["logits_dev"])
 
     def timed(fn) -> float:
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -149,6 +199,10 @@ def main() -> int:
 
     graph = None
     with torch.cuda.stream(stream):
+        # One untimed pass that also returns the selections (touched experts).
+        for st in state:
+            st["moe"].forward_device(x_dev, m, st["out_dev"], injected_logits=st["logits_dev"],
+                                     selected=st["sel_dev"])
         for _ in range(args.warmup):
             step()
         ctx.synchronize()
@@ -160,8 +214,8 @@ def main() -> int:
         prof = ctx.profile_read()
         ctx.profile(False)
         if args.graph:
-            # The same 24-layer step captured once as a HIP graph and replayed:
-            # identical kernels and arguments, without per-launch gaps.
+            # The same step captured once as a HIP graph and replayed: identical
+            # kernels and arguments, without per-launch gaps.
             ctx.capture_begin()
             step()
             graph = ctx.capture_end()
@@ -172,19 +226,36 @@ def main() -> int:
         else:
             ms_total = ms_eager
 
+    sel = [st["sel_dev"].cpu().numpy() for st in state]
+    if cfg["routing"] != "router":
+        assert all((s == stable_topk_sets(st["logits"], 4)).all() for s, st in zip(sel, state))
+    touched = sum(len(np.unique(s)) for s in sel)
+    routes = m * 4
+
     ms_step = ms_total / args.steps
-    layer_tokens = args.batch * args.layers
-    touched = sum(st["touched"] for st in state)
+    layer_tokens = m * L
     weight_bytes = touched * (GATE_UP_BYTES + DOWN_BYTES)
-    bias_bytes = touched * (5760 + 2880) * 4
-    act_bytes = args.layers * args.batch * (2880 * 2 + 32 * 4 + 2880 * 4)
-    step_bytes = weight_bytes + bias_bytes + act_bytes
+    bias_bytes = touched * (2 * INTER + HIDDEN) * 4
+    router_bytes = L * (E * HIDDEN * 2 + E * 4) if cfg["routing"] == "router" else 0
+    act_bytes = L * m * (HIDDEN * 2 + E * 4 + HIDDEN * 4)
+    step_bytes = weight_bytes + bias_bytes + router_bytes + act_bytes
     gbps = step_bytes / (ms_step * 1e-3) / 1e9
 
     gu = prof["gate_up"]
     gu_avg_ms = gu["total_ms"] / max(gu["launches"], 1)
-    gu_bytes_per_launch = touched * GATE_UP_BYTES / args.layers
+    gu_bytes_per_launch = touched * GATE_UP_BYTES / L
     gu_gbps = gu_bytes_per_launch / (gu_avg_ms * 1e-3) / 1e9
+    kernel = "gemm_kernel<kGateUp> (gate_up MXFP4 GEMM + SwiGLU + down-input quantization)"
+    if cfg["roofline"] == "hbm":
+        roofline = {"kernel": kernel, "bound": "hbm", "achieved": gu_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": gu_gbps / HBM_PEAK_GBPS, "traffic": None, "avg_launch_ms": gu_avg_ms,
+                    "bytes_per_launch": gu_bytes_per_launch}
+    else:
+        flops = 2.0 * routes * (2 * INTER) * HIDDEN
+        tflops = flops / (gu_avg_ms * 1e-3) / 1e12
+        roofline = {"kernel": kernel, "bound": "mfma", "achieved": tflops, "peak": F16_MFMA_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": tflops / F16_MFMA_PEAK_TFLOPS, "traffic": None,
+                    "avg_launch_ms": gu_avg_ms, "flops_per_launch": flops, "hbm_gbps": gu_gbps}
 
     out0 = state[0]["out_dev"].cpu().numpy()
     result = {
@@ -199,29 +270,24 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "mxfp4xq8->f32",
-        "data": "synthetic (seeded; random-init GPT-OSS-20B MoE weights generated on the device)",
+        "data": f"synthetic (seeded; random-init GPT-OSS-{'120B' if E == 128 else '20B'} MoE weights generated "
+                "on the device)",
         "config": {
-            "workload": "configs[1]: GPT-OSS-20B-shape MoE decode, batch 64, all 24 layers resident, "
-                        f"Zipf({args.zipf}) injected routing, top-4 of 32 experts",
-            "batch": args.batch, "layers": args.layers, "experts": 32, "top_k": 4, "hidden": 2880,
-            "intermediate": 2880, "touched_experts": touched,
+            "workload": cfg["workload"].format(**cfg),
+            "batch": m, "layers": L, "experts": E, "top_k": 4, "hidden": HIDDEN,
+            "intermediate": INTER, "touched_experts": touched,
         },
-        "tokens_per_s_through_all_layers": args.batch / (ms_step * 1e-3),
+        "tokens_per_s_through_all_layers": m / (ms_step * 1e-3),
         "hbm_gbps": gbps,
         "hbm_frac": gbps / HBM_PEAK_GBPS,
         "algorithmic_bytes_per_step": step_bytes,
-        "roofline": {
-            "kernel": "gemm_kernel<kGateUp> (gate_up MXFP4 GEMM + SwiGLU + down-input quantization)",
-            "bound": "hbm", "achieved": gu_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "frac": gu_gbps / HBM_PEAK_GBPS, "traffic": None,
-            "avg_launch_ms": gu_avg_ms, "bytes_per_launch": gu_bytes_per_launch,
-        },
+        "roofline": roofline,
         "stage_ms_per_step": {k: v["total_ms"] / args.steps for k, v in prof.items() if v["launches"]},
         "launch": "hip-graph" if args.graph else "eager",
         "eager_ms_per_step": ms_eager / args.steps,
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(x, state[0], out0, args.cpu_threads)
+        result["cpu_baseline"] = cpu_baseline(cfg, x, state[0], out0, args.cpu_threads)
     if graph is not None:
         graph.close()
     for st in state:

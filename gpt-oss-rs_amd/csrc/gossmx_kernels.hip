@@ -153,10 +153,10 @@ __device__ __forceinline__ void residual_q8_store(float v, int l32, size_t row, 
 }
 
 // ---------------------------------------------------------------------------
-// Router projection, top-k and routing softmax (blockIdx.y == 0; with
-// select = 0 only the bf16-rounded logits), and the gate_up input
-// quantization (blockIdx.y >= 1: 8 blocks of 32 values per work-group, one
-// per half wave), for row blockIdx.x (moe_batch routing loop,
+// Router projection, top-k and routing softmax (the first router_groups
+// work-groups of a row; with select = 0 only the bf16-rounded logits), and
+// the gate_up input quantization (the rest: 8 blocks of 32 values per
+// work-group, one per half wave), for row blockIdx.x (moe_batch routing loop,
 // cpu_runner.rs:2808-2854; quantize_residual_q8 of the row,
 // cpu_runner.rs:3224-3231).
 
@@ -213,14 +213,30 @@ __device__ __forceinline__ void select_row(const float* lg, int E, int K, int la
   }
 }
 
+// Router projection staging: a pass covers kRouterGroup experts (16 chains
+// each = 256 threads) over kRouterChunk hidden elements held in LDS (x as
+// f32, the weight rows as bf16, both loaded with coalesced 16-byte reads), so
+// every chain step reads LDS instead of waiting on a global load.
+constexpr int kRouterGroup = 16;
+constexpr int kRouterChunk = 1440;  // multiple of 16 (chain lanes) and 8 (16-byte pieces)
+
+__host__ __device__ __forceinline__ int router_groups(const RouteArgs& a) {
+  return a.select ? 1 : (a.experts + kRouterGroup - 1) / kRouterGroup;
+}
+
+// Grid (m, router_groups + quantization groups). With select = 1 one
+// work-group per row computes every expert's logit and selects; with
+// select = 0 work-group (r, g) computes experts [16 g, 16 g + 16) of row r and
+// writes their bf16 logits for select_dispatch_kernel.
 __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
-  const int r = blockIdx.x;
+  const int r = blockIdx.x, tid = threadIdx.x;
   const int E = a.experts, H = a.hidden, K = a.top_k;
   const uint16_t* x = a.x + (size_t)r * H;
-  if (blockIdx.y > 0) {
-    const int hw = threadIdx.x >> 5, l32 = threadIdx.x & 31;
+  const int n_router = router_groups(a);
+  if ((int)blockIdx.y >= n_router) {
+    const int hw = tid >> 5, l32 = tid & 31;
     const int blocks = H / kBlock;
-    const int b = (blockIdx.y - 1) * kRouteQuantBlocks + hw;
+    const int b = ((int)blockIdx.y - n_router) * kRouteQuantBlocks + hw;
     if (b < blocks) {  // uniform per half wave
       const float v = bf16_to_f32(x[b * kBlock + l32]);
       if (!isfinite(v)) atomicOr(a.err, kErrNonFiniteInput);
@@ -231,28 +247,48 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   __shared__ float s_chain[kMaxExperts * 16];
   __shared__ float s_logit[kMaxExperts];
   __shared__ int s_sel[kMaxTopK];
+  const int e_begin = a.select ? 0 : (int)blockIdx.y * kRouterGroup;
+  const int e_end = a.select ? E : min(E, e_begin + kRouterGroup);
 
   if (a.injected == nullptr) {
     // scalar_bf16_dot (lib.rs:1007-1029): 16 reduction lanes, lane j sums
     // w[i] * x[i] for i = j mod 16 in increasing i, multiply then add.
-    for (int c = threadIdx.x; c < E * 16; c += blockDim.x) {
-      const int e = c >> 4, l = c & 15;
-      const uint16_t* w = a.router_w + (size_t)e * H;
+    __shared__ float s_x[kRouterChunk];
+    __shared__ __align__(16) uint16_t s_w[kRouterGroup * kRouterChunk];
+    const int l = tid & 15, ge = tid >> 4;
+    for (int g0 = e_begin; g0 < e_end; g0 += kRouterGroup) {  // uniform
+      const int ng = min(kRouterGroup, e_end - g0);
       float acc = 0.0f;
-      for (int i = l; i < H; i += 16) acc = acc + bf16_to_f32(w[i]) * bf16_to_f32(x[i]);
-      s_chain[c] = acc;
+      for (int c0 = 0; c0 < H; c0 += kRouterChunk) {  // uniform
+        const int len = min(kRouterChunk, H - c0);
+        const int pieces = len / 8;
+        __syncthreads();  // the previous chunk's readers are done
+        for (int i = tid; i < len; i += 256) s_x[i] = bf16_to_f32(x[c0 + i]);
+        for (int p = tid; p < ng * pieces; p += 256) {
+          const int re = p / pieces, q = p - re * pieces;
+          *reinterpret_cast<uint4*>(&s_w[re * kRouterChunk + q * 8]) =
+              *reinterpret_cast<const uint4*>(a.router_w + (size_t)(g0 + re) * H + c0 + q * 8);
+        }
+        __syncthreads();
+        if (ge < ng) {
+          const uint16_t* w = s_w + ge * kRouterChunk;
+#pragma unroll 5
+          for (int i = l; i < len; i += 16) acc = acc + bf16_to_f32(w[i]) * s_x[i];
+        }
+      }
+      if (ge < ng) s_chain[(g0 + ge) * 16 + l] = acc;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    for (int e = e_begin + tid; e < e_end; e += blockDim.x) {
       float s = s_chain[e * 16];
-      for (int l = 1; l < 16; ++l) s = s + s_chain[e * 16 + l];
+      for (int j = 1; j < 16; ++j) s = s + s_chain[e * 16 + j];
       s_logit[e] = bf16r(s + a.router_b[e]);  // += bias (cpu_runner.rs:2781-2783), bf16 (:2829)
     }
   } else {
-    for (int e = threadIdx.x; e < E; e += blockDim.x) s_logit[e] = bf16r(a.injected[(size_t)r * E + e]);
+    for (int e = e_begin + tid; e < e_end; e += blockDim.x) s_logit[e] = bf16r(a.injected[(size_t)r * E + e]);
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+  for (int e = e_begin + tid; e < e_end; e += blockDim.x) {
     const float v = s_logit[e];
     if (!isfinite(v)) atomicOr(a.err, kErrNonFiniteLogits);
     if (a.logits) a.logits[(size_t)r * E + e] = v;
@@ -1187,7 +1223,8 @@ static inline unsigned grid1d(size_t n, unsigned block) { return (unsigned)((n +
 
 hipError_t launch_route(const RouteArgs& a, hipStream_t stream) {
   const int quant_groups = (a.hidden / kBlock + kRouteQuantBlocks - 1) / kRouteQuantBlocks;
-  hipLaunchKernelGGL(route_kernel, dim3(a.m, 1 + quant_groups), dim3(256), 0, stream, a);
+  if (a.hidden % 32 != 0 || a.experts > kMaxExperts) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(route_kernel, dim3(a.m, router_groups(a) + quant_groups), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
