@@ -23,6 +23,7 @@ namespace gossmx {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
 // Scalar helpers.
@@ -219,6 +220,7 @@ __device__ __forceinline__ void select_row(const float* lg, int E, int K, int la
 // every chain step reads LDS instead of waiting on a global load.
 constexpr int kRouterGroup = 16;
 constexpr int kRouterChunk = 1440;  // multiple of 16 (chain lanes) and 8 (16-byte pieces)
+constexpr int kRouterLoads = (kRouterGroup * kRouterChunk / 8 + 255) / 256;  // 16-byte reads per thread per chunk
 
 __host__ __device__ __forceinline__ int router_groups(const RouteArgs& a) {
   return a.select ? 1 : (a.experts + kRouterGroup - 1) / kRouterGroup;
@@ -262,13 +264,31 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
       for (int c0 = 0; c0 < H; c0 += kRouterChunk) {  // uniform
         const int len = min(kRouterChunk, H - c0);
         const int pieces = len / 8;
-        __syncthreads();  // the previous chunk's readers are done
-        for (int i = tid; i < len; i += 256) s_x[i] = bf16_to_f32(x[c0 + i]);
-        for (int p = tid; p < ng * pieces; p += 256) {
+        // Every global read of the chunk is issued before the first LDS
+        // write, so the chunk costs one memory round trip.
+        // Indices past the chunk are clamped to its last piece: such a lane
+        // reads and writes exactly what the piece's own lane does.
+        u32x4 wv[kRouterLoads];
+        uint32_t xv[kRouterChunk / 256 + 1];
+        const int n_pieces = ng * pieces;
+#pragma unroll
+        for (int k = 0; k < kRouterLoads; ++k) {
+          const int p = min(tid + k * 256, n_pieces - 1);
           const int re = p / pieces, q = p - re * pieces;
-          *reinterpret_cast<uint4*>(&s_w[re * kRouterChunk + q * 8]) =
-              *reinterpret_cast<const uint4*>(a.router_w + (size_t)(g0 + re) * H + c0 + q * 8);
+          wv[k] = *reinterpret_cast<const u32x4*>(a.router_w + (size_t)(g0 + re) * H + c0 + q * 8);
         }
+#pragma unroll
+        for (int k = 0; k < kRouterChunk / 256 + 1; ++k) xv[k] = x[c0 + min(tid + k * 256, len - 1)];
+        __syncthreads();  // the previous chunk's readers are done
+#pragma unroll
+        for (int k = 0; k < kRouterLoads; ++k) {
+          const int p = min(tid + k * 256, n_pieces - 1);
+          const int re = p / pieces, q = p - re * pieces;
+          *reinterpret_cast<u32x4*>(&s_w[re * kRouterChunk + q * 8]) = wv[k];
+        }
+#pragma unroll
+        for (int k = 0; k < kRouterChunk / 256 + 1; ++k)
+          s_x[min(tid + k * 256, len - 1)] = __uint_as_float(xv[k] << 16);
         __syncthreads();
         if (ge < ng) {
           const uint16_t* w = s_w + ge * kRouterChunk;
@@ -601,7 +621,6 @@ __device__ __forceinline__ float e8m0_select(uint32_t s) {
   return s == 0xffu ? __uint_as_float(0x7fc00000u) : v;
 }
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
 constexpr int kWaves = 8;                   // waves per GEMM work-group
