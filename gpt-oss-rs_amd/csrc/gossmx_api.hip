@@ -503,7 +503,8 @@ int gossmx_mxfp4_matmul(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
   g.bias_expert_stride = 0;  // this problem's single bias vector
   {
     OpScope scope(ctx, GOSSMX_OP_MATMUL);
-    HIP_TRY(launch_gemm(kPlain, g, (int)((m + kChunk - 1) / kChunk), ctx->stream), "matmul launch");
+    const int chunk = m <= (size_t)kSmallChunk ? kSmallChunk : kChunk;
+    HIP_TRY(launch_gemm(kPlain, g, chunk, (int)((m + chunk - 1) / chunk), ctx->stream), "matmul launch");
   }
   if (p->memory == GOSSMX_MEM_HOST) {
     HIP_TRY(hipMemcpy2DAsync(p->output, p->output_stride * sizeof(float), out, rows * sizeof(float),
@@ -577,7 +578,10 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   }
   if (int s = set_device(ctx->device)) return s;
   const bool host = io->memory == GOSSMX_MEM_HOST;
-  const size_t max_work = (R + kChunk - 1) / kChunk + std::min(E, R);
+  // Batches of at most kSmallChunk rows: every bucket is one work item of the
+  // small-batch geometry (more work-groups, fewer sequential K steps).
+  const int chunk = m <= (size_t)kSmallChunk ? kSmallChunk : kChunk;
+  const size_t max_work = (R + chunk - 1) / chunk + std::min(E, R);
 
   int s = GOSSMX_OK;
   if ((s = ensure(ctx, ctx->logits, m * E * 4)) || (s = ensure(ctx, ctx->selected, R * 4)) ||
@@ -645,6 +649,7 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   da.route_slot = static_cast<int*>(ctx->route_slot.p);
   da.work = work;
   da.n_work = n_work;
+  da.chunk = chunk;
   if (!fused || injected == nullptr) {
     OpScope sc(ctx, GOSSMX_OP_ROUTER_ROUTING);
     HIP_TRY(launch_route(ra, ctx->stream), "route launch");
@@ -685,11 +690,11 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   d.y = static_cast<uint16_t*>(ctx->y.p);
   {
     OpScope sc(ctx, GOSSMX_OP_GATE_UP);
-    HIP_TRY(launch_gemm(kGateUp, g, (int)max_work, ctx->stream), "gate_up launch");
+    HIP_TRY(launch_gemm(kGateUp, g, chunk, (int)max_work, ctx->stream), "gate_up launch");
   }
   {
     OpScope sc(ctx, GOSSMX_OP_DOWN);
-    HIP_TRY(launch_gemm(kDown, d, (int)max_work, ctx->stream), "down launch");
+    HIP_TRY(launch_gemm(kDown, d, chunk, (int)max_work, ctx->stream), "down launch");
   }
   {
     OpScope sc(ctx, GOSSMX_OP_WEIGHTING);

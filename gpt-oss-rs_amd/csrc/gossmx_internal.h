@@ -12,7 +12,9 @@ constexpr int kBlock = 32;      // values per MXFP4 / Q8 block (QUANT_BLOCK_SIZE
 constexpr int kRecord = 17;     // E8M0 byte + 16 packed nibble bytes per (row, block)
 constexpr int kTileRows = 16;   // rows per MFMA tile (one wave)
 constexpr int kWgRows = 64;     // gate_up rows (32 gate/up pairs) per 32-value block of the down input
-constexpr int kChunk = 16;      // activation rows per GEMM work item
+constexpr int kChunk = 16;      // activation rows per GEMM work item (batches of more than kSmallChunk rows)
+constexpr int kSmallChunk = 8;  // activation rows per work item for batches of at most 8 rows
+constexpr int kChunkMax = 16;
 constexpr int kMaxExperts = 128;
 constexpr int kMaxTopK = 8;
 
@@ -46,8 +48,9 @@ struct TiledWeights {
 // (and dword-granular tails) of the last tile unconditionally.
 constexpr size_t kPlaneSlack = 2048;
 // Extra bytes after each activation operand buffer: the GEMM's staging reads
-// a last partial K step as a whole 8-block step (up to 7 blocks past a row).
-constexpr size_t kActSlack = 1024;
+// a last partial K step as a whole step (up to 15 blocks of 128 bytes past a
+// row).
+constexpr size_t kActSlack = 2048;
 
 // Activation operand of the expert GEMM, one row per token or route:
 //  actv [row][block][part 0 = primary, 1 = residual][32] f16 (the Q8 codes,
@@ -104,6 +107,7 @@ struct DispatchArgs {
   int* route_slot;      // [routes]
   int* work;            // [max_work][2] (expert, first row of the chunk)
   int* n_work;
+  int chunk;            // rows per work item: kChunk, or kSmallChunk for batches of at most that many rows
 };
 
 // Batches whose logits fit one work-group's LDS take the fused selection +
@@ -120,7 +124,9 @@ hipError_t launch_dispatch(const DispatchArgs& a, hipStream_t stream);
 // select = 0. quantize = 1 adds the gate_up input quantization work-groups
 // (when no launch_route ran).
 hipError_t launch_select_dispatch(const RouteArgs& r, const DispatchArgs& d, int quantize, hipStream_t stream);
-hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream);
+// chunk: rows per work item (kChunk or kSmallChunk), selecting the kernel's
+// geometry; it must match the chunk the dispatch used.
+hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int chunk, int grid_work, hipStream_t stream);
 hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream);
 
 hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int top_k, int hidden, float* out,

@@ -324,7 +324,7 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
 // bucket_off[e] + #{j < i : expert(j) == e}. One work-group of 1024 threads;
 // in-wave ranks come from one ballot per expert present in the wave.
 //
-// Work items: every bucket is cut into kChunk-row chunks. Full chunks come
+// Work items: every bucket is cut into a.chunk-row chunks. Full chunks come
 // first (expert order), then the partial last chunks by descending size
 // (ties by expert), so the heaviest work items start first.
 
@@ -347,8 +347,8 @@ __device__ __forceinline__ void dispatch_body(const DispatchArgs& a, const int* 
   int c = 0, full = 0, sc = 0, sf = 0;
   if (wave < 2) {
     c = tid < E ? s_tot[tid] : 0;
-    full = c / kChunk;
-    s_part[tid] = c % kChunk;
+    full = c / a.chunk;
+    s_part[tid] = c % a.chunk;
     sc = c;
     sf = full;
 #pragma unroll
@@ -368,7 +368,7 @@ __device__ __forceinline__ void dispatch_body(const DispatchArgs& a, const int* 
       a.bucket_off[tid] = off;
       for (int i = 0; i < full; ++i) {
         a.work[2 * (full_before + i)] = tid;
-        a.work[2 * (full_before + i) + 1] = i * kChunk;
+        a.work[2 * (full_before + i) + 1] = i * a.chunk;
       }
       const int part = s_part[tid];
       int parts = 0, before = 0;
@@ -379,7 +379,7 @@ __device__ __forceinline__ void dispatch_body(const DispatchArgs& a, const int* 
       }
       if (part > 0) {
         a.work[2 * (total_full + before)] = tid;
-        a.work[2 * (total_full + before) + 1] = full * kChunk;
+        a.work[2 * (total_full + before) + 1] = full * a.chunk;
       }
       if (tid == 0) {
         *a.n_work = total_full + parts;
@@ -625,49 +625,69 @@ typedef __attribute__((address_space(3))) void* lds_ptr;
 
 constexpr int kWaves = 8;                   // waves per GEMM work-group
 constexpr int kGemmThreads = 64 * kWaves;   // 512
-constexpr int kWaveTiles = 2;               // 16-row weight tiles per wave
-constexpr int kWgTiles = kWaves * kWaveTiles;
-constexpr int kGemmRows = kTileRows * kWgTiles;  // weight rows per work-group (256)
-constexpr int kNtg = kChunk / 8;            // MFMA token groups per work item
-constexpr int kStep = 8;                    // K blocks per pipeline step
-constexpr int kSlotBytes = kStep * kChunk * 2 * kBlock * 2;  // f16 codes of one step in LDS
-constexpr int kCodeDma = kSlotBytes / (16 * kGemmThreads);   // 16-byte DMA per lane per step
 constexpr int kSclSlot = 64 * kWaves;       // floats written by one step's scale DMA (a dword per lane)
-static_assert(kSlotBytes == kCodeDma * 16 * kGemmThreads, "code DMA covers a slot exactly");
-static_assert(kStep * kChunk * 2 <= kSclSlot, "one dword DMA per lane covers a step's scales");
-static_assert(kChunk % 8 == 0 && kStep == 8, "token groups of 8, steps of two 4-block groups");
-static_assert(kGemmRows % 64 == 0, "a work-group's gate_up rows make whole 32-value down-input blocks");
-// Vector-memory instructions per wave and step: weights 2 x (nibbles, scale
-// dword) per tile; activations kCodeDma code pieces + 1 scale dword.
-constexpr int kLoadsW = 4 * kWaveTiles;
-constexpr int kLoadsD = kCodeDma + 1;
-// s_waitcnt immediate for "the DMA of step q has landed": issued after it are
-// W(q+1), D(q+1), W(q+2) (see k_loop). expcnt and lgkmcnt are not waited on.
-constexpr int kWaitVm = 2 * kLoadsW + kLoadsD;
-static_assert(kWaitVm < 64, "vmcnt field");
-constexpr int kWaitDma = (kWaitVm & 15) | ((kWaitVm >> 4) << 14) | (7 << 4) | (15 << 8);
+
+// Geometry of one GEMM instantiation. TILES 16-row weight tiles per wave,
+// work items of NTOK activation rows (NTOK / 8 MFMA token groups), K steps of
+// GROUPS 4-block groups. GemmBig (2 tiles, 16 rows, 8 blocks) serves every
+// batch; GemmSmall (1 tile, 8 rows, 16 blocks: twice the work-groups and half
+// the sequential steps) serves batches of at most 8 rows, whose work items
+// are one expert each and whose time is the weight stream's latency.
+template <int TILES, int NTOK, int GROUPS>
+struct GemmCfg {
+  static constexpr int kWaveTiles = TILES;
+  static constexpr int kWgTiles = kWaves * TILES;
+  static constexpr int kGemmRows = kTileRows * kWgTiles;  // weight rows per work-group
+  static constexpr int kChunk = NTOK;                     // activation rows per work item
+  static constexpr int kNtg = NTOK / 8;                   // MFMA token groups per work item
+  static constexpr int kGroups = GROUPS;                  // 4-block groups per step
+  static constexpr int kStep = 4 * GROUPS;                // K blocks per pipeline step
+  static constexpr int kSlotBytes = kStep * NTOK * 2 * kBlock * 2;  // f16 codes of one step in LDS
+  static constexpr int kCodeDma = kSlotBytes / (16 * kGemmThreads);  // 16-byte DMA per lane per step
+  // Vector-memory instructions per wave and step: weights GROUPS x (nibbles,
+  // scale dword) per tile; activations kCodeDma code pieces + 1 scale dword.
+  static constexpr int kLoadsW = 2 * GROUPS * TILES;
+  static constexpr int kLoadsD = kCodeDma + 1;
+  // s_waitcnt immediate for "the DMA of step q has landed": issued after it
+  // are W(q+1), D(q+1), W(q+2) (see k_loop). expcnt and lgkmcnt are not
+  // waited on.
+  static constexpr int kWaitVm = 2 * kLoadsW + kLoadsD;
+  static constexpr int kWaitDma = (kWaitVm & 15) | ((kWaitVm >> 4) << 14) | (7 << 4) | (15 << 8);
+  static_assert(kSlotBytes == kCodeDma * 16 * kGemmThreads, "code DMA covers a slot exactly");
+  static_assert(kStep * NTOK * 2 <= kSclSlot, "one dword DMA per lane covers a step's scales");
+  static_assert(NTOK % 8 == 0 && NTOK <= kChunkMax, "token groups of 8");
+  static_assert(kGemmRows % 64 == 0, "a work-group's gate_up rows make whole 32-value down-input blocks");
+  static_assert(kWaitVm < 64, "vmcnt field");
+  static_assert((kStep - 1) * 2 * kBlock * 2 <= (int)kActSlack, "a last partial step reads inside the slack");
+};
+using GemmBig = GemmCfg<2, 16, 2>;
+using GemmSmall = GemmCfg<1, 8, 4>;
+static_assert(GemmBig::kChunk == kChunk && GemmSmall::kChunk == kSmallChunk, "work item sizes");
 constexpr int kBufferFlags = 0x00020000;    // raw 32-bit buffer resource, gfx9 family
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, kBufferFlags);
 }
 
-// One step of a wave's weights: per tile, nibble groups 2q and 2q+1 and their
-// scale dwords.
+// One step of a wave's weights: per group of the step and tile, the nibble
+// group and its scale dword.
+template <class C>
 struct WStep {
-  u32x4 v0[kWaveTiles], v1[kWaveTiles];
-  uint32_t s0[kWaveTiles], s1[kWaveTiles];
+  u32x4 v[C::kGroups][C::kWaveTiles];
+  uint32_t s[C::kGroups][C::kWaveTiles];
 };
 
 // Accumulators of one wave: [tile][token group][token of the lane's pair].
-typedef float Acc[kWaveTiles][kNtg][2];
+template <class C>
+using Acc = float[C::kWaveTiles][C::kNtg][2];
 
 // LDS slot layout of one step (written by DMA, read as MFMA A operands): for
 // block j and token group tg, 1 KiB = [k-slice g (4)][vector i (16)][16 B]
 // with vector i = 2 * (row within the group) + part (0 primary, 1 residual),
 // so lane (g, i) of a wave reads the 16 bytes at lane * 16 (conflict-free).
 // Scales: float2 (primary, residual) at [j][row].
-__device__ __forceinline__ int slot_chunk(int j, int tg) { return j * kNtg + tg; }
+template <class C>
+__device__ __forceinline__ int slot_chunk(int j, int tg) { return j * C::kNtg + tg; }
 
 // One block j of the current step against NTG token groups and the wave's
 // tiles: one A operand and one scale read per token group feed an MFMA per
@@ -675,20 +695,20 @@ __device__ __forceinline__ int slot_chunk(int j, int tg) { return j * kNtg + tg;
 // carries the E8M0 scale (exact), so the MFMA returns (p / 2) * e8m0 and a
 // term is d * act_scale; otherwise a term is (d * e8m0) * act_scale. Both are
 // the reference's (p * (0.5 * e8m0)) * act_scale rounded once.
-template <bool RESIDUAL, bool SCALED, int NTG>
-__device__ __forceinline__ void block_update(Acc& tot, const char* codes, const float2* scl,
-                                             const half8 (&bop)[kWaveTiles], const float (&e8)[kWaveTiles],
+template <class C, bool RESIDUAL, bool SCALED, int NTG>
+__device__ __forceinline__ void block_update(Acc<C>& tot, const char* codes, const float2* scl,
+                                             const half8 (&bop)[C::kWaveTiles], const float (&e8)[C::kWaveTiles],
                                              const int j, const int lane, const int G) {
   const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int tg = 0; tg < NTG; ++tg) {
-    const half8 aop = *reinterpret_cast<const half8*>(codes + slot_chunk(j, tg) * 1024 + lane * 16);
-    const float4 sc = *reinterpret_cast<const float4*>(&scl[j * kChunk + tg * 8 + 2 * G]);
-    f32x4 d[kWaveTiles];
+    const half8 aop = *reinterpret_cast<const half8*>(codes + slot_chunk<C>(j, tg) * 1024 + lane * 16);
+    const float4 sc = *reinterpret_cast<const float4*>(&scl[j * C::kChunk + tg * 8 + 2 * G]);
+    f32x4 d[C::kWaveTiles];
 #pragma unroll
-    for (int t = 0; t < kWaveTiles; ++t) d[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop[t], zero, 0, 0, 0);
+    for (int t = 0; t < C::kWaveTiles; ++t) d[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop[t], zero, 0, 0, 0);
 #pragma unroll
-    for (int t = 0; t < kWaveTiles; ++t) {
+    for (int t = 0; t < C::kWaveTiles; ++t) {
       if (SCALED) {
         tot[t][tg][0] = tot[t][tg][0] + d[t][0] * sc.x;
         if (RESIDUAL) tot[t][tg][0] = tot[t][tg][0] + d[t][1] * sc.y;
@@ -709,17 +729,17 @@ __device__ __forceinline__ void block_update(Acc& tot, const char* codes, const 
 // in [kFastScaleLo, kFastScaleHi] (checked when the weights were stored), so
 // the conversion applies the scale exactly; otherwise the scale multiplies
 // the MFMA result, with the reference's 0x00 and 0xff encodings.
-template <bool RESIDUAL, int NTG, bool FAST>
-__device__ __forceinline__ void group_update(Acc& tot, const char* codes, const float2* scl,
-                                             const u32x4 (&v)[kWaveTiles], const uint32_t (&s)[kWaveTiles],
+template <class C, bool RESIDUAL, int NTG, bool FAST>
+__device__ __forceinline__ void group_update(Acc<C>& tot, const char* codes, const float2* scl,
+                                             const u32x4 (&v)[C::kWaveTiles], const uint32_t (&s)[C::kWaveTiles],
                                              const int jb, const int nb, const int lane, const int G) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     if (j < nb) {
-      half8 bop[kWaveTiles];
-      float e8[kWaveTiles];
+      half8 bop[C::kWaveTiles];
+      float e8[C::kWaveTiles];
 #pragma unroll
-      for (int t = 0; t < kWaveTiles; ++t) {
+      for (int t = 0; t < C::kWaveTiles; ++t) {
         const uint32_t sb = (s[t] >> (8 * j)) & 0xffu;
         if (FAST) {
           bop[t] = fp4x8_to_half8_scaled(v[t][j], __uint_as_float(sb << 23));
@@ -729,7 +749,7 @@ __device__ __forceinline__ void group_update(Acc& tot, const char* codes, const 
           e8[t] = e8m0_select(sb);
         }
       }
-      block_update<RESIDUAL, FAST, NTG>(tot, codes, scl, bop, e8, jb + j, lane, G);
+      block_update<C, RESIDUAL, FAST, NTG>(tot, codes, scl, bop, e8, jb + j, lane, G);
     }
   }
 }
@@ -738,8 +758,8 @@ __device__ __forceinline__ void group_update(Acc& tot, const char* codes, const 
 // or gate_up's SwiGLU and down-input quantization. `s_act` is LDS scratch of
 // at least count * (kGemmRows / 2 + 1) floats, free for reuse. Rows of tiles
 // past the end (row >= rows) are never stored.
-template <int MODE>
-__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc& tot, const int n_tg, const int count,
+template <class C, int MODE>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& tot, const int n_tg, const int count,
                                               const int start, const int route_base, const int tile0, float* s_act) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -748,11 +768,11 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc& tot,
 
   if (MODE == kPlain || MODE == kDown) {
 #pragma unroll
-    for (int t = 0; t < kWaveTiles; ++t) {
+    for (int t = 0; t < C::kWaveTiles; ++t) {
       const int row = (tile0 + t) * kTileRows + nl;
       if (row < rows) {
 #pragma unroll
-        for (int tg = 0; tg < kNtg; ++tg)
+        for (int tg = 0; tg < C::kNtg; ++tg)
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             const int c = tg * 8 + 2 * G + u;
@@ -774,14 +794,14 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc& tot,
     // values (cpu_runner.rs:3224-3231). The SwiGLU values reuse an LDS slot
     // as [kChunk rows][kGemmRows / 2 values]; tile t of wave w holds values
     // (w * kWaveTiles + t) * 8 .. + 7.
-    constexpr int kActStride = kGemmRows / 2 + 1;
+    constexpr int kActStride = C::kGemmRows / 2 + 1;
     // Lane pairs (even = gate row, odd = up row) hold both values for tokens
     // t0 = 2G and t1 = 2G + 1; the even lane finishes t0 and the odd lane t1.
     const bool odd = (nl & 1) != 0;
 #pragma unroll
-    for (int t = 0; t < kWaveTiles; ++t)
+    for (int t = 0; t < C::kWaveTiles; ++t)
 #pragma unroll
-      for (int tg = 0; tg < kNtg; ++tg) {
+      for (int tg = 0; tg < C::kNtg; ++tg) {
         if (tg < n_tg) {
           const float own0 = bf16r(tot[t][tg][0]), own1 = bf16r(tot[t][tg][1]);
           const float recv = __shfl_xor(odd ? own0 : own1, 1);
@@ -789,14 +809,14 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc& tot,
           const float up = odd ? own1 : recv;
           const int c = tg * 8 + 2 * G + (odd ? 1 : 0);
           if (c < count)
-            s_act[c * kActStride + (wave * kWaveTiles + t) * 8 + (nl >> 1)] =
+            s_act[c * kActStride + (wave * C::kWaveTiles + t) * 8 + (nl >> 1)] =
                 swiglu_one(gate, up, a.alpha, a.limit, a.sig_tab);
         }
       }
     __syncthreads();
     const int hw = tid >> 5, l32 = tid & 31;
     const int blocks_next = rows / kWgRows;
-    constexpr int kBlocksPerWg = kGemmRows / 64;
+    constexpr int kBlocksPerWg = C::kGemmRows / 64;
     for (int item = hw; item < count * kBlocksPerWg; item += kGemmThreads / 32) {
       const int c = item / kBlocksPerWg, h = item % kBlocksPerWg;
       if (blockIdx.x * kBlocksPerWg + h >= blocks_next) continue;  // uniform per half wave
@@ -812,61 +832,75 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc& tot,
 
 // Loop-invariant state of the K loop. All members but the DMA and weight
 // lane offsets are wave-uniform (scalar registers).
+template <class C>
 struct KLoop {
-  __amdgpu_buffer_rsrc_t nib[kWaveTiles], scl[kWaveTiles];  // this wave's tiles of the nibble and scale planes
+  __amdgpu_buffer_rsrc_t nib[C::kWaveTiles], scl[C::kWaveTiles];  // this wave's tiles of the nibble and scale planes
   __amdgpu_buffer_rsrc_t codes, scales;  // the activation operand buffers
   int B, nsteps, nfull4, last_group, wave, lane, G;
   bool wave_ok;                      // the wave's first tile exists
   int vl, vl_tail, vs;               // weight lane offsets: nibbles lane * 16 (full group) or lane * (B % 4) * 4
                                      // (the compact last group), scales (lane % 16) * 4
-  int voff[kCodeDma];                // DMA source of this lane's code pieces in step 0
+  int voff[C::kCodeDma];             // DMA source of this lane's code pieces in step 0
   int soff;                          // DMA source of this lane's scale dword in step 0
 };
 
-// Weights of step q (4-block groups 2q, 2q+1, clamped to the last group:
-// loads past the end are issued anyway so that every step has the same
-// instruction count, and their data is never used). The compact last group
-// (B % 4 blocks) is read with its own lane offset; the 16 bytes a lane loads
-// there end at most 772 bytes into the group, inside the tile or the plane
-// slack, and the dwords past the group's blocks are never used.
-__device__ __forceinline__ WStep load_wstep(const KLoop& k, int q) {
-  const int g0 = min(2 * q, k.last_group), g1 = min(2 * q + 1, k.last_group);
-  const int o0 = g0 < k.nfull4 ? k.vl : k.vl_tail, o1 = g1 < k.nfull4 ? k.vl : k.vl_tail;
-  WStep w;
+// Weights of step q (4-block groups kGroups q .. kGroups q + kGroups - 1,
+// clamped to the last group: loads past the end are issued anyway so that
+// every step has the same instruction count, and their data is never used).
+// The compact last group (B % 4 blocks) is read with its own lane offset; the
+// 16 bytes a lane loads there end at most 772 bytes into the group, inside
+// the tile or the plane slack, and the dwords past the group's blocks are
+// never used.
+template <class C>
+__device__ __forceinline__ WStep<C> load_wstep(const KLoop<C>& k, int q) {
+  WStep<C> w;
 #pragma unroll
-  for (int t = 0; t < kWaveTiles; ++t) {
-    w.v0[t] = __builtin_amdgcn_raw_buffer_load_b128(k.nib[t], o0, g0 * 1024, 0);
-    w.s0[t] = __builtin_amdgcn_raw_buffer_load_b32(k.scl[t], k.vs, g0 * 64, 0);
-    w.v1[t] = __builtin_amdgcn_raw_buffer_load_b128(k.nib[t], o1, g1 * 1024, 0);
-    w.s1[t] = __builtin_amdgcn_raw_buffer_load_b32(k.scl[t], k.vs, g1 * 64, 0);
+  for (int g = 0; g < C::kGroups; ++g) {
+    const int gi = min(C::kGroups * q + g, k.last_group);
+    const int o = gi < k.nfull4 ? k.vl : k.vl_tail;
+#pragma unroll
+    for (int t = 0; t < C::kWaveTiles; ++t) {
+      w.v[g][t] = __builtin_amdgcn_raw_buffer_load_b128(k.nib[t], o, gi * 1024, 0);
+      w.s[g][t] = __builtin_amdgcn_raw_buffer_load_b32(k.scl[t], k.vs, gi * 64, 0);
+    }
   }
   return w;
 }
 
-// The DMA of step q (clamped to the last step) into one ring slot.
-__device__ __forceinline__ void issue_dma(const KLoop& k, int q_raw, char* codes, float* scl) {
-  const int q = min(q_raw, k.nsteps - 1);
-#pragma unroll
-  for (int i = 0; i < kCodeDma; ++i)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(k.codes, (lds_ptr)(codes + (i * kWaves + k.wave) * 1024), 16, k.voff[i],
-                                             q * (kStep * 2 * kBlock * 2), 0, 0);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(k.scales, (lds_ptr)(reinterpret_cast<char*>(scl) + k.wave * 256), 4,
-                                           k.soff, q * (kStep * 8), 0, 0);
+// Buffer loads straight into LDS (16 bytes or one dword per lane; the LDS
+// address is wave-uniform, lane L lands at dst + L * size).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t src, char* dst, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (lds_ptr)dst, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t src, char* dst, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (lds_ptr)dst, 4, voff, soff, 0, 0);
 }
 
-// Compute of step q (q < nsteps).
-template <bool RESIDUAL, int NTG, bool FAST>
-__device__ __forceinline__ void step_update(const KLoop& k, Acc& tot, const char* codes, const float* scl,
-                                            const WStep& w, const int q) {
+// The DMA of step q (clamped to the last step) into one ring slot.
+template <class C>
+__device__ __forceinline__ void issue_dma(const KLoop<C>& k, int q_raw, char* codes, float* scl) {
+  const int q = min(q_raw, k.nsteps - 1);
+#pragma unroll
+  for (int i = 0; i < C::kCodeDma; ++i)
+    dma16(k.codes, codes + (i * kWaves + k.wave) * 1024, k.voff[i], q * (C::kStep * 2 * kBlock * 2));
+  dma4(k.scales, reinterpret_cast<char*>(scl) + k.wave * 256, k.soff, q * (C::kStep * 8));
+}
+
+// Compute of step q (q < nsteps): its groups, each full, partial or absent.
+template <class C, bool RESIDUAL, int NTG, bool FAST>
+__device__ __forceinline__ void step_update(const KLoop<C>& k, Acc<C>& tot, const char* codes, const float* scl,
+                                            const WStep<C>& w, const int q) {
   const float2* s2 = reinterpret_cast<const float2*>(scl);
-  if (8 * q + 8 <= k.B) {
-    group_update<RESIDUAL, NTG, FAST>(tot, codes, s2, w.v0, w.s0, 0, 4, k.lane, k.G);
-    group_update<RESIDUAL, NTG, FAST>(tot, codes, s2, w.v1, w.s1, 4, 4, k.lane, k.G);
+  if (C::kStep * q + C::kStep <= k.B) {
+#pragma unroll
+    for (int g = 0; g < C::kGroups; ++g)
+      group_update<C, RESIDUAL, NTG, FAST>(tot, codes, s2, w.v[g], w.s[g], 4 * g, 4, k.lane, k.G);
   } else {
-    // Last step: groups 2q and 2q+1, each full, partial or absent.
-    const int nb0 = min(4, k.B - 8 * q), nb1 = min(4, k.B - 8 * q - 4);
-    group_update<RESIDUAL, NTG, FAST>(tot, codes, s2, w.v0, w.s0, 0, nb0, k.lane, k.G);
-    if (nb1 > 0) group_update<RESIDUAL, NTG, FAST>(tot, codes, s2, w.v1, w.s1, 4, nb1, k.lane, k.G);
+#pragma unroll
+    for (int g = 0; g < C::kGroups; ++g) {
+      const int nb = min(4, k.B - C::kStep * q - 4 * g);
+      if (nb > 0) group_update<C, RESIDUAL, NTG, FAST>(tot, codes, s2, w.v[g], w.s[g], 4 * g, nb, k.lane, k.G);
+    }
   }
 }
 
@@ -876,18 +910,18 @@ __device__ __forceinline__ void step_update(const KLoop& k, Acc& tot, const char
 //   D(q+2) compute(q) W(q+3).
 // After D(q) come W(q+1), D(q+1), W(q+2) = kWaitVm instructions, and W(q)
 // was issued before D(q), so the wait also covers the weights of step q.
-template <bool RESIDUAL, int NTG, bool FAST>
-__device__ __forceinline__ void k_loop(const KLoop& k, Acc& tot, char* c0, char* c1, char* c2, float* s0, float* s1,
-                                       float* s2) {
-  WStep w0, w1, w2;
+template <class C, bool RESIDUAL, int NTG, bool FAST>
+__device__ __forceinline__ void k_loop(const KLoop<C>& k, Acc<C>& tot, char* c0, char* c1, char* c2, float* s0,
+                                       float* s1, float* s2) {
+  WStep<C> w0, w1, w2;
   __builtin_amdgcn_sched_barrier(0);
   w0 = load_wstep(k, 0);
   __builtin_amdgcn_sched_barrier(0);
-  issue_dma(k, 0, c0, s0);
+  issue_dma<C>(k, 0, c0, s0);
   __builtin_amdgcn_sched_barrier(0);
   w1 = load_wstep(k, 1);
   __builtin_amdgcn_sched_barrier(0);
-  issue_dma(k, 1, c1, s1);
+  issue_dma<C>(k, 1, c1, s1);
   __builtin_amdgcn_sched_barrier(0);
   w2 = load_wstep(k, 2);
   __builtin_amdgcn_sched_barrier(0);
@@ -895,12 +929,12 @@ __device__ __forceinline__ void k_loop(const KLoop& k, Acc& tot, char* c0, char*
   {                                                                                                  \
     const int q = (QV);                                                                              \
     __builtin_amdgcn_sched_barrier(0);                                                               \
-    __builtin_amdgcn_s_waitcnt(kWaitDma); /* this wave's DMA for step q has landed */               \
+    __builtin_amdgcn_s_waitcnt(C::kWaitDma); /* this wave's DMA for step q has landed */            \
     __builtin_amdgcn_s_barrier();         /* ... and every other wave's; the slot of q-1 is free */  \
     __builtin_amdgcn_sched_barrier(0);                                                               \
-    issue_dma(k, q + 2, NCODES, NSCL);                                                               \
+    issue_dma<C>(k, q + 2, NCODES, NSCL);                                                            \
     __builtin_amdgcn_sched_barrier(0);                                                               \
-    if (k.wave_ok && q < k.nsteps) step_update<RESIDUAL, NTG, FAST>(k, tot, CODES, SCL, SLOT, q);    \
+    if (k.wave_ok && q < k.nsteps) step_update<C, RESIDUAL, NTG, FAST>(k, tot, CODES, SCL, SLOT, q); \
     __builtin_amdgcn_sched_barrier(0);                                                               \
     SLOT = load_wstep(k, q + 3);                                                                     \
     __builtin_amdgcn_sched_barrier(0);                                                               \
@@ -914,7 +948,7 @@ __device__ __forceinline__ void k_loop(const KLoop& k, Acc& tot, char* c0, char*
 #undef GOSSMX_STEP
 }
 
-template <int MODE, bool RESIDUAL>
+template <class C, int MODE, bool RESIDUAL>
 __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -922,21 +956,21 @@ __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
   int expert, start, count, route_base = 0;
   if (MODE == kPlain) {
     expert = a.plain_expert;
-    start = blockIdx.y * kChunk;
-    count = min(kChunk, a.plain_m - start);
+    start = blockIdx.y * C::kChunk;
+    count = min(C::kChunk, a.plain_m - start);
   } else {
     const int wi = blockIdx.y;
     if (wi >= *a.n_work) return;  // uniform over the work-group
     expert = a.work[2 * wi];
     start = a.work[2 * wi + 1];
     route_base = a.bucket_off[expert];
-    count = min(kChunk, a.bucket_off[expert + 1] - route_base - start);
+    count = min(C::kChunk, a.bucket_off[expert + 1] - route_base - start);
   }
   // LDS ring of three steps, filled by DMA two steps ahead.
-  __shared__ __align__(16) char s_codes0[kSlotBytes], s_codes1[kSlotBytes], s_codes2[kSlotBytes];
+  __shared__ __align__(16) char s_codes0[C::kSlotBytes], s_codes1[C::kSlotBytes], s_codes2[C::kSlotBytes];
   __shared__ __align__(16) float s_scl0[kSclSlot], s_scl1[kSclSlot], s_scl2[kSclSlot];
-  __shared__ int s_row[kChunk];
-  if (tid < kChunk) {
+  __shared__ int s_row[C::kChunk];
+  if (tid < C::kChunk) {
     int r = -1;
     if (tid < count) {
       if (MODE == kPlain) r = start + tid;
@@ -948,13 +982,13 @@ __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
   __syncthreads();
 
   const int rows = (int)a.w.rows, B = (int)a.w.blocks;
-  const int tile0 = (blockIdx.x * kWaves + wave) * kWaveTiles;
+  const int tile0 = (blockIdx.x * kWaves + wave) * C::kWaveTiles;
   const int n_tg = (count + 7) >> 3;
   const int nq4 = (B + 3) >> 2;
 
-  KLoop k;
+  KLoop<C> k;
   k.B = B;
-  k.nsteps = (B + kStep - 1) / kStep;
+  k.nsteps = (B + C::kStep - 1) / C::kStep;
   k.nfull4 = B >> 2;
   k.last_group = nq4 - 1;
   k.wave = wave;
@@ -965,9 +999,9 @@ __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
   k.vl_tail = lane * (B & 3) * 4;
   k.vs = nl * 4;
   bool fast = true;
-  float b0[kWaveTiles];
+  float b0[C::kWaveTiles];
 #pragma unroll
-  for (int t = 0; t < kWaveTiles; ++t) {
+  for (int t = 0; t < C::kWaveTiles; ++t) {
     const int tile = tile0 + t;
     const bool ok = tile < (int)a.w.tiles;
     // Tiles past the end stream tile 0 and discard it.
@@ -982,11 +1016,11 @@ __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
     if (a.bias != nullptr && ok && row < rows) bias = a.bias[(size_t)expert * a.bias_expert_stride + row];
     b0[t] = bias + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
   }
-  Acc tot;
+  Acc<C> tot;
 #pragma unroll
-  for (int t = 0; t < kWaveTiles; ++t)
+  for (int t = 0; t < C::kWaveTiles; ++t)
 #pragma unroll
-    for (int tg = 0; tg < kNtg; ++tg) { tot[t][tg][0] = b0[t]; tot[t][tg][1] = b0[t]; }
+    for (int tg = 0; tg < C::kNtg; ++tg) { tot[t][tg][0] = b0[t]; tot[t][tg][1] = b0[t]; }
 
   // DMA lane map, the same for every step. Code piece i of this wave fills
   // slot bytes c * 16 with c = (i * kWaves + wave) * 64 + lane, i.e. block j,
@@ -995,36 +1029,36 @@ __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
   // block record. Scale dword d = wave * 64 + lane holds half d % 2 of
   // (block d / (2 kChunk), row (d / 2) % kChunk). Lanes with nothing to move
   // read the start of the buffer (valid memory) into slot bytes no row uses.
-  // A last partial step reads up to 7 blocks past a row, inside the
+  // A last partial step reads up to kStep - 1 blocks past a row, inside the
   // buffers' slack.
   k.codes = buffer_rsrc(a.actv);
   k.scales = buffer_rsrc(a.acts);
 #pragma unroll
-  for (int i = 0; i < kCodeDma; ++i) {
+  for (int i = 0; i < C::kCodeDma; ++i) {
     const int c = (i * kWaves + wave) * 64 + lane;
     const int ch = c >> 6, p = c & 63;
-    const int j = ch / kNtg, tg = ch % kNtg, g = p >> 4, v = p & 15;
+    const int j = ch / C::kNtg, tg = ch % C::kNtg, g = p >> 4, v = p & 15;
     const int t = tg * 8 + (v >> 1), part = v & 1;
     k.voff[i] = t < count ? ((s_row[t] * B + j) * 8 + part * 4 + g) * 16 : 0;
   }
   {
     const int d = wave * 64 + lane;
-    const int j = d / (kChunk * 2), t = (d >> 1) % kChunk;
-    k.soff = (d < kStep * kChunk * 2 && t < count) ? ((s_row[t] * B + j) * 2 + (d & 1)) * 4 : 0;
+    const int j = d / (C::kChunk * 2), t = (d >> 1) % C::kChunk;
+    k.soff = (d < C::kStep * C::kChunk * 2 && t < count) ? ((s_row[t] * B + j) * 2 + (d & 1)) * 4 : 0;
   }
 
   if (n_tg == 1) {
-    if (fast) k_loop<RESIDUAL, 1, true>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2);
-    else k_loop<RESIDUAL, 1, false>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2);
+    if (fast) k_loop<C, RESIDUAL, 1, true>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2);
+    else k_loop<C, RESIDUAL, 1, false>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2);
   } else {
-    if (fast) k_loop<RESIDUAL, kNtg, true>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2);
-    else k_loop<RESIDUAL, kNtg, false>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2);
+    if (fast) k_loop<C, RESIDUAL, C::kNtg, true>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2);
+    else k_loop<C, RESIDUAL, C::kNtg, false>(k, tot, s_codes0, s_codes1, s_codes2, s_scl0, s_scl1, s_scl2);
   }
   // Drain the trailing DMA into the ring before the LDS is reused or the
   // work-group ends.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  gemm_epilogue<MODE>(a, tot, n_tg, count, start, route_base, tile0, reinterpret_cast<float*>(s_codes0));
+  gemm_epilogue<C, MODE>(a, tot, n_tg, count, start, route_base, tile0, reinterpret_cast<float*>(s_codes0));
 }
 
 // Exactness flag per (expert, tile): 1 when every E8M0 byte of the tile's
@@ -1262,20 +1296,27 @@ hipError_t launch_select_dispatch(const RouteArgs& r, const DispatchArgs& d, int
   return hipGetLastError();
 }
 
-hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream) {
-  const dim3 grid((unsigned)((a.w.tiles + kWgTiles - 1) / kWgTiles), (unsigned)grid_work);
+template <class C>
+static hipError_t launch_gemm_cfg(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream) {
+  const dim3 grid((unsigned)((a.w.tiles + C::kWgTiles - 1) / C::kWgTiles), (unsigned)grid_work);
   const dim3 block(kGemmThreads);
   if (a.residual) {
     switch (mode) {
-      case kPlain: hipLaunchKernelGGL((gemm_kernel<kPlain, true>), grid, block, 0, stream, a); break;
-      case kGateUp: hipLaunchKernelGGL((gemm_kernel<kGateUp, true>), grid, block, 0, stream, a); break;
-      case kDown: hipLaunchKernelGGL((gemm_kernel<kDown, true>), grid, block, 0, stream, a); break;
+      case kPlain: hipLaunchKernelGGL((gemm_kernel<C, kPlain, true>), grid, block, 0, stream, a); break;
+      case kGateUp: hipLaunchKernelGGL((gemm_kernel<C, kGateUp, true>), grid, block, 0, stream, a); break;
+      case kDown: hipLaunchKernelGGL((gemm_kernel<C, kDown, true>), grid, block, 0, stream, a); break;
     }
   } else {
     if (mode != kPlain) return hipErrorInvalidValue;  // the MoE block always runs residual-Q8
-    hipLaunchKernelGGL((gemm_kernel<kPlain, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<C, kPlain, false>), grid, block, 0, stream, a);
   }
   return hipGetLastError();
+}
+
+hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int chunk, int grid_work, hipStream_t stream) {
+  if (chunk == GemmSmall::kChunk) return launch_gemm_cfg<GemmSmall>(mode, a, grid_work, stream);
+  if (chunk == GemmBig::kChunk) return launch_gemm_cfg<GemmBig>(mode, a, grid_work, stream);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream) {
