@@ -47,6 +47,11 @@ BLOCKS = HIDDEN // 32
 GATE_UP_BYTES = 2 * INTER * BLOCKS * 17   # 8,812,800 B per expert
 DOWN_BYTES = HIDDEN * BLOCKS * 17         # 4,406,400 B per expert
 SEED = 20251201
+# HBM bytes per gate_up launch measured with rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE on this workload (167,971 KiB x 2.0 + 3,152 KiB x 1.0, scaled by
+# what the counters read for a 1 GiB device copy); bench.py cannot read
+# counters itself, so only the configuration that was profiled reports it.
+PMC_GATE_UP_TRAFFIC = {1: 339_094 * 1024}
 
 CONFIGS = {
     0: {"batch": 1, "layers": 12, "experts": 32, "routing": "router", "zipf": None, "roofline": "hbm",
@@ -247,9 +252,12 @@ def main() -> int:
     gu_gbps = gu_bytes_per_launch / (gu_avg_ms * 1e-3) / 1e9
     kernel = "gemm_kernel<kGateUp> (gate_up MXFP4 GEMM + SwiGLU + down-input quantization)"
     if cfg["roofline"] == "hbm":
+        traffic = PMC_GATE_UP_TRAFFIC.get(args.config) if (args.layers, args.batch, args.zipf) == (None,) * 3 else None
         roofline = {"kernel": kernel, "bound": "hbm", "achieved": gu_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                    "frac": gu_gbps / HBM_PEAK_GBPS, "traffic": None, "avg_launch_ms": gu_avg_ms,
+                    "frac": gu_gbps / HBM_PEAK_GBPS, "traffic": traffic, "avg_launch_ms": gu_avg_ms,
                     "bytes_per_launch": gu_bytes_per_launch}
+        if traffic is not None:
+            roofline["traffic_source"] = "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE, profiles/gemm_decode64_pmc.md"
     else:
         flops = 2.0 * routes * (2 * INTER) * HIDDEN
         tflops = flops / (gu_avg_ms * 1e-3) / 1e12
