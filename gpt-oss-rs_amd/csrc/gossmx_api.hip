@@ -444,6 +444,15 @@ void gossmx_weights_destroy(gossmx_weights* w) {
   delete w;
 }
 
+// Rows per GEMM work item for a batch of m activation rows (it selects the
+// kernel geometry). Batches of at most kSmallChunk rows: every bucket is one
+// work item (more work-groups, fewer sequential K steps). Batches of at least
+// kHugeMinRows rows: 32-row items share each weight block's conversion.
+static int gemm_chunk(size_t m) {
+  if (m <= (size_t)kSmallChunk) return kSmallChunk;
+  return m >= (size_t)kHugeMinRows ? kHugeChunk : kChunk;
+}
+
 // --- kernel boundary ---------------------------------------------------------
 
 int gossmx_mxfp4_matmul_check(const gossmx_matmul_problem* p, size_t rows, size_t blocks, size_t experts) {
@@ -503,7 +512,7 @@ int gossmx_mxfp4_matmul(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
   g.bias_expert_stride = 0;  // this problem's single bias vector
   {
     OpScope scope(ctx, GOSSMX_OP_MATMUL);
-    const int chunk = m <= (size_t)kSmallChunk ? kSmallChunk : kChunk;
+    const int chunk = gemm_chunk(m);
     HIP_TRY(launch_gemm(kPlain, g, chunk, (int)((m + chunk - 1) / chunk), ctx->stream), "matmul launch");
   }
   if (p->memory == GOSSMX_MEM_HOST) {
@@ -578,9 +587,7 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   }
   if (int s = set_device(ctx->device)) return s;
   const bool host = io->memory == GOSSMX_MEM_HOST;
-  // Batches of at most kSmallChunk rows: every bucket is one work item of the
-  // small-batch geometry (more work-groups, fewer sequential K steps).
-  const int chunk = m <= (size_t)kSmallChunk ? kSmallChunk : kChunk;
+  const int chunk = gemm_chunk(m);
   const size_t max_work = (R + chunk - 1) / chunk + std::min(E, R);
 
   int s = GOSSMX_OK;

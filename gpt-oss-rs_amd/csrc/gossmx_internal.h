@@ -14,7 +14,9 @@ constexpr int kTileRows = 16;   // rows per MFMA tile (one wave)
 constexpr int kWgRows = 64;     // gate_up rows (32 gate/up pairs) per 32-value block of the down input
 constexpr int kChunk = 16;      // activation rows per GEMM work item (batches of more than kSmallChunk rows)
 constexpr int kSmallChunk = 8;  // activation rows per work item for batches of at most 8 rows
-constexpr int kChunkMax = 16;
+constexpr int kHugeChunk = 32;  // activation rows per work item for batches of at least kHugeMinRows rows
+constexpr int kHugeMinRows = 512;
+constexpr int kChunkMax = 32;
 constexpr int kMaxExperts = 128;
 constexpr int kMaxTopK = 8;
 
@@ -107,7 +109,7 @@ struct DispatchArgs {
   int* route_slot;      // [routes]
   int* work;            // [max_work][2] (expert, first row of the chunk)
   int* n_work;
-  int chunk;            // rows per work item: kChunk, or kSmallChunk for batches of at most that many rows
+  int chunk;            // rows per work item: kSmallChunk, kChunk or kHugeChunk (by batch size)
 };
 
 // Batches whose logits fit one work-group's LDS take the fused selection +
@@ -124,8 +126,8 @@ hipError_t launch_dispatch(const DispatchArgs& a, hipStream_t stream);
 // select = 0. quantize = 1 adds the gate_up input quantization work-groups
 // (when no launch_route ran).
 hipError_t launch_select_dispatch(const RouteArgs& r, const DispatchArgs& d, int quantize, hipStream_t stream);
-// chunk: rows per work item (kChunk or kSmallChunk), selecting the kernel's
-// geometry; it must match the chunk the dispatch used.
+// chunk: rows per work item (kSmallChunk, kChunk or kHugeChunk), selecting
+// the kernel's geometry; it must match the chunk the dispatch used.
 hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int chunk, int grid_work, hipStream_t stream);
 hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream);
 

@@ -632,7 +632,9 @@ constexpr int kSclSlot = 64 * kWaves;       // floats written by one step's scal
 // GROUPS 4-block groups. GemmBig (2 tiles, 16 rows, 8 blocks) serves every
 // batch; GemmSmall (1 tile, 8 rows, 16 blocks: twice the work-groups and half
 // the sequential steps) serves batches of at most 8 rows, whose work items
-// are one expert each and whose time is the weight stream's latency.
+// are one expert each and whose time is the weight stream's latency;
+// GemmHuge (2 tiles, 32 rows, 4 blocks) serves prefill-sized batches, where
+// the FP4->f16 conversion of a weight block is shared by four token groups.
 template <int TILES, int NTOK, int GROUPS>
 struct GemmCfg {
   static constexpr int kWaveTiles = TILES;
@@ -662,7 +664,9 @@ struct GemmCfg {
 };
 using GemmBig = GemmCfg<2, 16, 2>;
 using GemmSmall = GemmCfg<1, 8, 4>;
-static_assert(GemmBig::kChunk == kChunk && GemmSmall::kChunk == kSmallChunk, "work item sizes");
+using GemmHuge = GemmCfg<2, 32, 1>;
+static_assert(GemmBig::kChunk == kChunk && GemmSmall::kChunk == kSmallChunk && GemmHuge::kChunk == kHugeChunk,
+              "work item sizes");
 constexpr int kBufferFlags = 0x00020000;    // raw 32-bit buffer resource, gfx9 family
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base) {
@@ -794,7 +798,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& t
     // values (cpu_runner.rs:3224-3231). The SwiGLU values reuse an LDS slot
     // as [kChunk rows][kGemmRows / 2 values]; tile t of wave w holds values
     // (w * kWaveTiles + t) * 8 .. + 7.
-    constexpr int kActStride = C::kGemmRows / 2 + 1;
+    // (A padding float per row where it fits, against LDS bank conflicts.)
+    constexpr int kActStride =
+        C::kGemmRows / 2 + (C::kChunk * (C::kGemmRows / 2 + 1) * 4 <= C::kSlotBytes ? 1 : 0);
+    static_assert(C::kChunk * kActStride * 4 <= C::kSlotBytes, "SwiGLU values fit one code slot");
     // Lane pairs (even = gate row, odd = up row) hold both values for tokens
     // t0 = 2G and t1 = 2G + 1; the even lane finishes t0 and the odd lane t1.
     const bool odd = (nl & 1) != 0;
@@ -1316,6 +1323,7 @@ static hipError_t launch_gemm_cfg(GemmMode mode, const GemmArgs& a, int grid_wor
 hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int chunk, int grid_work, hipStream_t stream) {
   if (chunk == GemmSmall::kChunk) return launch_gemm_cfg<GemmSmall>(mode, a, grid_work, stream);
   if (chunk == GemmBig::kChunk) return launch_gemm_cfg<GemmBig>(mode, a, grid_work, stream);
+  if (chunk == GemmHuge::kChunk) return launch_gemm_cfg<GemmHuge>(mode, a, grid_work, stream);
   return hipErrorInvalidValue;
 }
 

@@ -91,8 +91,10 @@ def random_records(rng, m, blocks, kind):
 
 
 @pytest.mark.parametrize("kind", [G.ACT_RESIDUAL_Q8, G.ACT_Q8])
+# m <= 8, 8 < m < 512 and m >= 512 take the three GEMM geometries (8-, 16- and
+# 32-row work items); 600 = 18 x 32 + 24 leaves a ragged last item.
 @pytest.mark.parametrize("rows,blocks,m", [(1, 1, 1), (9, 5, 3), (17, 2, 9), (33, 7, 64), (70, 3, 65), (130, 4, 130),
-                                            (5760, 90, 2), (2880, 90, 11)])
+                                            (5760, 90, 2), (2880, 90, 11), (48, 6, 600), (130, 5, 512)])
 def test_matmul_bit_exact_tails(ctx, kind, rows, blocks, m):
     rng = np.random.default_rng(rows * 1000 + blocks * 10 + m)
     canonical = O.gen_mxfp4(rows, blocks, 1, rows, blocks)
