@@ -66,6 +66,7 @@ struct gossmx_ctx {
   uint64_t op_launches[GOSSMX_OP_COUNT] = {0};
   // scratch
   DevBuf x, injected, logits, selected, weights, act1v, act1s, bucket, route_tok, route_slot, work, act2v, act2s, y,
+      cnt,
       out, trace, rec, bias, mout;
 };
 
@@ -311,7 +312,7 @@ void gossmx_ctx_destroy(gossmx_ctx* ctx) {
   for (auto e : ctx->event_pool) hipEventDestroy(e);
   DevBuf* bufs[] = {&ctx->x, &ctx->injected, &ctx->logits, &ctx->selected, &ctx->weights, &ctx->act1v,
                     &ctx->act1s, &ctx->bucket, &ctx->route_tok, &ctx->route_slot, &ctx->work, &ctx->act2v,
-                    &ctx->act2s, &ctx->y, &ctx->out, &ctx->trace, &ctx->rec, &ctx->bias, &ctx->mout};
+                    &ctx->act2s, &ctx->y, &ctx->cnt, &ctx->out, &ctx->trace, &ctx->rec, &ctx->bias, &ctx->mout};
   for (DevBuf* b : bufs)
     if (b->p) hipFree(b->p);
   if (ctx->err) hipFree(ctx->err);
@@ -642,10 +643,16 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   ra.act = act1;
   ra.err = ctx->err;
   // Batches whose logits fit one work-group take the fused selection +
-  // dispatch kernel; the router projection (when the logits are not
-  // injected) stays a per-row kernel in front of it.
+  // dispatch kernel; larger ones a selection kernel with per-work-group
+  // expert counts and a placement kernel. The router projection (when the
+  // logits are not injected) is a kernel in front of either.
   const bool fused = m * (E + 1) <= (size_t)kSelectLds && R <= (size_t)kSelectMaxRoutes && K <= (size_t)kSelectTopK;
-  ra.select = fused ? 0 : 1;
+  int* cnt = nullptr;
+  if (!fused) {
+    const size_t n_sel = (m + select_rows_per_wg((int)E, (int)K) - 1) / select_rows_per_wg((int)E, (int)K);
+    if ((s = ensure(ctx, ctx->cnt, n_sel * E * 4))) return s;
+    cnt = static_cast<int*>(ctx->cnt.p);
+  }
   DispatchArgs da{};
   da.selected = selected;
   da.routes = (int)R;
@@ -657,18 +664,21 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   da.work = work;
   da.n_work = n_work;
   da.chunk = chunk;
-  if (!fused || injected == nullptr) {
+  if (injected == nullptr) {
     OpScope sc(ctx, GOSSMX_OP_ROUTER_ROUTING);
     HIP_TRY(launch_route(ra, ctx->stream), "route launch");
   }
   {
-    // In the fused path this stage also holds top-k, softmax and (with
-    // injected logits) the gate_up input quantization.
+    // This stage also holds top-k, softmax and (with injected logits) the
+    // gate_up input quantization.
     OpScope sc(ctx, GOSSMX_OP_DISPATCH);
-    if (fused)
-      HIP_TRY(launch_select_dispatch(ra, da, injected != nullptr ? 1 : 0, ctx->stream), "select/dispatch launch");
-    else
-      HIP_TRY(launch_dispatch(da, ctx->stream), "dispatch launch");
+    const int quantize = injected != nullptr ? 1 : 0;
+    if (fused) {
+      HIP_TRY(launch_select_dispatch(ra, da, quantize, ctx->stream), "select/dispatch launch");
+    } else {
+      HIP_TRY(launch_select_count(ra, quantize, cnt, ctx->stream), "select launch");
+      HIP_TRY(launch_place(da, (int)m, cnt, ctx->stream), "grouping launch");
+    }
   }
   GemmArgs g{};
   g.w = L->gate_up->t;

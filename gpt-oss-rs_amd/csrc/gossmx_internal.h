@@ -98,7 +98,6 @@ struct RouteArgs {
   float* weights;           // [m][top_k]
   ActBuffers act;           // gate_up input per token
   int* err;
-  int select;               // 1: top-k and softmax per row here; 0: logits only (select_dispatch follows)
 };
 
 struct DispatchArgs {
@@ -119,8 +118,15 @@ constexpr int kSelectMaxRoutes = 2048;  // m * top_k
 constexpr int kSelectTopK = 4;          // top_k (GPT-OSS routes to 4 experts)
 
 // Launchers (gossmx_kernels.hip). All are asynchronous on `stream`.
+// Router logits (bf16-rounded, into a.logits) and the gate_up input
+// quantization; followed by one of the two selection paths below.
 hipError_t launch_route(const RouteArgs& a, hipStream_t stream);
-hipError_t launch_dispatch(const DispatchArgs& a, hipStream_t stream);
+// Batches past the fused kernel's limits: selection with per-work-group
+// expert counts (cnt: ceil(m / select_rows_per_wg) x experts ints), then the
+// grouping. quantize = 1 adds the gate_up input quantization (no route_kernel).
+int select_rows_per_wg(int experts, int top_k);
+hipError_t launch_select_count(const RouteArgs& r, int quantize, int* cnt, hipStream_t stream);
+hipError_t launch_place(const DispatchArgs& a, int m, const int* cnt, hipStream_t stream);
 // Work-group 0: top-k, softmax and dispatch of all rows from r.injected (bf16
 // rounded here) or from the logits r.logits computed by launch_route with
 // select = 0. quantize = 1 adds the gate_up input quantization work-groups

@@ -154,65 +154,18 @@ __device__ __forceinline__ void residual_q8_store(float v, int l32, size_t row, 
 }
 
 // ---------------------------------------------------------------------------
-// Router projection, top-k and routing softmax (the first router_groups
-// work-groups of a row; with select = 0 only the bf16-rounded logits), and
-// the gate_up input quantization (the rest: 8 blocks of 32 values per
-// work-group, one per half wave), for row blockIdx.x (moe_batch routing loop,
-// cpu_runner.rs:2808-2854; quantize_residual_q8 of the row,
-// cpu_runner.rs:3224-3231).
+// Router projection and bias with the bf16-rounded logits (the first
+// router_groups work-groups of a row, one per 16 experts; the selection
+// kernels read the logits), and the gate_up input quantization (the rest: 8
+// blocks of 32 values per work-group, one per half wave), for row blockIdx.x
+// (moe_batch routing loop, cpu_runner.rs:2808-2854; quantize_residual_q8 of
+// the row, cpu_runner.rs:3224-3231).
 
 __device__ __forceinline__ bool route_better(float va, int ia, float vb, int ib) {
   return va > vb || (va == vb && ia < ib);  // stable_top_k order, cpu_runner.rs:3768-3778
 }
 
 constexpr int kRouteQuantBlocks = 8;  // quantized blocks per work-group (256 threads)
-
-// stable_top_k (cpu_runner.rs:3768-3778) and the routing softmax in rank
-// order (:3784-3795, then bf16 :2840-2843) of one row, by one wave. `lg` holds
-// the row's bf16-rounded logits and `s_k` is kMaxTopK ints of LDS owned by
-// the wave. Each lane owns experts lane and lane + 64; K rounds of a wave
-// argmax. NaN logits (already flagged as an error) rank as -inf so that every
-// round still returns a valid expert index. Writes sel[0..K) and w[0..K), and
-// sel_copy[0..K) when it is not null.
-__device__ __forceinline__ void select_row(const float* lg, int E, int K, int lane, int* s_k, int* sel, float* w,
-                                           int* sel_copy) {
-  bool taken0 = false, taken1 = false;
-  float v0 = lane < E ? lg[lane] : -INFINITY;
-  float v1 = lane + 64 < E ? lg[lane + 64] : -INFINITY;
-  if (isnan(v0)) v0 = -INFINITY;
-  if (isnan(v1)) v1 = -INFINITY;
-  for (int k = 0; k < K; ++k) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    if (lane < E && !taken0) { bv = v0; bi = lane; }
-    if (lane + 64 < E && !taken1 && route_better(v1, lane + 64, bv, bi)) { bv = v1; bi = lane + 64; }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oi = __shfl_xor(bi, o);
-      if (route_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-    }
-    if (bi < 0 || bi >= E) bi = 0;
-    if (bi == lane) taken0 = true;
-    if (bi == lane + 64) taken1 = true;
-    if (lane == 0) s_k[k] = bi;
-  }
-  if (lane == 0) {
-    float mx = -INFINITY;
-    for (int k = 0; k < K; ++k) mx = fmaxf(mx, lg[s_k[k]]);
-    float ex[kMaxTopK];
-    float sum = 0.0f;
-    for (int k = 0; k < K; ++k) {
-      ex[k] = expf_glibc(lg[s_k[k]] - mx);
-      sum = sum + ex[k];
-    }
-    for (int k = 0; k < K; ++k) {
-      sel[k] = s_k[k];
-      w[k] = bf16r(ex[k] / sum);
-      if (sel_copy) sel_copy[k] = s_k[k];
-    }
-  }
-}
 
 // Router projection staging: a pass covers kRouterGroup experts (16 chains
 // each = 256 threads) over kRouterChunk hidden elements held in LDS (x as
@@ -223,16 +176,14 @@ constexpr int kRouterChunk = 1440;  // multiple of 16 (chain lanes) and 8 (16-by
 constexpr int kRouterLoads = (kRouterGroup * kRouterChunk / 8 + 255) / 256;  // 16-byte reads per thread per chunk
 
 __host__ __device__ __forceinline__ int router_groups(const RouteArgs& a) {
-  return a.select ? 1 : (a.experts + kRouterGroup - 1) / kRouterGroup;
+  return (a.experts + kRouterGroup - 1) / kRouterGroup;
 }
 
-// Grid (m, router_groups + quantization groups). With select = 1 one
-// work-group per row computes every expert's logit and selects; with
-// select = 0 work-group (r, g) computes experts [16 g, 16 g + 16) of row r and
-// writes their bf16 logits for select_dispatch_kernel.
+// Grid (m, router_groups + quantization groups): work-group (r, g) computes
+// experts [16 g, 16 g + 16) of row r.
 __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   const int r = blockIdx.x, tid = threadIdx.x;
-  const int E = a.experts, H = a.hidden, K = a.top_k;
+  const int E = a.experts, H = a.hidden;
   const uint16_t* x = a.x + (size_t)r * H;
   const int n_router = router_groups(a);
   if ((int)blockIdx.y >= n_router) {
@@ -248,11 +199,10 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   }
   __shared__ float s_chain[kMaxExperts * 16];
   __shared__ float s_logit[kMaxExperts];
-  __shared__ int s_sel[kMaxTopK];
-  const int e_begin = a.select ? 0 : (int)blockIdx.y * kRouterGroup;
-  const int e_end = a.select ? E : min(E, e_begin + kRouterGroup);
+  const int e_begin = (int)blockIdx.y * kRouterGroup;
+  const int e_end = min(E, e_begin + kRouterGroup);
 
-  if (a.injected == nullptr) {
+  {
     // scalar_bf16_dot (lib.rs:1007-1029): 16 reduction lanes, lane j sums
     // w[i] * x[i] for i = j mod 16 in increasing i, multiply then add.
     __shared__ float s_x[kRouterChunk];
@@ -304,46 +254,30 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
       for (int j = 1; j < 16; ++j) s = s + s_chain[e * 16 + j];
       s_logit[e] = bf16r(s + a.router_b[e]);  // += bias (cpu_runner.rs:2781-2783), bf16 (:2829)
     }
-  } else {
-    for (int e = e_begin + tid; e < e_end; e += blockDim.x) s_logit[e] = bf16r(a.injected[(size_t)r * E + e]);
   }
   __syncthreads();
-  for (int e = e_begin + tid; e < e_end; e += blockDim.x) {
-    const float v = s_logit[e];
-    if (!isfinite(v)) atomicOr(a.err, kErrNonFiniteLogits);
-    if (a.logits) a.logits[(size_t)r * E + e] = v;
-  }
-
-  if (a.select && threadIdx.x < 64)
-    select_row(s_logit, E, K, threadIdx.x, s_sel, a.selected + (size_t)r * K, a.weights + (size_t)r * K, nullptr);
+  // The selection kernels check these logits for non-finite values.
+  for (int e = e_begin + tid; e < e_end; e += blockDim.x) a.logits[(size_t)r * E + e] = s_logit[e];
 }
 
 // ---------------------------------------------------------------------------
 // Stable grouping of routes by expert (stable_group_routes,
 // cpu_runner.rs:3780-3782): route i = row * top_k + rank goes to
-// bucket_off[e] + #{j < i : expert(j) == e}. One work-group of 1024 threads;
-// in-wave ranks come from one ballot per expert present in the wave.
+// bucket_off[e] + #{j < i : expert(j) == e}. Work-groups of 1024 threads; in
+// a wave, ranks come from one ballot per expert present in the wave.
 //
 // Work items: every bucket is cut into a.chunk-row chunks. Full chunks come
 // first (expert order), then the partial last chunks by descending size
 // (ties by expert), so the heaviest work items start first.
 
-// `sel` is the selected experts in route order (global memory or LDS).
-__device__ __forceinline__ void dispatch_body(const DispatchArgs& a, const int* sel) {
-  const int E = a.experts, R = a.routes;
+// From the per-expert totals s_tot (LDS): the bucket offsets s_off (LDS,
+// exclusive scan over experts) and, with `meta`, the global bucket_off, work
+// list and n_work. Waves 0 and 1 hold one expert per lane (kMaxExperts = 128).
+__device__ __forceinline__ void dispatch_offsets(const DispatchArgs& a, const int* s_tot, int* s_off, bool meta) {
+  const int E = a.experts;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  __shared__ int s_tot[kMaxExperts];
-  __shared__ int s_off[kMaxExperts];
   __shared__ int s_part[kMaxExperts];
-  __shared__ int s_run[kMaxExperts];
   __shared__ int s_scan[4];
-  __shared__ int s_wcnt[16][kMaxExperts];
-  for (int e = tid; e < kMaxExperts; e += 1024) { s_tot[e] = 0; s_run[e] = 0; }
-  __syncthreads();
-  for (int i = tid; i < R; i += 1024) atomicAdd(&s_tot[sel[i]], 1);
-  __syncthreads();
-  // Waves 0 and 1: lane = expert (kMaxExperts = 128). Inclusive scans of the
-  // row counts and of the full-chunk counts, then the carry of wave 0.
   int c = 0, full = 0, sc = 0, sf = 0;
   if (wave < 2) {
     c = tid < E ? s_tot[tid] : 0;
@@ -365,33 +299,45 @@ __device__ __forceinline__ void dispatch_body(const DispatchArgs& a, const int* 
     const int off = sc - c, full_before = sf - full;
     if (tid < E) {
       s_off[tid] = off;
-      a.bucket_off[tid] = off;
-      for (int i = 0; i < full; ++i) {
-        a.work[2 * (full_before + i)] = tid;
-        a.work[2 * (full_before + i) + 1] = i * a.chunk;
-      }
-      const int part = s_part[tid];
-      int parts = 0, before = 0;
-      for (int f = 0; f < E; ++f) {
-        const int pf = s_part[f];
-        parts += pf > 0;
-        before += pf > part || (pf == part && f < tid);
-      }
-      if (part > 0) {
-        a.work[2 * (total_full + before)] = tid;
-        a.work[2 * (total_full + before) + 1] = full * a.chunk;
-      }
-      if (tid == 0) {
-        *a.n_work = total_full + parts;
-        a.bucket_off[E] = s_scan[0] + s_scan[2];
+      if (meta) {
+        a.bucket_off[tid] = off;
+        for (int i = 0; i < full; ++i) {
+          a.work[2 * (full_before + i)] = tid;
+          a.work[2 * (full_before + i) + 1] = i * a.chunk;
+        }
+        const int part = s_part[tid];
+        int parts = 0, before = 0;
+        for (int f = 0; f < E; ++f) {
+          const int pf = s_part[f];
+          parts += pf > 0;
+          before += pf > part || (pf == part && f < tid);
+        }
+        if (part > 0) {
+          a.work[2 * (total_full + before)] = tid;
+          a.work[2 * (total_full + before) + 1] = full * a.chunk;
+        }
+        if (tid == 0) {
+          *a.n_work = total_full + parts;
+          a.bucket_off[E] = s_scan[0] + s_scan[2];
+        }
       }
     }
   }
   __syncthreads();
+}
+
+// Places routes [begin, end) of `sel` (global memory or LDS) in route order:
+// route i of expert e goes to s_base[e] + (its rank among the range's routes
+// of expert e). s_base (LDS) advances by each pass's counts.
+__device__ __forceinline__ void dispatch_place(const DispatchArgs& a, const int* sel, int begin, int end,
+                                               int* s_base) {
+  const int E = a.experts;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ int s_wcnt[16][kMaxExperts];
   const unsigned long long lt = (1ull << lane) - 1ull;
-  for (int base = 0; base < R; base += 1024) {
+  for (int base = begin; base < end; base += 1024) {  // uniform
     const int i = base + tid;
-    const int e = i < R ? sel[i] : -1;
+    const int e = i < end ? sel[i] : -1;
     for (int ee = lane; ee < E; ee += 64) s_wcnt[wave][ee] = 0;
     int rank = 0;
     unsigned long long pending = __ballot(e >= 0);
@@ -405,7 +351,7 @@ __device__ __forceinline__ void dispatch_body(const DispatchArgs& a, const int* 
     }
     __syncthreads();
     if (e >= 0) {
-      int pos = s_off[e] + s_run[e] + rank;
+      int pos = s_base[e] + rank;
       for (int w = 0; w < wave; ++w) pos += s_wcnt[w][e];
       a.route_tok[pos] = i / a.top_k;
       a.route_slot[pos] = i;
@@ -414,13 +360,26 @@ __device__ __forceinline__ void dispatch_body(const DispatchArgs& a, const int* 
     for (int ee = tid; ee < E; ee += 1024) {
       int add = 0;
       for (int w = 0; w < 16; ++w) add += s_wcnt[w][ee];
-      s_run[ee] += add;
+      s_base[ee] += add;
     }
     __syncthreads();
   }
 }
 
-__global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) { dispatch_body(a, a.selected); }
+// The whole grouping in one work-group; `sel` is the selected experts of
+// every route in route order (global memory or LDS).
+__device__ __forceinline__ void dispatch_body(const DispatchArgs& a, const int* sel) {
+  const int tid = threadIdx.x;
+  __shared__ int s_tot[kMaxExperts];
+  __shared__ int s_off[kMaxExperts];
+  for (int e = tid; e < kMaxExperts; e += 1024) s_tot[e] = 0;
+  __syncthreads();
+  for (int i = tid; i < a.routes; i += 1024) atomicAdd(&s_tot[sel[i]], 1);
+  __syncthreads();
+  dispatch_offsets(a, s_tot, s_off, true);
+  dispatch_place(a, sel, 0, a.routes, s_off);
+}
+
 
 // stable_top_k order (route_better) as one unsigned 64-bit key per (logit,
 // expert) for the fused kernel: NaN ranks as -inf and -0.0 as +0.0 (they
@@ -567,6 +526,86 @@ __global__ __launch_bounds__(1024) void select_dispatch_kernel(RouteArgs r, Disp
   }
   __syncthreads();
   dispatch_body(d, s_sel);
+}
+
+// Selection and grouping of batches past the fused kernel's limits, in two
+// launches. select_count_kernel: work-group w selects rows [w RW, w RW + RW)
+// with T = 1024 / RW lanes per row (RW a power of two with RW * (E + 1) <=
+// kSelectLds and RW * top_k <= 1024, so T >= top_k) and writes the per-expert
+// route counts of its rows to cnt[w][E]; work-groups past the selection ones
+// quantize the gate_up input when no route_kernel ran. place_kernel: work-group
+// w places the routes of the same rows at bucket_off[e] + (routes of expert e
+// in earlier work-groups) + (rank within its own routes); work-group 0 also
+// writes bucket_off and the work list.
+template <int KMAX>
+__global__ __launch_bounds__(1024) void select_count_kernel(RouteArgs r, int rows_per_wg, int n_sel, int* cnt) {
+  const int tid = threadIdx.x;
+  if ((int)blockIdx.x >= n_sel) {
+    const int blocks = r.hidden / kBlock;
+    const int g = ((int)blockIdx.x - n_sel) * kSelectQuantBlocks + (tid >> 5);
+    if (g < r.m * blocks) {  // uniform per half wave
+      const int row = g / blocks, b = g % blocks;
+      const float v = bf16_to_f32(r.x[(size_t)row * r.hidden + b * kBlock + (tid & 31)]);
+      if (!isfinite(v)) atomicOr(r.err, kErrNonFiniteInput);
+      residual_q8_store(v, tid & 31, (size_t)row, blocks, b, r.act);
+    }
+    return;
+  }
+  const int E = r.experts, K = r.top_k, stride = E + 1;
+  const int r0 = (int)blockIdx.x * rows_per_wg, nrows = min(rows_per_wg, r.m - r0);
+  __shared__ float s_lg[kSelectLds];
+  __shared__ int s_sel[1024];
+  __shared__ int s_cnt[kMaxExperts];
+  __shared__ uint64_t s_tab[32];
+  if (tid < 32) s_tab[tid] = kExp2Tab[tid];
+  if (tid < kMaxExperts) s_cnt[tid] = 0;
+  for (int i = tid; i < nrows * E; i += 1024) {
+    const size_t gi = (size_t)r0 * E + i;
+    float v;
+    if (r.injected != nullptr) {
+      v = bf16r(r.injected[gi]);
+      if (r.logits) r.logits[gi] = v;
+    } else {
+      v = r.logits[gi];
+    }
+    if (!isfinite(v)) atomicOr(r.err, kErrNonFiniteLogits);
+    s_lg[(i / E) * stride + i % E] = v;
+  }
+  __syncthreads();
+  const int T = 1024 / rows_per_wg;
+  const int lr = tid / T, j = tid % T;
+  const bool has_row = lr < nrows;
+  const int rr = has_row ? lr : 0;
+  select_row_lanes<KMAX>(s_lg + rr * stride, has_row, j, T, E, K, r.selected + (size_t)(r0 + rr) * K,
+                         r.weights + (size_t)(r0 + rr) * K, s_sel + rr * K, s_tab);
+  __syncthreads();
+  for (int i = tid; i < nrows * K; i += 1024) atomicAdd(&s_cnt[s_sel[i]], 1);
+  __syncthreads();
+  if (tid < E) cnt[(size_t)blockIdx.x * E + tid] = s_cnt[tid];
+}
+
+__global__ __launch_bounds__(1024) void place_kernel(DispatchArgs a, int routes_per_wg, int n_sel, const int* cnt) {
+  const int tid = threadIdx.x, E = a.experts, w = blockIdx.x;
+  __shared__ int s_tot[kMaxExperts];
+  __shared__ int s_pre[kMaxExperts];
+  __shared__ int s_off[kMaxExperts];
+  if (tid < kMaxExperts) {
+    int tot = 0, pre = 0;
+    if (tid < E)
+      for (int v = 0; v < n_sel; ++v) {
+        const int c = cnt[(size_t)v * E + tid];
+        tot += c;
+        if (v < w) pre += c;
+      }
+    s_tot[tid] = tot;
+    s_pre[tid] = pre;
+  }
+  __syncthreads();
+  dispatch_offsets(a, s_tot, s_off, w == 0);
+  if (tid < E) s_off[tid] += s_pre[tid];
+  __syncthreads();
+  const int begin = w * routes_per_wg;
+  dispatch_place(a, a.selected, begin, min(a.routes, begin + routes_per_wg), s_off);
 }
 
 // ---------------------------------------------------------------------------
@@ -1288,8 +1327,32 @@ hipError_t launch_route(const RouteArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_dispatch(const DispatchArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, stream, a);
+// Rows per selection work-group of the two-launch path (a power of two).
+int select_rows_per_wg(int experts, int top_k) {
+  int rw = 256;
+  while (rw > 16 && (rw * (experts + 1) > kSelectLds || rw * top_k > 1024)) rw >>= 1;
+  return rw;
+}
+
+hipError_t launch_select_count(const RouteArgs& r, int quantize, int* cnt, hipStream_t stream) {
+  const int rw = select_rows_per_wg(r.experts, r.top_k);
+  if (r.top_k > kMaxTopK || r.experts > kMaxExperts || rw * (r.experts + 1) > kSelectLds || rw * r.top_k > 1024 ||
+      1024 / rw > 64)
+    return hipErrorInvalidValue;
+  const int n_sel = (r.m + rw - 1) / rw;
+  const size_t qblocks = quantize ? (size_t)r.m * (r.hidden / kBlock) : 0;
+  const unsigned grid = (unsigned)n_sel + (unsigned)((qblocks + kSelectQuantBlocks - 1) / kSelectQuantBlocks);
+  if (r.top_k <= 4)
+    hipLaunchKernelGGL(select_count_kernel<4>, dim3(grid), dim3(1024), 0, stream, r, rw, n_sel, cnt);
+  else
+    hipLaunchKernelGGL(select_count_kernel<kMaxTopK>, dim3(grid), dim3(1024), 0, stream, r, rw, n_sel, cnt);
+  return hipGetLastError();
+}
+
+hipError_t launch_place(const DispatchArgs& a, int m, const int* cnt, hipStream_t stream) {
+  const int rw = select_rows_per_wg(a.experts, a.top_k);
+  const int n_sel = (m + rw - 1) / rw;
+  hipLaunchKernelGGL(place_kernel, dim3(n_sel), dim3(1024), 0, stream, a, rw * a.top_k, n_sel, cnt);
   return hipGetLastError();
 }
 
