@@ -1127,6 +1127,39 @@ __global__ __launch_bounds__(256) void tile_flags_kernel(TiledWeights w) {
 // Weighted combine by source row and rank (cpu_runner.rs:2959-2999):
 // out = 0; out += y_rank * w_rank in rank order; then bf16.
 
+// Eight consecutive outputs per thread: 16-byte bf16 loads of each rank's
+// row, two float4 stores. For 16-byte-aligned outputs (hidden % 8 == 0).
+__global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* y, const float* w, int top_k, int hidden,
+                                                      float* out, float* trace) {
+  const int r = blockIdx.y;
+  const int h = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (h >= hidden) return;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  for (int k = 0; k < top_k; ++k) {
+    const size_t slot = (size_t)r * top_k + k;
+    const u32x4 p = *reinterpret_cast<const u32x4*>(y + slot * hidden + h);
+    const float wk = w[slot];
+    float v[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      v[2 * q] = __uint_as_float(p[q] << 16);
+      v[2 * q + 1] = __uint_as_float(p[q] & 0xffff0000u);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = acc[e] + v[e] * wk;
+    if (trace) {
+      float4* t = reinterpret_cast<float4*>(trace + slot * hidden + h);
+      t[0] = make_float4(v[0], v[1], v[2], v[3]);
+      t[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+  }
+  float4* o = reinterpret_cast<float4*>(out + (size_t)r * hidden + h);
+  o[0] = make_float4(bf16r(acc[0]), bf16r(acc[1]), bf16r(acc[2]), bf16r(acc[3]));
+  o[1] = make_float4(bf16r(acc[4]), bf16r(acc[5]), bf16r(acc[6]), bf16r(acc[7]));
+}
+
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* y, const float* w, int top_k, int hidden,
                                                      float* out, float* trace) {
   const int r = blockIdx.y;
@@ -1398,8 +1431,14 @@ hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream) {
 
 hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int top_k, int hidden, float* out,
                           float* trace_down, hipStream_t stream) {
-  hipLaunchKernelGGL(combine_kernel, dim3(grid1d(hidden, 256), m), dim3(256), 0, stream, y, weights, top_k, hidden,
-                     out, trace_down);
+  const bool aligned = hidden % 8 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(out) % 16 == 0 && reinterpret_cast<uintptr_t>(trace_down) % 16 == 0;
+  if (aligned)
+    hipLaunchKernelGGL(combine8_kernel, dim3(grid1d(hidden / 8, 256), m), dim3(256), 0, stream, y, weights, top_k,
+                       hidden, out, trace_down);
+  else
+    hipLaunchKernelGGL(combine_kernel, dim3(grid1d(hidden, 256), m), dim3(256), 0, stream, y, weights, top_k,
+                       hidden, out, trace_down);
   return hipGetLastError();
 }
 
