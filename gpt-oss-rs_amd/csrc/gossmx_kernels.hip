@@ -609,23 +609,23 @@ __global__ __launch_bounds__(1024) void place_kernel(DispatchArgs a, int routes_
 }
 
 // ---------------------------------------------------------------------------
-// Expert GEMM on the resident v3 layout. One work-group = kWaves waves, one
-// 16-row weight tile per wave (kGemmRows rows), times one work item of at most
-// kChunk activation rows. Each lane owns one weight row (lane % 16) and two
-// activation rows per group of 8, and runs the reference's per-row float
-// chain in order:
+// Expert GEMM on the resident v3 layout. One work-group = C::kWaves waves,
+// C::kWaveTiles 16-row weight tiles per wave (C::kGemmRows rows), times one
+// work item of at most C::kChunk activation rows. Each lane owns one weight
+// row (lane % 16) per tile and two activation rows per group of 8, and runs
+// the reference's per-row float chain in order:
 //   total = bias; for each block: total += (p * ws) * ps; total += (r * ws) * rs
 // (mxfp4_residual_q8_gemv_rows lib.rs:673-696, scalar_matmul_range
 // matmul.rs:529-578).
 //
-// Pipeline: K advances in steps of kStep = 8 blocks, two 4-block groups of
-// the v3 layout. Each wave keeps its tile's nibbles (2 KiB per step, one
-// 16-byte load per lane and group) and scale dwords three steps deep in a
-// register ring. The step's activations (f16 codes and scales) move from
-// global memory into a ring of three LDS slots by DMA (buffer_load ... lds)
-// two steps ahead, published by one barrier per step. Every wave issues the
-// same vector-memory instructions in the same order, so one s_waitcnt
-// immediate covers every step, and all per-step addressing is scalar.
+// Pipeline: K advances in steps of C::kStep blocks (C::kGroups 4-block groups
+// of the v3 layout). Each wave keeps its tiles' nibbles (one 16-byte load per
+// lane, tile and group) and scale dwords three steps deep in a register ring.
+// The step's activations (f16 codes and scales) move from global memory into
+// a ring of three LDS slots by DMA (buffer_load ... lds) two steps ahead,
+// published by one barrier per step. Every wave issues the same vector-memory
+// instructions in the same order, so one s_waitcnt immediate covers every
+// step, and all per-step addressing is scalar.
 
 __device__ __forceinline__ half8 fp4x8_to_half8(uint32_t w) {
   const half2v h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0);
@@ -662,29 +662,36 @@ __device__ __forceinline__ float e8m0_select(uint32_t s) {
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
-constexpr int kWaves = 8;                   // waves per GEMM work-group
-constexpr int kGemmThreads = 64 * kWaves;   // 512
-constexpr int kSclSlot = 64 * kWaves;       // floats written by one step's scale DMA (a dword per lane)
+constexpr int kGemmMaxThreads = 512;        // largest GEMM work-group (8 waves)
 
 // Geometry of one GEMM instantiation. TILES 16-row weight tiles per wave,
 // work items of NTOK activation rows (NTOK / 8 MFMA token groups), K steps of
-// GROUPS 4-block groups. GemmBig (2 tiles, 16 rows, 8 blocks) serves every
-// batch; GemmSmall (1 tile, 8 rows, 16 blocks: twice the work-groups and half
-// the sequential steps) serves batches of at most 8 rows, whose work items
-// are one expert each and whose time is the weight stream's latency;
-// GemmHuge (2 tiles, 32 rows, 4 blocks) serves prefill-sized batches, where
-// the FP4->f16 conversion of a weight block is shared by four token groups.
-template <int TILES, int NTOK, int GROUPS>
+// GROUPS 4-block groups, WAVES waves per work-group, and MIN_WAVES waves per
+// SIMD that the register budget must allow.
+//  GemmBig (2 tiles, 16 rows, 4 blocks, 4 waves) serves batches of 9..511
+//    rows: 96 VGPRs and 27.7 KB of LDS give 5 work-groups per CU, 5 waves per
+//    SIMD to hide the LDS and MFMA latency of the ordered chain.
+//  GemmSmall (1 tile, 8 rows, 16 blocks, 8 waves) serves batches of at most 8
+//    rows, whose work items are one expert each and whose time is the weight
+//    stream's latency: many work-groups, few sequential steps.
+//  GemmHuge (2 tiles, 32 rows, 4 blocks, 8 waves) serves prefill-sized
+//    batches, where the FP4->f16 conversion of a weight block is shared by
+//    four token groups.
+template <int TILES, int NTOK, int GROUPS, int WAVES = 8, int MIN_WAVES = 4>
 struct GemmCfg {
+  static constexpr int kWaves = WAVES;                    // waves per work-group
+  static constexpr int kThreads = 64 * WAVES;
+  static constexpr int kMinWaves = MIN_WAVES;             // waves per SIMD the register budget must allow
+  static constexpr int kSclSlot = 64 * WAVES;             // floats written by one step's scale DMA (a dword per lane)
   static constexpr int kWaveTiles = TILES;
-  static constexpr int kWgTiles = kWaves * TILES;
+  static constexpr int kWgTiles = WAVES * TILES;
   static constexpr int kGemmRows = kTileRows * kWgTiles;  // weight rows per work-group
   static constexpr int kChunk = NTOK;                     // activation rows per work item
   static constexpr int kNtg = NTOK / 8;                   // MFMA token groups per work item
   static constexpr int kGroups = GROUPS;                  // 4-block groups per step
   static constexpr int kStep = 4 * GROUPS;                // K blocks per pipeline step
   static constexpr int kSlotBytes = kStep * NTOK * 2 * kBlock * 2;  // f16 codes of one step in LDS
-  static constexpr int kCodeDma = kSlotBytes / (16 * kGemmThreads);  // 16-byte DMA per lane per step
+  static constexpr int kCodeDma = kSlotBytes / (16 * kThreads);  // 16-byte DMA per lane per step
   // Vector-memory instructions per wave and step: weights GROUPS x (nibbles,
   // scale dword) per tile; activations kCodeDma code pieces + 1 scale dword.
   static constexpr int kLoadsW = 2 * GROUPS * TILES;
@@ -694,14 +701,14 @@ struct GemmCfg {
   // waited on.
   static constexpr int kWaitVm = 2 * kLoadsW + kLoadsD;
   static constexpr int kWaitDma = (kWaitVm & 15) | ((kWaitVm >> 4) << 14) | (7 << 4) | (15 << 8);
-  static_assert(kSlotBytes == kCodeDma * 16 * kGemmThreads, "code DMA covers a slot exactly");
+  static_assert(kSlotBytes == kCodeDma * 16 * kThreads, "code DMA covers a slot exactly");
   static_assert(kStep * NTOK * 2 <= kSclSlot, "one dword DMA per lane covers a step's scales");
   static_assert(NTOK % 8 == 0 && NTOK <= kChunkMax, "token groups of 8");
   static_assert(kGemmRows % 64 == 0, "a work-group's gate_up rows make whole 32-value down-input blocks");
   static_assert(kWaitVm < 64, "vmcnt field");
   static_assert((kStep - 1) * 2 * kBlock * 2 <= (int)kActSlack, "a last partial step reads inside the slack");
 };
-using GemmBig = GemmCfg<2, 16, 2>;
+using GemmBig = GemmCfg<2, 16, 1, 4, 5>;
 using GemmSmall = GemmCfg<1, 8, 4>;
 using GemmHuge = GemmCfg<2, 32, 1>;
 static_assert(GemmBig::kChunk == kChunk && GemmSmall::kChunk == kSmallChunk && GemmHuge::kChunk == kHugeChunk,
@@ -863,7 +870,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& t
     const int hw = tid >> 5, l32 = tid & 31;
     const int blocks_next = rows / kWgRows;
     constexpr int kBlocksPerWg = C::kGemmRows / 64;
-    for (int item = hw; item < count * kBlocksPerWg; item += kGemmThreads / 32) {
+    for (int item = hw; item < count * kBlocksPerWg; item += C::kThreads / 32) {
       const int c = item / kBlocksPerWg, h = item % kBlocksPerWg;
       if (blockIdx.x * kBlocksPerWg + h >= blocks_next) continue;  // uniform per half wave
       const float v = s_act[c * kActStride + h * kBlock + l32];
@@ -928,7 +935,7 @@ __device__ __forceinline__ void issue_dma(const KLoop<C>& k, int q_raw, char* co
   const int q = min(q_raw, k.nsteps - 1);
 #pragma unroll
   for (int i = 0; i < C::kCodeDma; ++i)
-    dma16(k.codes, codes + (i * kWaves + k.wave) * 1024, k.voff[i], q * (C::kStep * 2 * kBlock * 2));
+    dma16(k.codes, codes + (i * C::kWaves + k.wave) * 1024, k.voff[i], q * (C::kStep * 2 * kBlock * 2));
   dma4(k.scales, reinterpret_cast<char*>(scl) + k.wave * 256, k.soff, q * (C::kStep * 8));
 }
 
@@ -995,7 +1002,7 @@ __device__ __forceinline__ void k_loop(const KLoop<C>& k, Acc<C>& tot, char* c0,
 }
 
 template <class C, int MODE, bool RESIDUAL>
-__global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArgs a) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int nl = lane & 15, G = lane >> 4;
@@ -1014,7 +1021,7 @@ __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
   }
   // LDS ring of three steps, filled by DMA two steps ahead.
   __shared__ __align__(16) char s_codes0[C::kSlotBytes], s_codes1[C::kSlotBytes], s_codes2[C::kSlotBytes];
-  __shared__ __align__(16) float s_scl0[kSclSlot], s_scl1[kSclSlot], s_scl2[kSclSlot];
+  __shared__ __align__(16) float s_scl0[C::kSclSlot], s_scl1[C::kSclSlot], s_scl2[C::kSclSlot];
   __shared__ int s_row[C::kChunk];
   if (tid < C::kChunk) {
     int r = -1;
@@ -1028,7 +1035,7 @@ __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
   __syncthreads();
 
   const int rows = (int)a.w.rows, B = (int)a.w.blocks;
-  const int tile0 = (blockIdx.x * kWaves + wave) * C::kWaveTiles;
+  const int tile0 = (blockIdx.x * C::kWaves + wave) * C::kWaveTiles;
   const int n_tg = (count + 7) >> 3;
   const int nq4 = (B + 3) >> 2;
 
@@ -1069,7 +1076,7 @@ __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
     for (int tg = 0; tg < C::kNtg; ++tg) { tot[t][tg][0] = b0[t]; tot[t][tg][1] = b0[t]; }
 
   // DMA lane map, the same for every step. Code piece i of this wave fills
-  // slot bytes c * 16 with c = (i * kWaves + wave) * 64 + lane, i.e. block j,
+  // slot bytes c * 16 with c = (i * C::kWaves + wave) * 64 + lane, i.e. block j,
   // token group tg, k-slice g, vector v (row tg*8 + v/2, part v%2) in the
   // slot layout above; its source is piece (part, g) of the row's 128-byte
   // block record. Scale dword d = wave * 64 + lane holds half d % 2 of
@@ -1081,7 +1088,7 @@ __global__ __launch_bounds__(kGemmThreads, 4) void gemm_kernel(GemmArgs a) {
   k.scales = buffer_rsrc(a.acts);
 #pragma unroll
   for (int i = 0; i < C::kCodeDma; ++i) {
-    const int c = (i * kWaves + wave) * 64 + lane;
+    const int c = (i * C::kWaves + wave) * 64 + lane;
     const int ch = c >> 6, p = c & 63;
     const int j = ch / C::kNtg, tg = ch % C::kNtg, g = p >> 4, v = p & 15;
     const int t = tg * 8 + (v >> 1), part = v & 1;
@@ -1402,7 +1409,7 @@ hipError_t launch_select_dispatch(const RouteArgs& r, const DispatchArgs& d, int
 template <class C>
 static hipError_t launch_gemm_cfg(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream) {
   const dim3 grid((unsigned)((a.w.tiles + C::kWgTiles - 1) / C::kWgTiles), (unsigned)grid_work);
-  const dim3 block(kGemmThreads);
+  const dim3 block(C::kThreads);
   if (a.residual) {
     switch (mode) {
       case kPlain: hipLaunchKernelGGL((gemm_kernel<C, kPlain, true>), grid, block, 0, stream, a); break;
