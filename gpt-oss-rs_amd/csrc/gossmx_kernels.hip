@@ -671,9 +671,10 @@ constexpr int kGemmMaxThreads = 512;        // largest GEMM work-group (8 waves)
 //  GemmBig (2 tiles, 16 rows, 4 blocks, 4 waves) serves batches of 9..511
 //    rows: 96 VGPRs and 27.7 KB of LDS give 5 work-groups per CU, 5 waves per
 //    SIMD to hide the LDS and MFMA latency of the ordered chain.
-//  GemmSmall (1 tile, 8 rows, 16 blocks, 8 waves) serves batches of at most 8
+//  GemmSmall (1 tile, 8 rows, 8 blocks, 4 waves) serves batches of at most 8
 //    rows, whose work items are one expert each and whose time is the weight
-//    stream's latency: many work-groups, few sequential steps.
+//    stream's latency: 64-row work-groups (four times the big geometry's
+//    count per expert), 73 VGPRs, 5 work-groups per CU.
 //  GemmHuge (2 tiles, 32 rows, 4 blocks, 8 waves) serves prefill-sized
 //    batches, where the FP4->f16 conversion of a weight block is shared by
 //    four token groups.
@@ -709,7 +710,7 @@ struct GemmCfg {
   static_assert((kStep - 1) * 2 * kBlock * 2 <= (int)kActSlack, "a last partial step reads inside the slack");
 };
 using GemmBig = GemmCfg<2, 16, 1, 4, 5>;
-using GemmSmall = GemmCfg<1, 8, 4>;
+using GemmSmall = GemmCfg<1, 8, 2, 4, 5>;
 using GemmHuge = GemmCfg<2, 32, 1>;
 static_assert(GemmBig::kChunk == kChunk && GemmSmall::kChunk == kSmallChunk && GemmHuge::kChunk == kHugeChunk,
               "work item sizes");
