@@ -48,10 +48,10 @@ GATE_UP_BYTES = 2 * INTER * BLOCKS * 17   # 8,812,800 B per expert
 DOWN_BYTES = HIDDEN * BLOCKS * 17         # 4,406,400 B per expert
 SEED = 20251201
 # HBM bytes per gate_up launch measured with rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE on this workload (167,971 KiB x 2.0 + 3,152 KiB x 1.0, scaled by
+# WRITE_SIZE on this workload (166,485 KiB x 2.0 + 3,242 KiB x 1.0, scaled by
 # what the counters read for a 1 GiB device copy); bench.py cannot read
 # counters itself, so only the configuration that was profiled reports it.
-PMC_GATE_UP_TRAFFIC = {1: 339_094 * 1024}
+PMC_GATE_UP_TRAFFIC = {1: 336_212 * 1024}
 
 CONFIGS = {
     0: {"batch": 1, "layers": 12, "experts": 32, "routing": "router", "zipf": None, "roofline": "hbm",

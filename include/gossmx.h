@@ -185,11 +185,12 @@ typedef struct gossmx_moe_io {
 int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* layer, const gossmx_moe_io* io);
 
 /* Profiling with hipEvents on the context stream, in the reference's operation
- * vocabulary (CpuProfileOperation, cpu_profile.rs:30-51). Batches with
- * m * (experts + 1) <= 8448, m * top_k <= 2048 and top_k <= 4 run top-k, softmax and the
- * grouping in one kernel, recorded as GOSSMX_OP_DISPATCH; GOSSMX_OP_ROUTER_ROUTING
- * then holds the router projection and input quantization only, and has no
- * launch when the logits are injected. */
+ * vocabulary (CpuProfileOperation, cpu_profile.rs:30-51). Top-k, softmax and
+ * the grouping are recorded as GOSSMX_OP_DISPATCH on every path (one kernel
+ * when m * (experts + 1) <= 8448, m * top_k <= 2048 and top_k <= 4, two
+ * kernels otherwise). GOSSMX_OP_ROUTER_ROUTING holds the router projection
+ * and the input quantization only, and has no launch when the logits are
+ * injected; the quantization is then recorded under GOSSMX_OP_DISPATCH. */
 enum {
   GOSSMX_OP_ROUTER_ROUTING = 0,     /* RouterProjection + Routing + ResidualQ8Preparation */
   GOSSMX_OP_DISPATCH = 1,           /* stable_group_routes + bucket gather */
