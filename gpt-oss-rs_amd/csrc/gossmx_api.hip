@@ -596,7 +596,7 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
       (s = ensure(ctx, ctx->weights, R * 4)) || (s = ensure(ctx, ctx->act1v, m * B1 * 2 * kBlock * 2 + kActSlack)) ||
       (s = ensure(ctx, ctx->act1s, m * B1 * 8 + kActSlack)) || (s = ensure(ctx, ctx->bucket, (E + 1) * 4)) ||
       (s = ensure(ctx, ctx->route_tok, R * 4)) || (s = ensure(ctx, ctx->route_slot, R * 4)) ||
-      (s = ensure(ctx, ctx->work, (2 * max_work + 1) * 4)) ||
+      (s = ensure(ctx, ctx->work, (4 * max_work + 1) * 4)) ||
       (s = ensure(ctx, ctx->act2v, R * B2 * 2 * kBlock * 2 + kActSlack)) ||
       (s = ensure(ctx, ctx->act2s, R * B2 * 8 + kActSlack)) || (s = ensure(ctx, ctx->y, R * H * 2)))
     return s;
@@ -625,7 +625,7 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   float* weights = static_cast<float*>(ctx->weights.p);
   int* bucket = static_cast<int*>(ctx->bucket.p);
   int* work = static_cast<int*>(ctx->work.p);
-  int* n_work = work + 2 * max_work;
+  int* n_work = work + 4 * max_work;
   ActBuffers act1{static_cast<_Float16*>(ctx->act1v.p), static_cast<float*>(ctx->act1s.p)};
 
   RouteArgs ra{};
@@ -689,7 +689,6 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   g.residual = 1;
   g.work = work;
   g.n_work = n_work;
-  g.bucket_off = bucket;
   g.route_tok = da.route_tok;
   g.route_slot = da.route_slot;
   g.actv_next = static_cast<_Float16*>(ctx->act2v.p);

@@ -73,9 +73,8 @@ struct GemmArgs {
   int residual;          // 1 = residual-Q8 activations, 0 = Q8 (primary only)
   // work items
   int plain_expert, plain_m;          // kPlain
-  const int* work;                    // [n][2] (expert, chunk start)   (gate_up/down)
+  const int* work;                    // [n][4] (expert, first grouped route, rows, 0)   (gate_up/down)
   const int* n_work;
-  const int* bucket_off;              // [experts + 1]
   const int* route_tok;               // grouped route -> source row
   const int* route_slot;              // grouped route -> row * top_k + rank
   // outputs
@@ -106,7 +105,7 @@ struct DispatchArgs {
   int* bucket_off;      // [experts + 1]
   int* route_tok;       // [routes]
   int* route_slot;      // [routes]
-  int* work;            // [max_work][2] (expert, first row of the chunk)
+  int* work;            // [max_work][4] (expert, first grouped route, rows, 0): one record per item
   int* n_work;
   int chunk;            // rows per work item: kSmallChunk, kChunk or kHugeChunk (by batch size)
 };

@@ -301,10 +301,8 @@ __device__ __forceinline__ void dispatch_offsets(const DispatchArgs& a, const in
       s_off[tid] = off;
       if (meta) {
         a.bucket_off[tid] = off;
-        for (int i = 0; i < full; ++i) {
-          a.work[2 * (full_before + i)] = tid;
-          a.work[2 * (full_before + i) + 1] = i * a.chunk;
-        }
+        int4* const rec = reinterpret_cast<int4*>(a.work);
+        for (int i = 0; i < full; ++i) rec[full_before + i] = make_int4(tid, off + i * a.chunk, a.chunk, 0);
         const int part = s_part[tid];
         int parts = 0, before = 0;
         for (int f = 0; f < E; ++f) {
@@ -312,10 +310,7 @@ __device__ __forceinline__ void dispatch_offsets(const DispatchArgs& a, const in
           parts += pf > 0;
           before += pf > part || (pf == part && f < tid);
         }
-        if (part > 0) {
-          a.work[2 * (total_full + before)] = tid;
-          a.work[2 * (total_full + before) + 1] = full * a.chunk;
-        }
+        if (part > 0) rec[total_full + before] = make_int4(tid, off + full * a.chunk, part, 0);
         if (tid == 0) {
           *a.n_work = total_full + parts;
           a.bucket_off[E] = s_scan[0] + s_scan[2];
@@ -653,6 +648,16 @@ __device__ __forceinline__ half8 fp4x8_to_half8_scaled(uint32_t w, float scale) 
   return b;
 }
 
+// The scale operand of fp4x8_to_half8_scaled for E8M0 byte j of the dword s
+// (j a compile-time constant): one shift that moves the byte into the f32
+// exponent field. v_cvt_scalef32_pk_f16_fp4 reads only that field of its
+// scale operand (a probe over every FP4 byte, exponents 100..154 and set sign
+// and mantissa bits found no difference from the clean 2^(e - 127) scale), so
+// the neighbouring bytes that land in the sign and mantissa do not matter.
+__device__ __forceinline__ float e8m0_scale_operand(uint32_t s, int j) {
+  return __uint_as_float(j == 3 ? s >> 1 : s << (23 - 8 * j));
+}
+
 // e8m0_scale without branches (lib.rs:957-963).
 __device__ __forceinline__ float e8m0_select(uint32_t s) {
   const float normal = __uint_as_float(s << 23);
@@ -793,7 +798,7 @@ __device__ __forceinline__ void group_update(Acc<C>& tot, const char* codes, con
       for (int t = 0; t < C::kWaveTiles; ++t) {
         const uint32_t sb = (s[t] >> (8 * j)) & 0xffu;
         if (FAST) {
-          bop[t] = fp4x8_to_half8_scaled(v[t][j], __uint_as_float(sb << 23));
+          bop[t] = fp4x8_to_half8_scaled(v[t][j], e8m0_scale_operand(s[t], j));
           e8[t] = 0.0f;
         } else {
           bop[t] = fp4x8_to_half8(v[t][j]);
@@ -805,13 +810,68 @@ __device__ __forceinline__ void group_update(Acc<C>& tot, const char* codes, con
   }
 }
 
+// group_update for one token group, all 4 blocks present and the fast path,
+// software-pipelined by hand: the LDS reads of block j + 2 and the
+// conversion of block j + 1 are issued before the chain of block j, and the
+// MFMAs of block j + 1 right after it, so the LDS and MFMA latencies are
+// covered by a block's work instead of stalling each block. Every
+// accumulator sees the same operations in the same order as group_update.
+template <class C, bool RESIDUAL>
+__device__ __forceinline__ void group_update_pipelined(Acc<C>& tot, const char* codes, const float2* scl,
+                                                       const u32x4 (&v)[C::kWaveTiles],
+                                                       const uint32_t (&s)[C::kWaveTiles], const int jb,
+                                                       const int lane, const int G) {
+  const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  half8 aop[2];
+  float4 sc[3];
+  half8 bop[C::kWaveTiles];
+  f32x4 d[C::kWaveTiles];
+#define GOSSMX_LDS(J)                                                                               \
+  aop[(J) & 1] = *reinterpret_cast<const half8*>(codes + slot_chunk<C>(jb + (J), 0) * 1024 + lane * 16); \
+  sc[(J) % 3] = *reinterpret_cast<const float4*>(&scl[(jb + (J)) * C::kChunk + 2 * G]);
+#define GOSSMX_CVT(J)                                                                               \
+  _Pragma("unroll") for (int t = 0; t < C::kWaveTiles; ++t)                                        \
+      bop[t] = fp4x8_to_half8_scaled(v[t][(J)], e8m0_scale_operand(s[t], (J)));
+#define GOSSMX_MFMA(J)                                                                              \
+  _Pragma("unroll") for (int t = 0; t < C::kWaveTiles; ++t)                                        \
+      d[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop[(J) & 1], bop[t], zero, 0, 0, 0);
+#define GOSSMX_CHAIN(J)                                                                             \
+  _Pragma("unroll") for (int t = 0; t < C::kWaveTiles; ++t) {                                      \
+    const float4 c = sc[(J) % 3];                                                                   \
+    tot[t][0][0] = tot[t][0][0] + d[t][0] * c.x;                                                    \
+    if (RESIDUAL) tot[t][0][0] = tot[t][0][0] + d[t][1] * c.y;                                      \
+    tot[t][0][1] = tot[t][0][1] + d[t][2] * c.z;                                                    \
+    if (RESIDUAL) tot[t][0][1] = tot[t][0][1] + d[t][3] * c.w;                                      \
+  }
+  GOSSMX_LDS(0)
+  GOSSMX_LDS(1)
+  GOSSMX_CVT(0)
+  GOSSMX_MFMA(0)
+  GOSSMX_LDS(2)
+  GOSSMX_CVT(1)
+  GOSSMX_CHAIN(0)
+  GOSSMX_MFMA(1)
+  GOSSMX_LDS(3)
+  GOSSMX_CVT(2)
+  GOSSMX_CHAIN(1)
+  GOSSMX_MFMA(2)
+  GOSSMX_CVT(3)
+  GOSSMX_CHAIN(2)
+  GOSSMX_MFMA(3)
+  GOSSMX_CHAIN(3)
+#undef GOSSMX_LDS
+#undef GOSSMX_CVT
+#undef GOSSMX_MFMA
+#undef GOSSMX_CHAIN
+}
+
 // Shared GEMM epilogue: plain f32 stores, the down projection's bf16 rows,
 // or gate_up's SwiGLU and down-input quantization. `s_act` is LDS scratch of
 // at least count * (kGemmRows / 2 + 1) floats, free for reuse. Rows of tiles
 // past the end (row >= rows) are never stored.
 template <class C, int MODE>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& tot, const int n_tg, const int count,
-                                              const int start, const int route_base, const int tile0, float* s_act) {
+                                              const int start, const int tile0, float* s_act) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int nl = lane & 15, G = lane >> 4;
@@ -831,7 +891,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& t
               if (MODE == kPlain) {
                 a.out[(size_t)(start + c) * a.out_stride + row] = tot[t][tg][u];
               } else {
-                const int slot = a.route_slot[route_base + start + c];
+                const int slot = a.route_slot[start + c];
                 a.y[(size_t)slot * rows + row] = bf16_bits(tot[t][tg][u]);  // bf16 (cpu_runner.rs:2945-2947)
               }
             }
@@ -879,7 +939,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& t
       ActBuffers nx;
       nx.v = a.actv_next;
       nx.s = a.acts_next;
-      residual_q8_store(v, l32, (size_t)(route_base + start + c), blocks_next, blockIdx.x * kBlocksPerWg + h, nx);
+      residual_q8_store(v, l32, (size_t)(start + c), blocks_next, blockIdx.x * kBlocksPerWg + h, nx);
     }
   }
 }
@@ -947,8 +1007,12 @@ __device__ __forceinline__ void step_update(const KLoop<C>& k, Acc<C>& tot, cons
   const float2* s2 = reinterpret_cast<const float2*>(scl);
   if (C::kStep * q + C::kStep <= k.B) {
 #pragma unroll
-    for (int g = 0; g < C::kGroups; ++g)
-      group_update<C, RESIDUAL, NTG, FAST>(tot, codes, s2, w.v[g], w.s[g], 4 * g, 4, k.lane, k.G);
+    for (int g = 0; g < C::kGroups; ++g) {
+      if (NTG == 1 && FAST)
+        group_update_pipelined<C, RESIDUAL>(tot, codes, s2, w.v[g], w.s[g], 4 * g, k.lane, k.G);
+      else
+        group_update<C, RESIDUAL, NTG, FAST>(tot, codes, s2, w.v[g], w.s[g], 4 * g, 4, k.lane, k.G);
+    }
   } else {
 #pragma unroll
     for (int g = 0; g < C::kGroups; ++g) {
@@ -1007,39 +1071,29 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int nl = lane & 15, G = lane >> 4;
-  int expert, start, count, route_base = 0;
+  int expert, start, count;
   if (MODE == kPlain) {
     expert = a.plain_expert;
     start = blockIdx.y * C::kChunk;
     count = min(C::kChunk, a.plain_m - start);
   } else {
     const int wi = blockIdx.y;
-    if (wi >= *a.n_work) return;  // uniform over the work-group
-    expert = a.work[2 * wi];
-    start = a.work[2 * wi + 1];
-    route_base = a.bucket_off[expert];
-    count = min(C::kChunk, a.bucket_off[expert + 1] - route_base - start);
+    // The item count and the item's record in one round trip (records past
+    // the count are in bounds and ignored).
+    const int nw = *a.n_work;
+    const int4 rec = reinterpret_cast<const int4*>(a.work)[wi];
+    if (wi >= nw) return;  // uniform over the work-group
+    expert = rec.x;
+    start = rec.y;  // grouped index of the item's first route
+    count = rec.z;
   }
-  // LDS ring of three steps, filled by DMA two steps ahead.
-  __shared__ __align__(16) char s_codes0[C::kSlotBytes], s_codes1[C::kSlotBytes], s_codes2[C::kSlotBytes];
-  __shared__ __align__(16) float s_scl0[C::kSclSlot], s_scl1[C::kSclSlot], s_scl2[C::kSclSlot];
-  __shared__ int s_row[C::kChunk];
-  if (tid < C::kChunk) {
-    int r = -1;
-    if (tid < count) {
-      if (MODE == kPlain) r = start + tid;
-      else if (MODE == kGateUp) r = a.route_tok[route_base + start + tid];
-      else r = route_base + start + tid;
-    }
-    s_row[tid] = r;
-  }
-  __syncthreads();
-
   const int rows = (int)a.w.rows, B = (int)a.w.blocks;
   const int tile0 = (blockIdx.x * C::kWaves + wave) * C::kWaveTiles;
   const int n_tg = (count + 7) >> 3;
   const int nq4 = (B + 3) >> 2;
 
+  // Per-tile state first: its loads (fast-path flags, biases) only need the
+  // expert, so they are in flight together with the row indices below.
   KLoop<C> k;
   k.B = B;
   k.nsteps = (B + C::kStep - 1) / C::kStep;
@@ -1064,12 +1118,29 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
     const uint8_t* scl = a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)safe_tile * 64 * nq4;
     k.nib[t] = buffer_rsrc(nib);
     k.scl[t] = buffer_rsrc(scl);
-    fast = fast && (!ok || a.w.fast[(size_t)expert * a.w.tiles + tile] != 0);
+    const uint8_t tile_fast = a.w.fast[(size_t)expert * a.w.tiles + safe_tile];
+    fast = fast && (!ok || tile_fast != 0);
     const int row = tile * kTileRows + nl;
     float bias = 0.0f;
     if (a.bias != nullptr && ok && row < rows) bias = a.bias[(size_t)expert * a.bias_expert_stride + row];
     b0[t] = bias + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
   }
+
+  // LDS ring of three steps, filled by DMA two steps ahead.
+  __shared__ __align__(16) char s_codes0[C::kSlotBytes], s_codes1[C::kSlotBytes], s_codes2[C::kSlotBytes];
+  __shared__ __align__(16) float s_scl0[C::kSclSlot], s_scl1[C::kSclSlot], s_scl2[C::kSclSlot];
+  __shared__ int s_row[C::kChunk];
+  if (tid < C::kChunk) {
+    int r = -1;
+    if (tid < count) {
+      if (MODE == kPlain) r = start + tid;
+      else if (MODE == kGateUp) r = a.route_tok[start + tid];
+      else r = start + tid;
+    }
+    s_row[tid] = r;
+  }
+  __syncthreads();
+
   Acc<C> tot;
 #pragma unroll
   for (int t = 0; t < C::kWaveTiles; ++t)
@@ -1112,7 +1183,7 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
   // work-group ends.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  gemm_epilogue<C, MODE>(a, tot, n_tg, count, start, route_base, tile0, reinterpret_cast<float*>(s_codes0));
+  gemm_epilogue<C, MODE>(a, tot, n_tg, count, start, tile0, reinterpret_cast<float*>(s_codes0));
 }
 
 // Exactness flag per (expert, tile): 1 when every E8M0 byte of the tile's
