@@ -153,6 +153,57 @@ __device__ __forceinline__ void residual_q8_store(float v, int l32, size_t row, 
   }
 }
 
+// residual_q8_store for N blocks per half wave at once (block i is item
+// hw + i * stride: activation row first_row + item / per_row, block
+// first_blk + item % per_row); blocks with live[i] false are computed on
+// zeros and not stored. The same operations as residual_q8_store per block.
+template <int N>
+__device__ __forceinline__ void residual_q8_store_n(const float (&v)[N], const bool (&live)[N], int l32, int hw,
+                                                    int stride, int per_row, size_t first_row, int blocks,
+                                                    int first_blk, ActBuffers act) {
+  float mx[N], q[N], s[N], r[N], rq[N], rs[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) mx[i] = fabsf(v[i]);
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1)
+#pragma unroll
+    for (int i = 0; i < N; ++i) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], o));
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    s[i] = mx[i] / 127.0f;
+    const float inv = s[i] == 0.0f ? 0.0f : 1.0f / s[i];
+    q[i] = fminf(fmaxf(roundf(v[i] * inv), -127.0f), 127.0f);
+    r[i] = v[i] - q[i] * s[i];
+    mx[i] = fabsf(r[i]);
+  }
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1)
+#pragma unroll
+    for (int i = 0; i < N; ++i) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], o));
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    rs[i] = mx[i] / 127.0f;
+    const float inv = rs[i] == 0.0f ? 0.0f : 1.0f / rs[i];
+    rq[i] = fminf(fmaxf(roundf(r[i] * inv), -127.0f), 127.0f);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    if (!live[i]) continue;  // uniform per half wave
+    const int item = hw + i * stride;
+    const size_t row = first_row + item / per_row;
+    const int blk = first_blk + item % per_row;
+    _Float16* dst = act.v + ((row * blocks + blk) * 2) * kBlock;
+    dst[l32] = (_Float16)q[i];
+    dst[kBlock + l32] = (_Float16)rq[i];
+    if (l32 == 0) {
+      float2 sc;
+      sc.x = s[i];
+      sc.y = rs[i];
+      reinterpret_cast<float2*>(act.s)[row * blocks + blk] = sc;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Router projection and bias with the bf16-rounded logits (the first
 // router_groups work-groups of a row, one per 16 experts; the selection
@@ -931,16 +982,26 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& t
     const int hw = tid >> 5, l32 = tid & 31;
     const int blocks_next = rows / kWgRows;
     constexpr int kBlocksPerWg = C::kGemmRows / 64;
-    for (int item = hw; item < count * kBlocksPerWg; item += C::kThreads / 32) {
+    // Half wave hw quantizes blocks hw, hw + kHalfWaves, ... of the
+    // count x kBlocksPerWg; all of them at once, so that their shuffle and
+    // division chains overlap instead of running one block after another.
+    constexpr int kHalfWaves = C::kThreads / 32;
+    constexpr int kPer = (C::kChunk * kBlocksPerWg + kHalfWaves - 1) / kHalfWaves;
+    ActBuffers nx;
+    nx.v = a.actv_next;
+    nx.s = a.acts_next;
+    float v[kPer];
+    bool live[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int item = hw + i * kHalfWaves;
       const int c = item / kBlocksPerWg, h = item % kBlocksPerWg;
-      if (blockIdx.x * kBlocksPerWg + h >= blocks_next) continue;  // uniform per half wave
-      const float v = s_act[c * kActStride + h * kBlock + l32];
-      if (!isfinite(v)) atomicOr(a.err, kErrNonFiniteInput);
-      ActBuffers nx;
-      nx.v = a.actv_next;
-      nx.s = a.acts_next;
-      residual_q8_store(v, l32, (size_t)(start + c), blocks_next, blockIdx.x * kBlocksPerWg + h, nx);
+      live[i] = item < count * kBlocksPerWg && blockIdx.x * kBlocksPerWg + h < blocks_next;  // uniform per half wave
+      v[i] = live[i] ? s_act[c * kActStride + h * kBlock + l32] : 0.0f;
+      if (live[i] && !isfinite(v[i])) atomicOr(a.err, kErrNonFiniteInput);
     }
+    residual_q8_store_n<kPer>(v, live, l32, hw, kHalfWaves, kBlocksPerWg, (size_t)start, blocks_next,
+                              (int)blockIdx.x * kBlocksPerWg, nx);
   }
 }
 
