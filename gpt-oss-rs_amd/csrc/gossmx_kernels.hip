@@ -388,25 +388,32 @@ __device__ __forceinline__ void dispatch_place(const DispatchArgs& a, const int*
     int rank = 0;
     unsigned long long pending = __ballot(e >= 0);
     while (pending) {
+      // The leader lane is wave-uniform: a scalar read, not a shuffle.
       const int leader = __ffsll((long long)pending) - 1;
-      const int ee = __shfl(e, leader);
+      const int ee = __builtin_amdgcn_readlane(e, leader);
       const unsigned long long m = __ballot(e == ee);
       if (e == ee) rank = __popcll(m & lt);
       if (lane == 0) s_wcnt[wave][ee] = __popcll(m);
       pending &= ~m;
     }
     __syncthreads();
-    if (e >= 0) {
-      int pos = s_base[e] + rank;
-      for (int w = 0; w < wave; ++w) pos += s_wcnt[w][e];
-      a.route_tok[pos] = i / a.top_k;
-      a.route_slot[pos] = i;
+    // Per expert: the wave counts become the start of each wave's routes
+    // (s_base plus the counts of earlier waves); s_base advances past the pass.
+    for (int ee = tid; ee < E; ee += 1024) {
+      int run = s_base[ee];
+#pragma unroll
+      for (int w = 0; w < 16; ++w) {
+        const int c = s_wcnt[w][ee];
+        s_wcnt[w][ee] = run;
+        run += c;
+      }
+      s_base[ee] = run;
     }
     __syncthreads();
-    for (int ee = tid; ee < E; ee += 1024) {
-      int add = 0;
-      for (int w = 0; w < 16; ++w) add += s_wcnt[w][ee];
-      s_base[ee] += add;
+    if (e >= 0) {
+      const int pos = s_wcnt[wave][e] + rank;
+      a.route_tok[pos] = i / a.top_k;
+      a.route_slot[pos] = i;
     }
     __syncthreads();
   }
