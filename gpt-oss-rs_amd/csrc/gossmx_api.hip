@@ -66,7 +66,7 @@ struct gossmx_ctx {
   uint64_t op_launches[GOSSMX_OP_COUNT] = {0};
   // scratch
   DevBuf x, injected, logits, selected, weights, act1v, act1s, bucket, route_tok, route_slot, work, act2v, act2s, y,
-      cnt,
+      cnt, xn, normw, next,
       out, trace, rec, bias, mout;
 };
 
@@ -312,7 +312,8 @@ void gossmx_ctx_destroy(gossmx_ctx* ctx) {
   for (auto e : ctx->event_pool) hipEventDestroy(e);
   DevBuf* bufs[] = {&ctx->x, &ctx->injected, &ctx->logits, &ctx->selected, &ctx->weights, &ctx->act1v,
                     &ctx->act1s, &ctx->bucket, &ctx->route_tok, &ctx->route_slot, &ctx->work, &ctx->act2v,
-                    &ctx->act2s, &ctx->y, &ctx->cnt, &ctx->out, &ctx->trace, &ctx->rec, &ctx->bias, &ctx->mout};
+                    &ctx->act2s, &ctx->y, &ctx->cnt, &ctx->xn, &ctx->normw, &ctx->next, &ctx->out,
+                    &ctx->trace, &ctx->rec, &ctx->bias, &ctx->mout};
   for (DevBuf* b : bufs)
     if (b->p) hipFree(b->p);
   if (ctx->err) hipFree(ctx->err);
@@ -570,11 +571,20 @@ void gossmx_layer_destroy(gossmx_layer* L) {
   delete L;
 }
 
-int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_io* io) {
-  if (!ctx || !L || !io || !io->x || !io->output) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+// The MoE block; with norm_weight, also the decoder layer's post-attention
+// RMSNorm in front of it (io->x is then the residual stream) and the residual
+// add behind it into next_residual.
+static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_io* io,
+                            const float* norm_weight, float norm_eps, uint16_t* next_residual) {
+  const bool residual = norm_weight != nullptr;
+  if (!ctx || !L || !io || !io->x || (!io->output && !residual) || (residual && !next_residual))
+    return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
   if (io->memory != GOSSMX_MEM_HOST && io->memory != GOSSMX_MEM_DEVICE)
     return fail(GOSSMX_ERR_INVALID_ARGUMENT, "unknown memory kind %d", io->memory);
   if (io->m == 0) return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "empty MoE batch");
+  if (residual && L->cfg.hidden > (size_t)kNormMaxHidden)
+    return fail(GOSSMX_ERR_UNSUPPORTED, "hidden size %zu above the fused RMSNorm's %d", L->cfg.hidden,
+                kNormMaxHidden);
   if (ctx->capturing && io->memory == GOSSMX_MEM_HOST)
     return fail(GOSSMX_ERR_UNSUPPORTED, "host-memory calls cannot be captured");
   const size_t m = io->m, E = L->cfg.experts, H = L->cfg.hidden, I = L->cfg.intermediate, K = L->cfg.top_k;
@@ -615,11 +625,33 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
               "H2D logits");
       injected = static_cast<const float*>(ctx->injected.p);
     }
-    output = static_cast<float*>(ctx->out.p);
+    output = io->output ? static_cast<float*>(ctx->out.p) : nullptr;
     if (trace) {
       if ((s = ensure(ctx, ctx->trace, R * H * 4))) return s;
       trace = static_cast<float*>(ctx->trace.p);
     }
+  }
+  // Post-attention RMSNorm: the block runs on the normalized rows, the
+  // residual add reads the rows as given.
+  const uint16_t* resid = nullptr;
+  uint16_t* next = nullptr;
+  if (residual) {
+    if ((s = ensure(ctx, ctx->xn, m * H * 2))) return s;
+    const float* nw = norm_weight;
+    next = next_residual;
+    if (host) {
+      if ((s = ensure(ctx, ctx->normw, H * 4)) || (s = ensure(ctx, ctx->next, m * H * 2))) return s;
+      HIP_TRY(hipMemcpyAsync(ctx->normw.p, norm_weight, H * 4, hipMemcpyHostToDevice, ctx->stream), "H2D norm");
+      nw = static_cast<const float*>(ctx->normw.p);
+      next = static_cast<uint16_t*>(ctx->next.p);
+    }
+    {
+      OpScope sc(ctx, GOSSMX_OP_POST_ATTENTION_NORM);
+      HIP_TRY(launch_rmsnorm(x, nw, (int)m, (int)H, norm_eps, static_cast<uint16_t*>(ctx->xn.p), ctx->stream),
+              "RMSNorm launch");
+    }
+    resid = x;
+    x = static_cast<const uint16_t*>(ctx->xn.p);
   }
   int* selected = static_cast<int*>(ctx->selected.p);
   float* weights = static_cast<float*>(ctx->weights.p);
@@ -714,12 +746,16 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
   }
   {
     OpScope sc(ctx, GOSSMX_OP_WEIGHTING);
-    HIP_TRY(launch_combine(d.y, weights, (int)m, (int)K, (int)H, output, trace, ctx->stream), "combine launch");
+    HIP_TRY(launch_combine(d.y, weights, (int)m, (int)K, (int)H, output, trace, resid, next, ctx->stream),
+            "combine launch");
   }
 
   if (host) {
     if ((s = check_device_errors(ctx))) return s;
-    HIP_TRY(hipMemcpyAsync(io->output, output, m * H * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H output");
+    if (io->output)
+      HIP_TRY(hipMemcpyAsync(io->output, output, m * H * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H output");
+    if (residual)
+      HIP_TRY(hipMemcpyAsync(next_residual, next, m * H * 2, hipMemcpyDeviceToHost, ctx->stream), "D2H next");
     if (io->router_logits)
       HIP_TRY(hipMemcpyAsync(io->router_logits, logits, m * E * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H logits");
     if (io->selected)
@@ -740,6 +776,16 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_
       HIP_TRY(hipMemcpyAsync(io->route_order, da.route_slot, R * 4, hipMemcpyDeviceToDevice, ctx->stream), "D2D order");
   }
   return GOSSMX_OK;
+}
+
+int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_io* io) {
+  return moe_forward_impl(ctx, L, io, nullptr, 0.0f, nullptr);
+}
+
+int gossmx_moe_forward_residual(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_io* io,
+                                const float* norm_weight, float epsilon, uint16_t* next_residual) {
+  if (!norm_weight) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+  return moe_forward_impl(ctx, L, io, norm_weight, epsilon, next_residual);
 }
 
 // --- profiling, fault hook, self-test -------------------------------------------

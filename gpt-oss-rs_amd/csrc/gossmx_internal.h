@@ -19,6 +19,7 @@ constexpr int kHugeMinRows = 512;
 constexpr int kChunkMax = 32;
 constexpr int kMaxExperts = 128;
 constexpr int kMaxTopK = 8;
+constexpr int kNormMaxHidden = 8192;  // hidden sizes the fused post-attention RMSNorm stages in LDS
 
 // Device error flags (sticky until the host reads them).
 constexpr int kErrNonFiniteLogits = 1;
@@ -137,7 +138,10 @@ hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int chunk, int grid_wor
 hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream);
 
 hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int top_k, int hidden, float* out,
-                          float* trace_down, hipStream_t stream);
+                          float* trace_down, const uint16_t* resid, uint16_t* next, hipStream_t stream);
+// Post-attention RMSNorm rows -> bf16 (hidden <= kNormMaxHidden).
+hipError_t launch_rmsnorm(const uint16_t* x, const float* w, int m, int hidden, float eps, uint16_t* out,
+                          hipStream_t stream);
 hipError_t launch_prep_records(const uint8_t* records, int kind, size_t m, size_t blocks, size_t row_stride,
                                ActBuffers act, int* err, hipStream_t stream);
 hipError_t launch_repack(const uint8_t* src, int layout, TiledWeights w, hipStream_t stream);

@@ -1276,8 +1276,46 @@ __global__ __launch_bounds__(256) void tile_flags_kernel(TiledWeights w) {
 
 // Eight consecutive outputs per thread: 16-byte bf16 loads of each rank's
 // row, two float4 stores. For 16-byte-aligned outputs (hidden % 8 == 0).
+// Post-attention RMSNorm of the residual stream, rounded to bf16
+// (norm_boundary, cpu_runner.rs:2680-2687, over Kernels::rms_norm and
+// scalar_sum_squares, lib.rs:699-730, 1031-1043): lane l < 16 sums x_i * x_i
+// (multiply, then add) over i = l, l + 16, ... in order from +0.0; the lanes
+// are added 0..15; inverse = 1 / sqrt(sum / n + eps) with correctly rounded
+// division and square root; y_i = bf16((x_i * inverse) * w_i). One
+// work-group per row; the row is staged in LDS as f32.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const float* w, int hidden, float eps,
+                                                      uint16_t* out) {
+  __shared__ float s_x[kNormMaxHidden];
+  __shared__ float s_lane[16];
+  __shared__ float s_inv;
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const uint16_t* const xr = x + (size_t)r * hidden;
+  for (int i = tid; i < hidden; i += 256) s_x[i] = bf16_to_f32(xr[i]);
+  __syncthreads();
+  if (tid < 16) {
+    float acc = 0.0f;
+    for (int i = tid; i < hidden; i += 16) acc = acc + s_x[i] * s_x[i];
+    s_lane[tid] = acc;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float ss = -0.0f;
+    for (int l = 0; l < 16; ++l) ss = ss + s_lane[l];
+    s_inv = 1.0f / sqrtf(ss / (float)hidden + eps);
+  }
+  __syncthreads();
+  const float inv = s_inv;
+  uint16_t* const orow = out + (size_t)r * hidden;
+  for (int i = tid; i < hidden; i += 256) orow[i] = bf16_bits(s_x[i] * inv * w[i]);
+}
+
+// Combine (cpu_runner.rs:2959-2999): out = bf16(sum over ranks in order of
+// y_rank * w_rank), from 0.0. With `next`, also the residual add of the
+// decoder layer (add_residual, cpu_runner.rs:3732-3738): next =
+// bf16(resid + out). `out` may be null when only `next` is wanted.
 __global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* y, const float* w, int top_k, int hidden,
-                                                      float* out, float* trace) {
+                                                      float* out, float* trace, const uint16_t* resid,
+                                                      uint16_t* next) {
   const int r = blockIdx.y;
   const int h = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
   if (h >= hidden) return;
@@ -1302,13 +1340,30 @@ __global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* y, const 
       t[1] = make_float4(v[4], v[5], v[6], v[7]);
     }
   }
-  float4* o = reinterpret_cast<float4*>(out + (size_t)r * hidden + h);
-  o[0] = make_float4(bf16r(acc[0]), bf16r(acc[1]), bf16r(acc[2]), bf16r(acc[3]));
-  o[1] = make_float4(bf16r(acc[4]), bf16r(acc[5]), bf16r(acc[6]), bf16r(acc[7]));
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = bf16r(acc[e]);
+  if (out) {
+    float4* op = reinterpret_cast<float4*>(out + (size_t)r * hidden + h);
+    op[0] = make_float4(o[0], o[1], o[2], o[3]);
+    op[1] = make_float4(o[4], o[5], o[6], o[7]);
+  }
+  if (next) {
+    const u32x4 rp = *reinterpret_cast<const u32x4*>(resid + (size_t)r * hidden + h);
+    u32x4 np;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t lo = bf16_bits(__uint_as_float(rp[q] << 16) + o[2 * q]);
+      const uint32_t hi = bf16_bits(__uint_as_float(rp[q] & 0xffff0000u) + o[2 * q + 1]);
+      np[q] = lo | (hi << 16);
+    }
+    *reinterpret_cast<u32x4*>(next + (size_t)r * hidden + h) = np;
+  }
 }
 
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* y, const float* w, int top_k, int hidden,
-                                                     float* out, float* trace) {
+                                                     float* out, float* trace, const uint16_t* resid,
+                                                     uint16_t* next) {
   const int r = blockIdx.y;
   const int h = blockIdx.x * blockDim.x + threadIdx.x;
   if (h >= hidden) return;
@@ -1319,7 +1374,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* y, const f
     acc = acc + v * w[slot];
     if (trace) trace[slot * hidden + h] = v;
   }
-  out[(size_t)r * hidden + h] = bf16r(acc);
+  const float o = bf16r(acc);
+  if (out) out[(size_t)r * hidden + h] = o;
+  if (next) next[(size_t)r * hidden + h] = bf16_bits(bf16_to_f32(resid[(size_t)r * hidden + h]) + o);
 }
 
 // ---------------------------------------------------------------------------
@@ -1577,15 +1634,22 @@ hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream) {
 }
 
 hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int top_k, int hidden, float* out,
-                          float* trace_down, hipStream_t stream) {
-  const bool aligned = hidden % 8 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 &&
-                       reinterpret_cast<uintptr_t>(out) % 16 == 0 && reinterpret_cast<uintptr_t>(trace_down) % 16 == 0;
+                          float* trace_down, const uint16_t* resid, uint16_t* next, hipStream_t stream) {
+  const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  const bool aligned = hidden % 8 == 0 && a16(y) && a16(out) && a16(trace_down) && a16(resid) && a16(next);
   if (aligned)
     hipLaunchKernelGGL(combine8_kernel, dim3(grid1d(hidden / 8, 256), m), dim3(256), 0, stream, y, weights, top_k,
-                       hidden, out, trace_down);
+                       hidden, out, trace_down, resid, next);
   else
     hipLaunchKernelGGL(combine_kernel, dim3(grid1d(hidden, 256), m), dim3(256), 0, stream, y, weights, top_k,
-                       hidden, out, trace_down);
+                       hidden, out, trace_down, resid, next);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm(const uint16_t* x, const float* w, int m, int hidden, float eps, uint16_t* out,
+                          hipStream_t stream) {
+  if (hidden <= 0 || hidden > kNormMaxHidden) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(m), dim3(256), 0, stream, x, w, hidden, eps, out);
   return hipGetLastError();
 }
 

@@ -41,7 +41,7 @@ ACT_RESIDUAL_Q8 = 2
 MEM_HOST = 0
 MEM_DEVICE = 1
 
-OPS = ("router_routing", "dispatch", "gate_up", "down", "weighting", "matmul")
+OPS = ("router_routing", "dispatch", "gate_up", "down", "weighting", "matmul", "post_attention_norm")
 
 # The reference's activation records (lib.rs:732-742), 36 and 72 bytes.
 Q8_DTYPE = np.dtype([("scale", "<f4"), ("values", "i1", (32,))])
@@ -125,6 +125,7 @@ def load():
         "gossmx_layer_create": (i32, [vp, C.POINTER(MoeConfig), vp, vp, vp, vp, vp, vp, pp]),
         "gossmx_layer_destroy": (None, [vp]),
         "gossmx_moe_forward": (i32, [vp, vp, C.POINTER(MoeIo)]),
+        "gossmx_moe_forward_residual": (i32, [vp, vp, C.POINTER(MoeIo), vp, C.c_float, vp]),
         "gossmx_profile_enable": (i32, [vp, i32]),
         "gossmx_profile_read": (i32, [vp, C.POINTER(ProfileRecord), sz, C.POINTER(sz)]),
         "gossmx_profile_reset": (i32, [vp]),
@@ -413,6 +414,40 @@ class MoeLayer:
                    _ptr(res.get("trace_down")), MEM_HOST)
         _check(load().gossmx_moe_forward(self.ctx.handle, self._h, C.byref(io)))
         return res
+
+    def forward_residual(self, residual_bf16: np.ndarray, norm_weight: np.ndarray, epsilon: float = 1e-5,
+                         injected_logits: np.ndarray | None = None, want_output: bool = True) -> dict:
+        """The MoE half of a decoder layer (forward_layer_batch,
+        cpu_runner.rs:2519-2553) on the post-attention residual stream: the
+        block runs on norm_boundary(residual, norm_weight) and next_residual
+        [m][hidden] bf16 bits is add_residual(residual, output). The other
+        outputs are forward()'s; output is omitted with want_output=False."""
+        x = np.ascontiguousarray(residual_bf16, dtype=np.uint16)
+        w = np.ascontiguousarray(norm_weight, dtype=np.float32)
+        m = x.shape[0]
+        E, K, H = self.experts, self.top_k, self.hidden
+        res = {
+            "router_logits": np.zeros((m, E), np.float32),
+            "selected": np.zeros((m, K), np.uint32),
+            "routing_weights": np.zeros((m, K), np.float32),
+            "route_order": np.zeros(m * K, np.uint32),
+            "next_residual": np.zeros((m, H), np.uint16),
+        }
+        if want_output:
+            res["output"] = np.zeros((m, H), np.float32)
+        inj = None if injected_logits is None else np.ascontiguousarray(injected_logits, dtype=np.float32)
+        io = MoeIo(_ptr(x), m, _ptr(inj), _ptr(res["router_logits"]), _ptr(res["selected"]),
+                   _ptr(res["routing_weights"]), _ptr(res.get("output")), _ptr(res["route_order"]), None, MEM_HOST)
+        _check(load().gossmx_moe_forward_residual(self.ctx.handle, self._h, C.byref(io), _ptr(w), float(epsilon),
+                                                  _ptr(res["next_residual"])))
+        return res
+
+    def forward_residual_device(self, residual, m: int, norm_weight, epsilon: float, next_residual, output=None,
+                                injected_logits=None):
+        """forward_residual on device pointers (ints or torch tensors), asynchronous."""
+        io = MoeIo(_ptr(residual), m, _ptr(injected_logits), None, None, None, _ptr(output), None, None, MEM_DEVICE)
+        _check(load().gossmx_moe_forward_residual(self.ctx.handle, self._h, C.byref(io), _ptr(norm_weight),
+                                                  float(epsilon), _ptr(next_residual)))
 
     def forward_device(self, x, m: int, output, injected_logits=None, router_logits=None, selected=None,
                        routing_weights=None, route_order=None):

@@ -11,6 +11,9 @@
  *                                  constructors and validation matmul.rs:297-369
  *   - gossmx_moe_forward        <- CpuModel::moe_batch(layer, idx, inputs, capture, ...)
  *                                  crates/gpt-oss-model-runner/src/cpu_runner.rs:2794-3013
+ *   - gossmx_moe_forward_residual <- the MoE half of forward_layer_batch: norm_boundary of the
+ *                                  post-attention residual, moe_batch, add_residual
+ *                                  (cpu_runner.rs:2519-2553, 2680-2687, 3732-3738)
  *   - gossmx_weights_upload     <- CpuRepackCache::open_or_create + RepackedMxfp4::expert_view
  *                                  crates/gpt-oss-model-runner/src/cpu_repack.rs:149-216,302-318
  *                                  (the resident copy is a new GPU layout, see below)
@@ -184,6 +187,19 @@ typedef struct gossmx_moe_io {
 
 int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* layer, const gossmx_moe_io* io);
 
+/* The MoE half of a decoder layer on its residual stream (forward_layer_batch,
+ * cpu_runner.rs:2519-2553): io->x is after_attention [m][hidden] bf16, the
+ * block runs on norm_boundary(io->x, norm_weight) (the post-attention RMSNorm,
+ * Kernels::rms_norm lib.rs:699-730 with epsilon = rms_norm_eps, rounded to bf16,
+ * cpu_runner.rs:2680-2687), and next_residual [m][hidden] bf16 receives
+ * add_residual(io->x, output) (cpu_runner.rs:3732-3738), the next layer's
+ * input. norm_weight is the layer's post_attention_norm [hidden] f32. io->output
+ * may be null here; the other io fields are as in gossmx_moe_forward (router
+ * outputs and injected_logits refer to the normalized rows). norm_weight and
+ * next_residual are host or device memory as io->memory says. hidden <= 8192. */
+int gossmx_moe_forward_residual(gossmx_ctx* ctx, const gossmx_layer* layer, const gossmx_moe_io* io,
+                                const float* norm_weight, float epsilon, uint16_t* next_residual);
+
 /* Profiling with hipEvents on the context stream, in the reference's operation
  * vocabulary (CpuProfileOperation, cpu_profile.rs:30-51). Top-k, softmax and
  * the grouping are recorded as GOSSMX_OP_DISPATCH on every path (one kernel
@@ -198,7 +214,8 @@ enum {
   GOSSMX_OP_DOWN = 3,               /* DownProjection */
   GOSSMX_OP_WEIGHTING = 4,          /* ExpertWeightingAccumulation */
   GOSSMX_OP_MATMUL = 5,             /* gossmx_mxfp4_matmul kernel */
-  GOSSMX_OP_COUNT = 6
+  GOSSMX_OP_POST_ATTENTION_NORM = 6, /* PostAttentionNormalization (gossmx_moe_forward_residual) */
+  GOSSMX_OP_COUNT = 7
 };
 typedef struct gossmx_profile_record {
   int op;

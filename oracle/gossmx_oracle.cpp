@@ -616,6 +616,17 @@ void oracle_bf16_matvec(const uint16_t* w, size_t rows, size_t cols, const uint1
   for (size_t r = 0; r < rows; ++r) out[r] = bf16_dot(w + r * cols, x, cols);
 }
 void oracle_rms_norm(const float* in, const float* w, size_t n, float eps, float* out) { rms_norm(in, w, n, eps, out); }
+// norm_boundary, cpu_runner.rs:2680-2687: bf16 -> f32, rms_norm, -> bf16.
+void oracle_norm_boundary(const uint16_t* x, const float* w, size_t n, float eps, uint16_t* out) {
+  std::vector<float> in(n), o(n);
+  for (size_t i = 0; i < n; ++i) in[i] = bf16_to_f32(x[i]);
+  rms_norm(in.data(), w, n, eps, o.data());
+  for (size_t i = 0; i < n; ++i) out[i] = bf16_bits(o[i]);
+}
+// add_residual, cpu_runner.rs:3732-3738: bf16(residual.to_f32() + update).
+void oracle_add_residual(const uint16_t* residual, const float* update, size_t n, uint16_t* out) {
+  for (size_t i = 0; i < n; ++i) out[i] = bf16_bits(bf16_to_f32(residual[i]) + update[i]);
+}
 
 int oracle_swiglu(const float* gate_up, size_t intermediate, float alpha, float limit, float* out) {
   for (size_t i = 0; i < intermediate; ++i) out[i] = swiglu_one(gate_up[2 * i], gate_up[2 * i + 1], alpha, limit);

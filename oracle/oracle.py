@@ -83,6 +83,8 @@ def _declare(L):
         "oracle_bf16_matvec": (None, [vp, sz, sz, vp, vp]),
         "oracle_accumulate_mxfp4_bf16_block": (None, [vp, vp, vp]),
         "oracle_rms_norm": (None, [vp, vp, sz, f32, vp]),
+        "oracle_norm_boundary": (None, [vp, vp, sz, f32, vp]),
+        "oracle_add_residual": (None, [vp, vp, sz, vp]),
         "oracle_swiglu": (i32, [vp, sz, f32, f32, vp]),
         "oracle_stable_top_k": (None, [vp, sz, sz, vp]),
         "oracle_softmax": (None, [vp, sz, vp]),
@@ -297,3 +299,47 @@ def synthetic_layer(seed: int, layer: int, experts=32, hidden=2880, intermediate
 
 MXFP4_STREAM_GATE_UP = 4
 MXFP4_STREAM_DOWN = 5
+
+
+# ---------------------------------------------------------------------------
+# The MoE half of a decoder layer around moe_batch (forward_layer_batch,
+# cpu_runner.rs:2519-2553).
+
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """Kernels::rms_norm of one f32 row (lib.rs:699-730)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.zeros_like(x)
+    lib().oracle_rms_norm(_p(x), _p(w), x.size, np.float32(eps), _p(out))
+    return out
+
+
+def norm_boundary(x_bf16: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """norm_boundary (cpu_runner.rs:2680-2687) of every row: bf16 bits out."""
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.zeros_like(x)
+    for r in range(x.shape[0]):
+        lib().oracle_norm_boundary(_p(x[r]), _p(w), x.shape[1], np.float32(eps), _p(out[r]))
+    return out
+
+
+def add_residual(residual_bf16: np.ndarray, update: np.ndarray) -> np.ndarray:
+    """add_residual (cpu_runner.rs:3732-3738): bf16 bits of residual + update."""
+    r = np.ascontiguousarray(residual_bf16, np.uint16)
+    u = np.ascontiguousarray(update, np.float32)
+    out = np.zeros_like(r)
+    lib().oracle_add_residual(_p(r), _p(u), r.size, _p(out))
+    return out
+
+
+def moe_residual(layer: "MoeLayerHost", residual_bf16: np.ndarray, norm_weight: np.ndarray, eps: float,
+                 injected_logits=None) -> dict:
+    """norm_boundary -> moe_batch -> add_residual, as forward_layer_batch
+    runs them; moe_batch's outputs plus normalized and next_residual."""
+    normalized = norm_boundary(residual_bf16, norm_weight, eps)
+    res = moe_batch(layer, normalized, injected_logits=injected_logits)
+    res["normalized"] = normalized
+    if res["status"] == OK:
+        res["next_residual"] = add_residual(residual_bf16, res["output"])
+    return res

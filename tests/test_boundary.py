@@ -43,6 +43,7 @@ def test_null_arguments_are_rejected():
     L = G.load()
     assert L.gossmx_synchronize(None) == G.ERR_INVALID_ARGUMENT
     assert L.gossmx_moe_forward(None, None, None) == G.ERR_INVALID_ARGUMENT
+    assert L.gossmx_moe_forward_residual(None, None, None, None, 1e-5, None) == G.ERR_INVALID_ARGUMENT
     assert L.gossmx_mxfp4_matmul(None, None) == G.ERR_INVALID_ARGUMENT
     assert L.gossmx_inject_fault(None, 1) == G.ERR_INVALID_ARGUMENT
 

@@ -246,3 +246,85 @@ def test_profiler_counts_every_stage(ctx):
     for op in ("router_routing", "dispatch", "gate_up", "down", "weighting"):
         assert rec[op]["launches"] == 3 and rec[op]["total_ms"] > 0.0
     close(layer)
+
+
+def residual_stream(seed: int, m: int, hidden: int) -> np.ndarray:
+    """A post-attention residual stream: bf16 rows of N(0, 6^2), not normalized."""
+    return O.gen_bf16_normal(seed, 500 + m, m * hidden, 0.0, 6.0).reshape(m, hidden)
+
+
+def norm_weights(seed: int, hidden: int) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    return (1.0 + 0.25 * rng.standard_normal(hidden)).astype(np.float32)
+
+
+def assert_residual_equal(got, want, rows=None):
+    sel = slice(None) if rows is None else rows
+    for key in ("router_logits", "routing_weights", "output"):
+        if key not in got:
+            continue
+        g = np.ascontiguousarray(got[key][sel], np.float32).view(np.uint32)
+        w = np.ascontiguousarray(want[key], np.float32).view(np.uint32)
+        assert (g == w).all(), f"{key}: {int((g != w).sum())} mismatches"
+    assert (got["selected"][sel] == want["selected"]).all()
+    g = got["next_residual"][sel]
+    w = want["next_residual"]
+    assert (g == w).all(), f"next_residual: {int((g != w).sum())} mismatches, first {np.argwhere(g != w)[:3].tolist()}"
+
+
+@pytest.mark.parametrize("experts,hidden,inter,top_k,m", [(4, 96, 64, 2, 5), (8, 128, 96, 4, 17),
+                                                           (32, 256, 128, 4, 70)])
+def test_residual_small_layers_bit_exact(ctx, experts, hidden, inter, top_k, m):
+    """gossmx_moe_forward_residual = norm_boundary -> moe_batch -> add_residual
+    (cpu_runner.rs:2519-2553) against the oracle, every output bit-exact."""
+    host = O.synthetic_layer(13, 0, experts=experts, hidden=hidden, intermediate=inter, top_k=top_k)
+    x = residual_stream(13, m, hidden)
+    w = norm_weights(13, hidden)
+    want = O.moe_residual(host, x, w, 1e-5)
+    assert want["status"] == O.OK
+    layer = gpu_layer(ctx, host)
+    got = layer.forward_residual(x, w, 1e-5)
+    assert_residual_equal(got, want)
+    assert (got["route_order"] == want["route_order"]).all()
+    close(layer)
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_residual_20b_shape_bit_exact(layer20b, m):
+    host, layer = layer20b
+    x = residual_stream(2024, m, 2880)
+    w = norm_weights(2024, 2880)
+    want = O.moe_residual(host, x, w, 1e-5)
+    assert want["status"] == O.OK
+    assert_residual_equal(layer.forward_residual(x, w, 1e-5), want)
+
+
+def test_residual_20b_shape_batch64_rows_match(layer20b):
+    """configs[1] shape with injected Zipf(1.1) logits; only next_residual
+    requested (no f32 output); the oracle checks a sample of rows."""
+    host, layer = layer20b
+    rng = np.random.default_rng(65)
+    x = residual_stream(65, 64, 2880)
+    w = norm_weights(65, 2880)
+    logits = synth.zipf_logits(rng, 64, 32)
+    got = layer.forward_residual(x, w, 1e-5, injected_logits=logits, want_output=False)
+    assert "output" not in got
+    rows = [0, 31, 63]
+    want = O.moe_residual(host, x[rows], w, 1e-5, injected_logits=logits[rows])
+    assert_residual_equal(got, want, rows)
+
+
+def test_residual_zero_row_and_plain_forward_agree(layer20b):
+    """A zero residual row normalizes to zeros (sum 0: inverse 1/sqrt(eps));
+    and gossmx_moe_forward on the oracle's normalized rows gives the same
+    block outputs as the fused call."""
+    host, layer = layer20b
+    x = residual_stream(77, 3, 2880)
+    x[1] = 0
+    w = norm_weights(77, 2880)
+    fused = layer.forward_residual(x, w, 1e-5)
+    want = O.moe_residual(host, x, w, 1e-5)
+    assert_residual_equal(fused, want)
+    plain = layer.forward(want["normalized"])
+    for key in ("router_logits", "routing_weights", "output"):
+        assert (plain[key].view(np.uint32) == fused[key].view(np.uint32)).all(), key

@@ -341,6 +341,74 @@ def test_rms_norm_closed_form():
     assert np.allclose(out, 2.0 / math.sqrt(4.0 + 1e-5), rtol=1e-6)
 
 
+def _rms(x, w, eps):
+    x = np.asarray(x, np.float32)
+    return O.rms_norm(x, np.asarray(w, np.float32), eps)
+
+
+def test_rms_norm_sums_in_sixteen_lanes():
+    # scalar_sum_squares (lib.rs:1031-1043) keeps 16 lane sums. With x =
+    # [4096, 1 x 31]: lane 0 = 2^24 + 1 -> 2^24 (RNE), lanes 1..15 = 2, total
+    # 2^24 + 30. A sequential sum would stay at 2^24 (every + 1 rounds back).
+    x = np.ones(32, np.float32)
+    x[0] = 4096.0
+    out = _rms(x, np.ones(32), 0.0)
+    f = np.float32
+    lanes = f(1) / np.sqrt(f(16777246.0) / f(32))
+    sequential = f(1) / np.sqrt(f(16777216.0) / f(32))
+    assert lanes != sequential
+    assert out[1] == lanes  # x[1] = 1 and w[1] = 1: the output is the inverse itself
+
+
+def test_rms_norm_exact_rows_return_the_weights():
+    # Rows whose sum of squares, mean, root and inverse are exact: the output
+    # is 1 * w, bit for bit, for any weights (n = 16 and the 2880 of GPT-OSS).
+    rng = np.random.default_rng(7)
+    for n, v in ((16, 4.0), (2880, 2.0), (2880, 0.25)):
+        w = rng.standard_normal(n).astype(np.float32)
+        out = _rms(np.full(n, v), w, 0.0)
+        assert (out.view(np.uint32) == w.view(np.uint32)).all()
+
+
+def test_rms_norm_reference_weights_example():
+    # The reference's rms_norm_with_weights case (layers/norm.rs:217-228):
+    # [2, 2] with weights [0.5, 2] -> [0.5, 2.0] within 0.01; after the bf16
+    # boundary exactly.
+    out = _rms([2.0, 2.0], [0.5, 2.0], 1e-6)
+    assert abs(out[0] - 0.5) < 0.01 and abs(out[1] - 2.0) < 0.01
+    x = np.array([[O.bf16_bits(2.0), O.bf16_bits(2.0)]], np.uint16)
+    b = O.norm_boundary(x, np.array([0.5, 2.0], np.float32), 1e-6)
+    assert b.tolist() == [[0x3F00, 0x4000]]
+
+
+def test_rms_norm_multiplies_left_to_right():
+    # output = (x * inverse) * w (lib.rs:726-728), not x * (inverse * w): with
+    # x[0] = w[0] = 1 the first output is the inverse, and rows where the two
+    # orders differ show which one the oracle takes.
+    rng = np.random.default_rng(11)
+    f = np.float32
+    differ = 0
+    for _ in range(20):
+        x = rng.standard_normal(64).astype(np.float32) * f(3)
+        w = (rng.standard_normal(64).astype(np.float32) * f(0.7) + f(1)).astype(np.float32)
+        x[0], w[0] = 1.0, 1.0
+        out = _rms(x, w, 1e-5)
+        inv = out[0]
+        left = ((x * inv).astype(np.float32) * w).astype(np.float32)
+        right = (x * (inv * w).astype(np.float32)).astype(np.float32)
+        assert (out.view(np.uint32) == left.view(np.uint32)).all()
+        differ += int((left != right).sum())
+    assert differ > 0
+
+
+def test_add_residual_rounds_to_nearest_even():
+    # add_residual (cpu_runner.rs:3732-3738) = bf16(residual + update): ties
+    # of the bf16 grid (spacing 2^-7 at 1.0) go to the even mantissa.
+    res = np.array([0x3F80, 0x3F80, 0x3F80, 0xBF80], np.uint16)  # 1, 1, 1, -1
+    upd = np.array([2.0 ** -8, 3 * 2.0 ** -8, -2.0 ** -9, 1.0], np.float32)
+    assert O.add_residual(res, upd).tolist() == [0x3F80, 0x3F82, 0x3F80, 0x0000]
+
+
 def test_moe_one_hot_and_all_experts_invariants():
     # top_k == experts: every expert is used once per row, weights sum ~ 1.
     layer = tiny_layer(experts=3, hidden=64, intermediate=32, top_k=3)
