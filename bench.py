@@ -47,6 +47,7 @@ BLOCKS = HIDDEN // 32
 GATE_UP_BYTES = 2 * INTER * BLOCKS * 17   # 8,812,800 B per expert
 DOWN_BYTES = HIDDEN * BLOCKS * 17         # 4,406,400 B per expert
 SEED = 20251201
+RMS_EPS = 1e-5  # GPT-OSS rms_norm_eps
 # HBM bytes per gate_up launch measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE on this workload (166,485 KiB x 2.0 + 3,242 KiB x 1.0, scaled by
 # what the counters read for a 1 GiB device copy); bench.py cannot read
@@ -104,6 +105,9 @@ def build_workload(ctx, cfg: dict, rng):
             "logits_dev": None if logits is None else torch.from_numpy(logits).to(dev),
             "out_dev": torch.empty((m, HIDDEN), dtype=torch.float32, device=dev),
             "sel_dev": torch.empty((m, 4), dtype=torch.int32, device=dev),
+            # --residual: the layer's post-attention norm weight and the next residual stream
+            "norm_dev": torch.from_numpy((1.0 + 0.25 * rng.standard_normal(HIDDEN)).astype(np.float32)).to(dev),
+            "next_dev": torch.empty((m, HIDDEN), dtype=torch.int16, device=dev),
         })
     return x, x_dev, state
 
@@ -152,6 +156,9 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=None, help="override the config's batch")
     ap.add_argument("--zipf", type=float, default=None, help="override the config's Zipf exponent")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--residual", action="store_true",
+                    help="time gossmx_moe_forward_residual (post-attention RMSNorm + block + residual add) "
+                         "instead of the block alone; no CPU baseline")
     ap.add_argument("--no-graph", dest="graph", action="store_false",
                     help="time eager launches instead of the captured HIP graph of the step")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
@@ -189,7 +196,11 @@ def main() -> int:
 
     def step():
         for st in state:
-            st["moe"].forward_device(x_dev, m, st["out_dev"], injected_logits=st["logits_dev"])
+            if args.residual:
+                st["moe"].forward_residual_device(x_dev, m, st["norm_dev"], RMS_EPS, st["next_dev"],
+                                                  injected_logits=st["logits_dev"])
+            else:
+                st["moe"].forward_device(x_dev, m, st["out_dev"], injected_logits=st["logits_dev"])
 
     def timed(fn) -> float:
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -206,8 +217,12 @@ def main() -> int:
     with torch.cuda.stream(stream):
         # One untimed pass that also returns the selections (touched experts).
         for st in state:
-            st["moe"].forward_device(x_dev, m, st["out_dev"], injected_logits=st["logits_dev"],
-                                     selected=st["sel_dev"])
+            if args.residual:
+                st["moe"].forward_residual_device(x_dev, m, st["norm_dev"], RMS_EPS, st["next_dev"],
+                                                  injected_logits=st["logits_dev"], selected=st["sel_dev"])
+            else:
+                st["moe"].forward_device(x_dev, m, st["out_dev"], injected_logits=st["logits_dev"],
+                                         selected=st["sel_dev"])
         for _ in range(args.warmup):
             step()
         ctx.synchronize()
@@ -281,7 +296,10 @@ def main() -> int:
         "data": f"synthetic (seeded; random-init GPT-OSS-{'120B' if E == 128 else '20B'} MoE weights generated "
                 "on the device)",
         "config": {
-            "workload": cfg["workload"].format(**cfg),
+            "workload": cfg["workload"].format(**cfg) + (
+                "; MoE half of the decoder layer: post-attention RMSNorm + block + residual add"
+                if args.residual else ""),
+            "residual": bool(args.residual),
             "batch": m, "layers": L, "experts": E, "top_k": 4, "hidden": HIDDEN,
             "intermediate": INTER, "touched_experts": touched,
         },
@@ -294,7 +312,7 @@ def main() -> int:
         "launch": "hip-graph" if args.graph else "eager",
         "eager_ms_per_step": ms_eager / args.steps,
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not args.residual:
         result["cpu_baseline"] = cpu_baseline(cfg, x, state[0], out0, args.cpu_threads)
     if graph is not None:
         graph.close()

@@ -585,6 +585,9 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   if (residual && L->cfg.hidden > (size_t)kNormMaxHidden)
     return fail(GOSSMX_ERR_UNSUPPORTED, "hidden size %zu above the fused RMSNorm's %d", L->cfg.hidden,
                 kNormMaxHidden);
+  if (residual && io->memory == GOSSMX_MEM_DEVICE &&
+      (reinterpret_cast<uintptr_t>(io->x) % 16 != 0 || reinterpret_cast<uintptr_t>(norm_weight) % 16 != 0))
+    return fail(GOSSMX_ERR_INVALID_ARGUMENT, "device x and norm_weight must be 16-byte aligned");
   if (ctx->capturing && io->memory == GOSSMX_MEM_HOST)
     return fail(GOSSMX_ERR_UNSUPPORTED, "host-memory calls cannot be captured");
   const size_t m = io->m, E = L->cfg.experts, H = L->cfg.hidden, I = L->cfg.intermediate, K = L->cfg.top_k;
@@ -635,6 +638,7 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   // residual add reads the rows as given.
   const uint16_t* resid = nullptr;
   uint16_t* next = nullptr;
+  const float* route_norm_w = nullptr;
   if (residual) {
     if ((s = ensure(ctx, ctx->xn, m * H * 2))) return s;
     const float* nw = norm_weight;
@@ -645,13 +649,17 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
       nw = static_cast<const float*>(ctx->normw.p);
       next = static_cast<uint16_t*>(ctx->next.p);
     }
-    {
+    resid = x;
+    if (injected) {
+      // No router kernel runs: a kernel of its own normalizes the rows.
       OpScope sc(ctx, GOSSMX_OP_POST_ATTENTION_NORM);
       HIP_TRY(launch_rmsnorm(x, nw, (int)m, (int)H, norm_eps, static_cast<uint16_t*>(ctx->xn.p), ctx->stream),
               "RMSNorm launch");
+      x = static_cast<const uint16_t*>(ctx->xn.p);
+    } else {
+      // The router kernel normalizes each row as it reads it.
+      route_norm_w = nw;
     }
-    resid = x;
-    x = static_cast<const uint16_t*>(ctx->xn.p);
   }
   int* selected = static_cast<int*>(ctx->selected.p);
   float* weights = static_cast<float*>(ctx->weights.p);
@@ -665,6 +673,8 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   ra.router_w = L->router_w;
   ra.router_b = L->router_b;
   ra.injected = injected;
+  ra.norm_w = route_norm_w;
+  ra.norm_eps = norm_eps;
   ra.m = (int)m;
   ra.hidden = (int)H;
   ra.experts = (int)E;

@@ -92,6 +92,8 @@ struct RouteArgs {
   const uint16_t* router_w; // [experts][hidden]
   const float* router_b;    // [experts]
   const float* injected;    // [m][experts] or null
+  const float* norm_w;      // [hidden] post-attention RMSNorm weight (route_kernel), or null
+  float norm_eps;
   int m, hidden, experts, top_k;
   float* logits;            // [m][experts]
   int* selected;            // [m][top_k]

@@ -232,17 +232,59 @@ __host__ __device__ __forceinline__ int router_groups(const RouteArgs& a) {
 
 // Grid (m, router_groups + quantization groups): work-group (r, g) computes
 // experts [16 g, 16 g + 16) of row r.
+// The inverse RMS of row xr (hidden H, a multiple of 8, 16-byte aligned) as
+// rmsnorm_kernel computes it, by a whole 256-thread work-group (every thread
+// calls it and gets the value): the row is staged in LDS with 16-byte loads,
+// then 16 threads run the lane sums.
+__device__ __forceinline__ float row_inverse_rms(const uint16_t* xr, int H, float eps) {
+  __shared__ __align__(16) uint16_t s_row[kNormMaxHidden];
+  __shared__ float s_lane[16];
+  __shared__ float s_inv;
+  const int tid = threadIdx.x;
+#pragma unroll 4
+  for (int v = tid; v < H / 8; v += 256)
+    reinterpret_cast<u32x4*>(s_row)[v] = reinterpret_cast<const u32x4*>(xr)[v];
+  __syncthreads();
+  if (tid < 16) {
+    float acc = 0.0f;
+#pragma unroll 16
+    for (int i = tid; i < H; i += 16) {
+      const float v = bf16_to_f32(s_row[i]);
+      acc = acc + v * v;
+    }
+    s_lane[tid] = acc;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float ss = -0.0f;
+    for (int l = 0; l < 16; ++l) ss = ss + s_lane[l];
+    s_inv = 1.0f / sqrtf(ss / (float)H + eps);
+  }
+  __syncthreads();
+  return s_inv;
+}
+
+// x_i of the router's input: the row as given, or with a.norm_w the
+// post-attention RMSNorm of it rounded to bf16 (norm_boundary).
+__device__ __forceinline__ float route_input(const RouteArgs& a, float xf, int i, float inv) {
+  return a.norm_w ? bf16r(xf * inv * a.norm_w[i]) : xf;
+}
+
 __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   const int r = blockIdx.x, tid = threadIdx.x;
   const int E = a.experts, H = a.hidden;
   const uint16_t* x = a.x + (size_t)r * H;
   const int n_router = router_groups(a);
+  // With the fused post-attention RMSNorm every work-group of the row first
+  // computes the row's inverse RMS (uniform branch).
+  const float inv = a.norm_w ? row_inverse_rms(x, H, a.norm_eps) : 1.0f;
   if ((int)blockIdx.y >= n_router) {
     const int hw = tid >> 5, l32 = tid & 31;
     const int blocks = H / kBlock;
     const int b = ((int)blockIdx.y - n_router) * kRouteQuantBlocks + hw;
     if (b < blocks) {  // uniform per half wave
-      const float v = bf16_to_f32(x[b * kBlock + l32]);
+      const int i = b * kBlock + l32;
+      const float v = route_input(a, bf16_to_f32(x[i]), i, inv);
       if (!isfinite(v)) atomicOr(a.err, kErrNonFiniteInput);
       residual_q8_store(v, l32, (size_t)r, blocks, b, a.act);
     }
@@ -278,8 +320,12 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
           const int re = p / pieces, q = p - re * pieces;
           wv[k] = *reinterpret_cast<const u32x4*>(a.router_w + (size_t)(g0 + re) * H + c0 + q * 8);
         }
+        float nv[kRouterChunk / 256 + 1];  // norm weights of the same elements (fused RMSNorm)
 #pragma unroll
-        for (int k = 0; k < kRouterChunk / 256 + 1; ++k) xv[k] = x[c0 + min(tid + k * 256, len - 1)];
+        for (int k = 0; k < kRouterChunk / 256 + 1; ++k) {
+          xv[k] = x[c0 + min(tid + k * 256, len - 1)];
+          nv[k] = a.norm_w ? a.norm_w[c0 + min(tid + k * 256, len - 1)] : 1.0f;
+        }
         __syncthreads();  // the previous chunk's readers are done
 #pragma unroll
         for (int k = 0; k < kRouterLoads; ++k) {
@@ -288,8 +334,11 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
           *reinterpret_cast<u32x4*>(&s_w[re * kRouterChunk + q * 8]) = wv[k];
         }
 #pragma unroll
-        for (int k = 0; k < kRouterChunk / 256 + 1; ++k)
-          s_x[min(tid + k * 256, len - 1)] = __uint_as_float(xv[k] << 16);
+        for (int k = 0; k < kRouterChunk / 256 + 1; ++k) {
+          const int idx = min(tid + k * 256, len - 1);
+          const float xf = __uint_as_float(xv[k] << 16);
+          s_x[idx] = a.norm_w ? bf16r(xf * inv * nv[k]) : xf;
+        }
         __syncthreads();
         if (ge < ng) {
           const uint16_t* w = s_w + ge * kRouterChunk;
@@ -1282,18 +1331,36 @@ __global__ __launch_bounds__(256) void tile_flags_kernel(TiledWeights w) {
 // (multiply, then add) over i = l, l + 16, ... in order from +0.0; the lanes
 // are added 0..15; inverse = 1 / sqrt(sum / n + eps) with correctly rounded
 // division and square root; y_i = bf16((x_i * inverse) * w_i). One
-// work-group per row; the row is staged in LDS as f32.
+// work-group per row; the row and the weights are staged in LDS as f32.
+// hidden must be a multiple of 8 and x, w, out 16-byte aligned.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const float* w, int hidden, float eps,
                                                       uint16_t* out) {
-  __shared__ float s_x[kNormMaxHidden];
+  __shared__ __align__(16) float s_x[kNormMaxHidden];
+  __shared__ __align__(16) float s_w[kNormMaxHidden];
   __shared__ float s_lane[16];
   __shared__ float s_inv;
   const int r = blockIdx.x, tid = threadIdx.x;
-  const uint16_t* const xr = x + (size_t)r * hidden;
-  for (int i = tid; i < hidden; i += 256) s_x[i] = bf16_to_f32(xr[i]);
+  const int n8 = hidden / 8;  // hidden is a multiple of 32
+  const u32x4* const xr = reinterpret_cast<const u32x4*>(x + (size_t)r * hidden);
+  const float4* const w4 = reinterpret_cast<const float4*>(w);
+  // Row and weights to LDS with 16-byte loads, all issued before the first
+  // LDS write.
+#pragma unroll 4
+  for (int v = tid; v < n8; v += 256) {
+    const u32x4 p = xr[v];
+    const float4 wa = w4[2 * v], wb = w4[2 * v + 1];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      s_x[8 * v + 2 * q] = __uint_as_float(p[q] << 16);
+      s_x[8 * v + 2 * q + 1] = __uint_as_float(p[q] & 0xffff0000u);
+    }
+    reinterpret_cast<float4*>(s_w)[2 * v] = wa;
+    reinterpret_cast<float4*>(s_w)[2 * v + 1] = wb;
+  }
   __syncthreads();
   if (tid < 16) {
     float acc = 0.0f;
+#pragma unroll 16
     for (int i = tid; i < hidden; i += 16) acc = acc + s_x[i] * s_x[i];
     s_lane[tid] = acc;
   }
@@ -1305,8 +1372,17 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const f
   }
   __syncthreads();
   const float inv = s_inv;
-  uint16_t* const orow = out + (size_t)r * hidden;
-  for (int i = tid; i < hidden; i += 256) orow[i] = bf16_bits(s_x[i] * inv * w[i]);
+  u32x4* const orow = reinterpret_cast<u32x4*>(out + (size_t)r * hidden);
+#pragma unroll 4
+  for (int v = tid; v < n8; v += 256) {
+    u32x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = 8 * v + 2 * q;
+      o[q] = (uint32_t)bf16_bits(s_x[i] * inv * s_w[i]) | ((uint32_t)bf16_bits(s_x[i + 1] * inv * s_w[i + 1]) << 16);
+    }
+    orow[v] = o;
+  }
 }
 
 // Combine (cpu_runner.rs:2959-2999): out = bf16(sum over ranks in order of
@@ -1648,7 +1724,9 @@ hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int to
 
 hipError_t launch_rmsnorm(const uint16_t* x, const float* w, int m, int hidden, float eps, uint16_t* out,
                           hipStream_t stream) {
-  if (hidden <= 0 || hidden > kNormMaxHidden) return hipErrorInvalidValue;
+  const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  if (hidden <= 0 || hidden > kNormMaxHidden || hidden % 8 != 0 || !a16(x) || !a16(w) || !a16(out))
+    return hipErrorInvalidValue;
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(m), dim3(256), 0, stream, x, w, hidden, eps, out);
   return hipGetLastError();
 }

@@ -443,9 +443,10 @@ class MoeLayer:
         return res
 
     def forward_residual_device(self, residual, m: int, norm_weight, epsilon: float, next_residual, output=None,
-                                injected_logits=None):
+                                injected_logits=None, selected=None):
         """forward_residual on device pointers (ints or torch tensors), asynchronous."""
-        io = MoeIo(_ptr(residual), m, _ptr(injected_logits), None, None, None, _ptr(output), None, None, MEM_DEVICE)
+        io = MoeIo(_ptr(residual), m, _ptr(injected_logits), None, _ptr(selected), None, _ptr(output), None, None,
+                   MEM_DEVICE)
         _check(load().gossmx_moe_forward_residual(self.ctx.handle, self._h, C.byref(io), _ptr(norm_weight),
                                                   float(epsilon), _ptr(next_residual)))
 

@@ -196,7 +196,8 @@ int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* layer, const gossmx_
  * input. norm_weight is the layer's post_attention_norm [hidden] f32. io->output
  * may be null here; the other io fields are as in gossmx_moe_forward (router
  * outputs and injected_logits refer to the normalized rows). norm_weight and
- * next_residual are host or device memory as io->memory says. hidden <= 8192. */
+ * next_residual are host or device memory as io->memory says; in device memory
+ * io->x and norm_weight must be 16-byte aligned. hidden <= 8192. */
 int gossmx_moe_forward_residual(gossmx_ctx* ctx, const gossmx_layer* layer, const gossmx_moe_io* io,
                                 const float* norm_weight, float epsilon, uint16_t* next_residual);
 
