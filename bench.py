@@ -156,6 +156,8 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=None, help="override the config's batch")
     ap.add_argument("--zipf", type=float, default=None, help="override the config's Zipf exponent")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--host-steps", type=int, default=3,
+                    help="steps of the host-memory (PCIe-inclusive) rate reported beside value; 0 skips it")
     ap.add_argument("--residual", action="store_true",
                     help="time gossmx_moe_forward_residual (post-attention RMSNorm + block + residual add) "
                          "instead of the block alone; no CPU baseline")
@@ -246,6 +248,19 @@ def main() -> int:
         else:
             ms_total = ms_eager
 
+    # Host-memory mode (GOSSMX_MEM_HOST, the direct drop-in for Rust slices):
+    # every layer call copies x and the logits in and the outputs out, then
+    # synchronizes. PCIe-inclusive, reported beside value, never as value.
+    host_ms = None
+    if not args.residual and args.host_steps > 0:
+        for st in state:  # one untimed pass (host staging buffers)
+            st["moe"].forward(x, injected_logits=st["logits"])
+        t0 = time.perf_counter()
+        for _ in range(args.host_steps):
+            for st in state:
+                st["moe"].forward(x, injected_logits=st["logits"])
+        host_ms = (time.perf_counter() - t0) * 1e3 / args.host_steps
+
     sel = [st["sel_dev"].cpu().numpy() for st in state]
     if cfg["routing"] != "router":
         assert all((s == stable_topk_sets(st["logits"], 4)).all() for s, st in zip(sel, state))
@@ -312,6 +327,12 @@ def main() -> int:
         "launch": "hip-graph" if args.graph else "eager",
         "eager_ms_per_step": ms_eager / args.steps,
     }
+    if host_ms is not None:
+        result["host_memory"] = {
+            "ms_per_step": host_ms, "value": layer_tokens / (host_ms * 1e-3), "unit": "layer-tokens/s",
+            "steps": args.host_steps,
+            "note": "GOSSMX_MEM_HOST calls: x and logits copied in, outputs copied out, synchronized per layer",
+        }
     if not args.no_cpu_baseline and not args.residual:
         result["cpu_baseline"] = cpu_baseline(cfg, x, state[0], out0, args.cpu_threads)
     if graph is not None:
