@@ -9,7 +9,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libgossmx.so")
-SOURCES = ["gossmx_kernels.hip", "gossmx_api.hip"]
+SOURCES = ["gossmx_kernels.hip", "gossmx_api.hip", "gossmx_store.cpp"]
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 
 # -ffp-contract=off: the reference's float chains are ordered and unfused.
@@ -24,7 +24,7 @@ FLAGS = [
 def build(verbose: bool = False) -> str:
     objs = []
     for src in SOURCES:
-        obj = os.path.join(CSRC, src.replace(".hip", ".o"))
+        obj = os.path.join(CSRC, os.path.splitext(src)[0] + ".o")
         cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:

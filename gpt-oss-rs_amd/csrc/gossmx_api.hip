@@ -247,6 +247,47 @@ int validate_problem(const gossmx_matmul_problem* p, size_t rows, size_t blocks,
 
 }  // namespace
 
+// Hooks for the host-side store module (gossmx_store.cpp).
+namespace gossmx {
+
+int set_error(int status, const char* message) { return fail(status, "%s", message); }
+
+void tiled_image_bytes(size_t experts, size_t rows, size_t blocks, size_t* nib_bytes, size_t* scl_bytes) {
+  const TiledWeights t = make_tiled(experts, rows, blocks);
+  *nib_bytes = experts * t.nib_stride;
+  *scl_bytes = experts * t.scl_stride;
+}
+
+int tiled_image_read(gossmx_ctx* ctx, const gossmx_weights* w, uint8_t* nib, uint8_t* scl) {
+  if (!ctx || !w || !nib || !scl) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+  if (w->device != ctx->device) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "weights live on another device");
+  if (int s = set_device(ctx->device)) return s;
+  HIP_TRY(hipMemcpyAsync(nib, w->t.nib, w->t.experts * w->t.nib_stride, hipMemcpyDeviceToHost, ctx->stream),
+          "D2H nibble plane");
+  HIP_TRY(hipMemcpyAsync(scl, w->t.scl, w->t.experts * w->t.scl_stride, hipMemcpyDeviceToHost, ctx->stream),
+          "D2H scale plane");
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  return GOSSMX_OK;
+}
+
+int tiled_image_create(gossmx_ctx* ctx, size_t experts, size_t rows, size_t blocks, const uint8_t* nib,
+                       const uint8_t* scl, gossmx_weights** out) {
+  gossmx_weights* w = nullptr;
+  if (int s = alloc_tiled(ctx, experts, rows, blocks, &w)) return s;
+  hipError_t e = hipMemcpyAsync(w->t.nib, nib, experts * w->t.nib_stride, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(w->t.scl, scl, experts * w->t.scl_stride, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = launch_tile_flags(w->t, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    gossmx_weights_destroy(w);
+    return hip_fail(e, "weights image upload");
+  }
+  *out = w;
+  return GOSSMX_OK;
+}
+
+}  // namespace gossmx
+
 // ===========================================================================
 extern "C" {
 

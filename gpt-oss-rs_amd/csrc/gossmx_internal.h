@@ -155,3 +155,16 @@ hipError_t launch_build_sigmoid_table(uint16_t* tab, hipStream_t stream);
 hipError_t launch_selftest(float* out, hipStream_t stream);
 
 }  // namespace gossmx
+
+// Hooks of the C ABI host code (gossmx_api.hip) for the host-side store
+// module (gossmx_store.cpp): the last-error message, and the resident layout
+// v3 image (nibble plane and scale plane, experts x stride bytes each).
+struct gossmx_ctx;
+struct gossmx_weights;
+namespace gossmx {
+int set_error(int status, const char* message);
+void tiled_image_bytes(size_t experts, size_t rows, size_t blocks, size_t* nib_bytes, size_t* scl_bytes);
+int tiled_image_read(gossmx_ctx* ctx, const gossmx_weights* w, uint8_t* nib, uint8_t* scl);
+int tiled_image_create(gossmx_ctx* ctx, size_t experts, size_t rows, size_t blocks, const uint8_t* nib,
+                       const uint8_t* scl, gossmx_weights** out);
+}  // namespace gossmx

@@ -33,6 +33,7 @@ ERR_DEVICE = 6
 ERR_OUT_OF_MEMORY = 7
 ERR_NON_FINITE_LOGITS = 8
 ERR_INJECTED_FAULT = 9
+ERR_BAD_FILE = 10
 
 LAYOUT_CANONICAL_V1 = 1
 LAYOUT_X8_SPLIT_V2 = 2
@@ -68,6 +69,17 @@ class MatmulProblem(C.Structure):
 class MoeConfig(C.Structure):
     _fields_ = [("experts", C.c_size_t), ("hidden", C.c_size_t), ("intermediate", C.c_size_t),
                 ("top_k", C.c_size_t), ("alpha", C.c_float), ("limit", C.c_float)]
+
+
+class RepackInfo(C.Structure):
+    _fields_ = [("format_version", C.c_uint32), ("layout_version", C.c_uint32), ("experts", C.c_size_t),
+                ("rows", C.c_size_t), ("blocks", C.c_size_t), ("records", C.c_size_t),
+                ("payload_offset", C.c_size_t), ("payload_bytes", C.c_size_t)]
+
+
+class TensorInfo(C.Structure):
+    _fields_ = [("dtype", C.c_char * 16), ("rank", C.c_size_t), ("shape", C.c_size_t * 8), ("offset", C.c_size_t),
+                ("bytes", C.c_size_t)]
 
 
 class MoeIo(C.Structure):
@@ -125,6 +137,16 @@ def load():
         "gossmx_layer_create": (i32, [vp, C.POINTER(MoeConfig), vp, vp, vp, vp, vp, vp, pp]),
         "gossmx_layer_destroy": (None, [vp]),
         "gossmx_moe_forward": (i32, [vp, vp, C.POINTER(MoeIo)]),
+        "gossmx_repack_inspect": (i32, [C.c_char_p, C.POINTER(RepackInfo), C.c_char_p, sz]),
+        "gossmx_weights_load_repack": (i32, [vp, C.c_char_p, C.POINTER(vp)]),
+        "gossmx_weights_save_repack": (i32, [vp, vp, C.c_char_p, C.c_char_p, C.c_char_p, C.POINTER(C.c_char_p), sz]),
+        "gossmx_repack_cache_key": (i32, [C.c_char_p, C.POINTER(sz), i32, C.c_char_p, C.POINTER(C.c_char_p), sz,
+                                          C.c_char_p]),
+        "gossmx_safetensors_find": (i32, [C.c_char_p, C.c_char_p, C.POINTER(TensorInfo)]),
+        "gossmx_weights_from_safetensors": (i32, [vp, C.POINTER(C.c_char_p), sz, C.c_char_p, C.c_char_p,
+                                                  C.POINTER(vp)]),
+        "gossmx_weights_open_or_create": (i32, [vp, C.c_char_p, C.c_char_p, C.POINTER(C.c_char_p), sz,
+                                                C.POINTER(C.c_char_p), sz, C.c_char_p, C.c_char_p, C.POINTER(vp)]),
         "gossmx_moe_forward_residual": (i32, [vp, vp, C.POINTER(MoeIo), vp, C.c_float, vp]),
         "gossmx_profile_enable": (i32, [vp, i32]),
         "gossmx_profile_read": (i32, [vp, C.POINTER(ProfileRecord), sz, C.POINTER(sz)]),
@@ -297,6 +319,75 @@ class Weights:
         if self._h:
             load().gossmx_weights_destroy(self._h)
             self._h = C.c_void_p()
+
+    # --- on disk (CpuRepackCache) and from SafeTensors (CpuTensorStore) ---
+
+    @classmethod
+    def load_repack(cls, ctx: Context, path: str) -> "Weights":
+        """A GOSSMX4 container of layout 1, 2 or 3 (RepackedMxfp4::open)."""
+        h = C.c_void_p()
+        _check(load().gossmx_weights_load_repack(ctx.handle, os.fsencode(path), C.byref(h)))
+        return cls(ctx, h)
+
+    def save_repack(self, path: str, tensor_name: str, model_revision: str, source_hashes=()):
+        """This tensor as a layout-3 container, published atomically."""
+        hs = _cstrings(source_hashes)
+        _check(load().gossmx_weights_save_repack(self.ctx.handle, self._h, os.fsencode(path), tensor_name.encode(),
+                                                 model_revision.encode(), hs, len(source_hashes)))
+
+    @classmethod
+    def from_safetensors(cls, ctx: Context, shards, blocks_name: str, scales_name: str) -> "Weights":
+        sh = _cstrings([os.fsdecode(p) for p in shards])
+        h = C.c_void_p()
+        _check(load().gossmx_weights_from_safetensors(ctx.handle, sh, len(shards), blocks_name.encode(),
+                                                      scales_name.encode(), C.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def open_or_create(cls, ctx: Context, cache_root: str, model_revision: str, source_hashes, shards,
+                       blocks_name: str, scales_name: str) -> "Weights":
+        """CpuRepackCache::open_or_create with the resident layout 3."""
+        hs = _cstrings(source_hashes)
+        sh = _cstrings([os.fsdecode(p) for p in shards])
+        h = C.c_void_p()
+        _check(load().gossmx_weights_open_or_create(ctx.handle, os.fsencode(cache_root), model_revision.encode(), hs,
+                                                    len(source_hashes), sh, len(shards), blocks_name.encode(),
+                                                    scales_name.encode(), C.byref(h)))
+        return cls(ctx, h)
+
+
+def _cstrings(values):
+    arr = (C.c_char_p * max(1, len(values)))()
+    for i, v in enumerate(values):
+        arr[i] = v.encode() if isinstance(v, str) else bytes(v)
+    return arr
+
+
+def repack_cache_key(tensor_name: str, shape, layout: int, model_revision: str, source_hashes=()) -> str:
+    """SourceIdentity::cache_key (cpu_repack.rs:92-107)."""
+    shp = (C.c_size_t * 3)(*shape)
+    key = C.create_string_buffer(65)
+    _check(load().gossmx_repack_cache_key(tensor_name.encode(), shp, layout, model_revision.encode(),
+                                          _cstrings(source_hashes), len(source_hashes), key))
+    return key.value.decode()
+
+
+def repack_inspect(path: str) -> dict:
+    """The validated header of a GOSSMX4 container (no device access)."""
+    info = RepackInfo()
+    name = C.create_string_buffer(1024)
+    _check(load().gossmx_repack_inspect(os.fsencode(path), C.byref(info), name, len(name)))
+    d = {k: getattr(info, k) for k, _ in RepackInfo._fields_}
+    d["tensor_name"] = name.value.decode()
+    return d
+
+
+def safetensors_find(path: str, name: str) -> dict:
+    """One tensor of a SafeTensors shard: dtype, shape, absolute byte range."""
+    info = TensorInfo()
+    _check(load().gossmx_safetensors_find(os.fsencode(path), name.encode(), C.byref(info)))
+    return {"dtype": info.dtype.decode(), "shape": tuple(info.shape[:info.rank]), "offset": info.offset,
+            "bytes": info.bytes}
 
 
 def _problem(weights, expert, activations, m, bias, output, output_stride, kind, row_stride, memory,

@@ -14,6 +14,11 @@
  *   - gossmx_moe_forward_residual <- the MoE half of forward_layer_batch: norm_boundary of the
  *                                  post-attention residual, moe_batch, add_residual
  *                                  (cpu_runner.rs:2519-2553, 2680-2687, 3732-3738)
+ *   - gossmx_weights_open_or_create, _load_repack, _save_repack, gossmx_repack_*
+ *                               <- CpuRepackCache / RepackedMxfp4, cpu_repack.rs:21-480 (container,
+ *                                  cache key, lock, atomic publish) with a resident layout 3
+ *   - gossmx_safetensors_find, gossmx_weights_from_safetensors
+ *                               <- CpuTensorStore::open / tensor, cpu_tensor_store.rs:46-288
  *   - gossmx_weights_upload     <- CpuRepackCache::open_or_create + RepackedMxfp4::expert_view
  *                                  crates/gpt-oss-model-runner/src/cpu_repack.rs:149-216,302-318
  *                                  (the resident copy is a new GPU layout, see below)
@@ -57,7 +62,8 @@ typedef enum gossmx_status {
   GOSSMX_ERR_DEVICE = 6,              /* HIP runtime error */
   GOSSMX_ERR_OUT_OF_MEMORY = 7,
   GOSSMX_ERR_NON_FINITE_LOGITS = 8,   /* "CPU router produced non-finite logits" */
-  GOSSMX_ERR_INJECTED_FAULT = 9       /* gossmx_inject_fault test hook fired */
+  GOSSMX_ERR_INJECTED_FAULT = 9,      /* gossmx_inject_fault test hook fired */
+  GOSSMX_ERR_BAD_FILE = 10            /* missing, unreadable or malformed file (the store's ModelError / io::Error) */
 } gossmx_status;
 
 enum {
@@ -113,6 +119,69 @@ int gossmx_weights_export(gossmx_ctx* ctx, const gossmx_weights* w, uint8_t* out
 int gossmx_weights_shape(const gossmx_weights* w, size_t* experts, size_t* rows, size_t* blocks);
 size_t gossmx_weights_device_bytes(const gossmx_weights* w);
 void gossmx_weights_destroy(gossmx_weights* w);
+
+/* Resident weights on disk (CpuRepackCache, crates/gpt-oss-model-runner/src/cpu_repack.rs)
+ * and from SafeTensors checkpoints (CpuTensorStore, cpu_tensor_store.rs). Host file I/O.
+ *
+ * GOSSMX4 repack container (cpu_repack.rs:21-23, 120-130, 231-280, 400-480): the 8 bytes
+ * "GOSSMX4\0", the header length (u64 LE), the JSON RepackHeader {format_version,
+ * layout_version, layout_identifier, tensor_name, model_revision, source_hashes, shape
+ * [experts, rows, blocks], records}, then the payload. Layouts 1 (CanonicalAdjacentV1) and
+ * 2 (InterleavedSplitX8V2) carry records x 17 bytes as the reference writes them; layout 3
+ * (GpuTiledV3) carries this library's resident image: the nibble plane, then the scale
+ * plane, experts x stride bytes each. */
+typedef struct gossmx_repack_info {
+  uint32_t format_version;
+  uint32_t layout_version;
+  size_t experts, rows, blocks, records;
+  size_t payload_offset; /* bytes from the start of the file */
+  size_t payload_bytes;
+} gossmx_repack_info;
+
+/* Reads and validates a container header as RepackedMxfp4::open does (magic, header
+ * length, known layout identifier and version, records = experts * rows * blocks, file
+ * length = payload offset + payload bytes). No device access. tensor_name (nullable)
+ * receives the header's tensor name, cut to cap - 1 bytes and NUL-terminated. */
+int gossmx_repack_inspect(const char* path, gossmx_repack_info* info, char* tensor_name, size_t cap);
+/* Loads a container of any of the three layouts as resident weights (layouts 1 and 2
+ * through gossmx_weights_upload; layout 3 by copying the image). */
+int gossmx_weights_load_repack(gossmx_ctx* ctx, const char* path, gossmx_weights** out);
+/* Writes resident weights as a layout-3 container: a temporary file in the target's
+ * directory, synced, renamed over the target, then the directory synced (the atomic
+ * publish of open_or_create, cpu_repack.rs:190-204). */
+int gossmx_weights_save_repack(gossmx_ctx* ctx, const gossmx_weights* w, const char* path, const char* tensor_name,
+                               const char* model_revision, const char* const* source_hashes, size_t n_hashes);
+/* SourceIdentity::cache_key (cpu_repack.rs:92-107): SHA-256 of "gpt-oss-rs-mxfp4-repack",
+ * the format version 1 (u32 LE), the layout name, the layout identifier (u32 LE), the
+ * model revision, each source hash, the tensor name and each dimension (u64 LE), written
+ * to key as 64 lowercase hex digits and a NUL. layout is 1, 2 or 3. */
+int gossmx_repack_cache_key(const char* tensor_name, const size_t shape[3], int layout, const char* model_revision,
+                            const char* const* source_hashes, size_t n_hashes, char key[65]);
+
+/* One tensor of a SafeTensors shard, with parse_shard_header's checks
+ * (cpu_tensor_store.rs:176-288): dtype as spelled in the file, shape, absolute byte range. */
+typedef struct gossmx_tensor_info {
+  char dtype[16];
+  size_t rank;
+  size_t shape[8];
+  size_t offset;
+  size_t bytes;
+} gossmx_tensor_info;
+int gossmx_safetensors_find(const char* path, const char* name, gossmx_tensor_info* info);
+/* Resident weights from the U8 tensors blocks_name [experts][rows][blocks][16] and
+ * scales_name [experts][rows][blocks], each in exactly one of the shards (the source
+ * checks of open_or_create, cpu_repack.rs:155-174). */
+int gossmx_weights_from_safetensors(gossmx_ctx* ctx, const char* const* shards, size_t n_shards,
+                                    const char* blocks_name, const char* scales_name, gossmx_weights** out);
+/* CpuRepackCache::open_or_create (cpu_repack.rs:149-216) with layout 3: the container
+ * cache_root/mxfp4/<cache key of blocks_name>/weights.repack is loaded when its header
+ * matches this source; otherwise the weights come from the shards and the container is
+ * published under the lock file repack.lock ("pid=<pid>"; a lock whose process is gone
+ * is taken over; waits at most 120 s). */
+int gossmx_weights_open_or_create(gossmx_ctx* ctx, const char* cache_root, const char* model_revision,
+                                  const char* const* source_hashes, size_t n_hashes, const char* const* shards,
+                                  size_t n_shards, const char* blocks_name, const char* scales_name,
+                                  gossmx_weights** out);
 
 /* Kernel boundary: C[m, n] = A[m, K] . W[expert][n, K]^T + bias[n] for n < rows,
  * written at output[i * output_stride + n]; columns rows..output_stride-1 of each
