@@ -9,7 +9,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libgossmx.so")
-SOURCES = ["gossmx_kernels.hip", "gossmx_api.hip", "gossmx_store.cpp"]
+SOURCES = ["gossmx_kernels.hip", "gossmx_api.hip", "gossmx_store.cpp", "gossmx_dense.cpp"]
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 
 # -ffp-contract=off: the reference's float chains are ordered and unfused.
@@ -19,13 +19,20 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
 ]
+# Host-only sources (.cpp: the store and the dense CPU path) build as plain C++
+# with the HIP runtime headers.
+HOST_FLAGS = [
+    "-x", "c++", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", "-O3", "-std=c++17", "-fPIC",
+    "-ffp-contract=off", "-Wall", "-Wno-unused-function",
+]
 
 
 def build(verbose: bool = False) -> str:
     objs = []
     for src in SOURCES:
         obj = os.path.join(CSRC, os.path.splitext(src)[0] + ".o")
-        cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+        flags = HOST_FLAGS if src.endswith(".cpp") else FLAGS
+        cmd = [HIPCC, *flags, "-c", os.path.join(CSRC, src), "-o", obj]
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             sys.stderr.write(res.stdout + res.stderr)

@@ -247,10 +247,12 @@ int validate_problem(const gossmx_matmul_problem* p, size_t rows, size_t blocks,
 
 }  // namespace
 
-// Hooks for the host-side store module (gossmx_store.cpp).
+// Hooks for the host-side modules (gossmx_store.cpp, gossmx_dense.cpp).
 namespace gossmx {
 
 int set_error(int status, const char* message) { return fail(status, "%s", message); }
+
+const gossmx_moe_config* layer_config(const gossmx_layer* layer) { return layer ? &layer->cfg : nullptr; }
 
 void tiled_image_bytes(size_t experts, size_t rows, size_t blocks, size_t* nib_bytes, size_t* scl_bytes) {
   const TiledWeights t = make_tiled(experts, rows, blocks);

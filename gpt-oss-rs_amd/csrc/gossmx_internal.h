@@ -158,11 +158,15 @@ hipError_t launch_selftest(float* out, hipStream_t stream);
 
 // Hooks of the C ABI host code (gossmx_api.hip) for the host-side store
 // module (gossmx_store.cpp): the last-error message, and the resident layout
-// v3 image (nibble plane and scale plane, experts x stride bytes each).
+// v3 image (nibble plane and scale plane, experts x stride bytes each); and
+// for the dense path (gossmx_dense.cpp): a MoE layer's configuration.
 struct gossmx_ctx;
 struct gossmx_weights;
+struct gossmx_layer;
+struct gossmx_moe_config;
 namespace gossmx {
 int set_error(int status, const char* message);
+const gossmx_moe_config* layer_config(const gossmx_layer* layer);
 void tiled_image_bytes(size_t experts, size_t rows, size_t blocks, size_t* nib_bytes, size_t* scl_bytes);
 int tiled_image_read(gossmx_ctx* ctx, const gossmx_weights* w, uint8_t* nib, uint8_t* scl);
 int tiled_image_create(gossmx_ctx* ctx, size_t experts, size_t rows, size_t blocks, const uint8_t* nib,

@@ -96,6 +96,39 @@ class ProfileRecord(C.Structure):
 _lib = None
 
 
+class ModelConfig(C.Structure):
+    """gossmx_model_config (CpuGptOssConfig plus the sequence's context cap)."""
+    _fields_ = [("vocab", C.c_size_t), ("hidden", C.c_size_t), ("layers", C.c_size_t), ("heads", C.c_size_t),
+                ("kv_heads", C.c_size_t), ("head_dim", C.c_size_t), ("sliding_window", C.c_size_t),
+                ("context_cap", C.c_size_t), ("rms_norm_eps", C.c_float), ("rope_theta", C.c_double),
+                ("rope_yarn", C.c_int), ("rope_factor", C.c_double), ("rope_original_max_positions", C.c_size_t),
+                ("rope_beta_fast", C.c_double), ("rope_beta_slow", C.c_double), ("rope_truncate", C.c_int),
+                ("threads", C.c_size_t)]
+
+
+class DenseLayer(C.Structure):
+    """gossmx_dense_layer: one decoder layer's dense tensors and its MoE block."""
+    _fields_ = [("input_norm", C.c_void_p), ("q_weight", C.c_void_p), ("q_bias", C.c_void_p),
+                ("k_weight", C.c_void_p), ("k_bias", C.c_void_p), ("v_weight", C.c_void_p), ("v_bias", C.c_void_p),
+                ("o_weight", C.c_void_p), ("o_bias", C.c_void_p), ("sinks", C.c_void_p),
+                ("post_attention_norm", C.c_void_p), ("sliding", C.c_int), ("moe", C.c_void_p)]
+
+
+# GPT-OSS-20B's attention and RoPE configuration (config.json of the checkpoint).
+GPT_OSS_20B = dict(vocab=201088, hidden=2880, layers=24, heads=64, kv_heads=8, head_dim=64, sliding_window=128,
+                   rms_norm_eps=1e-5, rope_theta=150000.0, rope_yarn=1, rope_factor=32.0,
+                   rope_original_max_positions=4096, rope_beta_fast=32.0, rope_beta_slow=1.0, rope_truncate=0)
+
+
+def model_config(context_cap: int = 4096, threads: int = 0, **fields) -> ModelConfig:
+    """A ModelConfig from keyword fields (rope defaults as CpuRopeScaling's serde defaults)."""
+    c = ModelConfig()
+    c.rope_beta_fast, c.rope_beta_slow, c.context_cap, c.threads = 32.0, 1.0, context_cap, threads
+    for k, v in fields.items():
+        setattr(c, k, v)
+    return c
+
+
 def header_symbols() -> list[str]:
     """Every function the public header declares."""
     with open(HEADER) as fh:
@@ -157,6 +190,18 @@ def load():
         "gossmx_graph_launch": (i32, [vp, vp]),
         "gossmx_graph_destroy": (None, [vp]),
         "gossmx_selftest": (i32, [vp]),
+        "gossmx_model_create": (i32, [vp, C.POINTER(ModelConfig), vp, vp, vp, C.POINTER(DenseLayer), pp]),
+        "gossmx_model_destroy": (None, [vp]),
+        "gossmx_model_reset": (i32, [vp]),
+        "gossmx_model_prefill": (i32, [vp, vp, sz, vp]),
+        "gossmx_model_append": (i32, [vp, vp, sz, vp]),
+        "gossmx_model_decode": (i32, [vp, C.c_uint32, vp]),
+        "gossmx_model_position": (i32, [vp, C.POINTER(sz)]),
+        "gossmx_model_cache": (i32, [vp, sz, C.POINTER(sz), C.POINTER(sz)]),
+        "gossmx_model_times": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+        "gossmx_greedy_token": (i32, [vp, sz, C.POINTER(C.c_uint32)]),
+        "gossmx_yarn_rope": (i32, [C.POINTER(ModelConfig), vp, sz, sz]),
+        "gossmx_attention": (i32, [vp, vp, vp, sz, sz, vp, sz, sz, sz, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -559,3 +604,113 @@ class MoeLayer:
         if self._h:
             load().gossmx_layer_destroy(self._h)
             self._h = C.c_void_p()
+
+
+class Model:
+    """A GPT-OSS model on the dense CPU path with GPU MoE layers (gossmx_model_*).
+
+    `layers` is a list of dicts with the gossmx_dense_layer tensors (numpy
+    arrays: norms, biases and sinks f32, matrices bf16 bits as uint16), the
+    `sliding` flag and the `moe` MoeLayer. The arrays are kept alive here."""
+
+    def __init__(self, ctx: Context, config: ModelConfig, embedding, final_norm, lm_head, layers):
+        self.ctx, self.config = ctx, config
+        keep = []
+
+        def arr(a, dtype):
+            a = np.ascontiguousarray(a, dtype=dtype)
+            keep.append(a)
+            return a.ctypes.data
+
+        table = (DenseLayer * len(layers))()
+        for i, L in enumerate(layers):
+            d = table[i]
+            for name in ("input_norm", "q_bias", "k_bias", "v_bias", "o_bias", "sinks", "post_attention_norm"):
+                setattr(d, name, arr(L[name], np.float32))
+            for name in ("q_weight", "k_weight", "v_weight", "o_weight"):
+                setattr(d, name, arr(L[name], np.uint16))
+            d.sliding = 1 if L["sliding"] else 0
+            d.moe = L["moe"].handle if hasattr(L["moe"], "handle") else L["moe"]._h.value
+        emb, fin, head = arr(embedding, np.uint16), arr(final_norm, np.float32), arr(lm_head, np.uint16)
+        self._keep, self._table = keep, table
+        self._h = C.c_void_p()
+        _check(load().gossmx_model_create(ctx.handle, C.byref(config), emb, fin, head, table, C.byref(self._h)))
+
+    def _logits(self):
+        return np.zeros(self.config.vocab, np.float32)
+
+    def prefill(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = self._logits()
+        _check(load().gossmx_model_prefill(self._h, _ptr(t), t.size, _ptr(out)))
+        return out
+
+    def append(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = self._logits()
+        _check(load().gossmx_model_append(self._h, _ptr(t), t.size, _ptr(out)))
+        return out
+
+    def decode(self, token: int) -> np.ndarray:
+        out = self._logits()
+        _check(load().gossmx_model_decode(self._h, int(token), _ptr(out)))
+        return out
+
+    def reset(self):
+        _check(load().gossmx_model_reset(self._h))
+
+    @property
+    def position(self) -> int:
+        p = C.c_size_t()
+        _check(load().gossmx_model_position(self._h, C.byref(p)))
+        return p.value
+
+    def cache(self, layer: int) -> tuple[int, int]:
+        n, start = C.c_size_t(), C.c_size_t()
+        _check(load().gossmx_model_cache(self._h, layer, C.byref(n), C.byref(start)))
+        return n.value, start.value
+
+    def times(self) -> tuple[float, float]:
+        """(dense seconds, MoE seconds) accumulated over the model's steps."""
+        d, m = C.c_double(), C.c_double()
+        _check(load().gossmx_model_times(self._h, C.byref(d), C.byref(m)))
+        return d.value, m.value
+
+    def generate(self, prompt, decode_steps: int) -> tuple[np.ndarray, np.ndarray]:
+        """prefill then decode_steps greedy decodes: (tokens [decode_steps + 1], logits rows)."""
+        logits = [self.prefill(prompt)]
+        tokens = [greedy_token(logits[0])]
+        for _ in range(decode_steps):
+            logits.append(self.decode(tokens[-1]))
+            tokens.append(greedy_token(logits[-1]))
+        return np.array(tokens, np.uint32), np.stack(logits)
+
+    def close(self):
+        if self._h:
+            load().gossmx_model_destroy(self._h)
+            self._h = C.c_void_p()
+
+
+def greedy_token(logits) -> int:
+    v = np.ascontiguousarray(logits, dtype=np.float32)
+    t = C.c_uint32()
+    _check(load().gossmx_greedy_token(_ptr(v), v.size, C.byref(t)))
+    return t.value
+
+
+def yarn_rope(config: ModelConfig, values, heads: int, position: int) -> np.ndarray:
+    v = np.array(values, dtype=np.float32)
+    _check(load().gossmx_yarn_rope(C.byref(config), _ptr(v), heads, position))
+    return v
+
+
+def attention(query, keys, values, window: int, sinks, heads: int, kv_heads: int, head_dim: int) -> np.ndarray:
+    q = np.ascontiguousarray(query, dtype=np.float32)
+    k = np.ascontiguousarray(keys, dtype=np.uint16)
+    v = np.ascontiguousarray(values, dtype=np.uint16)
+    s = np.ascontiguousarray(sinks, dtype=np.float32)
+    out = np.zeros(heads * head_dim, np.float32)
+    tokens = k.size // (kv_heads * head_dim)
+    _check(load().gossmx_attention(_ptr(q), _ptr(k), _ptr(v), tokens, window, _ptr(s), heads, kv_heads, head_dim,
+                                   _ptr(out)))
+    return out

@@ -74,3 +74,34 @@ def zipf_logits(rng: np.random.Generator, m: int, experts: int, top_k: int = TOP
 def uniform_logits(rng: np.random.Generator, m: int, experts: int) -> np.ndarray:
     """Near-uniform routing: i.i.d. logits, bf16 values."""
     return bf16_to_f32(bf16_bits(rng.standard_normal((m, experts)).astype(np.float32)))
+
+
+def model_weights(config: dict, normal) -> dict:
+    """Dense tensors of a random-init GPT-OSS model (config: the gossmx_model_config
+    fields): embedding, lm_head and the q/k/v/o matrices bf16 N(0, 0.02); their
+    biases and the attention sinks N(0, 0.02) and the RMSNorm weights N(1, 0.02),
+    as f32 holding bf16 values. Layer i is sliding when i is even (GPT-OSS's
+    alternating layer_types). normal(n, std) returns n bf16 bit patterns."""
+    V, H = config["vocab"], config["hidden"]
+    QW, KW = config["heads"] * config["head_dim"], config["kv_heads"] * config["head_dim"]
+
+    def vec(n, mean=0.0):
+        return (bf16_to_f32(normal(n, 0.02)) + np.float32(mean)).astype(np.float32)
+
+    layers = []
+    for i in range(config["layers"]):
+        layers.append({
+            "input_norm": bf16_to_f32(bf16_bits(vec(H, 1.0))), "post_attention_norm": bf16_to_f32(bf16_bits(vec(H, 1.0))),
+            "q_weight": normal(QW * H, 0.02).reshape(QW, H), "q_bias": vec(QW),
+            "k_weight": normal(KW * H, 0.02).reshape(KW, H), "k_bias": vec(KW),
+            "v_weight": normal(KW * H, 0.02).reshape(KW, H), "v_bias": vec(KW),
+            "o_weight": normal(H * QW, 0.02).reshape(H, QW), "o_bias": vec(H),
+            "sinks": vec(config["heads"]), "sliding": i % 2 == 0,
+        })
+    return {"embedding": normal(V * H, 0.02).reshape(V, H), "lm_head": normal(V * H, 0.02).reshape(V, H),
+            "final_norm": bf16_to_f32(bf16_bits(vec(H, 1.0))), "layers": layers}
+
+
+def numpy_normal(rng: np.random.Generator):
+    """normal(n, std) for model_weights from a numpy generator (small models)."""
+    return lambda n, std: bf16_bits(rng.standard_normal(n, dtype=np.float32) * np.float32(std))

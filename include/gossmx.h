@@ -320,6 +320,95 @@ int gossmx_inject_fault(gossmx_ctx* ctx, int armed);
  * the reference; GOSSMX_ERR_UNSUPPORTED with a message on mismatch. */
 int gossmx_selftest(gossmx_ctx* ctx);
 
+/* ---------------------------------------------------------------------------
+ * The dense path around the block, on the host CPU (crates/gpt-oss-model-runner/
+ * src/cpu_runner.rs): a GPT-OSS model whose attention, RoPE, dense projections,
+ * norms and lm_head run as the reference's CPU runner runs them, bit for bit,
+ * and whose MoE halves run on the GPU through gossmx_moe_forward_residual
+ * (host memory). Weights are host memory, borrowed (they and the MoE layers must
+ * outlive the model). A model holds one sequence's KV caches. */
+typedef struct gossmx_model gossmx_model;
+
+/* CpuGptOssConfig (cpu_runner.rs:252-291) and the sequence's context cap
+ * (new_sequence_state, :1596-1627). */
+typedef struct gossmx_model_config {
+  size_t vocab;                       /* vocab_size */
+  size_t hidden;                      /* hidden_size; equal to every MoE layer's hidden */
+  size_t layers;                      /* num_hidden_layers */
+  size_t heads;                       /* num_attention_heads */
+  size_t kv_heads;                    /* num_key_value_heads; divides heads */
+  size_t head_dim;                    /* even */
+  size_t sliding_window;              /* KV tokens a sliding layer keeps */
+  size_t context_cap;                 /* KV tokens a full layer keeps; positions stay below it */
+  float rms_norm_eps;
+  double rope_theta;
+  int rope_yarn;                      /* rope_scaling present (YaRN): 1, absent: 0 */
+  double rope_factor;
+  size_t rope_original_max_positions; /* original_max_position_embeddings */
+  double rope_beta_fast;              /* 32 by default */
+  double rope_beta_slow;              /* 1 by default */
+  int rope_truncate;
+  size_t threads;                     /* host threads for the dense path; 0: all hardware threads (at most 64) */
+} gossmx_model_config;
+
+/* One decoder layer (CpuLayer, load_layer cpu_runner.rs:3526-3671). Vectors are
+ * f32 (the reference loads them to f32), matrices bf16 row-major [out][in]. */
+typedef struct gossmx_dense_layer {
+  const float* input_norm;          /* [hidden] */
+  const uint16_t* q_weight;         /* [heads * head_dim][hidden] */
+  const float* q_bias;              /* [heads * head_dim] */
+  const uint16_t* k_weight;         /* [kv_heads * head_dim][hidden] */
+  const float* k_bias;              /* [kv_heads * head_dim] */
+  const uint16_t* v_weight;         /* [kv_heads * head_dim][hidden] */
+  const float* v_bias;              /* [kv_heads * head_dim] */
+  const uint16_t* o_weight;         /* [hidden][heads * head_dim] */
+  const float* o_bias;              /* [hidden] */
+  const float* sinks;               /* [heads] */
+  const float* post_attention_norm; /* [hidden] */
+  int sliding;                      /* layer_types "sliding_attention" / "local_attention" */
+  const gossmx_layer* moe;          /* this layer's MoE block */
+} gossmx_dense_layer;
+
+/* CpuModel::load + new_sequence_state. embedding and lm_head bf16 [vocab][hidden],
+ * final_norm f32 [hidden], layers [config->layers]. */
+int gossmx_model_create(gossmx_ctx* ctx, const gossmx_model_config* config, const uint16_t* embedding,
+                        const float* final_norm, const uint16_t* lm_head, const gossmx_dense_layer* layers,
+                        gossmx_model** out);
+void gossmx_model_destroy(gossmx_model* model);
+/* CpuModelRunner::reset (:1803-1807): empty caches, position 0. */
+int gossmx_model_reset(gossmx_model* model);
+/* CpuModelRunner::prefill_layer_major (:1827-1855): reset, then all n tokens as
+ * one layer-major step (positions 0..n-1, each layer's MoE over the n rows);
+ * logits [vocab] of the last token, bf16 values (:2300-2312). */
+int gossmx_model_prefill(gossmx_model* model, const uint32_t* tokens, size_t n, float* logits);
+/* prepare_step + commit (:2080-2333, :1081-1113) of n more tokens of the
+ * sequence at its current position, as one layer-major step (a prompt chunk);
+ * logits of the last one. */
+int gossmx_model_append(gossmx_model* model, const uint32_t* tokens, size_t n, float* logits);
+/* CpuModelRunner::decode (:1877-1885): one token at the next position. */
+int gossmx_model_decode(gossmx_model* model, uint32_t token, float* logits);
+/* Steps are transactional (prepare/commit, :1081-1113): on any error the caches
+ * and the position are unchanged. */
+int gossmx_model_position(const gossmx_model* model, size_t* position);
+/* CpuKvCache::len / start_position of a layer's cache (:674-680). */
+int gossmx_model_cache(const gossmx_model* model, size_t layer, size_t* len, size_t* start_position);
+/* Wall time spent so far in the dense path and in the MoE calls (including
+ * their host<->device copies). */
+int gossmx_model_times(const gossmx_model* model, double* dense_seconds, double* moe_seconds);
+
+/* greedy_token (crates/gpt-oss-bench/src/bin/cpu_parity.rs:750-762): the
+ * largest finite logit, the lowest index on ties. */
+int gossmx_greedy_token(const float* logits, size_t n, uint32_t* token);
+/* YarnRope::new + apply (cpu_runner.rs:3933-4013) over values [heads][head_dim]
+ * in place, for one position (uses config->head_dim and the rope fields only). */
+int gossmx_yarn_rope(const gossmx_model_config* config, float* values, size_t heads, size_t position);
+/* attention_one_staged (cpu_runner.rs:3840-3924) for one query [heads][head_dim]
+ * over the last min(tokens, window) of `tokens` key/value rows bf16
+ * [tokens][kv_heads][head_dim] (a cache of capacity `window` after `tokens`
+ * appends); out [heads][head_dim] (bf16 values). */
+int gossmx_attention(const float* query, const uint16_t* keys, const uint16_t* values, size_t tokens, size_t window,
+                     const float* sinks, size_t heads, size_t kv_heads, size_t head_dim, float* out);
+
 #ifdef __cplusplus
 }
 #endif

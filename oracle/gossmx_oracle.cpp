@@ -809,3 +809,345 @@ void oracle_gen_hidden(uint64_t seed, uint64_t stream, size_t m, size_t h, int n
 }
 
 }  // extern "C"
+
+namespace {
+// ---------------------------------------------------------------------------
+// The dense path around the block (crates/gpt-oss-model-runner/src/cpu_runner.rs),
+// restated with the reference's own data structures: CpuKvCache's shifting
+// vectors, staged rows per step, rows attended one after another.
+
+// YarnRope::new (cpu_runner.rs:3933-3990) and apply (:3992-4012).
+struct OracleRope {
+  size_t head_dim;
+  double theta;
+  int32_t yarn;
+  double factor;
+  size_t original_max;
+  double beta_fast, beta_slow;
+  int32_t truncate;
+};
+
+void yarn_inv_freq(const OracleRope& c, std::vector<float>& inv_freq, float& attention_scale) {
+  const size_t dim = c.head_dim;
+  inv_freq.clear();
+  attention_scale = 1.0f;
+  if (!c.yarn) {
+    for (size_t index = 0; index < dim; index += 2)
+      inv_freq.push_back(1.0f / std::pow((float)c.theta, (float)index / (float)dim));
+    return;
+  }
+  const double pi = 3.141592653589793;
+  auto correction = [&](double rotations) {
+    return ((double)dim * std::log((double)c.original_max / (rotations * 2.0 * pi))) / (2.0 * std::log(c.theta));
+  };
+  double low = correction(c.beta_fast), high = correction(c.beta_slow);
+  if (c.truncate) {
+    low = std::floor(low);
+    high = std::ceil(high);
+  }
+  low = std::fmax(low, 0.0);
+  high = std::fmin(high, (double)(dim - 1));
+  const double range = std::fmax(std::fabs(high - low), 0.001);
+  for (size_t index = 0; index < dim / 2; ++index) {
+    const float frequency = std::pow((float)c.theta, (float)(index * 2) / (float)dim);
+    const float extrapolation = 1.0f / frequency;
+    const float interpolation = 1.0f / ((float)c.factor * frequency);
+    const float ramp = std::clamp(((float)index - (float)low) / (float)range, 0.0f, 1.0f);
+    inv_freq.push_back(interpolation * ramp + extrapolation * (1.0f - ramp));
+  }
+  attention_scale = (float)(0.1 * std::log(c.factor) + 1.0);
+}
+
+void yarn_apply(const std::vector<float>& inv_freq, float attention_scale, size_t head_dim, float* values,
+                size_t heads, size_t position) {
+  const size_t half = head_dim / 2;
+  for (size_t head = 0; head < heads; ++head) {
+    const size_t start = head * head_dim;
+    for (size_t index = 0; index < half; ++index) {
+      const float angle = (float)position * inv_freq[index];
+      const float cosine = bf16_round(std::cos(angle) * attention_scale);
+      const float sine = bf16_round(std::sin(angle) * attention_scale);
+      const float left = bf16_round(values[start + index]);
+      const float right = bf16_round(values[start + half + index]);
+      const float left_cosine = bf16_round(left * cosine);
+      const float right_sine = bf16_round(right * sine);
+      const float right_cosine = bf16_round(right * cosine);
+      const float left_sine = bf16_round(left * sine);
+      values[start + index] = bf16_round(left_cosine - right_sine);
+      values[start + half + index] = bf16_round(right_cosine + left_sine);
+    }
+  }
+}
+
+// CpuKvCache (cpu_runner.rs:653-740): append_validated drops the oldest row
+// when full by shifting the vectors.
+struct OracleKvCache {
+  std::vector<uint16_t> keys, values;
+  size_t len = 0, token_width = 0, capacity = 0, start_position = 0;
+  void append(size_t position, const uint16_t* key, const uint16_t* value) {
+    if (len == capacity) {
+      keys.erase(keys.begin(), keys.begin() + token_width);
+      values.erase(values.begin(), values.begin() + token_width);
+      --len;
+      ++start_position;
+    }
+    if (len == 0) start_position = position;
+    keys.insert(keys.end(), key, key + token_width);
+    values.insert(values.end(), value, value + token_width);
+    ++len;
+  }
+};
+
+struct StagedRow {
+  std::vector<uint16_t> key, value;
+};
+
+// attention_one_staged, cpu_runner.rs:3840-3924.
+void attention_one_staged(const float* query, const OracleKvCache& cache, const std::vector<StagedRow>& staged,
+                          const float* sinks, size_t num_heads, size_t num_kv_heads, size_t head_dim, float* output) {
+  const size_t groups = num_heads / num_kv_heads;
+  const float scale = 1.0f / std::sqrt((float)head_dim);
+  const size_t combined_len = cache.len + staged.size();
+  const size_t visible_len = std::min(combined_len, cache.capacity);
+  const size_t skipped = combined_len - visible_len;
+  std::fill(output, output + num_heads * head_dim, 0.0f);
+  for (size_t head = 0; head < num_heads; ++head) {
+    const float* q = query + head * head_dim;
+    const size_t kv_head = head / groups;
+    auto row = [&](size_t combined, bool key) -> const uint16_t* {
+      if (combined < cache.len)
+        return (key ? cache.keys.data() : cache.values.data()) + combined * cache.token_width + kv_head * head_dim;
+      const StagedRow& s = staged[combined - cache.len];
+      return (key ? s.key.data() : s.value.data()) + kv_head * head_dim;
+    };
+    std::vector<float> scores;
+    for (size_t token = 0; token < visible_len; ++token) {
+      const uint16_t* key = row(skipped + token, true);
+      float dot = -0.0f;
+      for (size_t d = 0; d < head_dim; ++d) dot += q[d] * bf16_to_f32(key[d]);
+      dot = bf16_round(dot);
+      scores.push_back(bf16_round(dot * scale));
+    }
+    float maximum = sinks[head];
+    for (float s : scores) maximum = std::fmax(maximum, s);
+    float sum = -0.0f;
+    for (float s : scores) sum += std::exp(s - maximum);
+    const float denominator = std::exp(sinks[head] - maximum) + sum;
+    float* destination = output + head * head_dim;
+    for (size_t token = 0; token < scores.size(); ++token) {
+      const float probability = bf16_round(std::exp(scores[token] - maximum) / denominator);
+      const uint16_t* value = row(skipped + token, false);
+      for (size_t d = 0; d < head_dim; ++d) destination[d] += probability * bf16_to_f32(value[d]);
+    }
+    for (size_t d = 0; d < head_dim; ++d) destination[d] = bf16_round(destination[d]);
+  }
+}
+
+// project_bf16_batch (cpu_runner.rs:2734-2792): out[r][o] = bf16_dot(w[o], x[r]) + bias[o],
+// output rows split over `threads` (each output element is one dot).
+void project_rows(const uint16_t* w, size_t rows, size_t cols, const uint16_t* x, size_t m, const float* bias,
+                  float* out, int threads) {
+  auto part = [&](size_t lo, size_t hi) {
+    for (size_t o = lo; o < hi; ++o)
+      for (size_t r = 0; r < m; ++r) {
+        float v = bf16_dot(w + o * cols, x + r * cols, cols);
+        if (bias) v += bias[o];
+        out[r * rows + o] = v;
+      }
+  };
+  const size_t t = (size_t)std::max(1, threads);
+  if (t == 1 || rows < 64) {
+    part(0, rows);
+    return;
+  }
+  std::vector<std::thread> pool;
+  for (size_t i = 0; i < t; ++i) pool.emplace_back(part, rows * i / t, rows * (i + 1) / t);
+  for (auto& th : pool) th.join();
+}
+
+}  // namespace
+
+extern "C" {
+
+// Weights of one decoder layer as load_layer produces them (cpu_runner.rs:3526-3671).
+struct OracleDenseLayer {
+  const float* input_norm;
+  const uint16_t* q_weight;
+  const float* q_bias;
+  const uint16_t* k_weight;
+  const float* k_bias;
+  const uint16_t* v_weight;
+  const float* v_bias;
+  const uint16_t* o_weight;
+  const float* o_bias;
+  const float* sinks;
+  const float* post_attention_norm;
+  int32_t sliding;
+  OracleLayer moe;
+};
+
+struct OracleModel {
+  size_t vocab, hidden, layers, heads, kv_heads, head_dim, sliding_window, context_cap;
+  float rms_norm_eps;
+  OracleRope rope;
+  const uint16_t* embedding;  // [vocab][hidden]
+  const float* final_norm;    // [hidden]
+  const uint16_t* lm_head;    // [vocab][hidden]
+  const OracleDenseLayer* layer;
+};
+
+int oracle_yarn_rope(const OracleRope* c, float* values, size_t heads, size_t position) {
+  std::vector<float> inv_freq;
+  float attention_scale;
+  yarn_inv_freq(*c, inv_freq, attention_scale);
+  yarn_apply(inv_freq, attention_scale, c->head_dim, values, heads, position);
+  return OK;
+}
+
+// attention_one over a cache of capacity `window` after appending `tokens`
+// rows (CpuKvCache::append then attention_one, cpu_runner.rs:3829-3838).
+int oracle_attention(const float* query, const uint16_t* keys, const uint16_t* values, size_t tokens, size_t window,
+                     const float* sinks, size_t heads, size_t kv_heads, size_t head_dim, float* out,
+                     size_t* cache_len, size_t* cache_start) {
+  OracleKvCache cache;
+  cache.token_width = kv_heads * head_dim;
+  cache.capacity = window;
+  for (size_t t = 0; t < tokens; ++t)
+    cache.append(t, keys + t * cache.token_width, values + t * cache.token_width);
+  attention_one_staged(query, cache, {}, sinks, heads, kv_heads, head_dim, out);
+  if (cache_len) *cache_len = cache.len;
+  if (cache_start) *cache_start = cache.start_position;
+  return OK;
+}
+
+// greedy_token, crates/gpt-oss-bench/src/bin/cpu_parity.rs:750-762.
+int oracle_greedy_token(const float* logits, size_t n, uint32_t* token) {
+  bool found = false;
+  size_t best = 0;
+  for (size_t i = 0; i < n; ++i) {
+    if (!std::isfinite(logits[i])) continue;
+    if (!found || logits[i] > logits[best]) best = i;  // ties keep the lower index
+    found = true;
+  }
+  if (!found) return NON_FINITE_LOGITS;
+  *token = (uint32_t)best;
+  return OK;
+}
+
+// prefill_layer_major (cpu_runner.rs:1827-1855) of `n` prompt tokens, then
+// `decode_steps` decode calls (:1877-1885), each fed the previous greedy token.
+// prefill_chunk > 0 splits the prompt into steps of that many rows (prepare_step
+// and commit per chunk); 0 keeps it one step. tokens_out [decode_steps + 1]
+// receives the greedy token after the prompt and after every decode step;
+// logits_out (nullable) [decode_steps + 1][vocab]. Each step runs
+// prepare_step_inner (:2103-2333) over its rows: forward_layer_batch
+// (:2335-2586) per layer, then the final norm and lm_head of the last row.
+int oracle_model_generate(const OracleModel* M, const uint32_t* prompt, size_t n, size_t prefill_chunk,
+                          size_t decode_steps, int threads, uint32_t* tokens_out, float* logits_out) {
+  const size_t H = M->hidden, V = M->vocab, QW = M->heads * M->head_dim, KW = M->kv_heads * M->head_dim;
+  if (!n || n + decode_steps > M->context_cap) return INVALID_DIMENSIONS;
+  std::vector<float> inv_freq;
+  float attention_scale;
+  yarn_inv_freq(M->rope, inv_freq, attention_scale);
+  std::vector<OracleKvCache> caches(M->layers);
+  for (size_t li = 0; li < M->layers; ++li) {
+    caches[li].token_width = KW;
+    caches[li].capacity = M->layer[li].sliding ? M->sliding_window : M->context_cap;
+  }
+  size_t position = 0;
+  std::vector<float> logits(V);
+  const size_t chunk = prefill_chunk ? prefill_chunk : n;
+  size_t consumed = std::min(chunk, n), step = 0;
+  std::vector<uint32_t> rows(prompt, prompt + consumed);
+  for (;;) {
+    const size_t m = rows.size();
+    std::vector<uint16_t> hidden(m * H), normalized(m * H), attention(m * QW), after(m * H), post(m * H);
+    std::vector<float> q(m * QW), k(m * KW), v(m * KW), ctx(QW), projected(m * H), moe_out(m * H);
+    std::vector<std::vector<StagedRow>> staged(M->layers);
+    for (size_t r = 0; r < m; ++r) {
+      if (rows[r] >= V) return INVALID_DIMENSIONS;
+      std::memcpy(&hidden[r * H], M->embedding + (size_t)rows[r] * H, H * 2);
+    }
+    for (size_t li = 0; li < M->layers; ++li) {
+      const OracleDenseLayer& L = M->layer[li];
+      for (size_t r = 0; r < m; ++r) oracle_norm_boundary(&hidden[r * H], L.input_norm, H, M->rms_norm_eps, &normalized[r * H]);
+      project_rows(L.q_weight, QW, H, normalized.data(), m, L.q_bias, q.data(), threads);
+      project_rows(L.k_weight, KW, H, normalized.data(), m, L.k_bias, k.data(), threads);
+      project_rows(L.v_weight, KW, H, normalized.data(), m, L.v_bias, v.data(), threads);
+      for (size_t r = 0; r < m; ++r) {
+        float* qr = &q[r * QW];
+        float* kr = &k[r * KW];
+        for (size_t i = 0; i < QW; ++i) qr[i] = bf16_round(qr[i]);
+        for (size_t i = 0; i < KW; ++i) kr[i] = bf16_round(kr[i]);
+        yarn_apply(inv_freq, attention_scale, M->head_dim, qr, M->heads, position + r);
+        yarn_apply(inv_freq, attention_scale, M->head_dim, kr, M->kv_heads, position + r);
+        for (size_t i = 0; i < QW; ++i) qr[i] = bf16_round(qr[i]);
+        for (size_t i = 0; i < KW; ++i) kr[i] = bf16_round(kr[i]);
+        StagedRow row;
+        for (size_t i = 0; i < KW; ++i) {
+          row.key.push_back(bf16_bits(kr[i]));
+          row.value.push_back(bf16_bits(v[r * KW + i]));
+        }
+        staged[li].push_back(std::move(row));
+        attention_one_staged(qr, caches[li], staged[li], L.sinks, M->heads, M->kv_heads, M->head_dim, ctx.data());
+        for (size_t i = 0; i < QW; ++i) attention[r * QW + i] = bf16_bits(ctx[i]);
+      }
+      project_rows(L.o_weight, H, QW, attention.data(), m, L.o_bias, projected.data(), threads);
+      for (size_t r = 0; r < m; ++r) {
+        for (size_t i = 0; i < H; ++i) projected[r * H + i] = bf16_round(projected[r * H + i]);
+        oracle_add_residual(&hidden[r * H], &projected[r * H], H, &after[r * H]);
+        oracle_norm_boundary(&after[r * H], L.post_attention_norm, H, M->rms_norm_eps, &post[r * H]);
+      }
+      const int st = oracle_moe_batch(&L.moe, post.data(), m, nullptr, nullptr, nullptr, nullptr, moe_out.data(),
+                                      nullptr, nullptr, nullptr, nullptr, 1, threads);
+      if (st) return st;
+      for (size_t r = 0; r < m; ++r) oracle_add_residual(&after[r * H], &moe_out[r * H], H, &hidden[r * H]);
+    }
+    std::vector<uint16_t> fin(H);
+    oracle_norm_boundary(&hidden[(m - 1) * H], M->final_norm, H, M->rms_norm_eps, fin.data());
+    project_rows(M->lm_head, V, H, fin.data(), 1, nullptr, logits.data(), threads);
+    for (float& x : logits) {
+      x = bf16_round(x);
+      if (!std::isfinite(x)) return NON_FINITE_LOGITS;
+    }
+    // PreparedCpuStep::commit: the staged rows enter the caches in order.
+    for (size_t li = 0; li < M->layers; ++li)
+      for (size_t r = 0; r < m; ++r) caches[li].append(position + r, staged[li][r].key.data(), staged[li][r].value.data());
+    position += m;
+    if (consumed < n) {  // the next prompt chunk
+      const size_t next = std::min(n, consumed + chunk);
+      rows.assign(prompt + consumed, prompt + next);
+      consumed = next;
+      continue;
+    }
+    if (logits_out) std::memcpy(logits_out + step * V, logits.data(), V * 4);
+    if (int st = oracle_greedy_token(logits.data(), V, &tokens_out[step])) return st;
+    if (step == decode_steps) break;
+    rows.assign(1, tokens_out[step]);
+    ++step;
+  }
+  return OK;
+}
+
+// Counter-hash Gaussian bf16 tensor split over threads (each element depends
+// only on its index, so the result is oracle_gen_bf16_normal's).
+void oracle_gen_bf16_normal_mt(uint64_t seed, uint64_t stream, size_t n, float mean, float stddev, uint16_t* out,
+                               int threads) {
+  const size_t t = (size_t)std::max(1, threads);
+  std::vector<std::thread> pool;
+  for (size_t i = 0; i < t; ++i) {
+    const size_t lo = n * i / t, hi = n * (i + 1) / t;
+    pool.emplace_back([=] {
+      for (size_t j = lo; j < hi; ++j) {
+        const uint64_t a = stream_hash(seed, stream, 2 * j), b = stream_hash(seed, stream, 2 * j + 1);
+        const double u1 = ((double)(a >> 11) + 1.0) * 0x1.0p-53;
+        const double u2 = (double)(b >> 11) * 0x1.0p-53;
+        const double z = std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
+        out[j] = bf16_bits((float)(mean + stddev * z));
+      }
+    });
+  }
+  for (auto& th : pool) th.join();
+}
+
+}  // extern "C"

@@ -58,6 +58,27 @@ class OracleLayer(C.Structure):
     ]
 
 
+class OracleRope(C.Structure):
+    _fields_ = [("head_dim", C.c_size_t), ("theta", C.c_double), ("yarn", C.c_int32), ("factor", C.c_double),
+                ("original_max", C.c_size_t), ("beta_fast", C.c_double), ("beta_slow", C.c_double),
+                ("truncate", C.c_int32)]
+
+
+class OracleDenseLayer(C.Structure):
+    _fields_ = [("input_norm", C.c_void_p), ("q_weight", C.c_void_p), ("q_bias", C.c_void_p),
+                ("k_weight", C.c_void_p), ("k_bias", C.c_void_p), ("v_weight", C.c_void_p), ("v_bias", C.c_void_p),
+                ("o_weight", C.c_void_p), ("o_bias", C.c_void_p), ("sinks", C.c_void_p),
+                ("post_attention_norm", C.c_void_p), ("sliding", C.c_int32), ("moe", OracleLayer)]
+
+
+class OracleModel(C.Structure):
+    _fields_ = [("vocab", C.c_size_t), ("hidden", C.c_size_t), ("layers", C.c_size_t), ("heads", C.c_size_t),
+                ("kv_heads", C.c_size_t), ("head_dim", C.c_size_t), ("sliding_window", C.c_size_t),
+                ("context_cap", C.c_size_t), ("rms_norm_eps", C.c_float), ("rope", OracleRope),
+                ("embedding", C.c_void_p), ("final_norm", C.c_void_p), ("lm_head", C.c_void_p),
+                ("layer", C.POINTER(OracleDenseLayer))]
+
+
 def _declare(L):
     vp, sz, i32, u32, f32, u64 = C.c_void_p, C.c_size_t, C.c_int, C.c_uint32, C.c_float, C.c_uint64
     sig = {
@@ -93,6 +114,11 @@ def _declare(L):
         "oracle_gen_mxfp4": (None, [u64, u64, sz, sz, sz, vp]),
         "oracle_gen_bf16_normal": (None, [u64, u64, sz, f32, f32, vp]),
         "oracle_gen_hidden": (None, [u64, u64, sz, sz, i32, vp]),
+        "oracle_gen_bf16_normal_mt": (None, [u64, u64, sz, f32, f32, vp, i32]),
+        "oracle_yarn_rope": (i32, [C.POINTER(OracleRope), vp, sz, sz]),
+        "oracle_attention": (i32, [vp, vp, vp, sz, sz, vp, sz, sz, sz, vp, C.POINTER(sz), C.POINTER(sz)]),
+        "oracle_greedy_token": (i32, [vp, sz, C.POINTER(u32)]),
+        "oracle_model_generate": (i32, [C.POINTER(OracleModel), vp, sz, sz, sz, i32, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -343,3 +369,98 @@ def moe_residual(layer: "MoeLayerHost", residual_bf16: np.ndarray, norm_weight: 
     if res["status"] == OK:
         res["next_residual"] = add_residual(residual_bf16, res["output"])
     return res
+
+
+# ---------------------------------------------------------------------------
+# The dense path around the block (cpu_runner.rs), test infrastructure only.
+
+def rope_struct(head_dim, theta=150000.0, yarn=True, factor=32.0, original_max=4096, beta_fast=32.0,
+                beta_slow=1.0, truncate=False) -> OracleRope:
+    return OracleRope(head_dim, theta, 1 if yarn else 0, factor, original_max, beta_fast, beta_slow,
+                      1 if truncate else 0)
+
+
+def yarn_rope(rope: OracleRope, values, heads: int, position: int) -> np.ndarray:
+    v = np.array(values, dtype=np.float32)
+    lib().oracle_yarn_rope(C.byref(rope), _p(v), heads, position)
+    return v
+
+
+def attention(query, keys, values, window, sinks, heads, kv_heads, head_dim):
+    """attention_one over a cache of capacity `window` after appending every
+    key/value row; returns (output, cache len, cache start_position)."""
+    q = np.ascontiguousarray(query, dtype=np.float32)
+    k = np.ascontiguousarray(keys, dtype=np.uint16)
+    v = np.ascontiguousarray(values, dtype=np.uint16)
+    s = np.ascontiguousarray(sinks, dtype=np.float32)
+    out = np.zeros(heads * head_dim, np.float32)
+    n, start = C.c_size_t(), C.c_size_t()
+    tokens = k.size // (kv_heads * head_dim)
+    lib().oracle_attention(_p(q), _p(k), _p(v), tokens, window, _p(s), heads, kv_heads, head_dim, _p(out),
+                           C.byref(n), C.byref(start))
+    return out, n.value, start.value
+
+
+def greedy_token(logits):
+    v = np.ascontiguousarray(logits, dtype=np.float32)
+    t = C.c_uint32()
+    st = lib().oracle_greedy_token(_p(v), v.size, C.byref(t))
+    return None if st else t.value
+
+
+def gen_bf16_normal_mt(seed, stream, n, mean=0.0, std=1.0, threads=8):
+    out = np.zeros(n, dtype=np.uint16)
+    lib().oracle_gen_bf16_normal_mt(seed, stream, n, mean, std, _p(out), threads)
+    return out
+
+
+class ModelHost:
+    """A GPT-OSS model in the reference's host formats: config dict (the
+    gossmx_model_config fields), embedding/lm_head bf16 [vocab][hidden], final
+    norm f32, and per layer the dense tensors plus a MoeLayerHost."""
+
+    def __init__(self, config: dict, embedding, final_norm, lm_head, layers):
+        self.config = dict(config)
+        self.embedding = np.ascontiguousarray(embedding, dtype=np.uint16)
+        self.final_norm = np.ascontiguousarray(final_norm, dtype=np.float32)
+        self.lm_head = np.ascontiguousarray(lm_head, dtype=np.uint16)
+        self.layers = layers
+
+    def struct(self):
+        c = self.config
+        m = OracleModel()
+        for k in ("vocab", "hidden", "layers", "heads", "kv_heads", "head_dim", "sliding_window", "context_cap"):
+            setattr(m, k, c[k])
+        m.rms_norm_eps = c["rms_norm_eps"]
+        m.rope = rope_struct(c["head_dim"], c["rope_theta"], bool(c["rope_yarn"]), c["rope_factor"],
+                             c["rope_original_max_positions"], c.get("rope_beta_fast", 32.0),
+                             c.get("rope_beta_slow", 1.0), bool(c.get("rope_truncate", 0)))
+        m.embedding, m.final_norm, m.lm_head = (self.embedding.ctypes.data, self.final_norm.ctypes.data,
+                                                self.lm_head.ctypes.data)
+        table = (OracleDenseLayer * len(self.layers))()
+        keep = []
+        for i, L in enumerate(self.layers):
+            d = table[i]
+            for name in ("input_norm", "q_bias", "k_bias", "v_bias", "o_bias", "sinks", "post_attention_norm"):
+                a = np.ascontiguousarray(L[name], dtype=np.float32)
+                keep.append(a)
+                setattr(d, name, a.ctypes.data)
+            for name in ("q_weight", "k_weight", "v_weight", "o_weight"):
+                a = np.ascontiguousarray(L[name], dtype=np.uint16)
+                keep.append(a)
+                setattr(d, name, a.ctypes.data)
+            d.sliding = 1 if L["sliding"] else 0
+            d.moe = L["moe_host"].struct()
+        m.layer = table
+        return m, (table, keep)
+
+
+def model_generate(model: ModelHost, prompt, decode_steps, prefill_chunk=0, threads=8):
+    """prefill_layer_major then greedy decodes; returns (status, tokens, logits)."""
+    p = np.ascontiguousarray(prompt, dtype=np.uint32)
+    tokens = np.zeros(decode_steps + 1, np.uint32)
+    logits = np.zeros((decode_steps + 1, model.config["vocab"]), np.float32)
+    s, keep = model.struct()
+    st = lib().oracle_model_generate(C.byref(s), _p(p), p.size, prefill_chunk, decode_steps, threads, _p(tokens),
+                                     _p(logits))
+    return st, tokens, logits
