@@ -145,12 +145,99 @@ def cpu_baseline(cfg: dict, x, st0, layer_out_gpu, threads: int):
     }
 
 
+def run_model(args) -> int:
+    """the random-init GPT-OSS-20B forward, a 63-token prefill and 8
+    greedy decode steps, on the dense CPU path (gossmx_model_*, host threads)
+    with every layer's MoE block on the GPU. Times whole generations and splits
+    them into dense and MoE wall time; the CPU baseline is the oracle's
+    whole-model run (dense path and MoE on the host) on the same weights, whose
+    tokens and logits bits must equal the product's."""
+    import torch
+
+    torch.cuda.init()
+    ctx = G.Context(0)
+    ctx.selftest()
+    layers = args.layers or 24
+    cfg = dict(G.GPT_OSS_20B, layers=layers, context_cap=4096)
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(SEED)
+
+    def normal(n, std):
+        t = torch.randn(n, generator=gen, device="cuda:0", dtype=torch.float32).mul_(std).to(torch.bfloat16)
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+    w = synth.model_weights(cfg, normal)
+    rng = np.random.default_rng(SEED)
+    keep, dense_layers = [], []
+    for i, L in enumerate(w["layers"]):
+        gu = G.Weights.generate(ctx, SEED, 16 * i + 4, 32, 2 * INTER, BLOCKS)
+        dn = G.Weights.generate(ctx, SEED, 16 * i + 5, 32, HIDDEN, BLOCKS)
+        p = synth.dense_layer_params(rng, 32)
+        moe = G.MoeLayer(ctx, 32, HIDDEN, INTER, 4, p["router_weight"], p["router_bias"], gu, p["gate_up_bias"], dn,
+                         p["down_bias"])
+        keep.append((gu, dn, moe, p))
+        dense_layers.append(dict(L, moe=moe))
+    model = G.Model(ctx, G.model_config(threads=args.cpu_threads, **cfg), w["embedding"], w["final_norm"],
+                    w["lm_head"], dense_layers)
+    prompt = rng.integers(0, cfg["vocab"], 63).astype(np.uint32)
+    decode_steps = 8
+    for _ in range(args.warmup):
+        model.generate(prompt, decode_steps)
+    d0, m0 = model.times()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        tokens, logits = model.generate(prompt, decode_steps)
+    wall = (time.perf_counter() - t0) / args.steps
+    d1, m1 = model.times()
+    dense_s, moe_s = (d1 - d0) / args.steps, (m1 - m0) / args.steps
+    forwards = prompt.size + decode_steps
+    line = {
+        "metric": "configs[3] GPT-OSS-20B forward: token forwards/s (63-token prefill + 8 greedy decodes)",
+        "value": forwards / wall, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": wall * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 dense path (host) + MXFP4 x residual-Q8 MoE (GPU)",
+        "data": "synthetic (random-init weights, random prompt)",
+        "config": {"workload": f"configs[3]: random-init GPT-OSS-20B, {layers} layers, 63-token prefill + "
+                               f"{decode_steps} greedy decode steps, dense path on {args.cpu_threads} host threads",
+                   "layers": layers, "prompt": int(prompt.size), "decode_steps": decode_steps},
+        "dense_s": dense_s, "moe_s": moe_s, "moe_share": moe_s / wall, "greedy_tokens": tokens.tolist(),
+        "roofline": None, "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+
+        for L, (gu, dn, moe, p) in zip(w["layers"], keep):
+            L["moe_host"] = O.MoeLayerHost(p["router_weight"], p["router_bias"], gu.export_canonical(),
+                                           p["gate_up_bias"], dn.export_canonical(), p["down_bias"], 32, HIDDEN,
+                                           INTER, 4)
+        host = O.ModelHost(cfg, w["embedding"], w["final_norm"], w["lm_head"], w["layers"])
+        t0 = time.perf_counter()
+        st, want_tokens, want_logits = O.model_generate(host, prompt, decode_steps, threads=args.cpu_threads)
+        cpu_wall = time.perf_counter() - t0
+        line["cpu_baseline"] = {
+            "value": forwards / cpu_wall, "unit": "tokens/s", "cores": args.cpu_threads, "kind": "port",
+            "sample": f"the whole generation once: oracle dense path and MoE (Auto lane) on the host, "
+                      f"{args.cpu_threads} threads for projections and expert matmuls, {cpu_wall:.1f} s",
+            "greedy_match": bool(st == 0 and (want_tokens == tokens).all()),
+            "logits_bits_equal": bool(st == 0 and (want_logits.view(np.uint32) == logits.view(np.uint32)).all()),
+        }
+    print(json.dumps(line))
+    model.close()
+    for gu, dn, moe, _ in keep:
+        moe.close()
+        gu.close()
+        dn.close()
+    ctx.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS),
+    ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS) + [3],
                     help="BASELINE.json configs[] index of the workload (default 1)")
     ap.add_argument("--layers", type=int, default=None, help="override the config's layer count")
     ap.add_argument("--batch", type=int, default=None, help="override the config's batch")
@@ -180,6 +267,8 @@ def main() -> int:
         print("bench.py measures the single-GPU MoE block only; multi-GPU runs are not part of this build "
               "(expert-parallel sharding is a design note, not an implementation)", file=sys.stderr)
         return 2
+    if args.config == 3:
+        return run_model(args)
     cfg = dict(CONFIGS[args.config])
     for key in ("layers", "batch", "zipf"):
         if getattr(args, key) is not None:

@@ -28,6 +28,13 @@
  *                                  and the non-finite router ModelError, cpu_runner.rs:2829-2834
  *   - gossmx_profile_*          <- CpuExecutionProfiler records, cpu_profile.rs:30-51
  *   - gossmx_inject_fault       <- CpuExecutionFailurePoint test hook, cpu_runner.rs:478-483
+ *   - gossmx_model_*            <- the dense CPU step around the block: CpuModel::load,
+ *                                  new_sequence_state, prefill_layer_major, prepare_step/commit,
+ *                                  decode (cpu_runner.rs:1115-1306, 1596-1627, 1827-1885,
+ *                                  2080-2586, 1081-1113), with each MoE half on the GPU
+ *   - gossmx_attention, gossmx_yarn_rope, gossmx_greedy_token
+ *                               <- attention_one_staged, YarnRope (cpu_runner.rs:3840-4013),
+ *                                  greedy_token (gpt-oss-bench/src/bin/cpu_parity.rs:750-762)
  *
  * Weight layouts accepted on upload (Mxfp4WeightLayout, lib.rs:70-90):
  *   GOSSMX_LAYOUT_CANONICAL_V1 : per (row, block) 17 bytes = E8M0 scale byte, then

@@ -22,6 +22,10 @@
 //       closed-form invariants (top_k == experts, one-hot routing)
 //   x8 AVX2 GEMV baseline lane - bit-identical to the scalar matmul on the
 //       golden fixtures
+//   dense path (attention, YaRN, KV window, greedy token, model step) - the
+//       cpu_runner.rs attention / sink / window / cache / YaRN KATs and the
+//       step invariants in tests/test_dense.py (chunked prefill == one step,
+//       a covering window == full attention, thread-count independence)
 #include <cmath>
 #include <cstdint>
 #include <cstring>
