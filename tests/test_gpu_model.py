@@ -104,6 +104,21 @@ def test_small_model_failed_step_changes_nothing(tiny):
         model.decode(1)  # decode needs a prefill
 
 
+def test_small_model_moe_failure_mid_step_changes_nothing(ctx, tiny):
+    # The first MoE call of the step fails (the library's one-shot injected
+    # fault, raised before any launch): the step reports it and commits nothing.
+    cfg, model, oracle = tiny
+    _, want_tokens, want_logits = O.model_generate(oracle, PROMPT, 1, threads=4)
+    model.prefill(PROMPT)
+    before = [model.cache(i) for i in range(cfg["layers"])]
+    ctx.inject_fault(True)
+    with pytest.raises(G.GossmxError) as e:
+        model.decode(want_tokens[0])
+    assert e.value.status == G.ERR_INJECTED_FAULT
+    assert model.position == PROMPT.size and [model.cache(i) for i in range(cfg["layers"])] == before
+    assert_bits(model.decode(want_tokens[0]), want_logits[1])
+
+
 def hash_normal(seed):
     """normal(n, std) for model_weights: the oracle's counter-hash Gaussian,
     one stream per tensor, generated on 16 host threads."""
