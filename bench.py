@@ -49,10 +49,10 @@ DOWN_BYTES = HIDDEN * BLOCKS * 17         # 4,406,400 B per expert
 SEED = 20251201
 RMS_EPS = 1e-5  # GPT-OSS rms_norm_eps
 # HBM bytes per gate_up launch measured with rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE on this workload (166,485 KiB x 2.0 + 3,242 KiB x 1.0, scaled by
-# what the counters read for a 1 GiB device copy); bench.py cannot read
-# counters itself, so only the configuration that was profiled reports it.
-PMC_GATE_UP_TRAFFIC = {1: 336_212 * 1024}
+# WRITE_SIZE on each workload (FETCH KiB x 2.0 + WRITE KiB x 1.0, the factors
+# the counters read for a 1 GiB device copy; configs[1]: 166,485 x 2 + 3,242).
+# bench.py cannot read counters itself, so these are the profiled values.
+PMC_GATE_UP_TRAFFIC = {0: 35_101 * 1024, 1: 336_212 * 1024, 2: 3_381_431 * 1024, 4: 1_395_462 * 1024}
 
 CONFIGS = {
     0: {"batch": 1, "layers": 12, "experts": 32, "routing": "router", "zipf": None, "roofline": "hbm",
