@@ -60,8 +60,8 @@ inline float bf16_round(float f) { return bf16_f32(bf16_bits(f)); }
 // the weight row is read once per NX outputs. Lane l of every variant holds
 // the products of elements i = l (mod 16) in increasing i, exactly as the
 // reference's lanes do; the multiply and the add are separate roundings (no
-// FMA: the avx2 target does not enable fma, and this file builds with
-// -ffp-contract=off).
+// FMA: this file builds with -ffp-contract=off, so the products and sums
+// below are never contracted).
 
 typedef float f32x8 __attribute__((vector_size(32)));
 typedef uint32_t u32x8 __attribute__((vector_size(32)));
@@ -102,6 +102,43 @@ __attribute__((target("avx2"))) void dots_avx2(const uint16_t* w, const uint16_t
   }
 }
 
+// The same 16 lanes as one 512-bit vector.
+typedef float f32x16 __attribute__((vector_size(64)));
+typedef uint32_t u32x16 __attribute__((vector_size(64)));
+typedef uint16_t u16x16 __attribute__((vector_size(32)));
+
+__attribute__((target("avx512f"), always_inline)) inline f32x16 widen16(const uint16_t* p) {
+  u16x16 h;
+  std::memcpy(&h, p, 32);
+  const u32x16 u = __builtin_convertvector(h, u32x16) << 16;
+  f32x16 f;
+  std::memcpy(&f, &u, 64);
+  return f;
+}
+
+template <int NX>
+__attribute__((target("avx512f"))) void dots_avx512(const uint16_t* w, const uint16_t* const* x, size_t n,
+                                                    float* out) {
+  f32x16 acc[NX];
+  for (int r = 0; r < NX; ++r) acc[r] = f32x16{};
+  size_t i = 0;
+  for (; i + 16 <= n; i += 16) {
+    const f32x16 wv = widen16(w + i);
+    for (int r = 0; r < NX; ++r) {
+      const f32x16 p = wv * widen16(x[r] + i);
+      acc[r] = acc[r] + p;
+    }
+  }
+  for (int r = 0; r < NX; ++r) {
+    float lanes[16];
+    std::memcpy(lanes, &acc[r], 64);
+    for (size_t j = i, l = 0; j < n; ++j, ++l) lanes[l] += bf16_f32(w[j]) * bf16_f32(x[r][j]);
+    float s = 0.0f;
+    for (int l = 0; l < 16; ++l) s += lanes[l];
+    out[r] = s;
+  }
+}
+
 float dot_scalar(const uint16_t* w, const uint16_t* x, size_t n) {
   float lanes[16] = {0};
   size_t i = 0;
@@ -113,17 +150,30 @@ float dot_scalar(const uint16_t* w, const uint16_t* x, size_t n) {
   return s;
 }
 
-bool have_avx2() {
-  static const bool yes = [] {
+// 2: AVX-512F, 1: AVX2, 0: neither (the host's widest vector unit).
+int vector_level() {
+  static const int level = [] {
     __builtin_cpu_init();
-    return __builtin_cpu_supports("avx2") != 0;
+    if (__builtin_cpu_supports("avx512f")) return 2;
+    return __builtin_cpu_supports("avx2") ? 1 : 0;
   }();
-  return yes;
+  return level;
 }
 
 // out[r] = dot(w, x[r]) for r < nx.
 void dots(const uint16_t* w, const uint16_t* const* x, size_t nx, size_t n, float* out) {
-  if (!have_avx2()) {
+  if (vector_level() == 2) {
+    size_t r = 0;
+    for (; r + 4 <= nx; r += 4) dots_avx512<4>(w, x + r, n, out + r);
+    switch (nx - r) {
+      case 3: dots_avx512<3>(w, x + r, n, out + r); break;
+      case 2: dots_avx512<2>(w, x + r, n, out + r); break;
+      case 1: dots_avx512<1>(w, x + r, n, out + r); break;
+      default: break;
+    }
+    return;
+  }
+  if (vector_level() == 0) {
     for (size_t r = 0; r < nx; ++r) out[r] = dot_scalar(w, x[r], n);
     return;
   }
