@@ -66,7 +66,7 @@ struct gossmx_ctx {
   uint64_t op_launches[GOSSMX_OP_COUNT] = {0};
   // scratch
   DevBuf x, injected, logits, selected, weights, act1v, act1s, bucket, route_tok, route_slot, work, act2v, act2s, y,
-      cnt, xn, normw, next,
+      cnt, normw, next,
       out, trace, rec, bias, mout;
 };
 
@@ -355,7 +355,7 @@ void gossmx_ctx_destroy(gossmx_ctx* ctx) {
   for (auto e : ctx->event_pool) hipEventDestroy(e);
   DevBuf* bufs[] = {&ctx->x, &ctx->injected, &ctx->logits, &ctx->selected, &ctx->weights, &ctx->act1v,
                     &ctx->act1s, &ctx->bucket, &ctx->route_tok, &ctx->route_slot, &ctx->work, &ctx->act2v,
-                    &ctx->act2s, &ctx->y, &ctx->cnt, &ctx->xn, &ctx->normw, &ctx->next, &ctx->out,
+                    &ctx->act2s, &ctx->y, &ctx->cnt, &ctx->normw, &ctx->next, &ctx->out,
                     &ctx->trace, &ctx->rec, &ctx->bias, &ctx->mout};
   for (DevBuf* b : bufs)
     if (b->p) hipFree(b->p);
@@ -683,7 +683,6 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   uint16_t* next = nullptr;
   const float* route_norm_w = nullptr;
   if (residual) {
-    if ((s = ensure(ctx, ctx->xn, m * H * 2))) return s;
     const float* nw = norm_weight;
     next = next_residual;
     if (host) {
@@ -693,16 +692,9 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
       next = static_cast<uint16_t*>(ctx->next.p);
     }
     resid = x;
-    if (injected) {
-      // No router kernel runs: a kernel of its own normalizes the rows.
-      OpScope sc(ctx, GOSSMX_OP_POST_ATTENTION_NORM);
-      HIP_TRY(launch_rmsnorm(x, nw, (int)m, (int)H, norm_eps, static_cast<uint16_t*>(ctx->xn.p), ctx->stream),
-              "RMSNorm launch");
-      x = static_cast<const uint16_t*>(ctx->xn.p);
-    } else {
-      // The router kernel normalizes each row as it reads it.
-      route_norm_w = nw;
-    }
+    // The router kernel normalizes each row as it reads it; with injected
+    // logits the selection kernels' quantization work-groups do.
+    route_norm_w = nw;
   }
   int* selected = static_cast<int*>(ctx->selected.p);
   float* weights = static_cast<float*>(ctx->weights.p);

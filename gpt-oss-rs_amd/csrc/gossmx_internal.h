@@ -141,9 +141,6 @@ hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream);
 
 hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int top_k, int hidden, float* out,
                           float* trace_down, const uint16_t* resid, uint16_t* next, hipStream_t stream);
-// Post-attention RMSNorm rows -> bf16 (hidden <= kNormMaxHidden).
-hipError_t launch_rmsnorm(const uint16_t* x, const float* w, int m, int hidden, float eps, uint16_t* out,
-                          hipStream_t stream);
 hipError_t launch_prep_records(const uint8_t* records, int kind, size_t m, size_t blocks, size_t row_stride,
                                ActBuffers act, int* err, hipStream_t stream);
 hipError_t launch_repack(const uint8_t* src, int layout, TiledWeights w, hipStream_t stream);

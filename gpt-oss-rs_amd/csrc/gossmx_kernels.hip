@@ -232,10 +232,14 @@ __host__ __device__ __forceinline__ int router_groups(const RouteArgs& a) {
 
 // Grid (m, router_groups + quantization groups): work-group (r, g) computes
 // experts [16 g, 16 g + 16) of row r.
-// The inverse RMS of row xr (hidden H, a multiple of 8, 16-byte aligned) as
-// rmsnorm_kernel computes it, by a whole 256-thread work-group (every thread
-// calls it and gets the value): the row is staged in LDS with 16-byte loads,
-// then 16 threads run the lane sums.
+// The inverse RMS of row xr (hidden H <= kNormMaxHidden, a multiple of 8,
+// 16-byte aligned) for the post-attention RMSNorm (norm_boundary,
+// cpu_runner.rs:2680-2687, over Kernels::rms_norm and scalar_sum_squares,
+// lib.rs:699-730, 1031-1043), by a whole work-group of 256 or more threads
+// (every thread calls it and gets the value): the row is staged in LDS with
+// 16-byte loads, then lane l < 16 sums x_i * x_i (multiply, then add) over
+// i = l, l + 16, ... in order; the lanes are added 0..15; the inverse is
+// 1 / sqrt(sum / H + eps) with correctly rounded division and square root.
 __device__ __forceinline__ float row_inverse_rms(const uint16_t* xr, int H, float eps) {
   __shared__ __align__(16) uint16_t s_row[kNormMaxHidden];
   __shared__ float s_lane[16];
@@ -582,17 +586,36 @@ __device__ __forceinline__ void select_row_lanes(const float* lg, bool has_row, 
 // values each, one per half wave.
 constexpr int kSelectQuantBlocks = 32;
 
+// Quantization work-group `qwg` of the select kernels: kSelectQuantBlocks
+// blocks of 32 values, one per half wave. With r.norm_w the values are the
+// post-attention RMSNorm of their row rounded to bf16 (norm_boundary,
+// cpu_runner.rs:2680-2687); the inverse RMS of every row the work-group
+// touches is computed first, by the whole work-group (uniform loop).
+__device__ __forceinline__ void select_quantize(const RouteArgs& r, int qwg) {
+  const int tid = threadIdx.x;
+  const int blocks = r.hidden / kBlock;
+  const int g0 = qwg * kSelectQuantBlocks, g = g0 + (tid >> 5), row = g / blocks;
+  float inv = 1.0f;
+  if (r.norm_w) {
+    const int last = min(g0 + kSelectQuantBlocks, r.m * blocks) - 1;
+    for (int rr = g0 / blocks; rr <= last / blocks; ++rr) {
+      const float v = row_inverse_rms(r.x + (size_t)rr * r.hidden, r.hidden, r.norm_eps);
+      if (rr == row) inv = v;
+    }
+  }
+  if (g < r.m * blocks) {  // uniform per half wave
+    const int b = g % blocks, i = b * kBlock + (tid & 31);
+    float v = bf16_to_f32(r.x[(size_t)row * r.hidden + i]);
+    if (r.norm_w) v = bf16r(v * inv * r.norm_w[i]);
+    if (!isfinite(v)) atomicOr(r.err, kErrNonFiniteInput);
+    residual_q8_store(v, tid & 31, (size_t)row, blocks, b, r.act);
+  }
+}
+
 __global__ __launch_bounds__(1024) void select_dispatch_kernel(RouteArgs r, DispatchArgs d) {
   const int tid = threadIdx.x;
   if (blockIdx.x > 0) {
-    const int blocks = r.hidden / kBlock;
-    const int g = (blockIdx.x - 1) * kSelectQuantBlocks + (tid >> 5);
-    if (g < r.m * blocks) {  // uniform per half wave
-      const int row = g / blocks, b = g % blocks;
-      const float v = bf16_to_f32(r.x[(size_t)row * r.hidden + b * kBlock + (tid & 31)]);
-      if (!isfinite(v)) atomicOr(r.err, kErrNonFiniteInput);
-      residual_q8_store(v, tid & 31, (size_t)row, blocks, b, r.act);
-    }
+    select_quantize(r, (int)blockIdx.x - 1);
     return;
   }
   const int E = r.experts, K = r.top_k, M = r.m, stride = E + 1;
@@ -643,14 +666,7 @@ template <int KMAX>
 __global__ __launch_bounds__(1024) void select_count_kernel(RouteArgs r, int rows_per_wg, int n_sel, int* cnt) {
   const int tid = threadIdx.x;
   if ((int)blockIdx.x >= n_sel) {
-    const int blocks = r.hidden / kBlock;
-    const int g = ((int)blockIdx.x - n_sel) * kSelectQuantBlocks + (tid >> 5);
-    if (g < r.m * blocks) {  // uniform per half wave
-      const int row = g / blocks, b = g % blocks;
-      const float v = bf16_to_f32(r.x[(size_t)row * r.hidden + b * kBlock + (tid & 31)]);
-      if (!isfinite(v)) atomicOr(r.err, kErrNonFiniteInput);
-      residual_q8_store(v, tid & 31, (size_t)row, blocks, b, r.act);
-    }
+    select_quantize(r, (int)blockIdx.x - n_sel);
     return;
   }
   const int E = r.experts, K = r.top_k, stride = E + 1;
@@ -1325,66 +1341,6 @@ __global__ __launch_bounds__(256) void tile_flags_kernel(TiledWeights w) {
 
 // Eight consecutive outputs per thread: 16-byte bf16 loads of each rank's
 // row, two float4 stores. For 16-byte-aligned outputs (hidden % 8 == 0).
-// Post-attention RMSNorm of the residual stream, rounded to bf16
-// (norm_boundary, cpu_runner.rs:2680-2687, over Kernels::rms_norm and
-// scalar_sum_squares, lib.rs:699-730, 1031-1043): lane l < 16 sums x_i * x_i
-// (multiply, then add) over i = l, l + 16, ... in order from +0.0; the lanes
-// are added 0..15; inverse = 1 / sqrt(sum / n + eps) with correctly rounded
-// division and square root; y_i = bf16((x_i * inverse) * w_i). One
-// work-group per row; the row and the weights are staged in LDS as f32.
-// hidden must be a multiple of 8 and x, w, out 16-byte aligned.
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const float* w, int hidden, float eps,
-                                                      uint16_t* out) {
-  __shared__ __align__(16) float s_x[kNormMaxHidden];
-  __shared__ __align__(16) float s_w[kNormMaxHidden];
-  __shared__ float s_lane[16];
-  __shared__ float s_inv;
-  const int r = blockIdx.x, tid = threadIdx.x;
-  const int n8 = hidden / 8;  // hidden is a multiple of 32
-  const u32x4* const xr = reinterpret_cast<const u32x4*>(x + (size_t)r * hidden);
-  const float4* const w4 = reinterpret_cast<const float4*>(w);
-  // Row and weights to LDS with 16-byte loads, all issued before the first
-  // LDS write.
-#pragma unroll 4
-  for (int v = tid; v < n8; v += 256) {
-    const u32x4 p = xr[v];
-    const float4 wa = w4[2 * v], wb = w4[2 * v + 1];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      s_x[8 * v + 2 * q] = __uint_as_float(p[q] << 16);
-      s_x[8 * v + 2 * q + 1] = __uint_as_float(p[q] & 0xffff0000u);
-    }
-    reinterpret_cast<float4*>(s_w)[2 * v] = wa;
-    reinterpret_cast<float4*>(s_w)[2 * v + 1] = wb;
-  }
-  __syncthreads();
-  if (tid < 16) {
-    float acc = 0.0f;
-#pragma unroll 16
-    for (int i = tid; i < hidden; i += 16) acc = acc + s_x[i] * s_x[i];
-    s_lane[tid] = acc;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float ss = -0.0f;
-    for (int l = 0; l < 16; ++l) ss = ss + s_lane[l];
-    s_inv = 1.0f / sqrtf(ss / (float)hidden + eps);
-  }
-  __syncthreads();
-  const float inv = s_inv;
-  u32x4* const orow = reinterpret_cast<u32x4*>(out + (size_t)r * hidden);
-#pragma unroll 4
-  for (int v = tid; v < n8; v += 256) {
-    u32x4 o;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int i = 8 * v + 2 * q;
-      o[q] = (uint32_t)bf16_bits(s_x[i] * inv * s_w[i]) | ((uint32_t)bf16_bits(s_x[i + 1] * inv * s_w[i + 1]) << 16);
-    }
-    orow[v] = o;
-  }
-}
-
 // Combine (cpu_runner.rs:2959-2999): out = bf16(sum over ranks in order of
 // y_rank * w_rank), from 0.0. With `next`, also the residual add of the
 // decoder layer (add_residual, cpu_runner.rs:3732-3738): next =
@@ -1719,15 +1675,6 @@ hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int to
   else
     hipLaunchKernelGGL(combine_kernel, dim3(grid1d(hidden, 256), m), dim3(256), 0, stream, y, weights, top_k,
                        hidden, out, trace_down, resid, next);
-  return hipGetLastError();
-}
-
-hipError_t launch_rmsnorm(const uint16_t* x, const float* w, int m, int hidden, float eps, uint16_t* out,
-                          hipStream_t stream) {
-  const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-  if (hidden <= 0 || hidden > kNormMaxHidden || hidden % 8 != 0 || !a16(x) || !a16(w) || !a16(out))
-    return hipErrorInvalidValue;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(m), dim3(256), 0, stream, x, w, hidden, eps, out);
   return hipGetLastError();
 }
 

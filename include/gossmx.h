@@ -291,7 +291,8 @@ enum {
   GOSSMX_OP_DOWN = 3,               /* DownProjection */
   GOSSMX_OP_WEIGHTING = 4,          /* ExpertWeightingAccumulation */
   GOSSMX_OP_MATMUL = 5,             /* gossmx_mxfp4_matmul kernel */
-  GOSSMX_OP_POST_ATTENTION_NORM = 6, /* PostAttentionNormalization (gossmx_moe_forward_residual) */
+  GOSSMX_OP_POST_ATTENTION_NORM = 6, /* PostAttentionNormalization: no launch of its own; the norm runs
+                                       inside ROUTER_ROUTING (computed router) or DISPATCH (injected logits) */
   GOSSMX_OP_COUNT = 7
 };
 typedef struct gossmx_profile_record {

@@ -272,18 +272,25 @@ def assert_residual_equal(got, want, rows=None):
     assert (g == w).all(), f"next_residual: {int((g != w).sum())} mismatches, first {np.argwhere(g != w)[:3].tolist()}"
 
 
+@pytest.mark.parametrize("inject", [False, True])
 @pytest.mark.parametrize("experts,hidden,inter,top_k,m", [(4, 96, 64, 2, 5), (8, 128, 96, 4, 17),
-                                                           (32, 256, 128, 4, 70)])
-def test_residual_small_layers_bit_exact(ctx, experts, hidden, inter, top_k, m):
+                                                           (32, 256, 128, 4, 70), (32, 64, 64, 4, 300)])
+def test_residual_small_layers_bit_exact(ctx, experts, hidden, inter, top_k, m, inject):
     """gossmx_moe_forward_residual = norm_boundary -> moe_batch -> add_residual
-    (cpu_runner.rs:2519-2553) against the oracle, every output bit-exact."""
+    (cpu_runner.rs:2519-2553) against the oracle, every output bit-exact. With
+    injected logits the norm runs in the selection kernels' quantization
+    work-groups, which at these hidden sizes span several rows each; m = 300
+    with 32 experts takes the two-launch selection path."""
     host = O.synthetic_layer(13, 0, experts=experts, hidden=hidden, intermediate=inter, top_k=top_k)
     x = residual_stream(13, m, hidden)
     w = norm_weights(13, hidden)
-    want = O.moe_residual(host, x, w, 1e-5)
+    logits = None
+    if inject:
+        logits = O.bf16_round_array(np.random.default_rng(m).standard_normal((m, experts)).astype(np.float32))
+    want = O.moe_residual(host, x, w, 1e-5, injected_logits=logits)
     assert want["status"] == O.OK
     layer = gpu_layer(ctx, host)
-    got = layer.forward_residual(x, w, 1e-5)
+    got = layer.forward_residual(x, w, 1e-5, injected_logits=logits)
     assert_residual_equal(got, want)
     assert (got["route_order"] == want["route_order"]).all()
     close(layer)
