@@ -17,7 +17,8 @@ BASELINE.md's CPU figures). Inputs and weights are resident before timing.
      decode batch 256 with Zipf(1.2) routing.
 
 Prints one JSON line. The per-kernel roofline uses the library's hipEvent
-profiler on the stream the kernels run on; `cpu_baseline` times the oracle's
+profiler on the stream the kernels run on (the GEMM launches record their own
+start and stop events, so the interval is the kernel's execution); `cpu_baseline` times the oracle's
 faithful Auto lane (x8 AVX2 GEMV for single-row buckets, scalar matmul for
 multi-row buckets, one thread, as moe_batch runs it) on a bounded sample of
 layer 0 of the same batch after checking that the GPU's rows are

@@ -145,6 +145,28 @@ struct OpScope {
   }
 };
 
+// A stage of exactly one kernel: the launch itself records the start and stop
+// events (hipExtLaunchKernelGGL), so the interval is the kernel's execution
+// alone, without the stream's launch gaps around it.
+struct KernelScope {
+  gossmx_ctx* ctx;
+  int op;
+  hipEvent_t start = nullptr, stop = nullptr;
+  KernelScope(gossmx_ctx* c, int o) : ctx(c), op(o) {
+    if (ctx->profiling && !ctx->capturing) {
+      start = take_event(ctx);
+      stop = start ? take_event(ctx) : nullptr;
+      if (!stop && start) {
+        ctx->event_pool.push_back(start);
+        start = nullptr;
+      }
+    }
+  }
+  ~KernelScope() {
+    if (start) ctx->marks.push_back({op, start, stop});
+  }
+};
+
 int fold_profile(gossmx_ctx* ctx) {
   if (ctx->marks.empty()) return GOSSMX_OK;
   HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
@@ -556,9 +578,10 @@ int gossmx_mxfp4_matmul(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
   g.err = ctx->err;
   g.bias_expert_stride = 0;  // this problem's single bias vector
   {
-    OpScope scope(ctx, GOSSMX_OP_MATMUL);
+    KernelScope scope(ctx, GOSSMX_OP_MATMUL);
     const int chunk = gemm_chunk(m);
-    HIP_TRY(launch_gemm(kPlain, g, chunk, (int)((m + chunk - 1) / chunk), ctx->stream), "matmul launch");
+    HIP_TRY(launch_gemm(kPlain, g, chunk, (int)((m + chunk - 1) / chunk), ctx->stream, scope.start, scope.stop),
+            "matmul launch");
   }
   if (p->memory == GOSSMX_MEM_HOST) {
     HIP_TRY(hipMemcpy2DAsync(p->output, p->output_stride * sizeof(float), out, rows * sizeof(float),
@@ -782,12 +805,12 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   d.bias_expert_stride = H;
   d.y = static_cast<uint16_t*>(ctx->y.p);
   {
-    OpScope sc(ctx, GOSSMX_OP_GATE_UP);
-    HIP_TRY(launch_gemm(kGateUp, g, chunk, (int)max_work, ctx->stream), "gate_up launch");
+    KernelScope sc(ctx, GOSSMX_OP_GATE_UP);
+    HIP_TRY(launch_gemm(kGateUp, g, chunk, (int)max_work, ctx->stream, sc.start, sc.stop), "gate_up launch");
   }
   {
-    OpScope sc(ctx, GOSSMX_OP_DOWN);
-    HIP_TRY(launch_gemm(kDown, d, chunk, (int)max_work, ctx->stream), "down launch");
+    KernelScope sc(ctx, GOSSMX_OP_DOWN);
+    HIP_TRY(launch_gemm(kDown, d, chunk, (int)max_work, ctx->stream, sc.start, sc.stop), "down launch");
   }
   {
     OpScope sc(ctx, GOSSMX_OP_WEIGHTING);

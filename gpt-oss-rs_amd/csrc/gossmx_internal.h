@@ -136,7 +136,9 @@ hipError_t launch_place(const DispatchArgs& a, int m, const int* cnt, hipStream_
 hipError_t launch_select_dispatch(const RouteArgs& r, const DispatchArgs& d, int quantize, hipStream_t stream);
 // chunk: rows per work item (kSmallChunk, kChunk or kHugeChunk), selecting
 // the kernel's geometry; it must match the chunk the dispatch used.
-hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int chunk, int grid_work, hipStream_t stream);
+// start/stop (nullable): events the launch itself records around the kernel.
+hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int chunk, int grid_work, hipStream_t stream,
+                       hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream);
 
 hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int top_k, int hidden, float* out,

@@ -16,6 +16,8 @@
 // bit: the first product is the same real number rounded once.
 #include "gossmx_internal.h"
 
+#include <hip/hip_ext.h>
+
 #include <cmath>
 
 namespace gossmx {
@@ -1636,26 +1638,32 @@ hipError_t launch_select_dispatch(const RouteArgs& r, const DispatchArgs& d, int
 }
 
 template <class C>
-static hipError_t launch_gemm_cfg(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream) {
+static hipError_t launch_gemm_cfg(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream,
+                                  hipEvent_t start, hipEvent_t stop) {
   const dim3 grid((unsigned)((a.w.tiles + C::kWgTiles - 1) / C::kWgTiles), (unsigned)grid_work);
   const dim3 block(C::kThreads);
+  if (!a.residual && mode != kPlain) return hipErrorInvalidValue;  // the MoE block always runs residual-Q8
+  auto go = [&](auto kernel) {
+    if (start) hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, start, stop, 0, a);
+    else hipLaunchKernelGGL(kernel, grid, block, 0, stream, a);
+  };
   if (a.residual) {
     switch (mode) {
-      case kPlain: hipLaunchKernelGGL((gemm_kernel<C, kPlain, true>), grid, block, 0, stream, a); break;
-      case kGateUp: hipLaunchKernelGGL((gemm_kernel<C, kGateUp, true>), grid, block, 0, stream, a); break;
-      case kDown: hipLaunchKernelGGL((gemm_kernel<C, kDown, true>), grid, block, 0, stream, a); break;
+      case kPlain: go(gemm_kernel<C, kPlain, true>); break;
+      case kGateUp: go(gemm_kernel<C, kGateUp, true>); break;
+      case kDown: go(gemm_kernel<C, kDown, true>); break;
     }
   } else {
-    if (mode != kPlain) return hipErrorInvalidValue;  // the MoE block always runs residual-Q8
-    hipLaunchKernelGGL((gemm_kernel<C, kPlain, false>), grid, block, 0, stream, a);
+    go(gemm_kernel<C, kPlain, false>);
   }
   return hipGetLastError();
 }
 
-hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int chunk, int grid_work, hipStream_t stream) {
-  if (chunk == GemmSmall::kChunk) return launch_gemm_cfg<GemmSmall>(mode, a, grid_work, stream);
-  if (chunk == GemmBig::kChunk) return launch_gemm_cfg<GemmBig>(mode, a, grid_work, stream);
-  if (chunk == GemmHuge::kChunk) return launch_gemm_cfg<GemmHuge>(mode, a, grid_work, stream);
+hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int chunk, int grid_work, hipStream_t stream,
+                       hipEvent_t start, hipEvent_t stop) {
+  if (chunk == GemmSmall::kChunk) return launch_gemm_cfg<GemmSmall>(mode, a, grid_work, stream, start, stop);
+  if (chunk == GemmBig::kChunk) return launch_gemm_cfg<GemmBig>(mode, a, grid_work, stream, start, stop);
+  if (chunk == GemmHuge::kChunk) return launch_gemm_cfg<GemmHuge>(mode, a, grid_work, stream, start, stop);
   return hipErrorInvalidValue;
 }
 
