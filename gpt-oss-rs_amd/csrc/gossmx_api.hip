@@ -4,6 +4,7 @@
 #include "gossmx_internal.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -16,6 +17,15 @@ using namespace gossmx;
 namespace {
 
 thread_local std::string g_last_error;
+
+// Process-wide circuit breaker of the GPU backend, the counterpart of the Xe
+// engine's PROCESS_XE_CIRCUIT_OPEN (crates/gpt-oss-xe/src/lib.rs:605-724): a
+// projection that fails at run time (a HIP error, or the injected device
+// fault) drains its stream and opens the circuit; while it is open every
+// projection call returns GOSSMX_ERR_CIRCUIT_OPEN after validating its
+// arguments, so the caller recomputes once on its CPU path and stays there
+// until gossmx_circuit_reset().
+std::atomic<bool> g_circuit_open{false};
 
 int fail(int status, const char* fmt, ...) {
   char buf[512];
@@ -57,8 +67,14 @@ struct gossmx_ctx {
   bool own_stream = false;
   int* err = nullptr;  // device error flags
   uint16_t* sig_tab = nullptr;  // SwiGLU sigmoid table (built at context creation)
+  bool fast_ok = true;          // the scaled FP4 conversion passed the self-test (see run_selftest)
   bool capturing = false;
-  bool fault_armed = false;
+  int fault_armed = 0;          // gossmx_inject_fault mode for the next projection call
+  // Instantiated graphs of this context still alive. While any is, scratch
+  // buffers that must grow are retired (kept until the last graph is
+  // destroyed) instead of freed: the graphs hold their addresses.
+  int live_graphs = 0;
+  std::vector<void*> retired;
   bool profiling = false;
   std::vector<ProfileMark> marks;
   std::vector<hipEvent_t> event_pool;
@@ -71,18 +87,19 @@ struct gossmx_ctx {
 };
 
 struct gossmx_weights {
-  gossmx_ctx* ctx = nullptr;
   int device = 0;
   TiledWeights t;
 };
 
 struct gossmx_graph {
+  gossmx_ctx* ctx = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   int device = 0;
 };
 
 struct gossmx_layer {
+  int device = 0;
   gossmx_moe_config cfg;
   const gossmx_weights* gate_up = nullptr;
   const gossmx_weights* down = nullptr;
@@ -99,8 +116,12 @@ int ensure(gossmx_ctx* ctx, DevBuf& b, size_t bytes) {
   if (ctx->capturing)
     return fail(GOSSMX_ERR_UNSUPPORTED, "scratch would grow during graph capture; run the same shapes eagerly first");
   if (b.p) {
-    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
-    HIP_TRY(hipFree(b.p), "hipFree");
+    if (ctx->live_graphs > 0) {
+      ctx->retired.push_back(b.p);  // a live graph still reads and writes it
+    } else {
+      HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+      HIP_TRY(hipFree(b.p), "hipFree");
+    }
     b.p = nullptr;
     b.cap = 0;
   }
@@ -200,6 +221,29 @@ int set_device(int device) {
   return GOSSMX_OK;
 }
 
+// The checks every projection call makes after validating its arguments and
+// before touching the device: the circuit breaker, then the fault hook.
+int projection_gate(gossmx_ctx* ctx) {
+  if (g_circuit_open.load(std::memory_order_acquire))
+    return fail(GOSSMX_ERR_CIRCUIT_OPEN, "GPU circuit breaker is open");
+  const int mode = ctx->fault_armed;
+  ctx->fault_armed = 0;
+  if (mode == 1) return fail(GOSSMX_ERR_INJECTED_FAULT, "injected fault before launch");
+  if (mode == 2) return fail(GOSSMX_ERR_DEVICE, "injected device fault before launch");
+  return GOSSMX_OK;
+}
+
+// A projection's result: a run-time failure (HIP error or out of memory,
+// including the injected device fault) drains the stream and opens the
+// circuit (execute_projection, crates/gpt-oss-xe/src/lib.rs:680-724).
+int projection_result(gossmx_ctx* ctx, int status) {
+  if (status == GOSSMX_ERR_DEVICE || status == GOSSMX_ERR_OUT_OF_MEMORY) {
+    if (ctx) (void)hipStreamSynchronize(ctx->stream);
+    g_circuit_open.store(true, std::memory_order_release);
+  }
+  return status;
+}
+
 TiledWeights make_tiled(size_t experts, size_t rows, size_t blocks) {
   TiledWeights t;
   t.experts = experts;
@@ -217,7 +261,6 @@ int alloc_tiled(gossmx_ctx* ctx, size_t experts, size_t rows, size_t blocks, gos
     return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "invalid MXFP4 tensor shape [%zu, %zu, %zu]", experts, rows, blocks);
   if (int s = set_device(ctx->device)) return s;
   auto* w = new gossmx_weights();
-  w->ctx = ctx;
   w->device = ctx->device;
   w->t = make_tiled(experts, rows, blocks);
   if (w->t.nib_stride > (size_t)INT32_MAX - kPlaneSlack || w->t.scl_stride > (size_t)INT32_MAX - kPlaneSlack) {
@@ -312,6 +355,8 @@ int tiled_image_create(gossmx_ctx* ctx, size_t experts, size_t rows, size_t bloc
 
 }  // namespace gossmx
 
+static int run_selftest(gossmx_ctx* ctx, bool* scaled_ok);
+
 // ===========================================================================
 extern "C" {
 
@@ -362,6 +407,17 @@ int gossmx_ctx_create(int device, void* stream, gossmx_ctx** out) {
     gossmx_ctx_destroy(ctx);
     return hip_fail(e, "context setup");
   }
+  // The lane layouts and the sigmoid table must hold on this device; the
+  // scaled-conversion fast path is used only if its dirty-operand cases are
+  // exact (otherwise every tile takes the masked E8M0 path).
+  bool scaled_ok = true;
+  if (int s = run_selftest(ctx, &scaled_ok)) {
+    const std::string msg = g_last_error;
+    gossmx_ctx_destroy(ctx);
+    return fail(s, "device self-test failed: %s", msg.c_str());
+  }
+  ctx->fast_ok = scaled_ok;
+  g_last_error.clear();
   *out = ctx;
   return GOSSMX_OK;
 }
@@ -381,6 +437,7 @@ void gossmx_ctx_destroy(gossmx_ctx* ctx) {
                     &ctx->trace, &ctx->rec, &ctx->bias, &ctx->mout};
   for (DevBuf* b : bufs)
     if (b->p) hipFree(b->p);
+  for (void* p : ctx->retired) hipFree(p);
   if (ctx->err) hipFree(ctx->err);
   if (ctx->sig_tab) hipFree(ctx->sig_tab);
   if (ctx->own_stream && ctx->stream) hipStreamDestroy(ctx->stream);
@@ -503,8 +560,10 @@ size_t gossmx_weights_device_bytes(const gossmx_weights* w) {
 
 void gossmx_weights_destroy(gossmx_weights* w) {
   if (!w) return;
+  // Work of any stream may still read the planes; the device-wide wait does
+  // not need the context, which may already be gone.
   hipSetDevice(w->device);
-  if (w->ctx && w->ctx->stream) hipStreamSynchronize(w->ctx->stream);
+  hipDeviceSynchronize();
   if (w->t.nib) hipFree(w->t.nib);
   if (w->t.scl) hipFree(w->t.scl);
   if (w->t.fast) hipFree(w->t.fast);
@@ -526,17 +585,15 @@ int gossmx_mxfp4_matmul_check(const gossmx_matmul_problem* p, size_t rows, size_
   return validate_problem(p, rows, blocks, experts);
 }
 
-int gossmx_mxfp4_matmul(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
+static int matmul_impl(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
   if (!ctx) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context");
   if (!p || !p->weights) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null problem or weights");
   const TiledWeights& w = p->weights->t;
   if (int s = validate_problem(p, w.rows, w.blocks, w.experts)) return s;
   if (ctx->capturing && p->memory == GOSSMX_MEM_HOST)
     return fail(GOSSMX_ERR_UNSUPPORTED, "host-memory calls cannot be captured");
-  if (ctx->fault_armed) {
-    ctx->fault_armed = false;
-    return fail(GOSSMX_ERR_INJECTED_FAULT, "injected fault before launch");
-  }
+  if (p->weights->device != ctx->device) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "weights live on another device");
+  if (int s = projection_gate(ctx)) return s;
   if (int s = set_device(ctx->device)) return s;
   const size_t m = p->m, rows = w.rows, B = w.blocks;
   const size_t rsz = p->activation_kind == GOSSMX_ACT_RESIDUAL_Q8 ? 72 : 36;
@@ -567,6 +624,7 @@ int gossmx_mxfp4_matmul(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
   }
   GemmArgs g{};
   g.w = w;
+  g.fast_ok = ctx->fast_ok ? 1 : 0;
   g.actv = act.v;
   g.acts = act.s;
   g.bias = bias;
@@ -592,6 +650,25 @@ int gossmx_mxfp4_matmul(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
   return GOSSMX_OK;
 }
 
+int gossmx_mxfp4_matmul(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
+  return projection_result(ctx, matmul_impl(ctx, p));
+}
+
+int gossmx_mxfp4_scratch_requirement(const gossmx_matmul_problem* p, size_t* size, size_t* alignment) {
+  if (!size || !alignment) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null output");
+  if (!p || !p->weights) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null problem or weights");
+  const TiledWeights& w = p->weights->t;
+  if (int s = validate_problem(p, w.rows, w.blocks, w.experts)) return s;
+  // The device keeps its own operand buffers: Mxfp4ScratchRequirement::NONE.
+  *size = 0;
+  *alignment = 1;
+  return GOSSMX_OK;
+}
+
+int gossmx_circuit_is_open(void) { return g_circuit_open.load(std::memory_order_acquire) ? 1 : 0; }
+
+void gossmx_circuit_reset(void) { g_circuit_open.store(false, std::memory_order_release); }
+
 // --- MoE block -------------------------------------------------------------
 
 int gossmx_layer_create(gossmx_ctx* ctx, const gossmx_moe_config* cfg, const uint16_t* router_weight_bf16,
@@ -609,6 +686,7 @@ int gossmx_layer_create(gossmx_ctx* ctx, const gossmx_moe_config* cfg, const uin
                 H / kBlock, E, H, I / kBlock);
   if (int s = set_device(ctx->device)) return s;
   auto* L = new gossmx_layer();
+  L->device = ctx->device;
   L->cfg = *cfg;
   L->gate_up = gate_up;
   L->down = down;
@@ -630,6 +708,8 @@ int gossmx_layer_create(gossmx_ctx* ctx, const gossmx_moe_config* cfg, const uin
 
 void gossmx_layer_destroy(gossmx_layer* L) {
   if (!L) return;
+  hipSetDevice(L->device);
+  hipDeviceSynchronize();
   if (L->router_w) hipFree(L->router_w);
   if (L->router_b) hipFree(L->router_b);
   if (L->gate_up_bias) hipFree(L->gate_up_bias);
@@ -661,10 +741,8 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   if (m > (size_t)(INT32_MAX / 8) / std::max<size_t>(H, E) ||
       R * std::max(B1, B2) * 2 * kBlock * sizeof(_Float16) >= (size_t)INT32_MAX - kActSlack)
     return fail(GOSSMX_ERR_UNSUPPORTED, "batch too large for this build");
-  if (ctx->fault_armed) {
-    ctx->fault_armed = false;
-    return fail(GOSSMX_ERR_INJECTED_FAULT, "injected fault before launch");
-  }
+  if (L->device != ctx->device) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "layer lives on another device");
+  if (int s = projection_gate(ctx)) return s;
   if (int s = set_device(ctx->device)) return s;
   const bool host = io->memory == GOSSMX_MEM_HOST;
   const int chunk = gemm_chunk(m);
@@ -782,6 +860,7 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   }
   GemmArgs g{};
   g.w = L->gate_up->t;
+  g.fast_ok = ctx->fast_ok ? 1 : 0;
   g.actv = act1.v;
   g.acts = act1.s;
   g.bias = L->gate_up_bias;
@@ -847,13 +926,13 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
 }
 
 int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_io* io) {
-  return moe_forward_impl(ctx, L, io, nullptr, 0.0f, nullptr);
+  return projection_result(ctx, moe_forward_impl(ctx, L, io, nullptr, 0.0f, nullptr));
 }
 
 int gossmx_moe_forward_residual(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_io* io,
                                 const float* norm_weight, float epsilon, uint16_t* next_residual) {
   if (!norm_weight) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
-  return moe_forward_impl(ctx, L, io, norm_weight, epsilon, next_residual);
+  return projection_result(ctx, moe_forward_impl(ctx, L, io, norm_weight, epsilon, next_residual));
 }
 
 // --- profiling, fault hook, self-test -------------------------------------------
@@ -911,6 +990,8 @@ int gossmx_capture_end(gossmx_ctx* ctx, gossmx_graph** out) {
     gossmx_graph_destroy(g);
     return hip_fail(e, "hipGraphInstantiate");
   }
+  g->ctx = ctx;
+  ++ctx->live_graphs;
   *out = g;
   return GOSSMX_OK;
 }
@@ -926,31 +1007,44 @@ int gossmx_graph_launch(gossmx_ctx* ctx, const gossmx_graph* g) {
 void gossmx_graph_destroy(gossmx_graph* g) {
   if (!g) return;
   hipSetDevice(g->device);
+  if (g->ctx) hipStreamSynchronize(g->ctx->stream);  // no replay still reads its buffers
   if (g->exec) hipGraphExecDestroy(g->exec);
   if (g->graph) hipGraphDestroy(g->graph);
+  if (g->ctx && --g->ctx->live_graphs == 0) {
+    for (void* p : g->ctx->retired) hipFree(p);
+    g->ctx->retired.clear();
+  }
   delete g;
 }
 
 int gossmx_inject_fault(gossmx_ctx* ctx, int armed) {
   if (!ctx) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context");
-  ctx->fault_armed = armed != 0;
+  if (armed < 0 || armed > 2) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "unknown fault mode %d", armed);
+  ctx->fault_armed = armed;
   return GOSSMX_OK;
 }
 
 // Checks the lane layouts of the FP4 conversion and the 16x16x32 f16 MFMA on
-// this device against what the GEMM assumes.
-int gossmx_selftest(gossmx_ctx* ctx) {
-  if (!ctx) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context");
+// this device against what the GEMM assumes, and the device SwiGLU sigmoid
+// table against the host expf. *scaled_ok reports whether the scaled
+// conversion with dirty scale operands (the GEMM's fast path) gave the exact
+// scaled values; the other checks fail the call.
+int gossmx_selftest(gossmx_ctx* ctx);
+}  // extern "C"
+
+static int run_selftest(gossmx_ctx* ctx, bool* scaled_ok) {
   if (int s = set_device(ctx->device)) return s;
   float* dev = nullptr;
-  HIP_TRY(hipMalloc(&dev, (8 + 256 + 8) * sizeof(float)), "hipMalloc(selftest)");
-  float host[8 + 256 + 8];
+  HIP_TRY(hipMalloc(&dev, kSelftestFloats * sizeof(float)), "hipMalloc(selftest)");
+  std::vector<float> host(kSelftestFloats);
   hipError_t e = launch_selftest(dev, ctx->stream);
-  if (e == hipSuccess) e = hipMemcpyAsync(host, dev, sizeof host, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(host.data(), dev, kSelftestFloats * sizeof(float), hipMemcpyDeviceToHost,
+                                          ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   hipFree(dev);
   if (e != hipSuccess) return hip_fail(e, "selftest");
-  const float codes[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+  const float codes[16] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f,
+                           -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
   for (int i = 0; i < 8; ++i)
     if (host[i] != codes[i])
       return fail(GOSSMX_ERR_UNSUPPORTED, "fp4 conversion element %d is %g, expected %g", i, host[i], codes[i]);
@@ -965,6 +1059,24 @@ int gossmx_selftest(gossmx_ctx* ctx) {
         return fail(GOSSMX_ERR_UNSUPPORTED, "mfma lane %d reg %d is %g, expected %g", lane, r, host[8 + 4 * lane + r],
                     want);
     }
+  // Dirty scale operands (selftest_kernel): every result must be the code's
+  // value times 2^(e - 127), with the sign of -0.0 codes kept.
+  const uint32_t dirty_exp[5] = {114, 120, 127, 133, 139};
+  *scaled_ok = true;
+  for (int c = 0; c < kSelftestDirty && *scaled_ok; ++c) {
+    const float scale = std::ldexp(1.0f, (int)dirty_exp[c / 24] - 127);
+    for (int i = 0; i < 16; ++i) {
+      const float want = codes[i] * scale, got = host[272 + 16 * c + i];
+      if (std::memcmp(&want, &got, 4) != 0) {
+        *scaled_ok = false;
+        fail(GOSSMX_ERR_UNSUPPORTED,
+             "scaled fp4 conversion with a dirty scale operand (exponent %u, byte %d, case %d) gave %g for code %d, "
+             "expected %g",
+             dirty_exp[c / 24], (c / 6) % 4, c, got, i, want);
+        break;
+      }
+    }
+  }
   // The device SwiGLU sigmoid table against the host libm expf on all 65,536
   // bf16 inputs (the reference's f32::exp is the host expf).
   std::vector<uint16_t> tab(65536);
@@ -985,6 +1097,24 @@ int gossmx_selftest(gossmx_ctx* ctx) {
     if (tab[i] != want)
       return fail(GOSSMX_ERR_UNSUPPORTED, "sigmoid table entry %#06x is %#06x, host expf gives %#06x", i, tab[i], want);
   }
+  return GOSSMX_OK;
+}
+
+extern "C" {
+
+int gossmx_selftest(gossmx_ctx* ctx) {
+  if (!ctx) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context");
+  const std::string prior = g_last_error;
+  bool scaled_ok = true;
+  if (int s = run_selftest(ctx, &scaled_ok)) return s;
+  if (!scaled_ok) return GOSSMX_ERR_UNSUPPORTED;  // message set by run_selftest
+  g_last_error = prior;
+  return GOSSMX_OK;
+}
+
+int gossmx_ctx_fast_path(const gossmx_ctx* ctx, int* enabled) {
+  if (!ctx || !enabled) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+  *enabled = ctx->fast_ok ? 1 : 0;
   return GOSSMX_OK;
 }
 

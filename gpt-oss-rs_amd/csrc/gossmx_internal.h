@@ -67,6 +67,7 @@ enum GemmMode { kPlain = 0, kGateUp = 1, kDown = 2 };
 
 struct GemmArgs {
   TiledWeights w;
+  int fast_ok;           // 0: never take the scaled-conversion fast path (self-test found it unsafe)
   const _Float16* actv;
   const float* acts;
   const float* bias;     // bias of expert e at bias + e * bias_expert_stride, or null
@@ -151,6 +152,13 @@ hipError_t launch_export(TiledWeights w, uint8_t* dst, hipStream_t stream);
 hipError_t launch_fill_tiled_padding(TiledWeights w, hipStream_t stream);
 hipError_t launch_clear_ints(int* p, size_t n, hipStream_t stream);
 hipError_t launch_build_sigmoid_table(uint16_t* tab, hipStream_t stream);
+// Self-test outputs (floats): kSelftestCodes conversion results, 256 MFMA
+// results, kSelftestCodes scaled results, then kSelftestDirty x 16 results of
+// the scaled conversion with the E8M0 byte in a dirty scale dword (see
+// selftest_kernel).
+constexpr int kSelftestCodes = 8;
+constexpr int kSelftestDirty = 5 * 4 * 6;  // exponents x byte positions x neighbour patterns
+constexpr int kSelftestFloats = kSelftestCodes + 256 + kSelftestCodes + 16 * kSelftestDirty;
 hipError_t launch_selftest(float* out, hipStream_t stream);
 
 }  // namespace gossmx

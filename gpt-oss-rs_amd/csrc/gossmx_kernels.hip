@@ -1254,7 +1254,7 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
     k.nib[t] = buffer_rsrc(nib);
     k.scl[t] = buffer_rsrc(scl);
     const uint8_t tile_fast = a.w.fast[(size_t)expert * a.w.tiles + safe_tile];
-    fast = fast && (!ok || tile_fast != 0);
+    fast = fast && (!ok || tile_fast != 0) && a.fast_ok;
     const int row = tile * kTileRows + nl;
     float bias = 0.0f;
     if (a.bias != nullptr && ok && row < rows) bias = a.bias[(size_t)expert * a.bias_expert_stride + row];
@@ -1561,11 +1561,21 @@ __global__ void clear_ints_kernel(int* p, size_t n) {
   if (i < n) p[i] = 0;
 }
 
+// E8M0 exponents, byte positions and neighbour-byte patterns of the dirty
+// scale operands the self-test converts with (every other byte of the scale
+// dword holds the pattern, so sign and mantissa bits of the operand are set).
+__constant__ uint32_t kDirtyExp[5] = {kFastScaleLo, 120, 127, 133, kFastScaleHi};
+__constant__ uint32_t kDirtyPattern[6] = {0x00, 0xff, 0x80, 0x7f, 0xa5, 0x01};
+
 // Lane-layout self-test of the two gfx950 builtins the GEMM relies on.
 // out[0..7]: v_cvt_scalef32_pk_f16_fp4 of codes 0..7 (bytes 0x10 0x32 0x54 0x76).
 // out[8 + 4 * lane + r]: D of a 16x16x32 f16 MFMA with A[i][k] = (k == i) and
 // B[k][j] = 10 k + j, expected 10 * (4 * (lane / 16) + r) + lane % 16.
 // out[264..271]: codes 0..7 converted with scale 2^-4.
+// out[272 + 16 * c + i], case c = (exponent x, byte j, pattern p) in that
+// order: code i (0..15) converted through e8m0_scale_operand(s, j) of the
+// dword s whose byte j is kDirtyExp[x] and whose other bytes are
+// kDirtyPattern[p]; expected decode(i) * 2^(e - 127).
 __global__ void selftest_kernel(float* out) {
   const int lane = threadIdx.x;
   const half8 w = fp4x8_to_half8(0x76543210u);
@@ -1584,6 +1594,24 @@ __global__ void selftest_kernel(float* out) {
   const half8 ws = fp4x8_to_half8_scaled(0x76543210u, __uint_as_float(123u << 23));
   if (lane == 0)
     for (int i = 0; i < 8; ++i) out[264 + i] = (float)ws[i];
+  for (int c = lane; c < kSelftestDirty; c += 64) {
+    const int x = c / 24, j = (c / 6) % 4, p = c % 6;
+    uint32_t s = kDirtyPattern[p] * 0x01010101u;
+    s = (s & ~(0xffu << (8 * j))) | (kDirtyExp[x] << (8 * j));
+    float sc;
+    switch (j) {  // e8m0_scale_operand takes its byte position as a constant
+      case 0: sc = e8m0_scale_operand(s, 0); break;
+      case 1: sc = e8m0_scale_operand(s, 1); break;
+      case 2: sc = e8m0_scale_operand(s, 2); break;
+      default: sc = e8m0_scale_operand(s, 3); break;
+    }
+    const half8 lo = fp4x8_to_half8_scaled(0x76543210u, sc);
+    const half8 hi = fp4x8_to_half8_scaled(0xfedcba98u, sc);
+    for (int i = 0; i < 8; ++i) {
+      out[272 + 16 * c + i] = (float)lo[i];
+      out[272 + 16 * c + 8 + i] = (float)hi[i];
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -34,6 +34,11 @@ ERR_OUT_OF_MEMORY = 7
 ERR_NON_FINITE_LOGITS = 8
 ERR_INJECTED_FAULT = 9
 ERR_BAD_FILE = 10
+ERR_CIRCUIT_OPEN = 11
+
+FAULT_NONE = 0
+FAULT_INJECTED = 1   # GOSSMX_ERR_INJECTED_FAULT, the breaker stays closed
+FAULT_DEVICE = 2     # GOSSMX_ERR_DEVICE, opens the breaker
 
 LAYOUT_CANONICAL_V1 = 1
 LAYOUT_X8_SPLIT_V2 = 2
@@ -167,6 +172,10 @@ def load():
         "gossmx_weights_destroy": (None, [vp]),
         "gossmx_mxfp4_matmul": (i32, [vp, C.POINTER(MatmulProblem)]),
         "gossmx_mxfp4_matmul_check": (i32, [C.POINTER(MatmulProblem), sz, sz, sz]),
+        "gossmx_mxfp4_scratch_requirement": (i32, [C.POINTER(MatmulProblem), C.POINTER(sz), C.POINTER(sz)]),
+        "gossmx_circuit_is_open": (i32, []),
+        "gossmx_circuit_reset": (None, []),
+        "gossmx_ctx_fast_path": (i32, [vp, C.POINTER(C.c_int)]),
         "gossmx_layer_create": (i32, [vp, C.POINTER(MoeConfig), vp, vp, vp, vp, vp, vp, pp]),
         "gossmx_layer_destroy": (None, [vp]),
         "gossmx_moe_forward": (i32, [vp, vp, C.POINTER(MoeIo)]),
@@ -226,6 +235,15 @@ def _ptr(a):
     return a.ctypes.data_as(C.c_void_p).value
 
 
+def circuit_is_open() -> bool:
+    """The process-wide circuit breaker (XeProjectionEngine::circuit_is_open)."""
+    return bool(load().gossmx_circuit_is_open())
+
+
+def circuit_reset():
+    load().gossmx_circuit_reset()
+
+
 def device_count() -> int:
     n = C.c_int(0)
     _check(load().gossmx_device_count(C.byref(n)))
@@ -257,8 +275,19 @@ class Context:
     def selftest(self):
         _check(load().gossmx_selftest(self._h))
 
-    def inject_fault(self, armed: bool = True):
-        _check(load().gossmx_inject_fault(self._h, 1 if armed else 0))
+    def inject_fault(self, armed: bool | int = True):
+        """Arms the fault hook of the next projection call: True or
+        FAULT_INJECTED (a model error), FAULT_DEVICE (a device fault that
+        opens the circuit breaker), False or FAULT_NONE (disarm)."""
+        mode = int(armed) if not isinstance(armed, bool) else (FAULT_INJECTED if armed else FAULT_NONE)
+        _check(load().gossmx_inject_fault(self._h, mode))
+
+    def fast_path(self) -> bool:
+        """Whether the GEMMs may take the scaled-conversion fast path (the
+        self-test at creation found the dirty-operand conversion exact)."""
+        v = C.c_int(0)
+        _check(load().gossmx_ctx_fast_path(self._h, C.byref(v)))
+        return bool(v.value)
 
     def profile(self, enabled: bool = True):
         _check(load().gossmx_profile_enable(self._h, 1 if enabled else 0))
@@ -500,6 +529,29 @@ def matmul_check(rows: int, blocks: int, experts: int, activations_len: int, m: 
     p.output_stride = output_stride
     p.memory = MEM_HOST
     return load().gossmx_mxfp4_matmul_check(C.byref(p), rows, blocks, experts)
+
+
+def scratch_requirement(weights: "Weights", m: int, kind: int = ACT_RESIDUAL_Q8) -> tuple[int, int]:
+    """Mxfp4MatmulBackend::scratch_requirement of the GPU backend for a dense
+    m-row problem on `weights`: (size, alignment)."""
+    p = MatmulProblem()
+    p.weights = weights.handle.value
+    p.expert = 0
+    p.activation_kind = kind
+    p.activations = 1
+    p.activations_len = m * weights.blocks
+    p.m = m
+    p.blocks_per_row = weights.blocks
+    p.row_stride = weights.blocks
+    p.bias = None
+    p.bias_len = 0
+    p.output = 1
+    p.output_len = m * weights.rows
+    p.output_stride = weights.rows
+    p.memory = MEM_HOST
+    size, align = C.c_size_t(), C.c_size_t()
+    _check(load().gossmx_mxfp4_scratch_requirement(C.byref(p), C.byref(size), C.byref(align)))
+    return size.value, align.value
 
 
 @dataclass

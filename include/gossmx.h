@@ -48,6 +48,10 @@
  * Threading: a context owns one HIP stream and is used by one thread at a time
  * (like CpuExecutionContext, cpu_runner.rs:868-876). Calls are asynchronous on that
  * stream unless they return host data; gossmx_synchronize() waits.
+ *
+ * Lifetimes: weights and layers do not refer to their context after creation
+ * (their destroy waits for the whole device), so they may outlive it. Graphs
+ * and models do: destroy them before their context.
  */
 #ifndef GOSSMX_H
 #define GOSSMX_H
@@ -70,7 +74,8 @@ typedef enum gossmx_status {
   GOSSMX_ERR_OUT_OF_MEMORY = 7,
   GOSSMX_ERR_NON_FINITE_LOGITS = 8,   /* "CPU router produced non-finite logits" */
   GOSSMX_ERR_INJECTED_FAULT = 9,      /* gossmx_inject_fault test hook fired */
-  GOSSMX_ERR_BAD_FILE = 10            /* missing, unreadable or malformed file (the store's ModelError / io::Error) */
+  GOSSMX_ERR_BAD_FILE = 10,           /* missing, unreadable or malformed file (the store's ModelError / io::Error) */
+  GOSSMX_ERR_CIRCUIT_OPEN = 11        /* XeError::CircuitOpen: an earlier run-time fault opened the breaker */
 } gossmx_status;
 
 enum {
@@ -96,8 +101,14 @@ int gossmx_version(void);
 int gossmx_device_count(int* count);
 
 /* Context: one device, one in-order HIP stream. `stream` may be NULL (the
- * context creates its own) or a caller hipStream_t (not destroyed by us). */
+ * context creates its own) or a caller hipStream_t (not destroyed by us).
+ * Creation runs the device self-test (gossmx_selftest) and fails with
+ * GOSSMX_ERR_UNSUPPORTED if a lane layout or the sigmoid table is wrong; if
+ * only the scaled FP4 conversion with dirty scale operands is, the context is
+ * created with the GEMM's scaled-conversion fast path off (same bits, slower). */
 int gossmx_ctx_create(int device, void* stream, gossmx_ctx** out);
+/* 1 when the context's GEMMs may take the scaled-conversion fast path. */
+int gossmx_ctx_fast_path(const gossmx_ctx* ctx, int* enabled);
 void gossmx_ctx_destroy(gossmx_ctx* ctx);
 int gossmx_ctx_set_stream(gossmx_ctx* ctx, void* stream);
 void* gossmx_ctx_stream(gossmx_ctx* ctx);
@@ -220,6 +231,23 @@ int gossmx_mxfp4_matmul(gossmx_ctx* ctx, const gossmx_matmul_problem* problem);
 /* The validation gossmx_mxfp4_matmul runs first, against a weights shape, with
  * no device access (Mxfp4MatmulProblem::new, matmul.rs:339-369). */
 int gossmx_mxfp4_matmul_check(const gossmx_matmul_problem* problem, size_t rows, size_t blocks, size_t experts);
+/* Mxfp4MatmulBackend::scratch_requirement (matmul.rs:58-93): caller-owned scratch
+ * the call needs. The GPU backend keeps its own operand buffers, so a valid
+ * problem gets size 0 and alignment 1 (Mxfp4ScratchRequirement::NONE, :124-129);
+ * an invalid one the validation's status. No device access. */
+int gossmx_mxfp4_scratch_requirement(const gossmx_matmul_problem* problem, size_t* size, size_t* alignment);
+
+/* Process-wide circuit breaker (the Xe engine's PROCESS_XE_CIRCUIT_OPEN,
+ * crates/gpt-oss-xe/src/lib.rs:605-724). A projection call (gossmx_mxfp4_matmul,
+ * gossmx_moe_forward, gossmx_moe_forward_residual) that fails at run time with
+ * GOSSMX_ERR_DEVICE or GOSSMX_ERR_OUT_OF_MEMORY drains its stream and opens the
+ * circuit; while it is open those calls validate their arguments and then return
+ * GOSSMX_ERR_CIRCUIT_OPEN without touching the device. The caller recomputes the
+ * failed call once on its CPU path (cpu_runner.rs:3365-3387) and keeps using the
+ * CPU until it resets the breaker. Argument, data (non-finite) and injected
+ * (mode 1) failures leave it closed. */
+int gossmx_circuit_is_open(void);
+void gossmx_circuit_reset(void);
 
 /* MoE layer (GPT-OSS): router [experts][hidden] bf16 + f32 bias, gate_up
  * [experts][2*intermediate][hidden/32] with gate/up rows interleaved even/odd
@@ -311,21 +339,33 @@ int gossmx_profile_reset(gossmx_ctx* ctx);
  * GOSSMX_MEM_DEVICE pointers are recorded, not run; host-memory calls and
  * profiling are refused, and scratch buffers must already be large enough
  * (run the same shapes once eagerly first). A graph replays on the context's
- * stream with the pointers it was recorded with; device-side checks surface at
- * gossmx_synchronize as usual. */
+ * stream with the pointers it was recorded with, including the context's
+ * scratch buffers: while a graph is alive, a later call that needs larger
+ * scratch gets new buffers and the old ones stay allocated until the last graph
+ * of the context is destroyed, so eager calls of any size may run between
+ * replays. Replays and eager calls share the scratch, so they must not overlap
+ * (both run on the context's stream, which orders them). Device-side checks
+ * surface at gossmx_synchronize as usual. Destroy graphs before the context. */
 typedef struct gossmx_graph gossmx_graph;
 int gossmx_capture_begin(gossmx_ctx* ctx);
 int gossmx_capture_end(gossmx_ctx* ctx, gossmx_graph** out);
 int gossmx_graph_launch(gossmx_ctx* ctx, const gossmx_graph* graph);
 void gossmx_graph_destroy(gossmx_graph* graph);
 
-/* Test hook: the next gossmx_moe_forward / gossmx_mxfp4_matmul on this context
- * fails with GOSSMX_ERR_INJECTED_FAULT before launching anything (outputs untouched). */
+/* Test hook for the next projection call on this context (gossmx_moe_forward,
+ * gossmx_moe_forward_residual, gossmx_mxfp4_matmul), after its argument checks
+ * and before it launches anything (outputs untouched): armed = 1 fails it with
+ * GOSSMX_ERR_INJECTED_FAULT (a model error, like CpuExecutionFailurePoint);
+ * armed = 2 fails it as a device fault, GOSSMX_ERR_DEVICE, which opens the
+ * circuit breaker; 0 disarms. */
 int gossmx_inject_fault(gossmx_ctx* ctx, int armed);
 
-/* Device self-test of the lane layouts the GEMM relies on (FP4 -> f16
- * conversion order, 16x16x32 MFMA operand/result layout). No counterpart in
- * the reference; GOSSMX_ERR_UNSUPPORTED with a message on mismatch. */
+/* Device self-test of what the GEMM relies on: the FP4 -> f16 conversion order,
+ * the 16x16x32 MFMA operand/result layout, the scaled conversion with clean
+ * and with dirty scale operands (E8M0 byte in the exponent field, the
+ * neighbouring bytes in the sign and mantissa bits), and the SwiGLU sigmoid
+ * table against the host expf. No counterpart in the reference;
+ * GOSSMX_ERR_UNSUPPORTED with a message on any mismatch. */
 int gossmx_selftest(gossmx_ctx* ctx);
 
 /* ---------------------------------------------------------------------------

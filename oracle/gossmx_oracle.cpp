@@ -638,6 +638,10 @@ int oracle_swiglu(const float* gate_up, size_t intermediate, float alpha, float 
 }
 void oracle_stable_top_k(const float* v, size_t n, size_t k, uint32_t* out) { stable_top_k(v, n, k, out); }
 void oracle_softmax(const float* v, size_t n, float* out) { softmax(v, n, out); }
+void combine_rows(const float* y, const float* w, size_t m, size_t K, size_t H, float* out);
+void oracle_combine(const float* y, const float* w, size_t m, size_t k, size_t h, float* out) {
+  combine_rows(y, w, m, k, h, out);
+}
 
 // The MoE block, CpuModel::moe_batch (cpu_runner.rs:2794-3013), with the
 // residual-Q8 expert projection (the default, cpu_runner.rs:49-90).
@@ -652,6 +656,23 @@ struct OracleLayer {
   size_t experts, hidden, intermediate, top_k;
   float alpha, limit;
 };
+
+// Weighted combine by source row and rank, then bf16 (cpu_runner.rs:2959-2999):
+// per row, output = 0.0; for rank 0..K-1 in order: weighted = y * weight (one
+// rounding), output += weighted (one rounding); then fp32_to_bf16_roundtrip.
+// y is [m][K][H] by (row, rank) slot, w [m][K].
+void combine_rows(const float* y, const float* w, size_t m, size_t K, size_t H, float* out) {
+  for (size_t r = 0; r < m; ++r) {
+    for (size_t h = 0; h < H; ++h) {
+      float acc = 0.0f;
+      for (size_t k = 0; k < K; ++k) {
+        const float weighted = y[(r * K + k) * H + h] * w[r * K + k];
+        acc = acc + weighted;
+      }
+      out[r * H + h] = bf16_round(acc);
+    }
+  }
+}
 
 // Outputs mirror CpuMoeStep (cpu_runner.rs:569-575); trace arrays mirror
 // CpuExpertTrace for every (row, rank) when non-null:
@@ -753,14 +774,7 @@ int oracle_moe_batch(const OracleLayer* L, const uint16_t* x, size_t m, const fl
     }
     s = e_end;
   }
-  // Weighted combine by source row and rank, then bf16 (cpu_runner.rs:2959-2999).
-  for (size_t r = 0; r < m; ++r) {
-    for (size_t h = 0; h < H; ++h) {
-      float acc = 0.0f;
-      for (size_t k = 0; k < K; ++k) acc += y[(r * K + k) * H + h] * wts[r * K + k];
-      output[r * H + h] = bf16_round(acc);
-    }
-  }
+  combine_rows(y.data(), wts.data(), m, K, H, output);
   if (logits) std::memcpy(logits, lg.data(), m * E * 4);
   if (selected) std::memcpy(selected, sel.data(), m * K * 4);
   if (weights) std::memcpy(weights, wts.data(), m * K * 4);

@@ -109,6 +109,7 @@ def _declare(L):
         "oracle_swiglu": (i32, [vp, sz, f32, f32, vp]),
         "oracle_stable_top_k": (None, [vp, sz, sz, vp]),
         "oracle_softmax": (None, [vp, sz, vp]),
+        "oracle_combine": (None, [vp, vp, sz, sz, sz, vp]),
         "oracle_moe_batch": (i32, [C.POINTER(OracleLayer), vp, sz, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32]),
         "oracle_stream_hash": (u64, [u64, u64, u64]),
         "oracle_gen_mxfp4": (None, [u64, u64, sz, sz, sz, vp]),
@@ -245,6 +246,26 @@ def softmax(v):
     v = np.ascontiguousarray(v, dtype=np.float32)
     out = np.zeros_like(v)
     lib().oracle_softmax(_p(v), v.size, _p(out))
+    return out
+
+
+def combine(y, w):
+    """The weighted combine of moe_batch (cpu_runner.rs:2959-2999): y [m][k][h]
+    f32, w [m][k] f32 -> [m][h] bf16 values."""
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    m, k, h = y.shape
+    out = np.zeros((m, h), np.float32)
+    lib().oracle_combine(_p(y), _p(w), m, k, h, _p(out))
+    return out
+
+
+def bf16_matvec(w_bits, x_bits):
+    """Kernels::bf16_matvec rows of w [rows][cols] against x [cols], bf16 bits."""
+    w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    out = np.zeros(w.shape[0], np.float32)
+    lib().oracle_bf16_matvec(_p(w), w.shape[0], w.shape[1], _p(x), _p(out))
     return out
 
 

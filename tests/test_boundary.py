@@ -48,6 +48,17 @@ def test_null_arguments_are_rejected():
     assert L.gossmx_inject_fault(None, 1) == G.ERR_INVALID_ARGUMENT
 
 
+def test_circuit_breaker_without_device():
+    assert not G.circuit_is_open()
+    G.circuit_reset()
+    assert not G.circuit_is_open()
+    L = G.load()
+    size, align = C.c_size_t(7), C.c_size_t(7)
+    assert L.gossmx_mxfp4_scratch_requirement(None, C.byref(size), C.byref(align)) == G.ERR_INVALID_ARGUMENT
+    assert L.gossmx_ctx_fast_path(None, C.byref(C.c_int())) == G.ERR_INVALID_ARGUMENT
+    assert L.gossmx_inject_fault(None, 2) == G.ERR_INVALID_ARGUMENT
+
+
 ROWS, BLOCKS = 40, 3
 
 

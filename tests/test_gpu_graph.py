@@ -55,3 +55,48 @@ def test_captured_forward_replays_match_eager_and_oracle():
         layer.close()
         gu.close()
         dn.close()
+
+
+def test_graph_survives_eager_calls_that_grow_the_scratch():
+    """A graph captured at a small batch keeps the scratch addresses it was
+    recorded with: an eager call at a much larger batch (which needs larger
+    scratch buffers) runs in between, and the replay still equals the
+    oracle bit for bit. The buffers the graph holds are freed only when the
+    graph is destroyed."""
+    with G.Context(0) as ctx:
+        E, H, I, K = 8, 128, 64, 4
+        host = O.synthetic_layer(23, 0, experts=E, hidden=H, intermediate=I, top_k=K)
+        gu = G.Weights.upload(ctx, host.gate_up, E, 2 * I, H // 32)
+        dn = G.Weights.upload(ctx, host.down, E, H, I // 32)
+        layer = G.MoeLayer(ctx, E, H, I, K, host.router_weight, host.router_bias, gu, host.gate_up_bias, dn,
+                           host.down_bias)
+        small, big = 12, 700
+        xs = O.gen_hidden(23, 1, small, H)
+        xb = O.gen_hidden(23, 2, big, H)
+        want_s = O.moe_batch(host, xs)["output"]
+        dxs, douts = ctx.malloc(xs.nbytes), ctx.malloc(small * H * 4)
+        ctx.h2d(dxs, xs)
+        layer.forward_device(dxs, small, douts)
+        ctx.synchronize()
+        ctx.capture_begin()
+        layer.forward_device(dxs, small, douts)
+        graph = ctx.capture_end()
+        for rep in range(2):
+            got_b = layer.forward(xb)  # grows every scratch buffer while the graph lives
+            rows = [0, 350, big - 1]
+            want_b = O.moe_batch(host, xb[rows])
+            assert (got_b["output"][rows].view(np.uint32) == want_b["output"].view(np.uint32)).all()
+            ctx.h2d(douts, np.full((small, H), np.nan, np.float32))
+            graph.launch()
+            ctx.synchronize()
+            got = np.empty((small, H), np.float32)
+            ctx.d2h(got, douts)
+            assert (got.view(np.uint32) == want_s.view(np.uint32)).all(), f"replay {rep}"
+        graph.close()
+        # after the graph is gone the context keeps working at both sizes
+        assert (layer.forward(xs)["output"].view(np.uint32) == want_s.view(np.uint32)).all()
+        ctx.free(dxs)
+        ctx.free(douts)
+        layer.close()
+        gu.close()
+        dn.close()

@@ -171,6 +171,44 @@ def test_120b_shape_zipf_batch256_rows_match(layer120b):
     assert (got["route_order"] == np.argsort(sel, kind="stable")).all()
 
 
+@pytest.mark.parametrize("hidden,offset", [(64, 0), (2880, 1424)])
+def test_router_dot_order_pins(ctx, hidden, offset):
+    """The router rows of test_oracle's 16-lane pin (sequential, pairwise,
+    tree-folded, reversed and other lane counts give other logits): the GPU's
+    router logits equal the oracle's bits, 15 and 0 on the pinned rows. At
+    hidden 2880 the construction straddles the router kernel's staging
+    chunks."""
+    from test_oracle import router_pin_case
+    w, bias, x = router_pin_case(hidden, offset)
+    host = O.MoeLayerHost(w, bias, O.gen_mxfp4(1, 1, 4, 64, hidden // 32), np.zeros(4 * 64, np.float32),
+                          O.gen_mxfp4(1, 2, 4, hidden, 1), np.zeros(4 * hidden, np.float32), 4, hidden, 32, 2)
+    want = O.moe_batch(host, x[None, :])
+    assert want["status"] == O.OK
+    layer = gpu_layer(ctx, host)
+    got = layer.forward(x[None, :])
+    assert got["router_logits"][0, :2].tolist() == [15.0, 0.0]
+    assert_moe_equal(got, want)
+    close(layer)
+
+
+def test_softmax_order_pins(ctx):
+    """Injected rows whose bf16 routing weights depend on the softmax
+    denominator's rank order (test_oracle.SOFTMAX_PIN_ROWS)."""
+    from test_oracle import SOFTMAX_PIN_ROWS
+    host = O.synthetic_layer(41, 0, experts=8, hidden=64, intermediate=32, top_k=4)
+    logits = np.full((len(SOFTMAX_PIN_ROWS), 8), -20.0, np.float32)
+    for r, row in enumerate(SOFTMAX_PIN_ROWS):
+        logits[r, [5, 1, 6, 2]] = row
+    x = O.gen_hidden(41, 1, len(SOFTMAX_PIN_ROWS), 64)
+    want = O.moe_batch(host, x, injected_logits=logits)
+    assert want["status"] == O.OK
+    layer = gpu_layer(ctx, host)
+    got = layer.forward(x, injected_logits=logits)
+    assert (got["selected"] == [[5, 1, 6, 2]] * len(SOFTMAX_PIN_ROWS)).all()
+    assert_moe_equal(got, want)
+    close(layer)
+
+
 def test_all_experts_selected(ctx):
     host = O.synthetic_layer(5, 0, experts=4, hidden=64, intermediate=64, top_k=4)
     x = O.gen_hidden(5, 1, 9, 64)
@@ -230,6 +268,61 @@ def test_injected_fault_leaves_outputs_untouched(ctx):
         layer.forward(x)
     assert e.value.status == G.ERR_INJECTED_FAULT
     assert_moe_equal(layer.forward(x), O.moe_batch(host, x))
+    close(layer)
+
+
+def test_device_fault_opens_the_circuit_breaker(ctx):
+    """A run-time fault (the injected device fault) fails the call with
+    GOSSMX_ERR_DEVICE and opens the process-wide breaker; while it is open
+    projection calls still validate their arguments, then return
+    GOSSMX_ERR_CIRCUIT_OPEN; after the reset the block runs again and matches
+    the oracle (XeProjectionEngine::execute_projection,
+    crates/gpt-oss-xe/src/lib.rs:680-724)."""
+    host = O.synthetic_layer(8, 1, experts=4, hidden=64, intermediate=32, top_k=2)
+    layer = gpu_layer(ctx, host)
+    x = O.gen_hidden(8, 2, 2, 64)
+    want = O.moe_batch(host, x)
+    try:
+        assert not G.circuit_is_open()
+        ctx.inject_fault(G.FAULT_DEVICE)
+        with pytest.raises(G.GossmxError) as e:
+            layer.forward(x)
+        assert e.value.status == G.ERR_DEVICE
+        assert G.circuit_is_open()
+        with pytest.raises(G.GossmxError) as e:
+            layer.forward(x)
+        assert e.value.status == G.ERR_CIRCUIT_OPEN
+        with pytest.raises(G.GossmxError) as e:  # argument checks come first
+            layer.forward(x[:0])
+        assert e.value.status == G.ERR_INVALID_DIMENSIONS
+        rec = np.zeros(2 * 2, G.RQ8_DTYPE)
+        with pytest.raises(G.GossmxError) as e:
+            G.mxfp4_matmul(ctx, layer.down, 0, rec, 2, None, np.zeros((2, 64), np.float32))
+        assert e.value.status == G.ERR_CIRCUIT_OPEN
+        assert G.circuit_is_open()
+    finally:
+        G.circuit_reset()
+    assert not G.circuit_is_open()
+    assert_moe_equal(layer.forward(x), want)
+    # a model-error fault (mode 1) leaves the breaker closed
+    ctx.inject_fault(G.FAULT_INJECTED)
+    with pytest.raises(G.GossmxError) as e:
+        layer.forward(x)
+    assert e.value.status == G.ERR_INJECTED_FAULT
+    assert not G.circuit_is_open()
+    close(layer)
+
+
+def test_scratch_requirement_is_none_and_selftest_passes(ctx):
+    host = O.synthetic_layer(8, 2, experts=2, hidden=64, intermediate=32, top_k=1)
+    layer = gpu_layer(ctx, host)
+    assert G.scratch_requirement(layer.gate_up, 5) == (0, 1)
+    assert G.scratch_requirement(layer.down, 1, G.ACT_Q8) == (0, 1)
+    with pytest.raises(G.GossmxError) as e:
+        G.scratch_requirement(layer.down, 0)
+    assert e.value.status == G.ERR_INVALID_DIMENSIONS
+    ctx.selftest()  # lane layouts, dirty scale operands, sigmoid table
+    assert ctx.fast_path()
     close(layer)
 
 

@@ -428,3 +428,162 @@ def test_moe_rejects_non_finite_logits():
     x = O.gen_hidden(3, 9, 1, 64)
     logits = np.array([[0.0, float("inf"), 1.0]], np.float32)
     assert O.moe_batch(layer, x, injected_logits=logits)["status"] == O.NON_FINITE_LOGITS
+
+
+# --- order-defined float chains: inputs where the plausible other orders give
+# other bits (each alternative is computed here in float32 and must differ) ---
+
+F = np.float32
+B24 = float(2 ** 24)  # ulp(2^24) = 2: adding 1 ties back to 2^24
+
+
+def _bits(v):
+    return np.float32(v).view(np.uint32)
+
+
+def _tree(v):
+    v = [F(t) for t in v]
+    while len(v) > 1:
+        if len(v) % 2:
+            v.append(F(0))
+        v = [F(v[2 * i] + v[2 * i + 1]) for i in range(len(v) // 2)]
+    return v[0]
+
+
+def _lane_sums(p, lanes):
+    acc = [F(0)] * lanes
+    for i, t in enumerate(p):
+        acc[i % lanes] = F(acc[i % lanes] + F(t))
+    return acc
+
+
+def _fold(v, start=-0.0):
+    s = F(start)
+    for t in v:
+        s = F(s + F(t))
+    return s
+
+
+def dot_alternatives(p):
+    """Other summation orders of the products p a bf16 dot might use."""
+    return {
+        "sequential": _fold(p, 0.0),
+        "pairwise tree": _tree(p),
+        "16 lanes folded as a tree": _tree(_lane_sums(p, 16)),
+        "16 lanes folded 15..0": _fold(_lane_sums(p, 16)[::-1]),
+        "8 lanes": _fold(_lane_sums(p, 8)),
+        "32 lanes": _fold(_lane_sums(p, 32)),
+        "16 blocked lanes": _fold([_fold(p[j * len(p) // 16:(j + 1) * len(p) // 16], 0.0) for j in range(16)]),
+        "float64": F(np.sum(np.asarray(p, np.float64))),
+    }
+
+
+def router_pin_case(hidden=64, offset=0):
+    """Router rows whose bf16 logits depend on scalar_bf16_dot's order
+    (lib.rs:1007-1029): 16 lanes, lane j sums products i = j mod 16 in order,
+    lanes folded 0..15. The products are exact (bf16 x bf16); with x[offset] =
+    x[offset + 16] = 2^12:
+      row 0: products 2^24 at offset (lane 0), -2^24 at offset + 16 (lane 0
+        again), 1 at offset + 1..15. Lane 0 cancels before the small lanes
+        join: logit 15. A sequential sum absorbs the 1s into 2^24 first
+        (logit 0), pairwise trees and other lane counts keep some (14, 0).
+      row 1: 2^24 at offset, 1 at offset + 1..15, bias -2^24. Folding the
+        lanes 0..15 absorbs every 1 (logit 0); a tree fold keeps 14, a
+        reversed fold 16 (the 15 ones sum to 15, then tie to even).
+      rows 2, 3: N(0, 0.02) weights, bias 0.
+    offset places the construction (a multiple of 16; with hidden 2880 and
+    offset 1424 it straddles the router kernel's 1440-element staging)."""
+    rng = np.random.default_rng(3)
+    x = O.bf16_round_array(rng.standard_normal(hidden).astype(np.float32))
+    x[offset:offset + 32] = 1.0
+    x[offset] = x[offset + 16] = 4096.0
+    w = np.zeros((4, hidden), np.float32)
+    w[0, offset], w[0, offset + 16] = 4096.0, -4096.0
+    w[0, offset + 1:offset + 16] = 1.0
+    w[1, offset] = 4096.0
+    w[1, offset + 1:offset + 16] = 1.0
+    w[2:] = O.bf16_round_array(rng.standard_normal((2, hidden)).astype(np.float32) * F(0.02))
+    bias = np.array([0.0, -B24, 0.0, 0.0], np.float32)
+    to_bits = lambda a: (np.ascontiguousarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    return to_bits(w), bias, to_bits(x)
+
+
+@pytest.mark.parametrize("hidden,offset", [(64, 0), (2880, 1424)])
+def test_bf16_dot_sums_in_sixteen_ordered_lanes(hidden, offset):
+    w, bias, x = router_pin_case(hidden, offset)
+    got = O.bf16_matvec(w, x)
+    wf, xf = O.bf16_to_f32(w), O.bf16_to_f32(x)
+    expected = {0: 15.0, 1: B24}
+    for row, want in expected.items():
+        assert got[row] == want
+        p = (wf[row] * xf).astype(np.float32)  # exact products
+        ref_logit = O.bf16_round_array(np.array([F(got[row] + bias[row])]))[0]
+        for name, alt in dot_alternatives(p).items():
+            if alt == got[row]:
+                continue
+            alt_logit = O.bf16_round_array(np.array([F(alt + bias[row])]))[0]
+            assert alt_logit != ref_logit, f"row {row}: {name} would give the same logit"
+    # every alternative order differs from the reference on one of the rows
+    # (at offset 1424 the 32-lane split lands like the 16-lane one)
+    for name in dot_alternatives([0.0]):
+        if offset % 32 == 0 or name != "32 lanes":
+            assert any(dot_alternatives((wf[r] * xf).astype(np.float32))[name] != got[r] for r in (0, 1)), name
+    # the router logits through moe_batch: bf16(dot + bias)
+    layer = O.MoeLayerHost(w, bias, O.gen_mxfp4(1, 1, 4, 64, hidden // 32), np.zeros(4 * 64, np.float32),
+                           O.gen_mxfp4(1, 2, 4, hidden, 1), np.zeros(4 * hidden, np.float32), 4, hidden, 32, 2)
+    r = O.moe_batch(layer, x[None, :])
+    assert r["status"] == O.OK
+    assert r["router_logits"][0, 0] == 15.0 and r["router_logits"][0, 1] == 0.0
+
+
+# Rank-ordered bf16 logits whose routing weights depend on the softmax
+# denominator's order (cpu_runner.rs:3784-3795: sum of expf(v - max) folded in
+# rank order): found by search over random bf16 quadruples, each weight
+# checked against the other orders below.
+SOFTMAX_PIN_ROWS = [
+    [3.859375, -0.8046875, -0.93359375, -4.78125],    # reversed and float64 sums round a weight differently
+    [3.375, 0.80078125, 0.71484375, -1.515625],      # the pairwise sum does
+]
+
+
+def _expf(v):
+    return np.float32(LIBM_EXPF(float(v)))
+
+
+LIBM_EXPF = C.CDLL("libm.so.6").expf
+LIBM_EXPF.restype = C.c_float
+LIBM_EXPF.argtypes = [C.c_float]
+
+
+def test_softmax_denominator_folds_in_rank_order():
+    differs = set()
+    for row in SOFTMAX_PIN_ROWS:
+        v = np.array(row, np.float32)
+        e = [_expf(F(t - v[0])) for t in v]
+        seq = _fold(e)
+        want = np.array([F(t / seq) for t in e], np.float32)
+        got = O.softmax(v)
+        assert (got.view(np.uint32) == want.view(np.uint32)).all()
+        alts = {"reversed": _fold(e[::-1], 0.0), "pairwise": F(F(e[0] + e[1]) + F(e[2] + e[3])),
+                "float64": F(np.sum(np.asarray(e, np.float64)))}
+        for name, d in alts.items():
+            w_alt = O.bf16_round_array(np.array([F(t / d) for t in e], np.float32))
+            if (w_alt.view(np.uint32) != O.bf16_round_array(want).view(np.uint32)).any():
+                differs.add(name)
+    assert differs == {"reversed", "pairwise", "float64"}
+
+
+def test_combine_adds_weighted_ranks_in_rank_order():
+    # weighted = y * w (exact here: bf16 x bf16), output += weighted in rank
+    # order from 0.0, then bf16 (cpu_runner.rs:2959-2999).
+    y = np.array([[[B24], [1.0], [-B24], [1.0]],     # in order: 2^24 absorbs the first 1 -> 1
+                  [[1.0], [B24], [1.0], [-B24]],     # in order: both 1s absorbed -> 0
+                  [[3.0], [-2.0], [0.5], [0.25]]], np.float32)
+    w = np.array([[1.0, 1.0, 1.0, 1.0], [1.0, 1.0, 1.0, 1.0], [0.5, 0.25, 1.0, 2.0]], np.float32)
+    got = O.combine(y, w)[:, 0]
+    assert got.tolist() == [1.0, 0.0, 2.0]
+    alts = {"reversed": lambda p: _fold(p[::-1], 0.0), "pairwise": lambda p: F(F(p[0] + p[1]) + F(p[2] + p[3])),
+            "float64": lambda p: F(np.sum(np.asarray(p, np.float64)))}
+    for name, fn in alts.items():
+        outs = [fn([F(y[r, k, 0] * w[r, k]) for k in range(4)]) for r in range(2)]
+        assert outs != got[:2].tolist(), name
