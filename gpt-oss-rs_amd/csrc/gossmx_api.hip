@@ -9,6 +9,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -17,6 +18,18 @@ using namespace gossmx;
 namespace {
 
 thread_local std::string g_last_error;
+
+// Fixed scratch of gossmx_moe_forward_noalloc, for callers that cannot
+// allocate: one copy per device (each device holds its own until the process
+// ends). Host code never passes the array's name to a kernel or a copy: it
+// is a host-side stand-in; the device address comes from hipGetSymbolAddress
+// (scratch_address), taken once per device at context creation.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+int g_scratch_state[kMaxDevices] = {};  // 0: not looked up, 1: found, -1: lookup failed
 
 // Process-wide circuit breaker of the GPU backend, the counterpart of the Xe
 // engine's PROCESS_XE_CIRCUIT_OPEN (crates/gpt-oss-xe/src/lib.rs:605-724): a
@@ -131,6 +144,32 @@ int ensure(gossmx_ctx* ctx, DevBuf& b, size_t bytes) {
   return GOSSMX_OK;
 }
 
+// A fixed block of device memory that a call's scratch is carved from
+// (256-byte aligned pieces), instead of the context's grow-only buffers.
+struct ScratchArena {
+  char* base = nullptr;
+  size_t cap = 0;
+  size_t used = 0;
+};
+
+// `bytes` of scratch for one buffer role: carved from `arena` when one is
+// given (failing, before anything is launched, when it is full), else the
+// context's grow-only buffer `b`.
+template <class T>
+int take(gossmx_ctx* ctx, ScratchArena* arena, DevBuf& b, size_t bytes, T** out) {
+  if (arena) {
+    const size_t off = (arena->used + 255) & ~(size_t)255;
+    if (off > arena->cap || bytes > arena->cap - off)
+      return fail(GOSSMX_ERR_UNSUPPORTED, "this call needs more than the %zu bytes of fixed scratch", arena->cap);
+    *out = reinterpret_cast<T*>(arena->base + off);
+    arena->used = off + bytes;
+    return GOSSMX_OK;
+  }
+  if (int s = ensure(ctx, b, bytes)) return s;
+  *out = static_cast<T*>(b.p);
+  return GOSSMX_OK;
+}
+
 hipEvent_t take_event(gossmx_ctx* ctx) {
   if (!ctx->event_pool.empty()) {
     hipEvent_t e = ctx->event_pool.back();
@@ -219,6 +258,25 @@ int check_device_errors(gossmx_ctx* ctx) {
 int set_device(int device) {
   HIP_TRY(hipSetDevice(device), "hipSetDevice");
   return GOSSMX_OK;
+}
+
+// Looks up the device address of `scratch` on `device` (which must be
+// current) the first time a context is created on it.
+void scratch_lookup(int device) {
+  if (device < 0 || device >= kMaxDevices) return;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_state[device] != 0) return;
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  g_scratch_ptr[device] = e == hipSuccess ? ptr : nullptr;
+  g_scratch_state[device] = (e == hipSuccess && ptr != nullptr) ? 1 : -1;
+}
+
+// The device address of `scratch` on `device`, or null.
+void* scratch_address(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  return g_scratch_state[device] == 1 ? g_scratch_ptr[device] : nullptr;
 }
 
 // The checks every projection call makes after validating its arguments and
@@ -386,6 +444,7 @@ int gossmx_ctx_create(int device, void* stream, gossmx_ctx** out) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return fail(GOSSMX_ERR_UNAVAILABLE_BACKEND, "device %d is %s, this build needs gfx950", device, prop.gcnArchName);
   if (int s = set_device(device)) return s;
+  scratch_lookup(device);
   auto* ctx = new gossmx_ctx();
   ctx->device = device;
   if (stream) {
@@ -721,7 +780,8 @@ void gossmx_layer_destroy(gossmx_layer* L) {
 // RMSNorm in front of it (io->x is then the residual stream) and the residual
 // add behind it into next_residual.
 static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_io* io,
-                            const float* norm_weight, float norm_eps, uint16_t* next_residual) {
+                            const float* norm_weight, float norm_eps, uint16_t* next_residual,
+                            ScratchArena* arena = nullptr) {
   const bool residual = norm_weight != nullptr;
   if (!ctx || !L || !io || !io->x || (!io->output && !residual) || (residual && !next_residual))
     return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
@@ -748,20 +808,41 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   const int chunk = gemm_chunk(m);
   const size_t max_work = (R + chunk - 1) / chunk + std::min(E, R);
 
+  // Scratch: the context's grow-only buffers, or the no-allocation entry
+  // point's fixed arena. Every piece is taken here, before the first launch.
   int s = GOSSMX_OK;
-  if ((s = ensure(ctx, ctx->logits, m * E * 4)) || (s = ensure(ctx, ctx->selected, R * 4)) ||
-      (s = ensure(ctx, ctx->weights, R * 4)) || (s = ensure(ctx, ctx->act1v, m * B1 * 2 * kBlock * 2 + kActSlack)) ||
-      (s = ensure(ctx, ctx->act1s, m * B1 * 8 + kActSlack)) || (s = ensure(ctx, ctx->bucket, (E + 1) * 4)) ||
-      (s = ensure(ctx, ctx->route_tok, R * 4)) || (s = ensure(ctx, ctx->route_slot, R * 4)) ||
-      (s = ensure(ctx, ctx->work, (4 * max_work + 1) * 4)) ||
-      (s = ensure(ctx, ctx->act2v, R * B2 * 2 * kBlock * 2 + kActSlack)) ||
-      (s = ensure(ctx, ctx->act2s, R * B2 * 8 + kActSlack)) || (s = ensure(ctx, ctx->y, R * H * 2)))
+  float* logits_buf = nullptr;
+  int *selected = nullptr, *bucket = nullptr, *work = nullptr, *route_tok = nullptr, *route_slot = nullptr;
+  float* weights = nullptr;
+  ActBuffers act1, act2;
+  uint16_t* ybuf = nullptr;
+  if ((s = take(ctx, arena, ctx->logits, m * E * 4, &logits_buf)) || (s = take(ctx, arena, ctx->selected, R * 4, &selected)) ||
+      (s = take(ctx, arena, ctx->weights, R * 4, &weights)) ||
+      (s = take(ctx, arena, ctx->act1v, m * B1 * 2 * kBlock * 2 + kActSlack, &act1.v)) ||
+      (s = take(ctx, arena, ctx->act1s, m * B1 * 8 + kActSlack, &act1.s)) ||
+      (s = take(ctx, arena, ctx->bucket, (E + 1) * 4, &bucket)) ||
+      (s = take(ctx, arena, ctx->route_tok, R * 4, &route_tok)) ||
+      (s = take(ctx, arena, ctx->route_slot, R * 4, &route_slot)) ||
+      (s = take(ctx, arena, ctx->work, (4 * max_work + 1) * 4, &work)) ||
+      (s = take(ctx, arena, ctx->act2v, R * B2 * 2 * kBlock * 2 + kActSlack, &act2.v)) ||
+      (s = take(ctx, arena, ctx->act2s, R * B2 * 8 + kActSlack, &act2.s)) ||
+      (s = take(ctx, arena, ctx->y, R * H * 2, &ybuf)))
     return s;
+  // Batches whose logits fit one work-group take the fused selection +
+  // dispatch kernel; larger ones a selection kernel with per-work-group
+  // expert counts and a placement kernel. The router projection (when the
+  // logits are not injected) is a kernel in front of either.
+  const bool fused = m * (E + 1) <= (size_t)kSelectLds && R <= (size_t)kSelectMaxRoutes && K <= (size_t)kSelectTopK;
+  int* cnt = nullptr;
+  if (!fused) {
+    const size_t n_sel = (m + select_rows_per_wg((int)E, (int)K) - 1) / select_rows_per_wg((int)E, (int)K);
+    if ((s = take(ctx, arena, ctx->cnt, n_sel * E * 4, &cnt))) return s;
+  }
   const uint16_t* x = io->x;
   const float* injected = io->injected_logits;
   float* output = io->output;
   float* trace = io->trace_down;
-  float* logits = (!host && io->router_logits) ? io->router_logits : static_cast<float*>(ctx->logits.p);
+  float* logits = (!host && io->router_logits) ? io->router_logits : logits_buf;
   if (host) {
     if ((s = ensure(ctx, ctx->x, m * H * 2)) || (s = ensure(ctx, ctx->out, m * H * 4))) return s;
     HIP_TRY(hipMemcpyAsync(ctx->x.p, io->x, m * H * 2, hipMemcpyHostToDevice, ctx->stream), "H2D x");
@@ -797,12 +878,7 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
     // logits the selection kernels' quantization work-groups do.
     route_norm_w = nw;
   }
-  int* selected = static_cast<int*>(ctx->selected.p);
-  float* weights = static_cast<float*>(ctx->weights.p);
-  int* bucket = static_cast<int*>(ctx->bucket.p);
-  int* work = static_cast<int*>(ctx->work.p);
   int* n_work = work + 4 * max_work;
-  ActBuffers act1{static_cast<_Float16*>(ctx->act1v.p), static_cast<float*>(ctx->act1s.p)};
 
   RouteArgs ra{};
   ra.x = x;
@@ -820,25 +896,14 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   ra.weights = weights;
   ra.act = act1;
   ra.err = ctx->err;
-  // Batches whose logits fit one work-group take the fused selection +
-  // dispatch kernel; larger ones a selection kernel with per-work-group
-  // expert counts and a placement kernel. The router projection (when the
-  // logits are not injected) is a kernel in front of either.
-  const bool fused = m * (E + 1) <= (size_t)kSelectLds && R <= (size_t)kSelectMaxRoutes && K <= (size_t)kSelectTopK;
-  int* cnt = nullptr;
-  if (!fused) {
-    const size_t n_sel = (m + select_rows_per_wg((int)E, (int)K) - 1) / select_rows_per_wg((int)E, (int)K);
-    if ((s = ensure(ctx, ctx->cnt, n_sel * E * 4))) return s;
-    cnt = static_cast<int*>(ctx->cnt.p);
-  }
   DispatchArgs da{};
   da.selected = selected;
   da.routes = (int)R;
   da.top_k = (int)K;
   da.experts = (int)E;
   da.bucket_off = bucket;
-  da.route_tok = static_cast<int*>(ctx->route_tok.p);
-  da.route_slot = static_cast<int*>(ctx->route_slot.p);
+  da.route_tok = route_tok;
+  da.route_slot = route_slot;
   da.work = work;
   da.n_work = n_work;
   da.chunk = chunk;
@@ -870,8 +935,8 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   g.n_work = n_work;
   g.route_tok = da.route_tok;
   g.route_slot = da.route_slot;
-  g.actv_next = static_cast<_Float16*>(ctx->act2v.p);
-  g.acts_next = static_cast<float*>(ctx->act2s.p);
+  g.actv_next = act2.v;
+  g.acts_next = act2.s;
   g.alpha = L->cfg.alpha;
   g.limit = L->cfg.limit;
   g.sig_tab = ctx->sig_tab;
@@ -882,7 +947,7 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   d.acts = g.acts_next;
   d.bias = L->down_bias;
   d.bias_expert_stride = H;
-  d.y = static_cast<uint16_t*>(ctx->y.p);
+  d.y = ybuf;
   {
     KernelScope sc(ctx, GOSSMX_OP_GATE_UP);
     HIP_TRY(launch_gemm(kGateUp, g, chunk, (int)max_work, ctx->stream, sc.start, sc.stop), "gate_up launch");
@@ -933,6 +998,24 @@ int gossmx_moe_forward_residual(gossmx_ctx* ctx, const gossmx_layer* L, const go
                                 const float* norm_weight, float epsilon, uint16_t* next_residual) {
   if (!norm_weight) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
   return projection_result(ctx, moe_forward_impl(ctx, L, io, norm_weight, epsilon, next_residual));
+}
+
+int gossmx_moe_forward_noalloc(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_io* io) {
+  if (!ctx || !L || !io) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+  if (io->memory != GOSSMX_MEM_DEVICE)
+    return fail(GOSSMX_ERR_INVALID_ARGUMENT, "gossmx_moe_forward_noalloc takes device memory only");
+  void* base = scratch_address(ctx->device);
+  if (!base) return fail(GOSSMX_ERR_DEVICE, "no fixed scratch on device %d (symbol lookup failed)", ctx->device);
+  ScratchArena arena;
+  arena.base = static_cast<char*>(base);
+  arena.cap = kNoAllocScratchBytes;
+  // Profiling events are created on demand; a call that must not allocate
+  // records none.
+  const bool profiling = ctx->profiling;
+  ctx->profiling = false;
+  const int s = moe_forward_impl(ctx, L, io, nullptr, 0.0f, nullptr, &arena);
+  ctx->profiling = profiling;
+  return projection_result(ctx, s);
 }
 
 // --- profiling, fault hook, self-test -------------------------------------------

@@ -179,6 +179,7 @@ def load():
         "gossmx_layer_create": (i32, [vp, C.POINTER(MoeConfig), vp, vp, vp, vp, vp, vp, pp]),
         "gossmx_layer_destroy": (None, [vp]),
         "gossmx_moe_forward": (i32, [vp, vp, C.POINTER(MoeIo)]),
+        "gossmx_moe_forward_noalloc": (i32, [vp, vp, C.POINTER(MoeIo)]),
         "gossmx_repack_inspect": (i32, [C.c_char_p, C.POINTER(RepackInfo), C.c_char_p, sz]),
         "gossmx_weights_load_repack": (i32, [vp, C.c_char_p, C.POINTER(vp)]),
         "gossmx_weights_save_repack": (i32, [vp, vp, C.c_char_p, C.c_char_p, C.c_char_p, C.POINTER(C.c_char_p), sz]),

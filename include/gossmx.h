@@ -291,6 +291,19 @@ typedef struct gossmx_moe_io {
 
 int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* layer, const gossmx_moe_io* io);
 
+/* gossmx_moe_forward without allocating (no counterpart in the reference; for
+ * callers that cannot allocate device memory: code under HIP-graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Same outputs, bit for
+ * bit. All io pointers must be device memory (GOSSMX_MEM_DEVICE). The call's
+ * scratch is carved from a fixed 64 MiB device array that each device holds
+ * from the first context created on it until the process ends (about 84.5 KB
+ * per row at the GPT-OSS-20B shape, so batches up to about 780 rows);
+ * a larger call returns GOSSMX_ERR_UNSUPPORTED before launching anything. Every
+ * call on one device shares that array and it keeps the last call's contents:
+ * calls that overlap on one device (other streams or contexts) race. Nothing in
+ * it needs to start at zero. No profiling events are recorded. */
+int gossmx_moe_forward_noalloc(gossmx_ctx* ctx, const gossmx_layer* layer, const gossmx_moe_io* io);
+
 /* The MoE half of a decoder layer on its residual stream (forward_layer_batch,
  * cpu_runner.rs:2519-2553): io->x is after_attention [m][hidden] bf16, the
  * block runs on norm_boundary(io->x, norm_weight) (the post-attention RMSNorm,
