@@ -96,7 +96,7 @@ struct gossmx_ctx {
   // scratch
   DevBuf x, injected, logits, selected, weights, act1v, act1s, bucket, route_tok, route_slot, work, act2v, act2s, y,
       cnt, normw, next,
-      out, trace, rec, bias, mout;
+      out, trace, trace_gu, trace_sw, rec, bias, mout;
 };
 
 struct gossmx_weights {
@@ -493,7 +493,7 @@ void gossmx_ctx_destroy(gossmx_ctx* ctx) {
   DevBuf* bufs[] = {&ctx->x, &ctx->injected, &ctx->logits, &ctx->selected, &ctx->weights, &ctx->act1v,
                     &ctx->act1s, &ctx->bucket, &ctx->route_tok, &ctx->route_slot, &ctx->work, &ctx->act2v,
                     &ctx->act2s, &ctx->y, &ctx->cnt, &ctx->normw, &ctx->next, &ctx->out,
-                    &ctx->trace, &ctx->rec, &ctx->bias, &ctx->mout};
+                    &ctx->trace, &ctx->trace_gu, &ctx->trace_sw, &ctx->rec, &ctx->bias, &ctx->mout};
   for (DevBuf* b : bufs)
     if (b->p) hipFree(b->p);
   for (void* p : ctx->retired) hipFree(p);
@@ -739,6 +739,9 @@ int gossmx_layer_create(gossmx_ctx* ctx, const gossmx_moe_config* cfg, const uin
   if (E == 0 || E > (size_t)kMaxExperts || K == 0 || K > (size_t)kMaxTopK || K > E || H == 0 || I == 0 ||
       H % kBlock || I % kBlock)
     return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "invalid MoE config E=%zu H=%zu I=%zu K=%zu", E, H, I, K);
+  if (cfg->projection != GOSSMX_PROJECTION_RESIDUAL_Q8 && cfg->projection != GOSSMX_PROJECTION_Q8 &&
+      cfg->projection != GOSSMX_PROJECTION_EXACT_BF16)
+    return fail(GOSSMX_ERR_INVALID_ARGUMENT, "unknown expert projection %d", cfg->projection);
   if (gate_up->t.experts != E || gate_up->t.rows != 2 * I || gate_up->t.blocks != H / kBlock ||
       down->t.experts != E || down->t.rows != H || down->t.blocks != I / kBlock)
     return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "expert tensors do not match [%zu, %zu, %zu] / [%zu, %zu, %zu]", E, 2 * I,
@@ -805,6 +808,7 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   if (int s = projection_gate(ctx)) return s;
   if (int s = set_device(ctx->device)) return s;
   const bool host = io->memory == GOSSMX_MEM_HOST;
+  const int proj = L->cfg.projection;
   const int chunk = gemm_chunk(m);
   const size_t max_work = (R + chunk - 1) / chunk + std::min(E, R);
 
@@ -842,6 +846,8 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   const float* injected = io->injected_logits;
   float* output = io->output;
   float* trace = io->trace_down;
+  float* trace_gu = io->trace_gate_up;
+  float* trace_sw = io->trace_swiglu;
   float* logits = (!host && io->router_logits) ? io->router_logits : logits_buf;
   if (host) {
     if ((s = ensure(ctx, ctx->x, m * H * 2)) || (s = ensure(ctx, ctx->out, m * H * 4))) return s;
@@ -857,6 +863,14 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
     if (trace) {
       if ((s = ensure(ctx, ctx->trace, R * H * 4))) return s;
       trace = static_cast<float*>(ctx->trace.p);
+    }
+    if (trace_gu) {
+      if ((s = ensure(ctx, ctx->trace_gu, R * 2 * I * 4))) return s;
+      trace_gu = static_cast<float*>(ctx->trace_gu.p);
+    }
+    if (trace_sw) {
+      if ((s = ensure(ctx, ctx->trace_sw, R * I * 4))) return s;
+      trace_sw = static_cast<float*>(ctx->trace_sw.p);
     }
   }
   // Post-attention RMSNorm: the block runs on the normalized rows, the
@@ -895,6 +909,11 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   ra.selected = selected;
   ra.weights = weights;
   ra.act = act1;
+  // Quantization work-groups: every quantized projection; the exact-BF16
+  // projection reads its input rows directly, or (with the fused RMSNorm)
+  // the normalized bf16 rows those work-groups store into act1.
+  ra.qmode = proj;
+  ra.quant = (proj != GOSSMX_PROJECTION_EXACT_BF16 || residual) ? 1 : 0;
   ra.err = ctx->err;
   DispatchArgs da{};
   da.selected = selected;
@@ -915,7 +934,7 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
     // This stage also holds top-k, softmax and (with injected logits) the
     // gate_up input quantization.
     OpScope sc(ctx, GOSSMX_OP_DISPATCH);
-    const int quantize = injected != nullptr ? 1 : 0;
+    const int quantize = (injected != nullptr && ra.quant) ? 1 : 0;
     if (fused) {
       HIP_TRY(launch_select_dispatch(ra, da, quantize, ctx->stream), "select/dispatch launch");
     } else {
@@ -930,7 +949,11 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   g.acts = act1.s;
   g.bias = L->gate_up_bias;
   g.bias_expert_stride = 2 * I;
-  g.residual = 1;
+  g.residual = proj == GOSSMX_PROJECTION_RESIDUAL_Q8 ? 1 : 0;
+  g.trace_gu = trace_gu;
+  g.trace_sw = trace_sw;
+  g.xin = residual ? reinterpret_cast<const uint16_t*>(act1.v) : x;
+  g.act_next16 = reinterpret_cast<uint16_t*>(act2.v);
   g.work = work;
   g.n_work = n_work;
   g.route_tok = da.route_tok;
@@ -948,13 +971,26 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   d.bias = L->down_bias;
   d.bias_expert_stride = H;
   d.y = ybuf;
-  {
-    KernelScope sc(ctx, GOSSMX_OP_GATE_UP);
-    HIP_TRY(launch_gemm(kGateUp, g, chunk, (int)max_work, ctx->stream, sc.start, sc.stop), "gate_up launch");
-  }
-  {
-    KernelScope sc(ctx, GOSSMX_OP_DOWN);
-    HIP_TRY(launch_gemm(kDown, d, chunk, (int)max_work, ctx->stream, sc.start, sc.stop), "down launch");
+  d.trace_gu = d.trace_sw = nullptr;
+  d.xin = g.act_next16;
+  if (proj == GOSSMX_PROJECTION_EXACT_BF16) {
+    {
+      OpScope sc(ctx, GOSSMX_OP_GATE_UP);
+      HIP_TRY(launch_exact(kGateUp, g, (int)max_work, ctx->stream), "exact gate_up launch");
+    }
+    {
+      OpScope sc(ctx, GOSSMX_OP_DOWN);
+      HIP_TRY(launch_exact(kDown, d, (int)max_work, ctx->stream), "exact down launch");
+    }
+  } else {
+    {
+      KernelScope sc(ctx, GOSSMX_OP_GATE_UP);
+      HIP_TRY(launch_gemm(kGateUp, g, chunk, (int)max_work, ctx->stream, sc.start, sc.stop), "gate_up launch");
+    }
+    {
+      KernelScope sc(ctx, GOSSMX_OP_DOWN);
+      HIP_TRY(launch_gemm(kDown, d, chunk, (int)max_work, ctx->stream, sc.start, sc.stop), "down launch");
+    }
   }
   {
     OpScope sc(ctx, GOSSMX_OP_WEIGHTING);
@@ -978,6 +1014,12 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
       HIP_TRY(hipMemcpyAsync(io->route_order, da.route_slot, R * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H order");
     if (io->trace_down)
       HIP_TRY(hipMemcpyAsync(io->trace_down, trace, R * H * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H trace");
+    if (io->trace_gate_up)
+      HIP_TRY(hipMemcpyAsync(io->trace_gate_up, trace_gu, R * 2 * I * 4, hipMemcpyDeviceToHost, ctx->stream),
+              "D2H gate_up trace");
+    if (io->trace_swiglu)
+      HIP_TRY(hipMemcpyAsync(io->trace_swiglu, trace_sw, R * I * 4, hipMemcpyDeviceToHost, ctx->stream),
+              "D2H SwiGLU trace");
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
   } else {
     if (io->selected)

@@ -65,6 +65,9 @@ struct ActBuffers {
 
 enum GemmMode { kPlain = 0, kGateUp = 1, kDown = 2 };
 
+// CpuExpertProjection (cpu_runner.rs:49-90): how expert inputs are prepared.
+enum Projection { kProjResidualQ8 = 0, kProjQ8 = 1, kProjExactBf16 = 2 };
+
 struct GemmArgs {
   TiledWeights w;
   int fast_ok;           // 0: never take the scaled-conversion fast path (self-test found it unsafe)
@@ -85,6 +88,12 @@ struct GemmArgs {
   float alpha, limit;                 // kGateUp
   const uint16_t* sig_tab;            // kGateUp: SwiGLU sigmoid per bf16 input (65,536 entries)
   uint16_t* y;                        // kDown: [m * top_k][rows] bf16
+  float* trace_gu;                    // kGateUp, nullable: [m * top_k][rows] bf16-rounded gate_up by (row, rank) slot
+  float* trace_sw;                    // kGateUp, nullable: [m * top_k][rows / 2] SwiGLU values by slot
+  // Exact-BF16 projection: input rows (gate_up: [m][K] by source row, down:
+  // [routes][K] by grouped route) and gate_up's bf16 SwiGLU output by grouped route.
+  const uint16_t* xin;
+  uint16_t* act_next16;
   int* err;
 };
 
@@ -100,6 +109,12 @@ struct RouteArgs {
   int* selected;            // [m][top_k]
   float* weights;           // [m][top_k]
   ActBuffers act;           // gate_up input per token
+  // How the quantization work-groups store each input block (Projection):
+  // residual-Q8, Q8 (residual codes and scale zero), or the bf16 values
+  // themselves (exact-BF16 after the fused RMSNorm: act.v holds [m][hidden]
+  // bf16). quant = 0 launches no quantization work-groups.
+  int qmode;
+  int quant;
   int* err;
 };
 
@@ -141,6 +156,9 @@ hipError_t launch_select_dispatch(const RouteArgs& r, const DispatchArgs& d, int
 hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int chunk, int grid_work, hipStream_t stream,
                        hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream);
+// Exact-BF16 expert projection over the work list (mode kGateUp or kDown);
+// chunk <= kChunkMax.
+hipError_t launch_exact(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream);
 
 hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int top_k, int hidden, float* out,
                           float* trace_down, const uint16_t* resid, uint16_t* next, hipStream_t stream);

@@ -137,11 +137,19 @@ __device__ __forceinline__ void q8_half_wave(float v, float& q, float& scale) {
 }
 
 // quantize_residual_q8 (lib.rs:382-409) of one block held by a half wave;
-// writes the f16 codes and the two scales of (row, blk) into `act`.
-__device__ __forceinline__ void residual_q8_store(float v, int l32, size_t row, int blocks, int blk, ActBuffers act) {
+// writes the f16 codes and the two scales of (row, blk) into `act`. With
+// qmode kProjQ8, quantize_q8 (lib.rs:347-378): the primary block only, the
+// residual codes and scale stored as zeros. With kProjExactBf16 the value's
+// bf16 bits go to act.v viewed as [row][blocks * 32] bf16.
+__device__ __forceinline__ void residual_q8_store(float v, int l32, size_t row, int blocks, int blk, ActBuffers act,
+                                                  int qmode = kProjResidualQ8) {
+  if (qmode == kProjExactBf16) {
+    reinterpret_cast<uint16_t*>(act.v)[(row * blocks + blk) * kBlock + l32] = bf16_bits(v);
+    return;
+  }
   float q, s;
   q8_half_wave(v, q, s);
-  const float r = v - q * s;
+  const float r = qmode == kProjQ8 ? 0.0f : v - q * s;
   float rq, rs;
   q8_half_wave(r, rq, rs);
   _Float16* dst = act.v + ((row * blocks + blk) * 2) * kBlock;
@@ -159,7 +167,7 @@ __device__ __forceinline__ void residual_q8_store(float v, int l32, size_t row, 
 // hw + i * stride: activation row first_row + item / per_row, block
 // first_blk + item % per_row); blocks with live[i] false are computed on
 // zeros and not stored. The same operations as residual_q8_store per block.
-template <int N>
+template <int N, bool RESIDUAL>
 __device__ __forceinline__ void residual_q8_store_n(const float (&v)[N], const bool (&live)[N], int l32, int hw,
                                                     int stride, int per_row, size_t first_row, int blocks,
                                                     int first_blk, ActBuffers act) {
@@ -175,7 +183,7 @@ __device__ __forceinline__ void residual_q8_store_n(const float (&v)[N], const b
     s[i] = mx[i] / 127.0f;
     const float inv = s[i] == 0.0f ? 0.0f : 1.0f / s[i];
     q[i] = fminf(fmaxf(roundf(v[i] * inv), -127.0f), 127.0f);
-    r[i] = v[i] - q[i] * s[i];
+    r[i] = RESIDUAL ? v[i] - q[i] * s[i] : 0.0f;  // quantize_q8: no residual block
     mx[i] = fabsf(r[i]);
   }
 #pragma unroll
@@ -291,8 +299,9 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
     if (b < blocks) {  // uniform per half wave
       const int i = b * kBlock + l32;
       const float v = route_input(a, bf16_to_f32(x[i]), i, inv);
-      if (!isfinite(v)) atomicOr(a.err, kErrNonFiniteInput);
-      residual_q8_store(v, l32, (size_t)r, blocks, b, a.act);
+      // The exact-BF16 projection takes its input unchecked (prepare_expert_input, cpu_runner.rs:3108).
+      if (a.qmode != kProjExactBf16 && !isfinite(v)) atomicOr(a.err, kErrNonFiniteInput);
+      residual_q8_store(v, l32, (size_t)r, blocks, b, a.act, a.qmode);
     }
     return;
   }
@@ -609,8 +618,8 @@ __device__ __forceinline__ void select_quantize(const RouteArgs& r, int qwg) {
     const int b = g % blocks, i = b * kBlock + (tid & 31);
     float v = bf16_to_f32(r.x[(size_t)row * r.hidden + i]);
     if (r.norm_w) v = bf16r(v * inv * r.norm_w[i]);
-    if (!isfinite(v)) atomicOr(r.err, kErrNonFiniteInput);
-    residual_q8_store(v, tid & 31, (size_t)row, blocks, b, r.act);
+    if (r.qmode != kProjExactBf16 && !isfinite(v)) atomicOr(r.err, kErrNonFiniteInput);
+    residual_q8_store(v, tid & 31, (size_t)row, blocks, b, r.act, r.qmode);
   }
 }
 
@@ -994,7 +1003,7 @@ __device__ __forceinline__ void group_update_pipelined(Acc<C>& tot, const char* 
 // or gate_up's SwiGLU and down-input quantization. `s_act` is LDS scratch of
 // at least count * (kGemmRows / 2 + 1) floats, free for reuse. Rows of tiles
 // past the end (row >= rows) are never stored.
-template <class C, int MODE>
+template <class C, int MODE, bool RESIDUAL>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& tot, const int n_tg, const int count,
                                               const int start, const int tile0, float* s_act) {
   const int tid = threadIdx.x;
@@ -1047,9 +1056,19 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& t
           const float gate = odd ? recv : own0;
           const float up = odd ? own1 : recv;
           const int c = tg * 8 + 2 * G + (odd ? 1 : 0);
-          if (c < count)
-            s_act[c * kActStride + (wave * C::kWaveTiles + t) * 8 + (nl >> 1)] =
-                swiglu_one(gate, up, a.alpha, a.limit, a.sig_tab);
+          const int row = (tile0 + t) * kTileRows + nl;
+          if (a.trace_gu != nullptr && row < rows) {  // CpuExpertTrace::gate_up_projection (bf16 values)
+            for (int u = 0; u < 2; ++u) {
+              const int cu = tg * 8 + 2 * G + u;
+              if (cu < count) a.trace_gu[(size_t)a.route_slot[start + cu] * rows + row] = u ? own1 : own0;
+            }
+          }
+          if (c < count) {
+            const float act = swiglu_one(gate, up, a.alpha, a.limit, a.sig_tab);
+            s_act[c * kActStride + (wave * C::kWaveTiles + t) * 8 + (nl >> 1)] = act;
+            if (a.trace_sw != nullptr && row < rows)  // CpuExpertTrace::swiglu
+              a.trace_sw[(size_t)a.route_slot[start + c] * (rows / 2) + (row >> 1)] = act;
+          }
         }
       }
     __syncthreads();
@@ -1074,8 +1093,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& t
       v[i] = live[i] ? s_act[c * kActStride + h * kBlock + l32] : 0.0f;
       if (live[i] && !isfinite(v[i])) atomicOr(a.err, kErrNonFiniteInput);
     }
-    residual_q8_store_n<kPer>(v, live, l32, hw, kHalfWaves, kBlocksPerWg, (size_t)start, blocks_next,
-                              (int)blockIdx.x * kBlocksPerWg, nx);
+    residual_q8_store_n<kPer, RESIDUAL>(v, live, l32, hw, kHalfWaves, kBlocksPerWg, (size_t)start, blocks_next,
+                                        (int)blockIdx.x * kBlocksPerWg, nx);
   }
 }
 
@@ -1318,7 +1337,99 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
   // work-group ends.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  gemm_epilogue<C, MODE>(a, tot, n_tg, count, start, tile0, reinterpret_cast<float*>(s_codes0));
+  gemm_epilogue<C, MODE, RESIDUAL>(a, tot, n_tg, count, start, tile0, reinterpret_cast<float*>(s_codes0));
+}
+
+// ---------------------------------------------------------------------------
+// Exact-BF16 expert projection (CpuExpertProjection::ExactBf16; project_mxfp4,
+// cpu_runner.rs:3497-3519): per output, total = bias; total += the 16 lane
+// sums folded 0..15 from -0.0. Lane l sums bf16(decode(code) * e8m0) * x over
+// the input values k = l mod 16 in increasing k, multiply then add
+// (accumulate_mxfp4_bf16_block, lib.rs:932-945: value v of a block feeds lane
+// v % 16, so lane l takes k = 32 b + l, then 32 b + l + 16, block after
+// block). A conformance path, VALU only: a work-group is one 16-row weight
+// tile x 16 lanes (one thread per row and lane) over one work item of the
+// dispatch's list (at most kChunkMax routes, one accumulator each).
+// gate_up: bf16 round trip, SwiGLU pairs (rows 2i, 2i + 1 of the tile) into
+// the down input [grouped route][rows / 2] bf16; down: y [slot][rows] bf16.
+
+__constant__ float kE2M1[16] = {0.0f,  0.5f,  1.0f,  1.5f,  2.0f,  3.0f,  4.0f,  6.0f,
+                                -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+
+template <int MODE>
+__global__ __launch_bounds__(256) void exact_kernel(GemmArgs a) {
+  const int tid = threadIdx.x, nn = tid >> 4, l = tid & 15;
+  const int wi = blockIdx.y;
+  const int nw = *a.n_work;
+  const int4 rec = reinterpret_cast<const int4*>(a.work)[wi];
+  if (wi >= nw) return;  // uniform over the work-group
+  const int expert = rec.x, start = rec.y, count = rec.z;
+  const int rows = (int)a.w.rows, B = (int)a.w.blocks, K = B * kBlock;
+  const int tile = blockIdx.x, n = tile * kTileRows + nn;
+  const int nq4 = (B + 3) >> 2;
+  const uint8_t* nib = a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)tile * 256 * B;
+  const uint8_t* scl = a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)tile * 64 * nq4;
+  __shared__ const uint16_t* s_in[kChunkMax];
+  if (tid < kChunkMax) {
+    const int t = min(tid, count - 1);
+    const size_t src = MODE == kGateUp ? (size_t)a.route_tok[start + t] : (size_t)(start + t);
+    s_in[tid] = a.xin + src * K;
+  }
+  __syncthreads();
+  float acc[kChunkMax];
+#pragma unroll
+  for (int t = 0; t < kChunkMax; ++t) acc[t] = 0.0f;
+  const int g_lo = l >> 3, shift = 4 * (l & 7);
+  for (int b = 0; b < B; ++b) {
+    const int q = b >> 2, j = b & 3, nb = min(4, B - 4 * q);
+    // Codes l and l + 16 of row nn: k-slices l / 8 and 2 + l / 8 of the group.
+    const uint32_t d0 = *reinterpret_cast<const uint32_t*>(nib + q * 1024 + (g_lo * 16 + nn) * nb * 4 + j * 4);
+    const uint32_t d1 = *reinterpret_cast<const uint32_t*>(nib + q * 1024 + ((2 + g_lo) * 16 + nn) * nb * 4 + j * 4);
+    const float scale = e8m0(scl[q * 64 + nn * 4 + j]);
+    const float w0 = bf16r(kE2M1[(d0 >> shift) & 15u] * scale);
+    const float w1 = bf16r(kE2M1[(d1 >> shift) & 15u] * scale);
+#pragma unroll
+    for (int t = 0; t < kChunkMax; ++t) {
+      if (t < count) {
+        const uint16_t* xr = s_in[t] + b * kBlock;
+        acc[t] = acc[t] + w0 * bf16_to_f32(xr[l]);
+        acc[t] = acc[t] + w1 * bf16_to_f32(xr[l + 16]);
+      }
+    }
+  }
+  __shared__ float s_lane[kTileRows][16][kChunkMax + 1];
+  __shared__ float s_gu[kTileRows][kChunkMax];
+#pragma unroll
+  for (int t = 0; t < kChunkMax; ++t)
+    if (t < count) s_lane[nn][l][t] = acc[t];
+  __syncthreads();
+  for (int t = l; t < count; t += 16) {
+    float sum = -0.0f;
+    for (int ll = 0; ll < 16; ++ll) sum = sum + s_lane[nn][ll][t];
+    const float bias = (a.bias != nullptr && n < rows) ? a.bias[(size_t)expert * a.bias_expert_stride + n] : 0.0f;
+    const float total = bias + sum;
+    const int slot = a.route_slot[start + t];
+    if (MODE == kDown) {
+      if (n < rows) a.y[(size_t)slot * rows + n] = bf16_bits(total);  // bf16 (cpu_runner.rs:2945-2947)
+    } else {
+      const float gu = bf16r(total);  // bf16 (cpu_runner.rs:2905)
+      s_gu[nn][t] = gu;
+      if (a.trace_gu != nullptr && n < rows) a.trace_gu[(size_t)slot * rows + n] = gu;
+    }
+  }
+  if (MODE == kGateUp) {
+    __syncthreads();
+    const int half = rows / 2;
+    for (int idx = tid; idx < (kTileRows / 2) * count; idx += blockDim.x) {
+      const int p = idx % (kTileRows / 2), t = idx / (kTileRows / 2);
+      const int i = tile * (kTileRows / 2) + p;
+      if (i < half) {
+        const float act = swiglu_one(s_gu[2 * p][t], s_gu[2 * p + 1][t], a.alpha, a.limit, a.sig_tab);
+        a.act_next16[(size_t)(start + t) * half + i] = bf16_bits(act);  // activated_bf16 (cpu_runner.rs:2917)
+        if (a.trace_sw != nullptr) a.trace_sw[(size_t)a.route_slot[start + t] * half + i] = act;
+      }
+    }
+  }
 }
 
 // Exactness flag per (expert, tile): 1 when every E8M0 byte of the tile's
@@ -1620,7 +1731,7 @@ __global__ void selftest_kernel(float* out) {
 static inline unsigned grid1d(size_t n, unsigned block) { return (unsigned)((n + block - 1) / block); }
 
 hipError_t launch_route(const RouteArgs& a, hipStream_t stream) {
-  const int quant_groups = (a.hidden / kBlock + kRouteQuantBlocks - 1) / kRouteQuantBlocks;
+  const int quant_groups = a.quant ? (a.hidden / kBlock + kRouteQuantBlocks - 1) / kRouteQuantBlocks : 0;
   if (a.hidden % 32 != 0 || a.experts > kMaxExperts) return hipErrorInvalidValue;
   hipLaunchKernelGGL(route_kernel, dim3(a.m, router_groups(a) + quant_groups), dim3(256), 0, stream, a);
   return hipGetLastError();
@@ -1670,7 +1781,6 @@ static hipError_t launch_gemm_cfg(GemmMode mode, const GemmArgs& a, int grid_wor
                                   hipEvent_t start, hipEvent_t stop) {
   const dim3 grid((unsigned)((a.w.tiles + C::kWgTiles - 1) / C::kWgTiles), (unsigned)grid_work);
   const dim3 block(C::kThreads);
-  if (!a.residual && mode != kPlain) return hipErrorInvalidValue;  // the MoE block always runs residual-Q8
   auto go = [&](auto kernel) {
     if (start) hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, start, stop, 0, a);
     else hipLaunchKernelGGL(kernel, grid, block, 0, stream, a);
@@ -1682,7 +1792,11 @@ static hipError_t launch_gemm_cfg(GemmMode mode, const GemmArgs& a, int grid_wor
       case kDown: go(gemm_kernel<C, kDown, true>); break;
     }
   } else {
-    go(gemm_kernel<C, kPlain, false>);
+    switch (mode) {
+      case kPlain: go(gemm_kernel<C, kPlain, false>); break;
+      case kGateUp: go(gemm_kernel<C, kGateUp, false>); break;
+      case kDown: go(gemm_kernel<C, kDown, false>); break;
+    }
   }
   return hipGetLastError();
 }
@@ -1693,6 +1807,14 @@ hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int chunk, int grid_wor
   if (chunk == GemmBig::kChunk) return launch_gemm_cfg<GemmBig>(mode, a, grid_work, stream, start, stop);
   if (chunk == GemmHuge::kChunk) return launch_gemm_cfg<GemmHuge>(mode, a, grid_work, stream, start, stop);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_exact(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream) {
+  const dim3 grid((unsigned)a.w.tiles, (unsigned)grid_work);
+  if (mode == kGateUp) hipLaunchKernelGGL(exact_kernel<kGateUp>, grid, dim3(256), 0, stream, a);
+  else if (mode == kDown) hipLaunchKernelGGL(exact_kernel<kDown>, grid, dim3(256), 0, stream, a);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream) {

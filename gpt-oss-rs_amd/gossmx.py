@@ -71,9 +71,14 @@ class MatmulProblem(C.Structure):
     ]
 
 
+PROJECTION_RESIDUAL_Q8 = 0   # CpuExpertProjection::ResidualQ8 (the default)
+PROJECTION_Q8 = 1            # CpuExpertProjection::Q8
+PROJECTION_EXACT_BF16 = 2    # CpuExpertProjection::ExactBf16
+
+
 class MoeConfig(C.Structure):
     _fields_ = [("experts", C.c_size_t), ("hidden", C.c_size_t), ("intermediate", C.c_size_t),
-                ("top_k", C.c_size_t), ("alpha", C.c_float), ("limit", C.c_float)]
+                ("top_k", C.c_size_t), ("alpha", C.c_float), ("limit", C.c_float), ("projection", C.c_int)]
 
 
 class RepackInfo(C.Structure):
@@ -91,7 +96,7 @@ class MoeIo(C.Structure):
     _fields_ = [("x", C.c_void_p), ("m", C.c_size_t), ("injected_logits", C.c_void_p),
                 ("router_logits", C.c_void_p), ("selected", C.c_void_p), ("routing_weights", C.c_void_p),
                 ("output", C.c_void_p), ("route_order", C.c_void_p), ("trace_down", C.c_void_p),
-                ("memory", C.c_int)]
+                ("memory", C.c_int), ("trace_gate_up", C.c_void_p), ("trace_swiglu", C.c_void_p)]
 
 
 class ProfileRecord(C.Structure):
@@ -569,10 +574,12 @@ class MoeLayer:
 
     def __init__(self, ctx: Context, experts: int, hidden: int, intermediate: int, top_k: int,
                  router_weight: np.ndarray, router_bias: np.ndarray, gate_up: Weights, gate_up_bias: np.ndarray,
-                 down: Weights, down_bias: np.ndarray, alpha: float = 1.702, limit: float = 7.0):
+                 down: Weights, down_bias: np.ndarray, alpha: float = 1.702, limit: float = 7.0,
+                 projection: int = PROJECTION_RESIDUAL_Q8):
         self.ctx = ctx
         self.experts, self.hidden, self.intermediate, self.top_k = experts, hidden, intermediate, top_k
-        cfg = MoeConfig(experts, hidden, intermediate, top_k, alpha, limit)
+        self.projection = projection
+        cfg = MoeConfig(experts, hidden, intermediate, top_k, alpha, limit, projection)
         rw = np.ascontiguousarray(router_weight, dtype=np.uint16)
         rb = np.ascontiguousarray(router_bias, dtype=np.float32)
         gb = np.ascontiguousarray(gate_up_bias, dtype=np.float32)
@@ -584,7 +591,8 @@ class MoeLayer:
 
     def forward(self, x_bf16: np.ndarray, injected_logits: np.ndarray | None = None, trace: bool = False) -> dict:
         """All outputs as arrays: router_logits, selected, routing_weights,
-        output, route_order (+ trace_down)."""
+        output, route_order (+ trace_down, trace_gate_up, trace_swiglu: the
+        CpuExpertTrace vectors of every (row, rank))."""
         x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
         m = x.shape[0]
         E, K, H = self.experts, self.top_k, self.hidden
@@ -597,10 +605,13 @@ class MoeLayer:
         }
         if trace:
             res["trace_down"] = np.zeros((m, K, H), np.float32)
+            res["trace_gate_up"] = np.zeros((m, K, 2 * self.intermediate), np.float32)
+            res["trace_swiglu"] = np.zeros((m, K, self.intermediate), np.float32)
         inj = None if injected_logits is None else np.ascontiguousarray(injected_logits, dtype=np.float32)
         io = MoeIo(_ptr(x), m, _ptr(inj), _ptr(res["router_logits"]), _ptr(res["selected"]),
                    _ptr(res["routing_weights"]), _ptr(res["output"]), _ptr(res["route_order"]),
-                   _ptr(res.get("trace_down")), MEM_HOST)
+                   _ptr(res.get("trace_down")), MEM_HOST, _ptr(res.get("trace_gate_up")),
+                   _ptr(res.get("trace_swiglu")))
         _check(load().gossmx_moe_forward(self.ctx.handle, self._h, C.byref(io)))
         return res
 

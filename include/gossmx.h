@@ -254,6 +254,13 @@ void gossmx_circuit_reset(void);
  * and f32 bias [experts][2*intermediate], down [experts][hidden][intermediate/32]
  * and f32 bias [experts][hidden]. Host arrays are copied; weights are borrowed
  * (they must outlive the layer). */
+/* CpuExpertProjection (cpu_runner.rs:49-90): how the expert projections
+ * prepare their inputs. RESIDUAL_Q8 (the reference's default): quantize_residual_q8
+ * and two integer dots per block; Q8: quantize_q8, one dot; EXACT_BF16: the bf16
+ * inputs against bf16(decode * scale) weights in 16 ordered float lanes
+ * (accumulate_mxfp4_bf16_block, lib.rs:932-945; a conformance path, VALU only). */
+enum { GOSSMX_PROJECTION_RESIDUAL_Q8 = 0, GOSSMX_PROJECTION_Q8 = 1, GOSSMX_PROJECTION_EXACT_BF16 = 2 };
+
 typedef struct gossmx_moe_config {
   size_t experts;      /* num_local_experts, <= 128 */
   size_t hidden;       /* hidden_size, multiple of 32 */
@@ -261,6 +268,7 @@ typedef struct gossmx_moe_config {
   size_t top_k;        /* num_experts_per_tok, 1..8 and <= experts */
   float alpha;         /* 1.702 */
   float limit;         /* swiglu_limit, 7.0 */
+  int projection;      /* GOSSMX_PROJECTION_*; 0 = residual-Q8 */
 } gossmx_moe_config;
 
 int gossmx_layer_create(gossmx_ctx* ctx, const gossmx_moe_config* config, const uint16_t* router_weight_bf16,
@@ -274,8 +282,11 @@ void gossmx_layer_destroy(gossmx_layer* layer);
  * projection output before its bf16 round trip; router_logits [m][experts];
  * selected [m][top_k]; routing_weights [m][top_k]; route_order [m*top_k] receives
  * row * top_k + rank in the grouped (expert, row, rank) order; trace_down
- * [m][top_k][hidden] receives each rank's bf16-rounded down projection.
- * All pointers are host or device memory as `memory` says. */
+ * [m][top_k][hidden] receives each rank's bf16-rounded down projection,
+ * trace_gate_up [m][top_k][2 * intermediate] its bf16-rounded gate_up
+ * projection and trace_swiglu [m][top_k][intermediate] its SwiGLU values
+ * (CpuExpertTrace, cpu_runner.rs:2970-2984). All pointers are host or device
+ * memory as `memory` says. */
 typedef struct gossmx_moe_io {
   const uint16_t* x;
   size_t m;
@@ -287,6 +298,8 @@ typedef struct gossmx_moe_io {
   uint32_t* route_order;
   float* trace_down;
   int memory;
+  float* trace_gate_up;
+  float* trace_swiglu;
 } gossmx_moe_io;
 
 int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* layer, const gossmx_moe_io* io);

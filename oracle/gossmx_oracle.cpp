@@ -681,9 +681,41 @@ void combine_rows(const float* y, const float* w, size_t m, size_t K, size_t H, 
 // injected_logits (nullable) replaces the router projection output before the
 // bf16 round trip. `threads` > 1 and `auto_lane` select the baseline lanes for
 // the expert projections (1/false is the scalar oracle).
+// The exact-BF16 projection of one row (project_mxfp4, cpu_runner.rs:3497-3519):
+// total = bias; 16 lanes fed by accumulate_mxfp4_bf16_block block after block
+// (lib.rs:932-945); total += the lanes summed 0..15 from -0.0.
+void exact_bf16_project(const uint8_t* canonical, size_t rows, size_t blocks, const uint16_t* x, const float* bias,
+                        float* out) {
+  for (size_t r = 0; r < rows; ++r) {
+    float lanes[16] = {0};
+    for (size_t b = 0; b < blocks; ++b)
+      oracle_accumulate_mxfp4_bf16_block(canonical + (r * blocks + b) * kRecord, x + b * kBlock, lanes);
+    float sum = -0.0f;
+    for (int l = 0; l < 16; ++l) sum = sum + lanes[l];
+    out[r] = bias[r] + sum;
+  }
+}
+
+int oracle_moe_batch_ex(const OracleLayer* L, const uint16_t* x, size_t m, const float* injected_logits,
+                        float* logits, uint32_t* selected, float* weights, float* output, uint32_t* route_order,
+                        float* trace_gate_up, float* trace_swiglu, float* trace_down, int auto_lane, int threads,
+                        int projection);
+
 int oracle_moe_batch(const OracleLayer* L, const uint16_t* x, size_t m, const float* injected_logits, float* logits,
                      uint32_t* selected, float* weights, float* output, uint32_t* route_order, float* trace_gate_up,
                      float* trace_swiglu, float* trace_down, int auto_lane, int threads) {
+  return oracle_moe_batch_ex(L, x, m, injected_logits, logits, selected, weights, output, route_order, trace_gate_up,
+                             trace_swiglu, trace_down, auto_lane, threads, 0);
+}
+
+// projection: 0 residual-Q8 (the serving default), 1 Q8, 2 exact-BF16
+// (CpuExpertProjection, cpu_runner.rs:49-90; prepare_expert_input and
+// project_mxfp4_batch, :3092-3440).
+int oracle_moe_batch_ex(const OracleLayer* L, const uint16_t* x, size_t m, const float* injected_logits,
+                        float* logits, uint32_t* selected, float* weights, float* output, uint32_t* route_order,
+                        float* trace_gate_up, float* trace_swiglu, float* trace_down, int auto_lane, int threads,
+                        int projection) {
+  if (projection < 0 || projection > 2) return INVALID_DIMENSIONS;
   const size_t E = L->experts, H = L->hidden, I = L->intermediate, K = L->top_k;
   if (m == 0 || K == 0 || K > E || H % kBlock || I % kBlock) return INVALID_DIMENSIONS;
   const size_t N1 = 2 * I, B1 = H / kBlock, N2 = H, B2 = I / kBlock;
@@ -720,17 +752,26 @@ int oracle_moe_batch(const OracleLayer* L, const uint16_t* x, size_t m, const fl
     while (e_end < routes.size() && routes[e_end].expert == routes[s].expert) ++e_end;
     const size_t e = routes[s].expert, mb = e_end - s;
     // gate_up over the bucket's gathered rows (cpu_runner.rs:2878-2901).
-    std::vector<ResidualQ8Block> qa(mb * B1);
-    for (size_t i = 0; i < mb; ++i) {
-      for (size_t h = 0; h < H; ++h) xf[h] = bf16_to_f32(x[routes[s + i].row * H + h]);
-      int st = quantize_residual_q8(xf.data(), H, &qa[i * B1]);
-      if (st) return st;
-    }
     gu.assign(mb * N1, 0.0f);
     const uint8_t* wgu = L->gate_up + e * N1 * B1 * kRecord;
+    std::vector<ResidualQ8Block> qa(mb * B1);
+    std::vector<Q8Block> qa1(mb * B1);
+    for (size_t i = 0; i < mb && projection != 2; ++i) {
+      for (size_t h = 0; h < H; ++h) xf[h] = bf16_to_f32(x[routes[s + i].row * H + h]);
+      int st = projection == 1 ? quantize_q8(xf.data(), H, &qa1[i * B1])
+                               : quantize_residual_q8(xf.data(), H, &qa[i * B1]);
+      if (st) return st;
+    }
     MatmulArgs a1{wgu, N1, B1, 1, 2, qa.data(), mb, B1, L->gate_up_bias + e * N1, gu.data(), N1};
+    if (projection == 1) {
+      a1.kind = 1;
+      a1.act = qa1.data();
+    }
     std::vector<uint8_t> x8;
-    if (auto_lane) {
+    if (projection == 2) {
+      for (size_t i = 0; i < mb; ++i)
+        exact_bf16_project(wgu, N1, B1, x + routes[s + i].row * H, L->gate_up_bias + e * N1, &gu[i * N1]);
+    } else if (auto_lane && projection == 0) {
       x8.resize(N1 * B1 * kRecord);
       oracle_pack_x8(wgu, N1, B1, x8.data());
       a1.weights = x8.data();
@@ -748,14 +789,25 @@ int oracle_moe_batch(const OracleLayer* L, const uint16_t* x, size_t m, const fl
     }
     // Down projection over the activated rows (cpu_runner.rs:2933-2947).
     std::vector<ResidualQ8Block> qd(mb * B2);
-    for (size_t i = 0; i < mb; ++i) {
-      int st = quantize_residual_q8(&act[i * I], I, &qd[i * B2]);
+    std::vector<Q8Block> qd1(mb * B2);
+    for (size_t i = 0; i < mb && projection != 2; ++i) {
+      int st = projection == 1 ? quantize_q8(&act[i * I], I, &qd1[i * B2]) : quantize_residual_q8(&act[i * I], I, &qd[i * B2]);
       if (st) return st;
     }
     dn.assign(mb * N2, 0.0f);
     const uint8_t* wdn = L->down + e * N2 * B2 * kRecord;
     MatmulArgs a2{wdn, N2, B2, 1, 2, qd.data(), mb, B2, L->down_bias + e * N2, dn.data(), N2};
-    if (auto_lane) {
+    if (projection == 1) {
+      a2.kind = 1;
+      a2.act = qd1.data();
+    }
+    if (projection == 2) {
+      std::vector<uint16_t> act16(I);
+      for (size_t i = 0; i < mb; ++i) {
+        for (size_t n = 0; n < I; ++n) act16[n] = bf16_bits(act[i * I + n]);  // activated_bf16 (:2917)
+        exact_bf16_project(wdn, N2, B2, act16.data(), L->down_bias + e * N2, &dn[i * N2]);
+      }
+    } else if (auto_lane && projection == 0) {
       x8.resize(N2 * B2 * kRecord);
       oracle_pack_x8(wdn, N2, B2, x8.data());
       a2.weights = x8.data();

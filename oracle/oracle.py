@@ -111,6 +111,7 @@ def _declare(L):
         "oracle_softmax": (None, [vp, sz, vp]),
         "oracle_combine": (None, [vp, vp, sz, sz, sz, vp]),
         "oracle_moe_batch": (i32, [C.POINTER(OracleLayer), vp, sz, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32]),
+        "oracle_moe_batch_ex": (i32, [C.POINTER(OracleLayer), vp, sz, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32]),
         "oracle_stream_hash": (u64, [u64, u64, u64]),
         "oracle_gen_mxfp4": (None, [u64, u64, sz, sz, sz, vp]),
         "oracle_gen_bf16_normal": (None, [u64, u64, sz, f32, f32, vp]),
@@ -296,9 +297,13 @@ class MoeLayerHost:
         return s
 
 
+PROJECTION_RESIDUAL_Q8, PROJECTION_Q8, PROJECTION_EXACT_BF16 = 0, 1, 2
+
+
 def moe_batch(layer: MoeLayerHost, x_bf16: np.ndarray, injected_logits=None, trace=False, auto_lane=False,
-              threads=1):
-    """CpuModel::moe_batch restated; returns a dict of outputs (or raises)."""
+              threads=1, projection=PROJECTION_RESIDUAL_Q8):
+    """CpuModel::moe_batch restated; returns a dict of outputs (or raises).
+    projection selects CpuExpertProjection (residual-Q8, Q8, exact-BF16)."""
     x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
     m = x.shape[0]
     E, H, I, K = layer.experts, layer.hidden, layer.intermediate, layer.top_k
@@ -315,10 +320,10 @@ def moe_batch(layer: MoeLayerHost, x_bf16: np.ndarray, injected_logits=None, tra
         res["down"] = np.zeros((m, K, H), np.float32)
     inj = None if injected_logits is None else np.ascontiguousarray(injected_logits, dtype=np.float32)
     s = layer.struct()
-    st = lib().oracle_moe_batch(C.byref(s), _p(x), m, _p(inj), _p(res["router_logits"]), _p(res["selected"]),
-                                _p(res["routing_weights"]), _p(res["output"]), _p(res["route_order"]),
-                                _p(res.get("gate_up")), _p(res.get("swiglu")), _p(res.get("down")),
-                                1 if auto_lane else 0, threads)
+    st = lib().oracle_moe_batch_ex(C.byref(s), _p(x), m, _p(inj), _p(res["router_logits"]), _p(res["selected"]),
+                                   _p(res["routing_weights"]), _p(res["output"]), _p(res["route_order"]),
+                                   _p(res.get("gate_up")), _p(res.get("swiglu")), _p(res.get("down")),
+                                   1 if auto_lane else 0, threads, projection)
     res["status"] = st
     return res
 
@@ -381,11 +386,11 @@ def add_residual(residual_bf16: np.ndarray, update: np.ndarray) -> np.ndarray:
 
 
 def moe_residual(layer: "MoeLayerHost", residual_bf16: np.ndarray, norm_weight: np.ndarray, eps: float,
-                 injected_logits=None) -> dict:
+                 injected_logits=None, projection=PROJECTION_RESIDUAL_Q8) -> dict:
     """norm_boundary -> moe_batch -> add_residual, as forward_layer_batch
     runs them; moe_batch's outputs plus normalized and next_residual."""
     normalized = norm_boundary(residual_bf16, norm_weight, eps)
-    res = moe_batch(layer, normalized, injected_logits=injected_logits)
+    res = moe_batch(layer, normalized, injected_logits=injected_logits, projection=projection)
     res["normalized"] = normalized
     if res["status"] == OK:
         res["next_residual"] = add_residual(residual_bf16, res["output"])

@@ -19,12 +19,19 @@ def ctx():
     c.close()
 
 
-def gpu_layer(ctx, host: O.MoeLayerHost):
+def gpu_layer(ctx, host: O.MoeLayerHost, projection: int = G.PROJECTION_RESIDUAL_Q8):
     E, H, I = host.experts, host.hidden, host.intermediate
     gu = G.Weights.upload(ctx, host.gate_up, E, 2 * I, H // 32)
     dn = G.Weights.upload(ctx, host.down, E, H, I // 32)
     return G.MoeLayer(ctx, E, H, I, host.top_k, host.router_weight, host.router_bias, gu, host.gate_up_bias, dn,
-                      host.down_bias, host.alpha, host.limit)
+                      host.down_bias, host.alpha, host.limit, projection)
+
+
+def assert_traces_equal(got, want):
+    """CpuExpertTrace vectors of every (row, rank): gate_up, SwiGLU, down."""
+    for gk, wk in (("trace_gate_up", "gate_up"), ("trace_swiglu", "swiglu"), ("trace_down", "down")):
+        g, w = got[gk].view(np.uint32), want[wk].view(np.uint32)
+        assert (g == w).all(), f"{gk}: {int((g != w).sum())} mismatches, first {np.argwhere(g != w)[:3].tolist()}"
 
 
 def close(layer):
@@ -55,6 +62,67 @@ def test_small_layers_bit_exact(ctx, experts, hidden, inter, top_k, m):
     assert_moe_equal(got, want)
     assert (got["trace_down"].view(np.uint32) == want["down"].view(np.uint32)).all()
     close(layer)
+
+
+PROJECTIONS = [G.PROJECTION_RESIDUAL_Q8, G.PROJECTION_Q8, G.PROJECTION_EXACT_BF16]
+
+
+@pytest.mark.parametrize("projection", PROJECTIONS, ids=["residual-q8", "q8", "exact-bf16"])
+@pytest.mark.parametrize("experts,hidden,inter,top_k,m,inject", [(4, 96, 64, 2, 5, False), (8, 128, 96, 4, 17, True),
+                                                                  (32, 256, 128, 4, 70, False),
+                                                                  (32, 64, 64, 4, 600, True)])
+def test_projection_modes_bit_exact_with_traces(ctx, projection, experts, hidden, inter, top_k, m, inject):
+    """Every CpuExpertProjection (cpu_runner.rs:49-90) against the oracle's
+    moe_batch in the same mode: outputs, routing and the gate_up / SwiGLU /
+    down traces bit for bit. m = 600 takes the 32-row work items."""
+    host = O.synthetic_layer(17, 0, experts=experts, hidden=hidden, intermediate=inter, top_k=top_k)
+    x = O.gen_hidden(17, 100 + m, m, hidden)
+    logits = None
+    if inject:
+        logits = O.bf16_round_array(np.random.default_rng(m).standard_normal((m, experts)).astype(np.float32))
+    want = O.moe_batch(host, x, injected_logits=logits, trace=True, projection=projection)
+    assert want["status"] == O.OK
+    layer = gpu_layer(ctx, host, projection)
+    got = layer.forward(x, injected_logits=logits, trace=True)
+    assert_moe_equal(got, want)
+    assert_traces_equal(got, want)
+    close(layer)
+
+
+@pytest.mark.parametrize("projection", [G.PROJECTION_Q8, G.PROJECTION_EXACT_BF16], ids=["q8", "exact-bf16"])
+def test_projection_modes_20b_shape(ctx, projection):
+    host = O.synthetic_layer(2026, 0)
+    x = O.gen_hidden(2026, 5, 3, 2880)
+    want = O.moe_batch(host, x, trace=True, projection=projection)
+    assert want["status"] == O.OK
+    layer = gpu_layer(ctx, host, projection)
+    got = layer.forward(x, trace=True)
+    assert_moe_equal(got, want)
+    assert_traces_equal(got, want)
+    close(layer)
+
+
+def test_exact_bf16_sums_in_sixteen_ordered_lanes(ctx):
+    """The oracle's exact-BF16 lane pin (test_oracle.exact_pin_layer): gate_up
+    row 0 of expert 0 is 15 in the 16-lane order, where a sequential sum
+    gives 0; the GPU's trace and outputs equal the oracle's bits."""
+    from test_oracle import exact_pin_layer
+    host, x, logits = exact_pin_layer()
+    want = O.moe_batch(host, x, injected_logits=logits, trace=True, projection=O.PROJECTION_EXACT_BF16)
+    assert want["status"] == O.OK and want["gate_up"][0, 0, 0] == 15.0
+    layer = gpu_layer(ctx, host, G.PROJECTION_EXACT_BF16)
+    got = layer.forward(x, injected_logits=logits, trace=True)
+    assert got["trace_gate_up"][0, 0, 0] == 15.0
+    assert_moe_equal(got, want)
+    assert_traces_equal(got, want)
+    close(layer)
+
+
+def test_unknown_projection_is_rejected(ctx):
+    host = O.synthetic_layer(3, 0, experts=2, hidden=64, intermediate=32, top_k=1)
+    with pytest.raises(G.GossmxError) as e:
+        gpu_layer(ctx, host, 3)
+    assert e.value.status == G.ERR_INVALID_ARGUMENT
 
 
 @pytest.fixture(scope="module")
@@ -369,6 +437,19 @@ def assert_residual_equal(got, want, rows=None):
 @pytest.mark.parametrize("experts,hidden,inter,top_k,m", [(4, 96, 64, 2, 5), (8, 128, 96, 4, 17),
                                                            (32, 256, 128, 4, 70), (32, 64, 64, 4, 300)])
 def test_residual_small_layers_bit_exact(ctx, experts, hidden, inter, top_k, m, inject):
+    _residual_case(ctx, experts, hidden, inter, top_k, m, inject, G.PROJECTION_RESIDUAL_Q8)
+
+
+@pytest.mark.parametrize("projection", [G.PROJECTION_Q8, G.PROJECTION_EXACT_BF16], ids=["q8", "exact-bf16"])
+@pytest.mark.parametrize("inject", [False, True])
+def test_residual_projection_modes(ctx, projection, inject):
+    """The MoE half of the decoder layer in the Q8 and exact-BF16 modes (the
+    exact mode reads the normalized rows the quantization work-groups store)."""
+    _residual_case(ctx, 8, 128, 96, 4, 17, inject, projection)
+    _residual_case(ctx, 32, 64, 64, 4, 300, inject, projection)
+
+
+def _residual_case(ctx, experts, hidden, inter, top_k, m, inject, projection):
     """gossmx_moe_forward_residual = norm_boundary -> moe_batch -> add_residual
     (cpu_runner.rs:2519-2553) against the oracle, every output bit-exact. With
     injected logits the norm runs in the selection kernels' quantization
@@ -380,9 +461,9 @@ def test_residual_small_layers_bit_exact(ctx, experts, hidden, inter, top_k, m, 
     logits = None
     if inject:
         logits = O.bf16_round_array(np.random.default_rng(m).standard_normal((m, experts)).astype(np.float32))
-    want = O.moe_residual(host, x, w, 1e-5, injected_logits=logits)
+    want = O.moe_residual(host, x, w, 1e-5, injected_logits=logits, projection=projection)
     assert want["status"] == O.OK
-    layer = gpu_layer(ctx, host)
+    layer = gpu_layer(ctx, host, projection)
     got = layer.forward_residual(x, w, 1e-5, injected_logits=logits)
     assert_residual_equal(got, want)
     assert (got["route_order"] == want["route_order"]).all()

@@ -587,3 +587,49 @@ def test_combine_adds_weighted_ranks_in_rank_order():
     for name, fn in alts.items():
         outs = [fn([F(y[r, k, 0] * w[r, k]) for k in range(4)]) for r in range(2)]
         assert outs != got[:2].tolist(), name
+
+
+def _record(scale, codes):
+    """A canonical MXFP4 record: scale byte, then code(2j) | code(2j+1) << 4."""
+    return np.array([scale] + [codes[2 * j] | (codes[2 * j + 1] << 4) for j in range(16)], np.uint8)
+
+
+def exact_pin_layer():
+    """A one-block layer (hidden = intermediate = 32, 2 experts, top-1,
+    routing injected to expert 0) whose exact-BF16 gate_up row 0 depends on
+    the 16-lane order of accumulate_mxfp4_bf16_block (lib.rs:932-945): with
+    scale 2^10, codes 6 (4.0) and 14 (-4.0) at k = 0 and 16 against x = 2^12
+    give products 2^24 and -2^24, both in lane 0, and code 2 (1.0) at k =
+    1..15 against x = 2^-10 gives 1 in lanes 1..15. Lane 0 cancels first:
+    the row is 15; a sequential sum over k absorbs the 1s into 2^24 (0)."""
+    host = O.synthetic_layer(19, 0, experts=2, hidden=32, intermediate=32, top_k=1)
+    codes = [6] + [2] * 15 + [14] + [0] * 15
+    gate_up = host.gate_up.copy().reshape(2, 64, 17)
+    gate_up[0, 0] = _record(137, codes)
+    bias = host.gate_up_bias.copy()
+    bias[0] = 0.0
+    layer = O.MoeLayerHost(host.router_weight, host.router_bias, gate_up.ravel(), bias, host.down,
+                           host.down_bias, 2, 32, 32, 1)
+    x = np.zeros(32, np.float32)
+    x[0] = x[16] = 4096.0
+    x[1:16] = 2.0 ** -10
+    xb = (x.view(np.uint32) >> 16).astype(np.uint16)[None, :]
+    return layer, xb, np.array([[1.0, 0.0]], np.float32)
+
+
+def test_exact_bf16_projection_sums_in_sixteen_ordered_lanes():
+    layer, x, logits = exact_pin_layer()
+    r = O.moe_batch(layer, x, injected_logits=logits, trace=True, projection=O.PROJECTION_EXACT_BF16)
+    assert r["status"] == O.OK
+    assert r["gate_up"][0, 0, 0] == 15.0
+    codes = [6] + [2] * 15 + [14] + [0] * 15
+    w = np.array([[0.0, 0.5, 1, 1.5, 2, 3, 4, 6, -0.0, -0.5, -1, -1.5, -2, -3, -4, -6][c] * 1024.0 for c in codes],
+                 np.float32)
+    p = (w * O.bf16_to_f32(x[0])).astype(np.float32)
+    for name, alt in dot_alternatives(p).items():
+        if name not in ("16 lanes folded as a tree", "16 lanes folded 15..0", "float64"):
+            assert alt != 15.0, name
+    # The exact path's lane KAT and the residual/Q8 modes agree on routing.
+    for proj in (O.PROJECTION_RESIDUAL_Q8, O.PROJECTION_Q8):
+        q = O.moe_batch(layer, x, injected_logits=logits, projection=proj)
+        assert q["status"] == O.OK and (q["selected"] == r["selected"]).all()
