@@ -46,6 +46,7 @@ enum Status : int {
   OK = 0,
   INVALID_DIMENSIONS = 3,
   NON_FINITE_INPUT = 4,
+  UNAVAILABLE_BACKEND = 5,
   NON_FINITE_LOGITS = 8,
 };
 
@@ -449,6 +450,153 @@ void auto_matmul(const MatmulArgs& a, int threads) {
 }
 
 // ---------------------------------------------------------------------------
+// The reference's forced multi-row lanes (Mxfp4MatmulBackend::Avx2 and
+// ::Avx512Vnni): avx2_matmul / avx512_vnni_matmul (matmul.rs:829-961) over
+// mxfp4_matmul_x8_avx2 / _avx512_vnni (x86.rs:449-520, 660-732). Input rows
+// go in panels of P (4 for AVX2, 8 for AVX-512); per complete 8-output x8
+// group the panel rows start from the bias (or +0.0), and per K block the
+// eight exact integer dots of every panel row are taken from the block's
+// decoded weights, then each row adds ((dot * 0.5) * e8m0) * act_scale,
+// primary then residual. The output-row tail (n % 8) takes the scalar rows.
+// Integer dots are exact in any order, so the dots here are this restatement's
+// own: the block's eight weight rows are widened to 16 bits once and reused
+// by every panel row (the reference decodes each x8 chunk once per panel too),
+// then 16-bit multiply-adds (256-bit on the AVX2 lane, 512-bit on the
+// AVX-512 lane; the reference's AVX-512 lane uses VNNI); the float chain is
+// the reference's.
+
+// The 32 LUT integers (2 x E2M1) of each of the eight rows of an x8 record:
+// w[row][k], codes k = 0..31 of the block.
+void x8_decode(const uint8_t* rec, int16_t w[8][32]) {
+  static const int16_t lut[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+  for (int lane = 0; lane < 8; ++lane)
+    for (int c = 0; c < 2; ++c)
+      for (int i = 0; i < 8; ++i) {
+        const uint8_t b = rec[8 + c * 64 + lane * 8 + i];  // split byte 8c + i: code(8c + i) | code(8c + i + 16) << 4
+        w[lane][8 * c + i] = lut[b & 0x0f];
+        w[lane][8 * c + i + 16] = lut[b >> 4];
+      }
+}
+
+// The eight 8-lane partial-sum vectors s[o] reduced to one vector of eight sums.
+__attribute__((target("avx2")))
+inline __m256i reduce8(const __m256i s[8]) {
+  const __m256i s01 = _mm256_hadd_epi32(s[0], s[1]), s23 = _mm256_hadd_epi32(s[2], s[3]);
+  const __m256i s45 = _mm256_hadd_epi32(s[4], s[5]), s67 = _mm256_hadd_epi32(s[6], s[7]);
+  const __m256i s0123 = _mm256_hadd_epi32(s01, s23), s4567 = _mm256_hadd_epi32(s45, s67);
+  return _mm256_add_epi32(_mm256_permute2x128_si256(s0123, s4567, 0x20),
+                          _mm256_permute2x128_si256(s0123, s4567, 0x31));
+}
+
+__attribute__((target("avx2")))
+void panel_dots_avx2(const int16_t w[8][32], const int8_t* act, int32_t d[8]) {
+  const __m256i a = _mm256_loadu_si256((const __m256i*)act);
+  const __m256i a_lo = _mm256_cvtepi8_epi16(_mm256_castsi256_si128(a));
+  const __m256i a_hi = _mm256_cvtepi8_epi16(_mm256_extracti128_si256(a, 1));
+  __m256i sums[8];
+  for (int o = 0; o < 8; ++o)
+    sums[o] = _mm256_add_epi32(_mm256_madd_epi16(_mm256_loadu_si256((const __m256i*)w[o]), a_lo),
+                               _mm256_madd_epi16(_mm256_loadu_si256((const __m256i*)(w[o] + 16)), a_hi));
+  _mm256_storeu_si256((__m256i*)d, reduce8(sums));
+}
+
+__attribute__((target("avx2,avx512f,avx512bw,avx512vl")))
+void panel_dots_avx512(const int16_t w[8][32], const int8_t* act, int32_t d[8]) {
+  const __m512i a = _mm512_cvtepi8_epi16(_mm256_loadu_si256((const __m256i*)act));
+  __m256i sums[8];
+  for (int o = 0; o < 8; ++o) {
+    const __m512i p = _mm512_madd_epi16(_mm512_loadu_si512(w[o]), a);
+    sums[o] = _mm256_add_epi32(_mm512_castsi512_si256(p), _mm512_extracti64x4_epi64(p, 1));
+  }
+  _mm256_storeu_si256((__m256i*)d, reduce8(sums));
+}
+
+bool host_has_avx512_vnni() {
+  return __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+         __builtin_cpu_supports("avx512vl") && __builtin_cpu_supports("avx512vnni");
+}
+
+// One 8-output group of the panel lane for panel rows [r0, r0 + rows).
+void panel_group(const MatmulArgs& a, size_t group, size_t r0, size_t rows, bool avx512) {
+  const bool residual = a.kind == 2;
+  float acc[8][8];
+  for (size_t r = 0; r < rows; ++r)
+    for (int o = 0; o < 8; ++o) acc[r][o] = a.bias ? a.bias[group * 8 + o] : 0.0f;
+  alignas(64) int16_t w[8][32];
+  for (size_t b = 0; b < a.blocks; ++b) {
+    const uint8_t* rec = a.weights + (group * a.blocks + b) * 136;
+    x8_decode(rec, w);
+    float ws[8];
+    for (int o = 0; o < 8; ++o) ws[o] = e8m0_scale(rec[o]);
+    for (size_t r = 0; r < rows; ++r) {
+      const size_t i = (r0 + r) * a.act_stride + b;
+      const int8_t* pv;
+      float ps;
+      const int8_t* rv = nullptr;
+      float rs = 0.0f;
+      if (residual) {
+        const ResidualQ8Block& blk = static_cast<const ResidualQ8Block*>(a.act)[i];
+        pv = blk.primary.values;
+        ps = blk.primary.scale;
+        rv = blk.residual.values;
+        rs = blk.residual.scale;
+      } else {
+        const Q8Block& blk = static_cast<const Q8Block*>(a.act)[i];
+        pv = blk.values;
+        ps = blk.scale;
+      }
+      int32_t pd[8], rd[8];
+      if (avx512) panel_dots_avx512(w, pv, pd);
+      else panel_dots_avx2(w, pv, pd);
+      if (residual) {
+        if (avx512) panel_dots_avx512(w, rv, rd);
+        else panel_dots_avx2(w, rv, rd);
+      }
+      for (int o = 0; o < 8; ++o) {
+        float c = (((float)pd[o] * 0.5f) * ws[o]) * ps;
+        acc[r][o] = acc[r][o] + c;
+        if (residual) {
+          c = (((float)rd[o] * 0.5f) * ws[o]) * rs;
+          acc[r][o] = acc[r][o] + c;
+        }
+      }
+    }
+  }
+  for (size_t r = 0; r < rows; ++r)
+    for (int o = 0; o < 8; ++o) a.out[(r0 + r) * a.out_stride + group * 8 + o] = acc[r][o];
+}
+
+// lane 4: AVX2 4x8 panels; lane 8: AVX-512/VNNI 8x8 panels. x8 layout only.
+// threads > 1 spreads (panel, group) units over threads (the forced lanes of
+// the reference run one thread per problem).
+void panel_matmul(const MatmulArgs& a, int lane, int threads) {
+  const size_t P = lane == 8 ? 8 : 4, groups = a.rows / 8, panels = (a.m + P - 1) / P;
+  const bool avx512 = lane == 8;
+  auto unit = [&](size_t u) {
+    const size_t panel = u / std::max<size_t>(groups, 1), g = u % std::max<size_t>(groups, 1);
+    const size_t r0 = panel * P, rows = std::min(P, a.m - r0);
+    panel_group(a, g, r0, rows, avx512);
+  };
+  const size_t units = panels * groups;
+  if (threads <= 1 || units < 2) {
+    for (size_t u = 0; u < units; ++u) unit(u);
+  } else {
+    std::vector<std::thread> pool;
+    std::atomic<size_t> next{0};
+    for (int t = 0; t < threads; ++t)
+      pool.emplace_back([&] {
+        for (;;) {
+          const size_t u = next.fetch_add(1);
+          if (u >= units) break;
+          unit(u);
+        }
+      });
+    for (auto& th : pool) th.join();
+  }
+  if (groups * 8 != a.rows) scalar_matmul_rows(a, 0, a.m, groups * 8, a.rows);
+}
+
+// ---------------------------------------------------------------------------
 // Deterministic synthetic data (shared with the GPU library's generator).
 inline uint64_t splitmix64(uint64_t x) {
   uint64_t z = x + 0x9E3779B97F4A7C15ull;
@@ -555,6 +703,19 @@ int oracle_mxfp4_matmul_auto(const uint8_t* data, size_t rows, size_t blocks, in
 }
 
 int oracle_has_avx2() { return host_has_avx2() ? 1 : 0; }
+int oracle_has_avx512_vnni() { return host_has_avx512_vnni() ? 1 : 0; }
+
+// The forced panel lanes on x8 weights: lane 4 (AVX2 4x8) or 8 (AVX-512/VNNI
+// 8x8); kind 1 (Q8) or 2 (residual-Q8).
+int oracle_mxfp4_matmul_lane(const uint8_t* data, size_t rows, size_t blocks, int kind, const void* act, size_t m,
+                             const float* bias, float* out, size_t out_stride, int lane, int threads) {
+  if ((lane != 4 && lane != 8) || (kind != 1 && kind != 2)) return INVALID_DIMENSIONS;
+  if (lane == 4 && !host_has_avx2()) return UNAVAILABLE_BACKEND;
+  if (lane == 8 && !host_has_avx512_vnni()) return UNAVAILABLE_BACKEND;
+  MatmulArgs a{data, rows, blocks, 2, kind, act, m, blocks, bias, out, out_stride};
+  panel_matmul(a, lane, threads);
+  return OK;
+}
 
 // Fixture generators of mxfp4_matrix_bench.rs:524-570 (make_weights, make_q8,
 // make_residual, make_bias) and pack_x8 (:572-597).
@@ -582,6 +743,44 @@ void oracle_bench_residual(size_t rows, size_t blocks, void* out) {
 void oracle_bench_bias(size_t rows, float* bias) {
   for (size_t i = 0; i < rows; ++i) bias[i] = (float)i * 0.00003125f - 0.25f;
 }
+void pack_x8_groups(const uint8_t* canonical, size_t blocks, uint8_t* out, size_t g_lo, size_t g_hi) {
+  for (size_t g = g_lo; g < g_hi; ++g)
+    for (size_t b = 0; b < blocks; ++b) {
+      uint8_t* p = out + (g * blocks + b) * 136;
+      for (size_t lane = 0; lane < 8; ++lane) *p++ = canonical[((g * 8 + lane) * blocks + b) * kRecord];
+      uint8_t split[8][16];
+      for (size_t lane = 0; lane < 8; ++lane)
+        adjacent_to_split(canonical + ((g * 8 + lane) * blocks + b) * kRecord + 1, split[lane]);
+      for (int chunk = 0; chunk < 2; ++chunk)
+        for (size_t lane = 0; lane < 8; ++lane) {
+          std::memcpy(p, split[lane] + chunk * 8, 8);
+          p += 8;
+        }
+    }
+}
+
+// pack_x8 with the complete groups spread over threads (same bytes).
+void pack_x8_threaded(const uint8_t* canonical, size_t rows, size_t blocks, uint8_t* out, int threads) {
+  const size_t groups = rows / 8;
+  if (threads <= 1 || groups < 64) {
+    pack_x8_groups(canonical, blocks, out, 0, groups);
+  } else {
+    std::vector<std::thread> pool;
+    const size_t per = (groups + threads - 1) / threads;
+    for (int t = 0; t < threads; ++t) {
+      const size_t lo = std::min(groups, t * per), hi = std::min(groups, lo + per);
+      pool.emplace_back([=] { pack_x8_groups(canonical, blocks, out, lo, hi); });
+    }
+    for (auto& th : pool) th.join();
+  }
+  uint8_t* p = out + groups * blocks * 136;
+  for (size_t r = groups * 8; r < rows; ++r)
+    for (size_t b = 0; b < blocks; ++b) {
+      std::memcpy(p, canonical + (r * blocks + b) * kRecord, kRecord);
+      p += kRecord;
+    }
+}
+
 void oracle_pack_x8(const uint8_t* canonical, size_t rows, size_t blocks, uint8_t* out) {
   uint8_t* p = out;
   for (size_t g = 0; g < rows / 8; ++g)
@@ -708,6 +907,9 @@ int oracle_moe_batch(const OracleLayer* L, const uint16_t* x, size_t m, const fl
                              trace_swiglu, trace_down, auto_lane, threads, 0);
 }
 
+// lane: 0 the scalar matmul, 1 the faithful Auto lane (x8 GEMV for single-row
+// buckets), 4 / 8 the forced AVX2 4x8 / AVX-512 8x8 panel lanes; threads
+// spread a bucket's work (1 is the reference's one thread per bucket).
 // projection: 0 residual-Q8 (the serving default), 1 Q8, 2 exact-BF16
 // (CpuExpertProjection, cpu_runner.rs:49-90; prepare_expert_input and
 // project_mxfp4_batch, :3092-3440).
@@ -716,6 +918,7 @@ int oracle_moe_batch_ex(const OracleLayer* L, const uint16_t* x, size_t m, const
                         float* trace_gate_up, float* trace_swiglu, float* trace_down, int auto_lane, int threads,
                         int projection) {
   if (projection < 0 || projection > 2) return INVALID_DIMENSIONS;
+  if ((auto_lane == 4 && !host_has_avx2()) || (auto_lane == 8 && !host_has_avx512_vnni())) return UNAVAILABLE_BACKEND;
   const size_t E = L->experts, H = L->hidden, I = L->intermediate, K = L->top_k;
   if (m == 0 || K == 0 || K > E || H % kBlock || I % kBlock) return INVALID_DIMENSIONS;
   const size_t N1 = 2 * I, B1 = H / kBlock, N2 = H, B2 = I / kBlock;
@@ -771,12 +974,18 @@ int oracle_moe_batch_ex(const OracleLayer* L, const uint16_t* x, size_t m, const
     if (projection == 2) {
       for (size_t i = 0; i < mb; ++i)
         exact_bf16_project(wgu, N1, B1, x + routes[s + i].row * H, L->gate_up_bias + e * N1, &gu[i * N1]);
-    } else if (auto_lane && projection == 0) {
+    } else if (auto_lane == 1 && projection == 0) {
       x8.resize(N1 * B1 * kRecord);
       oracle_pack_x8(wgu, N1, B1, x8.data());
       a1.weights = x8.data();
       a1.layout = 2;
       auto_matmul(a1, threads);
+    } else if (auto_lane == 4 || auto_lane == 8) {
+      x8.resize(N1 * B1 * kRecord);
+      pack_x8_threaded(wgu, N1, B1, x8.data(), threads);
+      a1.weights = x8.data();
+      a1.layout = 2;
+      panel_matmul(a1, auto_lane, threads);
     } else {
       scalar_matmul_rows(a1, 0, mb, 0, N1);
     }
@@ -807,12 +1016,18 @@ int oracle_moe_batch_ex(const OracleLayer* L, const uint16_t* x, size_t m, const
         for (size_t n = 0; n < I; ++n) act16[n] = bf16_bits(act[i * I + n]);  // activated_bf16 (:2917)
         exact_bf16_project(wdn, N2, B2, act16.data(), L->down_bias + e * N2, &dn[i * N2]);
       }
-    } else if (auto_lane && projection == 0) {
+    } else if (auto_lane == 1 && projection == 0) {
       x8.resize(N2 * B2 * kRecord);
       oracle_pack_x8(wdn, N2, B2, x8.data());
       a2.weights = x8.data();
       a2.layout = 2;
       auto_matmul(a2, threads);
+    } else if (auto_lane == 4 || auto_lane == 8) {
+      x8.resize(N2 * B2 * kRecord);
+      pack_x8_threaded(wdn, N2, B2, x8.data(), threads);
+      a2.weights = x8.data();
+      a2.layout = 2;
+      panel_matmul(a2, auto_lane, threads);
     } else {
       scalar_matmul_rows(a2, 0, mb, 0, N2);
     }

@@ -97,6 +97,8 @@ def _declare(L):
         "oracle_mxfp4_matmul": (i32, [vp, sz, sz, sz, i32, i32, vp, sz, sz, sz, sz, vp, sz, vp, sz, sz]),
         "oracle_mxfp4_matmul_auto": (i32, [vp, sz, sz, i32, vp, sz, vp, vp, sz, i32]),
         "oracle_has_avx2": (i32, []),
+        "oracle_has_avx512_vnni": (i32, []),
+        "oracle_mxfp4_matmul_lane": (i32, [vp, sz, sz, i32, vp, sz, vp, vp, sz, i32, i32]),
         "oracle_bench_weights": (None, [sz, sz, vp]),
         "oracle_bench_residual": (None, [sz, sz, vp]),
         "oracle_bench_bias": (None, [sz, vp]),
@@ -298,12 +300,37 @@ class MoeLayerHost:
 
 
 PROJECTION_RESIDUAL_Q8, PROJECTION_Q8, PROJECTION_EXACT_BF16 = 0, 1, 2
+UNAVAILABLE_BACKEND = 5
+
+# Expert-matmul lanes of moe_batch: the scalar matmul, the faithful Auto lane,
+# and the reference's forced AVX2 4x8 / AVX-512 8x8 panel lanes.
+LANE_SCALAR, LANE_AUTO, LANE_AVX2_4X8, LANE_AVX512_8X8 = 0, 1, 4, 8
+
+
+def fastest_lane() -> int:
+    """The forced panel lane this host runs (every lane is bit-identical)."""
+    if lib().oracle_has_avx512_vnni():
+        return LANE_AVX512_8X8
+    return LANE_AVX2_4X8 if lib().oracle_has_avx2() else LANE_SCALAR
+
+
+def mxfp4_matmul_lane(data_x8, rows, blocks, act, m, bias, lane, threads=1, kind=2):
+    """A forced panel lane (Mxfp4MatmulBackend::Avx2 / Avx512Vnni) on x8 weights."""
+    out = np.full(m * rows, np.nan, dtype=np.float32)
+    st = lib().oracle_mxfp4_matmul_lane(_p(data_x8), rows, blocks, kind, _p(act), m, _p(bias), _p(out), rows, lane,
+                                        threads)
+    if st != OK:
+        raise RuntimeError(f"oracle lane {lane}: status {st}")
+    return out
 
 
 def moe_batch(layer: MoeLayerHost, x_bf16: np.ndarray, injected_logits=None, trace=False, auto_lane=False,
-              threads=1, projection=PROJECTION_RESIDUAL_Q8):
+              threads=1, projection=PROJECTION_RESIDUAL_Q8, lane=None):
     """CpuModel::moe_batch restated; returns a dict of outputs (or raises).
-    projection selects CpuExpertProjection (residual-Q8, Q8, exact-BF16)."""
+    projection selects CpuExpertProjection (residual-Q8, Q8, exact-BF16);
+    lane the expert-matmul lane (LANE_*; auto_lane=True is LANE_AUTO)."""
+    if lane is None:
+        lane = LANE_AUTO if auto_lane else LANE_SCALAR
     x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
     m = x.shape[0]
     E, H, I, K = layer.experts, layer.hidden, layer.intermediate, layer.top_k
@@ -323,7 +350,7 @@ def moe_batch(layer: MoeLayerHost, x_bf16: np.ndarray, injected_logits=None, tra
     st = lib().oracle_moe_batch_ex(C.byref(s), _p(x), m, _p(inj), _p(res["router_logits"]), _p(res["selected"]),
                                    _p(res["routing_weights"]), _p(res["output"]), _p(res["route_order"]),
                                    _p(res.get("gate_up")), _p(res.get("swiglu")), _p(res.get("down")),
-                                   1 if auto_lane else 0, threads, projection)
+                                   lane, threads, projection)
     res["status"] = st
     return res
 

@@ -53,6 +53,15 @@ def test_cpu_baseline_lanes_reproduce_golden_hash(case):
     for threads in (1, 4):
         out = O.mxfp4_matmul_auto(x8, n, 90, res, m, bias, threads=threads)
         assert sha(out) == case["sha256"]
+    # The forced panel lanes (Mxfp4MatmulBackend::Avx2 4x8, ::Avx512Vnni 8x8;
+    # matmul.rs:829-961), one thread as the reference runs them and spread.
+    lanes = [lane for lane, ok in ((O.LANE_AVX2_4X8, O.lib().oracle_has_avx2()),
+                                   (O.LANE_AVX512_8X8, O.lib().oracle_has_avx512_vnni())) if ok]
+    assert lanes, "this host runs neither panel lane"
+    for lane in lanes:
+        for threads in (1, 3):
+            out = O.mxfp4_matmul_lane(x8, n, 90, res, m, bias, lane, threads)
+            assert sha(out) == case["sha256"], (lane, threads)
 
 
 # --- known-answer tests of crates/gpt-oss-cpu-kernels/src/lib.rs ---
@@ -633,3 +642,41 @@ def test_exact_bf16_projection_sums_in_sixteen_ordered_lanes():
     for proj in (O.PROJECTION_RESIDUAL_Q8, O.PROJECTION_Q8):
         q = O.moe_batch(layer, x, injected_logits=logits, projection=proj)
         assert q["status"] == O.OK and (q["selected"] == r["selected"]).all()
+
+
+def test_moe_lanes_and_modes_agree_with_the_scalar_matmul():
+    """moe_batch on every expert-matmul lane (scalar, Auto, forced panels,
+    threaded) gives the scalar lane's bits, for the residual-Q8 and Q8 modes
+    (the panel lanes also serve the Q8 kind)."""
+    layer = O.synthetic_layer(33, 0, experts=4, hidden=96, intermediate=64, top_k=2)
+    x = O.gen_hidden(33, 1, 13, 96)
+    for projection in (O.PROJECTION_RESIDUAL_Q8, O.PROJECTION_Q8):
+        want = O.moe_batch(layer, x, trace=True, projection=projection)
+        assert want["status"] == O.OK
+        for lane in (O.LANE_AUTO, O.LANE_AVX2_4X8, O.LANE_AVX512_8X8):
+            for threads in (1, 4):
+                got = O.moe_batch(layer, x, trace=True, projection=projection, lane=lane, threads=threads)
+                if got["status"] == O.UNAVAILABLE_BACKEND:
+                    continue
+                for key in ("output", "gate_up", "down"):
+                    assert (got[key].view(np.uint32) == want[key].view(np.uint32)).all(), (projection, lane, key)
+
+
+def test_panel_lanes_finish_output_tails_with_scalar_rows():
+    """rows % 8 != 0: the complete x8 groups on the panel lane, the tail rows
+    on the scalar chain (avx2_matmul, matmul.rs:876-884), for 1..9 input
+    rows (partial and full panels) and both activation kinds."""
+    rows, blocks = 20, 3
+    canonical, _, _, bias = O.bench_fixtures(rows, blocks, 1)
+    x8 = O.pack_x8(canonical, rows, blocks)
+    for m in (1, 4, 5, 8, 9):
+        _, _, res, _ = O.bench_fixtures(rows, blocks, m)
+        q8 = np.ascontiguousarray(res["primary"])
+        for kind, act in ((2, res), (1, q8)):
+            st, want = O.mxfp4_matmul(canonical, rows, blocks, 1, act, m, bias, kind=kind)
+            assert st == O.OK
+            for lane in (O.LANE_AVX2_4X8, O.LANE_AVX512_8X8):
+                if not (O.lib().oracle_has_avx512_vnni() if lane == 8 else O.lib().oracle_has_avx2()):
+                    continue
+                got = O.mxfp4_matmul_lane(x8, rows, blocks, act, m, bias, lane, 2, kind=kind)
+                assert (got.view(np.uint32) == want.view(np.uint32)).all(), (m, kind, lane)
