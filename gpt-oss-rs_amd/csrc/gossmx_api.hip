@@ -328,6 +328,12 @@ int alloc_tiled(gossmx_ctx* ctx, size_t experts, size_t rows, size_t blocks, gos
   hipError_t e = hipMalloc(&w->t.nib, experts * w->t.nib_stride + kPlaneSlack);
   if (e == hipSuccess) e = hipMalloc(&w->t.scl, experts * w->t.scl_stride + kPlaneSlack);
   if (e == hipSuccess) e = hipMalloc(&w->t.fast, experts * w->t.tiles);
+  // The scale bytes of the blocks past the last one in a compact last group
+  // are never stored: zero them (E8M0 2^-127), so that every byte of the
+  // plane converts to finite values (gemv_kernel converts whole groups).
+  if (e == hipSuccess)
+    e = launch_clear_ints(reinterpret_cast<int*>(w->t.scl), (experts * w->t.scl_stride + kPlaneSlack) / 4,
+                          ctx->stream);
   if (e == hipSuccess) e = launch_fill_tiled_padding(w->t, ctx->stream);
   if (e != hipSuccess) {
     if (w->t.nib) hipFree(w->t.nib);
@@ -638,6 +644,13 @@ static int gemm_chunk(size_t m) {
   return m >= (size_t)kHugeMinRows ? kHugeChunk : kChunk;
 }
 
+// Batches of at most kTinyMaxRows rows on weights of at most kTinyMaxBlocks
+// blocks per row take the small-batch GEMV (whole K range per wave in
+// registers) instead of the stepped GEMM.
+static bool use_gemv(size_t m, size_t blocks, bool residual) {
+  return residual && m <= (size_t)kTinyMaxRows && blocks <= (size_t)kTinyMaxBlocks;
+}
+
 // --- kernel boundary ---------------------------------------------------------
 
 int gossmx_mxfp4_matmul_check(const gossmx_matmul_problem* p, size_t rows, size_t blocks, size_t experts) {
@@ -696,9 +709,13 @@ static int matmul_impl(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
   g.bias_expert_stride = 0;  // this problem's single bias vector
   {
     KernelScope scope(ctx, GOSSMX_OP_MATMUL);
-    const int chunk = gemm_chunk(m);
-    HIP_TRY(launch_gemm(kPlain, g, chunk, (int)((m + chunk - 1) / chunk), ctx->stream, scope.start, scope.stop),
-            "matmul launch");
+    if (use_gemv(m, B, g.residual != 0)) {
+      HIP_TRY(launch_gemv(kPlain, g, (int)m, 1, ctx->stream, scope.start, scope.stop), "matmul launch");
+    } else {
+      const int chunk = gemm_chunk(m);
+      HIP_TRY(launch_gemm(kPlain, g, chunk, (int)((m + chunk - 1) / chunk), ctx->stream, scope.start, scope.stop),
+              "matmul launch");
+    }
   }
   if (p->memory == GOSSMX_MEM_HOST) {
     HIP_TRY(hipMemcpy2DAsync(p->output, p->output_stride * sizeof(float), out, rows * sizeof(float),
@@ -985,11 +1002,17 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   } else {
     {
       KernelScope sc(ctx, GOSSMX_OP_GATE_UP);
-      HIP_TRY(launch_gemm(kGateUp, g, chunk, (int)max_work, ctx->stream, sc.start, sc.stop), "gate_up launch");
+      if (use_gemv(m, B1, g.residual != 0))
+        HIP_TRY(launch_gemv(kGateUp, g, (int)m, (int)max_work, ctx->stream, sc.start, sc.stop), "gate_up launch");
+      else
+        HIP_TRY(launch_gemm(kGateUp, g, chunk, (int)max_work, ctx->stream, sc.start, sc.stop), "gate_up launch");
     }
     {
       KernelScope sc(ctx, GOSSMX_OP_DOWN);
-      HIP_TRY(launch_gemm(kDown, d, chunk, (int)max_work, ctx->stream, sc.start, sc.stop), "down launch");
+      if (use_gemv(m, B2, d.residual != 0))
+        HIP_TRY(launch_gemv(kDown, d, (int)m, (int)max_work, ctx->stream, sc.start, sc.stop), "down launch");
+      else
+        HIP_TRY(launch_gemm(kDown, d, chunk, (int)max_work, ctx->stream, sc.start, sc.stop), "down launch");
     }
   }
   {

@@ -17,6 +17,11 @@ constexpr int kSmallChunk = 8;  // activation rows per work item for batches of 
 constexpr int kHugeChunk = 32;  // activation rows per work item for batches of at least kHugeMinRows rows
 constexpr int kHugeMinRows = 512;
 constexpr int kChunkMax = 32;
+// Small-batch GEMV (gemv_kernel): batches of at most kTinyMaxRows rows whose
+// blocks per row are at most kTinyMaxBlocks (the activation image of the
+// whole K range fits the work-group's LDS).
+constexpr int kTinyMaxRows = 4;
+constexpr int kTinyMaxBlocks = 96;
 constexpr int kMaxExperts = 128;
 constexpr int kMaxTopK = 8;
 constexpr int kNormMaxHidden = 8192;  // hidden sizes the fused post-attention RMSNorm stages in LDS
@@ -156,6 +161,12 @@ hipError_t launch_select_dispatch(const RouteArgs& r, const DispatchArgs& d, int
 hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int chunk, int grid_work, hipStream_t stream,
                        hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream);
+// Small-batch GEMV over the work list (kGateUp, kDown) or a plain problem
+// (kPlain): same arguments and outputs as launch_gemm with chunk kSmallChunk,
+// for residual-Q8 activations; requires every work item (and, for kPlain, m)
+// to hold at most rows_max <= kTinyMaxRows rows and blocks <= kTinyMaxBlocks.
+hipError_t launch_gemv(GemmMode mode, const GemmArgs& a, int rows_max, int grid_work, hipStream_t stream,
+                       hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 // Exact-BF16 expert projection over the work list (mode kGateUp or kDown);
 // chunk <= kChunkMax.
 hipError_t launch_exact(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream);

@@ -1341,6 +1341,274 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
 }
 
 // ---------------------------------------------------------------------------
+// Small-batch GEMV: batches of at most kTinyMaxRows rows (every work item is
+// at most kTinyMaxRows tokens of one expert) with at most kTinyMaxBlocks
+// blocks per row. A work-group is 4 waves, one 16-row weight tile each (64
+// rows: whole 32-value blocks of the down input for the gate_up epilogue),
+// each over the whole K range.
+//
+// Block packing. With the launch's tokens per item padded to mp in {1, 2, 4},
+// a block has V = 2 mp activation vectors (token, part), so the 16 rows of an MFMA A
+// operand hold P = 16 / V consecutive blocks of one "set": row i = p V + v is
+// vector v (token v / 2, part v % 2) of block s P + p. MFMA p of set s takes
+// the weights of block s P + p and an A operand whose rows of the other
+// positions are zero (those lanes read a zero piece of LDS), and the P MFMAs
+// of a set accumulate into one result, so each row of the result holds
+// exactly one block's integer dot (the other MFMAs add +0 to it; the sign of
+// a zero term never changes the chain, whose running total is never -0.0).
+// Every lane of the wave then holds useful dots, where one block per MFMA
+// leaves 7 of every 8 vectors empty at one token.
+// Lane (G, n) holds result rows 4G..4G+3 of weight row n; its term for row i
+// is (D_i * e8) * act_scale(block, token, part): the reference's
+// (p * ws) * ps rounded once (on the fast path the conversion applied the
+// E8M0 scale exactly and e8 is 1.0; otherwise e8 is e8m0_scale of the
+// block). The terms go through per-wave LDS buffers laid out
+// [p][token][row][part], from which lane 16 t + n runs the ordered chain of
+// (row n, token t): total += term_p; total += term_r, block after block,
+// the same sequence of operations per output as gemm_kernel's.
+//
+// LDS (dynamic, sized for mp): the activation image, set s at
+// s * kTinySetBytes as 64 pieces of 16 bytes [position][vector][k-slice]
+// (piece 4 i + g: k-slice g of row i) followed by a zero piece; the
+// activation scales [block][token][part] f32 (the 16 scales of set s at
+// 16 s); kTinyTermBufs term buffers of 1 KiB per wave.
+
+constexpr int kTinyGroups = kTinyMaxBlocks / 4;
+constexpr int kTinySuper = 8;  // blocks per set at one token
+// Weight groups in flight per wave (measured at one token: 8 and 16 groups
+// run alike, the whole K range at once is slower); fewer at four tokens,
+// whose sets hold more operands in registers.
+__host__ __device__ constexpr int tiny_ring(int P) { return P == 2 ? 12 : 16; }
+constexpr int kTinySetBytes = 1024 + 16;                        // a set's 64 pieces and its zero piece
+constexpr int kTinyTermBytes = 1024;                            // [8 (position, token)][16 rows][2] f32
+constexpr int kTinyTermBufs = 4;                                // term buffers per wave (the chain lags 2 sets)
+static_assert(kTinyMaxBlocks % kTinySuper == 0, "whole sets");
+
+__host__ __device__ constexpr int tiny_sets(int mp) { return kTinyMaxBlocks * mp / 8; }
+__host__ __device__ constexpr int tiny_image_bytes(int mp) { return tiny_sets(mp) * kTinySetBytes; }
+__host__ __device__ constexpr int tiny_lds_bytes(int mp) {
+  return tiny_image_bytes(mp) + tiny_sets(mp) * 64 + 4 * kTinyTermBufs * kTinyTermBytes;
+}
+
+// The geometry fields gemm_epilogue reads.
+struct GemmTinyCfg {
+  static constexpr int kWaves = 4;
+  static constexpr int kThreads = 256;
+  static constexpr int kWaveTiles = 1;
+  static constexpr int kWgTiles = 4;
+  static constexpr int kGemmRows = kTileRows * kWgTiles;
+  static constexpr int kChunk = kSmallChunk;                   // token slots of a work item
+  static constexpr int kNtg = 1;
+  static constexpr int kSlotBytes = tiny_image_bytes(1);     // LDS the epilogue may reuse
+};
+
+struct GemvLoads {
+  __amdgpu_buffer_rsrc_t nib, scl;
+  int vl, vl_tail, vs, nq4, nfull4;
+};
+
+__device__ __forceinline__ void gemv_load(const GemvLoads& L, int q, u32x4& wn, uint32_t& ws) {
+  const int gi = min(q, L.nq4 - 1);  // groups past the end re-load the last one (unused)
+  wn = __builtin_amdgcn_raw_buffer_load_b128(L.nib, gi < L.nfull4 ? L.vl : L.vl_tail, gi * 1024, 0);
+  ws = __builtin_amdgcn_raw_buffer_load_b32(L.scl, L.vs, gi * 64, 0);
+}
+
+// The K loop of one wave for sets of P blocks (mp = 8 / P tokens), straight
+// line over all kTinyMaxBlocks blocks. Blocks past B contribute +0.0 terms,
+// which leave the running total unchanged (it is never -0.0). Their weights
+// are the last group's bytes (loads past the end are clamped to it) or the
+// plane slack: E2M1 codes and zeroed or stored scale bytes, all of which
+// convert to finite values, so the zero rows of the A operand keep every real
+// row exact (0 x finite = 0). With `fast` the conversion applies the tile's
+// scales (all in the exact range) and e8 is 1.0 (d * 1.0 is d); otherwise the
+// conversion is unscaled and e8 is e8m0_scale of the block.
+template <int P>
+__device__ __forceinline__ float gemv_sets(float tot, const GemvLoads& L, u32x4 (&wn)[tiny_ring(P)],
+                                           uint32_t (&ws)[tiny_ring(P)], const char* img, const float* scl,
+                                           float* terms, const int B, const int lane, const bool fast) {
+  constexpr int V = 16 / P, mp = 8 / P, R = tiny_ring(P);
+  constexpr int kSetsAll = kTinyMaxBlocks / P;
+  const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int G = lane >> 4, n = lane & 15;
+  // A operand of MFMA p: lane (g = lane / 16, i = lane % 16) reads piece
+  // 4 i + g of the set when row i belongs to position p, else the zero piece.
+  int off[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) off[p] = (n / V == p) ? (4 * n + G) * 16 : 1024;
+  // Positions of this lane's result rows 4G, 4G+1 and 4G+2, 4G+3.
+  const int pos_a = (4 * G) / V, pos_b = (4 * G + 2) / V;
+  // Chain lane 16 t + n reads entry p * mp + t of the term buffer (t past mp
+  // folds onto a real token; its total is never stored).
+  const int t_read = G & (mp - 1);
+  // Set s's terms go to buffer s % kTinyTermBufs; the chain of set s - 2
+  // runs after set s is produced, so its LDS round trip and the chain's adds
+  // overlap the MFMAs of the sets in between.
+  auto chain = [&](const int s) {
+    const float* tb = terms + (s % kTinyTermBufs) * (kTinyTermBytes / 4);
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const float2 v = reinterpret_cast<const float2*>(tb)[(p * mp + t_read) * 16 + n];
+      tot = tot + v.x;
+      tot = tot + v.y;
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < kSetsAll; ++s) {
+    f32x4 d = zero;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int b = s * P + p, q = b >> 2, j = b & 3;
+      const uint32_t sw = ws[q % R];
+      const half8 bop = fp4x8_to_half8_scaled(wn[q % R][j], fast ? e8m0_scale_operand(sw, j) : 1.0f);
+      const half8 aop = *reinterpret_cast<const half8*>(img + s * kTinySetBytes + off[p]);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, d, 0, 0, 0);
+    }
+    // e8 of the blocks of this lane's rows (branch-free, then 1.0 on the
+    // fast path).
+    float e8a, e8b;
+    if (P == 8) {  // rows 4G, 4G+1: block 8 s + 2G; rows 4G+2, 4G+3: block 8 s + 2G + 1 (group 2 s + G / 2)
+      const uint32_t sw = G < 2 ? ws[(2 * s) % R] : ws[(2 * s + 1) % R];
+      const int sh = 16 * (G & 1);
+      e8a = e8m0_select((sw >> sh) & 0xffu);
+      e8b = e8m0_select((sw >> (sh + 8)) & 0xffu);
+    } else if (P == 4) {  // block 4 s + G (group s)
+      e8a = e8b = e8m0_select((ws[s % R] >> (8 * G)) & 0xffu);
+    } else {  // block 2 s + G / 2 (group s / 2, byte 2 (s % 2) + G / 2)
+      e8a = e8b = e8m0_select((ws[(s / 2) % R] >> (8 * (2 * (s & 1) + (G >> 1)))) & 0xffu);
+    }
+    e8a = fast ? 1.0f : e8a;
+    e8b = fast ? 1.0f : e8b;
+    // Groups whose blocks are all converted take the group R ahead.
+#pragma unroll
+    for (int q = (s * P) / 4; q < ((s + 1) * P) / 4; ++q)
+      if (q + R < kTinyGroups) gemv_load(L, q + R, wn[q % R], ws[q % R]);
+    const float4 sc = *reinterpret_cast<const float4*>(scl + s * 16 + 4 * G);
+    // Terms of blocks past B become +0.0 by a bit mask (no branch).
+    const uint32_t ma = s * P + pos_a < B ? ~0u : 0u, mb = s * P + pos_b < B ? ~0u : 0u;
+    float2 t01, t23;
+    t01.x = __uint_as_float(__float_as_uint((d[0] * e8a) * sc.x) & ma);
+    t01.y = __uint_as_float(__float_as_uint((d[1] * e8a) * sc.y) & ma);
+    t23.x = __uint_as_float(__float_as_uint((d[2] * e8b) * sc.z) & mb);
+    t23.y = __uint_as_float(__float_as_uint((d[3] * e8b) * sc.w) & mb);
+    // Rows 4G, 4G+1 are entry 2G, rows 4G+2, 4G+3 entry 2G+1 ([p][token]).
+    float* tb = terms + (s % kTinyTermBufs) * (kTinyTermBytes / 4);
+    reinterpret_cast<float2*>(tb)[(2 * G) * 16 + n] = t01;
+    reinterpret_cast<float2*>(tb)[(2 * G + 1) * 16 + n] = t23;
+    if (s >= 2) chain(s - 2);
+  }
+  chain(kSetsAll - 2);
+  chain(kSetsAll - 1);
+  return tot;
+}
+
+template <int MODE, int P>
+__global__ __launch_bounds__(256, 2) void gemv_kernel(GemmArgs a) {
+  using C = GemmTinyCfg;
+  extern __shared__ __align__(16) char s_dyn[];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int nl = lane & 15;
+  int expert, start, count;
+  if (MODE == kPlain) {
+    expert = a.plain_expert;
+    start = blockIdx.y * kTinyMaxRows;
+    count = min(kTinyMaxRows, a.plain_m - start);
+  } else {
+    const int wi = blockIdx.y;
+    const int nw = *a.n_work;
+    const int4 rec = reinterpret_cast<const int4*>(a.work)[wi];
+    if (wi >= nw) return;  // uniform over the work-group
+    expert = rec.x;
+    start = rec.y;
+    count = rec.z;
+  }
+  constexpr int mp = 8 / P, V = 2 * mp;  // every item of the launch holds at most mp tokens
+  const int rows = (int)a.w.rows, B = (int)a.w.blocks;
+  const int tile0 = blockIdx.x * C::kWaves + wave;
+  const bool ok = tile0 < (int)a.w.tiles;
+  const int safe_tile = ok ? tile0 : 0;  // tiles past the end stream tile 0 and discard it
+  const int nq4 = (B + 3) >> 2;
+
+  // Per-tile state first (fast-path flag, bias).
+  const bool fast = a.fast_ok && a.w.fast[(size_t)expert * a.w.tiles + safe_tile] != 0;
+  const int row = tile0 * kTileRows + nl;
+  float bias = 0.0f;
+  if (a.bias != nullptr && ok && row < rows) bias = a.bias[(size_t)expert * a.bias_expert_stride + row];
+
+  // The first four weight groups, then the activation rows, then the rest of
+  // the ring: the weights need only the expert.
+  GemvLoads L;
+  L.nib = buffer_rsrc(a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)safe_tile * 256 * B);
+  L.scl = buffer_rsrc(a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)safe_tile * 64 * nq4);
+  L.vl = lane * 16;
+  L.vl_tail = lane * (B & 3) * 4;
+  L.vs = nl * 4;
+  L.nq4 = nq4;
+  L.nfull4 = B >> 2;
+  constexpr int R = tiny_ring(P);
+  u32x4 wn[R];
+  uint32_t ws[R];
+  constexpr int kFirst = 4;
+#pragma unroll
+  for (int q = 0; q < kFirst; ++q) gemv_load(L, q, wn[q], ws[q]);
+
+  // Activation rows of the item's tokens (absent tokens read row 0: valid
+  // memory whose products are never stored).
+  int r[kTinyMaxRows];
+#pragma unroll
+  for (int t = 0; t < kTinyMaxRows; ++t)
+    r[t] = t < count ? (MODE == kGateUp ? a.route_tok[start + t] : start + t) : 0;
+
+  char* img = s_dyn;
+  float* s_scl = reinterpret_cast<float*>(s_dyn + tiny_image_bytes(mp));
+  float* terms = reinterpret_cast<float*>(s_dyn + tiny_image_bytes(mp) + tiny_sets(mp) * 64) +
+                 wave * (kTinyTermBufs * kTinyTermBytes / 4);
+  const int nsets = (B + P - 1) / P;
+  const __amdgpu_buffer_rsrc_t act_codes = buffer_rsrc(a.actv), act_scl = buffer_rsrc(a.acts);
+  {
+    // Image piece `lane` of set k: row i = lane / 4 (position i / V, vector
+    // i % V), k-slice lane % 4.
+    const int i = lane >> 2, g = lane & 3, v = i % V, t = v >> 1, part = v & 1;
+    const int rt = t == 0 ? r[0] : (t == 1 ? r[1] : (t == 2 ? r[2] : r[3]));
+    for (int k = wave; k < nsets; k += C::kWaves) {  // uniform per wave
+      const int b = k * P + i / V;
+      const int voff = (b < B && t < count) ? ((rt * B + b) * 2 + part) * 64 + g * 16 : 0;
+      dma16(act_codes, img + k * kTinySetBytes, voff, 0);
+    }
+    // Scale f of the image: block f / (2 mp), token (f / 2) % mp, part f % 2.
+    for (int k = wave; k * 64 < nsets * 16; k += C::kWaves) {  // uniform per wave
+      const int f = k * 64 + lane;
+      const int b = f / (2 * mp), ts = (f >> 1) % mp, ps = f & 1;
+      const int rs = ts == 0 ? r[0] : (ts == 1 ? r[1] : (ts == 2 ? r[2] : r[3]));
+      const int voff = (b < B && ts < count) ? ((rs * B + b) * 2 + ps) * 4 : 0;
+      dma4(act_scl, reinterpret_cast<char*>(s_scl) + k * 256, voff, 0);
+    }
+  }
+  for (int k = tid; k < nsets; k += C::kThreads) *reinterpret_cast<u32x4*>(img + k * kTinySetBytes + 1024) = u32x4{};
+#pragma unroll
+  for (int q = kFirst; q < R; ++q) gemv_load(L, q, wn[q], ws[q]);
+  // The DMA and the first groups have landed once at most the later groups'
+  // loads are outstanding; then every wave's part is in.
+  constexpr int kWait = 2 * (R - kFirst);
+  static_assert(kWait < 64, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((kWait & 15) | ((kWait >> 4) << 14) | (7 << 4) | (15 << 8));
+  __syncthreads();
+
+  float tot = bias + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
+  tot = gemv_sets<P>(tot, L, wn, ws, img, s_scl, terms, B, lane, fast);
+
+  // Lane 16 t + n holds (row n, token t); the epilogue's lane (G, n) holds
+  // tokens 2G and 2G + 1.
+  const int G = lane >> 4;
+  Acc<C> acc;
+  acc[0][0][0] = __shfl(tot, ((2 * G) * 16 + nl) & 63);
+  acc[0][0][1] = __shfl(tot, ((2 * G + 1) * 16 + nl) & 63);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();  // every wave is done with the LDS image before the epilogue reuses it
+  gemm_epilogue<C, MODE, true>(a, acc, 1, count, start, tile0, reinterpret_cast<float*>(s_dyn));
+}
+
+// ---------------------------------------------------------------------------
 // Exact-BF16 expert projection (CpuExpertProjection::ExactBf16; project_mxfp4,
 // cpu_runner.rs:3497-3519): per output, total = bias; total += the 16 lane
 // sums folded 0..15 from -0.0. Lane l sums bf16(decode(code) * e8m0) * x over
@@ -1807,6 +2075,34 @@ hipError_t launch_gemm(GemmMode mode, const GemmArgs& a, int chunk, int grid_wor
   if (chunk == GemmBig::kChunk) return launch_gemm_cfg<GemmBig>(mode, a, grid_work, stream, start, stop);
   if (chunk == GemmHuge::kChunk) return launch_gemm_cfg<GemmHuge>(mode, a, grid_work, stream, start, stop);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemv(GemmMode mode, const GemmArgs& a, int rows_max, int grid_work, hipStream_t stream,
+                       hipEvent_t start, hipEvent_t stop) {
+  if (a.w.blocks > (size_t)kTinyMaxBlocks || rows_max < 1 || rows_max > kTinyMaxRows) return hipErrorInvalidValue;
+  // Residual-Q8 activations only: the Q8 projection (no residual term) runs
+  // the tiled GEMM at every batch size.
+  if (!a.residual) return hipErrorInvalidValue;
+  const int mp_max = rows_max <= 1 ? 1 : (rows_max <= 2 ? 2 : 4);
+  const dim3 grid((unsigned)((a.w.tiles + GemmTinyCfg::kWgTiles - 1) / GemmTinyCfg::kWgTiles), (unsigned)grid_work);
+  const dim3 block(GemmTinyCfg::kThreads);
+  const unsigned lds = (unsigned)tiny_lds_bytes(mp_max);
+  auto go = [&](auto kernel) {
+    if (start) hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, start, stop, 0, a);
+    else hipLaunchKernelGGL(kernel, grid, block, lds, stream, a);
+  };
+  // Sets of P = 8 / mp_max blocks for every item of the launch.
+  auto pick = [&](auto k8, auto k4, auto k2) {
+    if (mp_max == 1) go(k8);
+    else if (mp_max == 2) go(k4);
+    else go(k2);
+  };
+  switch (mode) {
+    case kPlain: pick(gemv_kernel<kPlain, 8>, gemv_kernel<kPlain, 4>, gemv_kernel<kPlain, 2>); break;
+    case kGateUp: pick(gemv_kernel<kGateUp, 8>, gemv_kernel<kGateUp, 4>, gemv_kernel<kGateUp, 2>); break;
+    case kDown: pick(gemv_kernel<kDown, 8>, gemv_kernel<kDown, 4>, gemv_kernel<kDown, 2>); break;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_exact(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream) {
