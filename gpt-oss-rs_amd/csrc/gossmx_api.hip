@@ -78,7 +78,7 @@ struct gossmx_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   bool own_stream = false;
-  int* err = nullptr;  // device error flags
+  int* err = nullptr;  // [0]: device error flags; [1]: route_select_kernel's arrival counter (0 between launches)
   uint16_t* sig_tab = nullptr;  // SwiGLU sigmoid table (built at context creation)
   bool fast_ok = true;          // the scaled FP4 conversion passed the self-test (see run_selftest)
   bool capturing = false;
@@ -943,11 +943,17 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   da.work = work;
   da.n_work = n_work;
   da.chunk = chunk;
-  if (injected == nullptr) {
+  // Small batches with a computed router: router, selection and dispatch in
+  // one launch (the route counter is the second int of the flags buffer).
+  const bool route_fused = injected == nullptr && fused && m <= (size_t)kFusedRouteRows && H <= (size_t)kFusedRouteHidden;
+  if (route_fused) {
+    OpScope sc(ctx, GOSSMX_OP_ROUTER_ROUTING);
+    HIP_TRY(launch_route_select(ra, da, ctx->err + 1, ctx->stream), "route/select launch");
+  } else if (injected == nullptr) {
     OpScope sc(ctx, GOSSMX_OP_ROUTER_ROUTING);
     HIP_TRY(launch_route(ra, ctx->stream), "route launch");
   }
-  {
+  if (!route_fused) {
     // This stage also holds top-k, softmax and (with injected logits) the
     // gate_up input quantization.
     OpScope sc(ctx, GOSSMX_OP_DISPATCH);

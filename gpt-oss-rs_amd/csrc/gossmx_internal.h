@@ -140,6 +140,11 @@ constexpr int kSelectLds = 8448;        // m * (experts + 1) floats
 constexpr int kSelectMaxRoutes = 2048;  // m * top_k
 constexpr int kSelectTopK = 4;          // top_k (GPT-OSS routes to 4 experts)
 
+// Computed router logits of small batches take one launch for the router,
+// the selection and the dispatch (route_select_kernel).
+constexpr int kFusedRouteRows = 4;
+constexpr int kFusedRouteHidden = 4096;
+
 // Launchers (gossmx_kernels.hip). All are asynchronous on `stream`.
 // Router logits (bf16-rounded, into a.logits) and the gate_up input
 // quantization; followed by one of the two selection paths below.
@@ -155,6 +160,10 @@ hipError_t launch_place(const DispatchArgs& a, int m, const int* cnt, hipStream_
 // select = 0. quantize = 1 adds the gate_up input quantization work-groups
 // (when no launch_route ran).
 hipError_t launch_select_dispatch(const RouteArgs& r, const DispatchArgs& d, int quantize, hipStream_t stream);
+// Router logits, top-k, softmax, dispatch and (r.quant) the gate_up input
+// quantization of m <= kFusedRouteRows rows in one launch. `counter`: a
+// device int that is 0 before the launch; the launch leaves it 0.
+hipError_t launch_route_select(const RouteArgs& r, const DispatchArgs& d, int* counter, hipStream_t stream);
 // chunk: rows per work item (kSmallChunk, kChunk or kHugeChunk), selecting
 // the kernel's geometry; it must match the chunk the dispatch used.
 // start/stop (nullable): events the launch itself records around the kernel.

@@ -623,20 +623,71 @@ __device__ __forceinline__ void select_quantize(const RouteArgs& r, int qwg) {
   }
 }
 
-__global__ __launch_bounds__(1024) void select_dispatch_kernel(RouteArgs r, DispatchArgs d) {
-  const int tid = threadIdx.x;
-  if (blockIdx.x > 0) {
-    select_quantize(r, (int)blockIdx.x - 1);
-    return;
+// stable_top_k and the routing softmax of rows w, w + 16, ... by wave w of a
+// 1024-thread work-group (experts <= kMaxExperts): lane e holds the keys of
+// experts e and e + 64, and a key's rank is the number of larger keys among
+// all experts (keys are distinct, so ranks are too); ranks below K are the
+// selection in stable_top_k order. The softmax then follows
+// select_row_lanes's operations: max folded in rank order, each rank's
+// exponential, the sum folded in rank order from 0.0f.
+__device__ __forceinline__ void select_rows_ranked(const RouteArgs& r, const float* s_lg, int stride, int* s_sel,
+                                                   const uint64_t* tab) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int E = r.experts, K = r.top_k, M = r.m;
+  __shared__ uint64_t s_key[16][kMaxExperts];
+  __shared__ int s_pick[16][kMaxTopK];
+  __shared__ float s_ex[16][kMaxTopK];
+  for (int row = wave; row < M; row += 16) {  // uniform per wave
+    const float* lg = s_lg + row * stride;
+    const uint64_t k0 = lane < E ? route_key(lg[lane], lane) : 0;
+    const uint64_t k1 = lane + 64 < E ? route_key(lg[lane + 64], lane + 64) : 0;
+    s_key[wave][lane] = k0;
+    s_key[wave][lane + 64] = k1;
+    __builtin_amdgcn_wave_barrier();  // LDS of one wave is in order: the keys are in place
+    int r0 = 0, r1 = 0;
+#pragma unroll 8
+    for (int f = 0; f < E; ++f) {
+      const uint64_t kf = s_key[wave][f];
+      r0 += kf > k0;
+      r1 += kf > k1;
+    }
+    if (lane < E && r0 < K) s_pick[wave][r0] = lane;
+    if (lane + 64 < E && r1 < K) s_pick[wave][r1] = lane + 64;
+    __builtin_amdgcn_wave_barrier();
+    float mx = -INFINITY;
+    for (int k = 0; k < K; ++k) mx = fmaxf(mx, lg[s_pick[wave][k]]);
+    const int my_e = s_pick[wave][lane < K ? lane : 0];
+    const float ex = expf_glibc(lg[my_e] - mx, tab);
+    if (lane < K) s_ex[wave][lane] = ex;
+    __builtin_amdgcn_wave_barrier();
+    float sum = 0.0f;
+    for (int k = 0; k < K; ++k) sum = sum + s_ex[wave][k];
+    if (lane < K) {
+      r.selected[(size_t)row * K + lane] = my_e;
+      r.weights[(size_t)row * K + lane] = bf16r(ex / sum);
+      s_sel[row * K + lane] = my_e;
+    }
+    __builtin_amdgcn_wave_barrier();  // the next row's key writes follow this row's reads
   }
+}
+
+// Top-k, softmax and dispatch of every row by one work-group of 1024 threads.
+// SMALL (route_select_kernel, m <= kFusedRouteRows): the logits were written
+// by other work-groups of this launch and are read with device-scope atomic
+// loads, and the selection is select_rows_ranked.
+template <bool SMALL>
+__device__ __forceinline__ void select_dispatch_body(const RouteArgs& r, const DispatchArgs& d) {
+  const int tid = threadIdx.x;
   const int E = r.experts, K = r.top_k, M = r.m, stride = E + 1;
-  __shared__ float s_lg[kSelectLds];
-  __shared__ int s_sel[kSelectMaxRoutes];
+  __shared__ float s_lg[SMALL ? kFusedRouteRows * (kMaxExperts + 1) : kSelectLds];
+  __shared__ int s_sel[SMALL ? kFusedRouteRows * kMaxTopK : kSelectMaxRoutes];
   __shared__ uint64_t s_tab[32];
   if (tid < 32) s_tab[tid] = kExp2Tab[tid];
   for (int i = tid; i < M * E; i += 1024) {
     float v;
-    if (r.injected != nullptr) {
+    if (SMALL) {
+      v = __hip_atomic_load(r.logits + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if (r.injected != nullptr) {
       v = bf16r(r.injected[i]);
       if (r.logits) r.logits[i] = v;
     } else {
@@ -652,7 +703,11 @@ __global__ __launch_bounds__(1024) void select_dispatch_kernel(RouteArgs r, Disp
   while (T > 1 && (T * M > 1024 || 4 * T > E)) T >>= 1;
   while (T < K) T <<= 1;
   const int rows_per_pass = 1024 / T;
-  for (int base = 0; base < M; base += rows_per_pass) {  // uniform
+  if (SMALL) select_rows_ranked(r, s_lg, stride, s_sel, s_tab);
+  for (int base = 0; !SMALL && base < M; base += rows_per_pass) {  // uniform
+    // A row's T lanes share a wave: waves whose first row is past the batch
+    // have nothing to select and skip (wave-uniform).
+    if (base + (tid & ~63) / T >= M) continue;
     const int row = base + tid / T, j = tid % T;
     const bool has_row = row < M;
     const int rr = has_row ? row : 0;
@@ -662,6 +717,104 @@ __global__ __launch_bounds__(1024) void select_dispatch_kernel(RouteArgs r, Disp
   }
   __syncthreads();
   dispatch_body(d, s_sel);
+}
+
+__global__ __launch_bounds__(1024) void select_dispatch_kernel(RouteArgs r, DispatchArgs d) {
+  if (blockIdx.x > 0) {
+    select_quantize(r, (int)blockIdx.x - 1);
+    return;
+  }
+  select_dispatch_body<false>(r, d);
+}
+
+// Router, selection and dispatch of a small batch (m <= kFusedRouteRows,
+// hidden <= kFusedRouteHidden) in one launch. Work-group e < experts
+// computes expert e's logit for every row: the rows (normalized as
+// route_kernel does) and the router row are staged in LDS, lane l of a row
+// sums w[i] * x[i] over i = l mod 16 in increasing i (scalar_bf16_dot,
+// lib.rs:1007-1029), the lanes are added 0..15, then bias and bf16
+// (cpu_runner.rs:2781-2783, 2829). Each work-group releases its logits
+// (device-scope release fence) and counts itself on `counter`; the last one
+// to arrive (it has seen every other count) reads them all with device-scope
+// atomic loads, resets the counter for the next launch and runs
+// select_dispatch_body. Work-groups past the experts quantize the gate_up
+// input (select_quantize).
+__global__ __launch_bounds__(1024) void route_select_kernel(RouteArgs r, DispatchArgs d, int* counter) {
+  const int tid = threadIdx.x;
+  const int E = r.experts, H = r.hidden, M = r.m;
+  if ((int)blockIdx.x >= E) {
+    select_quantize(r, (int)blockIdx.x - E);
+    return;
+  }
+  const int e = blockIdx.x;
+  // Products w[i] * x[i] (f32, rounded as the reference's multiply) by chain
+  // lane: element i of a row sits at [i % 16][i / 16] (lanes padded by 16
+  // bytes against bank conflicts), so lane l adds its products 4 at a time in
+  // increasing i; the pad up to a multiple of 4 is +0.0, which leaves the
+  // chain unchanged (it is never -0.0).
+  constexpr int kLane = kFusedRouteHidden / 16 + 4;
+  __shared__ __align__(16) float s_pt[kFusedRouteRows][16][kLane];
+  __shared__ float s_chain[kFusedRouteRows][16];
+  __shared__ float s_inv[kFusedRouteRows];
+  __shared__ int s_last;
+  if (r.norm_w) {
+    for (int rr = 0; rr < M; ++rr) {  // uniform
+      const float v = row_inverse_rms(r.x + (size_t)rr * H, H, r.norm_eps);
+      if (tid == 0) s_inv[rr] = v;
+    }
+    __syncthreads();
+  }
+  const int per_lane = H / 16, padded = (per_lane + 3) & ~3;
+  for (int v = tid; v < M * 16 * (padded - per_lane); v += 1024) {  // the pad
+    const int rr = v / (16 * (padded - per_lane)), rest = v % (16 * (padded - per_lane));
+    s_pt[rr][rest / (padded - per_lane)][per_lane + rest % (padded - per_lane)] = 0.0f;
+  }
+  const int pieces = H / 8;  // 16-byte pieces: elements 8c..8c+7 are lanes (8c) % 16 + 0..7 at k = c / 2
+  for (int v = tid; v < M * pieces; v += 1024) {
+    const int rr = v / pieces, c = v - rr * pieces;
+    const int l0 = (c & 1) * 8, k = c >> 1;
+    const u32x4 wv = reinterpret_cast<const u32x4*>(r.router_w + (size_t)e * H)[c];
+    const u32x4 xv = reinterpret_cast<const u32x4*>(r.x + (size_t)rr * H)[c];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float lo = bf16_to_f32((uint16_t)(xv[q] & 0xffffu)), hi = bf16_to_f32((uint16_t)(xv[q] >> 16));
+      if (r.norm_w) {  // post-attention RMSNorm, bf16 (norm_boundary; route_input)
+        const int i = c * 8 + 2 * q;
+        lo = bf16r(lo * s_inv[rr] * r.norm_w[i]);
+        hi = bf16r(hi * s_inv[rr] * r.norm_w[i + 1]);
+      }
+      s_pt[rr][l0 + 2 * q][k] = __uint_as_float(wv[q] << 16) * lo;
+      s_pt[rr][l0 + 2 * q + 1][k] = __uint_as_float(wv[q] & 0xffff0000u) * hi;
+    }
+  }
+  __syncthreads();
+  if (tid < M * 16) {
+    const int rr = tid >> 4, l = tid & 15;
+    const float4* pl = reinterpret_cast<const float4*>(s_pt[rr][l]);
+    float acc = 0.0f;
+#pragma unroll 4
+    for (int c = 0; c < padded / 4; ++c) {
+      const float4 v = pl[c];
+      acc = acc + v.x;
+      acc = acc + v.y;
+      acc = acc + v.z;
+      acc = acc + v.w;
+    }
+    s_chain[rr][l] = acc;
+  }
+  __syncthreads();
+  if (tid < M) {
+    float sum = s_chain[tid][0];
+    for (int j = 1; j < 16; ++j) sum = sum + s_chain[tid][j];
+    r.logits[(size_t)tid * E + e] = bf16r(sum + r.router_b[e]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // this row's logit reaches device scope before the count
+  }
+  __syncthreads();
+  if (tid == 0) s_last = atomicAdd(counter, 1) == E - 1;
+  __syncthreads();
+  if (!s_last) return;
+  if (tid == 0) atomicExch(counter, 0);
+  select_dispatch_body<true>(r, d);
 }
 
 // Selection and grouping of batches past the fused kernel's limits, in two
@@ -705,8 +858,9 @@ __global__ __launch_bounds__(1024) void select_count_kernel(RouteArgs r, int row
   const int lr = tid / T, j = tid % T;
   const bool has_row = lr < nrows;
   const int rr = has_row ? lr : 0;
-  select_row_lanes<KMAX>(s_lg + rr * stride, has_row, j, T, E, K, r.selected + (size_t)(r0 + rr) * K,
-                         r.weights + (size_t)(r0 + rr) * K, s_sel + rr * K, s_tab);
+  if ((tid & ~63) / T < nrows)  // waves with no row of the batch skip (wave-uniform)
+    select_row_lanes<KMAX>(s_lg + rr * stride, has_row, j, T, E, K, r.selected + (size_t)(r0 + rr) * K,
+                           r.weights + (size_t)(r0 + rr) * K, s_sel + rr * K, s_tab);
   __syncthreads();
   for (int i = tid; i < nrows * K; i += 1024) atomicAdd(&s_cnt[s_sel[i]], 1);
   __syncthreads();
@@ -2041,6 +2195,17 @@ hipError_t launch_select_dispatch(const RouteArgs& r, const DispatchArgs& d, int
   const size_t qblocks = quantize ? (size_t)r.m * (r.hidden / kBlock) : 0;
   const unsigned grid = 1u + (unsigned)((qblocks + kSelectQuantBlocks - 1) / kSelectQuantBlocks);
   hipLaunchKernelGGL(select_dispatch_kernel, dim3(grid), dim3(1024), 0, stream, r, d);
+  return hipGetLastError();
+}
+
+hipError_t launch_route_select(const RouteArgs& r, const DispatchArgs& d, int* counter, hipStream_t stream) {
+  if (r.m < 1 || r.m > kFusedRouteRows || r.hidden > kFusedRouteHidden || r.hidden % 32 != 0 || r.injected != nullptr ||
+      r.m * (r.experts + 1) > kSelectLds || d.routes > kSelectMaxRoutes || r.top_k > kSelectTopK ||
+      r.experts > kMaxExperts)
+    return hipErrorInvalidValue;
+  const size_t qblocks = r.quant ? (size_t)r.m * (r.hidden / kBlock) : 0;
+  const unsigned grid = (unsigned)r.experts + (unsigned)((qblocks + kSelectQuantBlocks - 1) / kSelectQuantBlocks);
+  hipLaunchKernelGGL(route_select_kernel, dim3(grid), dim3(1024), 0, stream, r, d, counter);
   return hipGetLastError();
 }
 

@@ -10,9 +10,12 @@ import oracle as O
 pytestmark = pytest.mark.gpu
 
 
-def test_captured_forward_replays_match_eager_and_oracle():
+@pytest.mark.parametrize("m", [3, 12])
+def test_captured_forward_replays_match_eager_and_oracle(m):
+    """m = 3 takes the one-launch router/selection kernel, whose arrival
+    counter must be back at zero after every launch, eager or replayed."""
     with G.Context(0) as ctx:
-        E, H, I, K, m = 8, 128, 64, 4, 12
+        E, H, I, K = 8, 128, 64, 4
         host = O.synthetic_layer(21, 0, experts=E, hidden=H, intermediate=I, top_k=K)
         gu = G.Weights.upload(ctx, host.gate_up, E, 2 * I, H // 32)
         dn = G.Weights.upload(ctx, host.down, E, H, I // 32)

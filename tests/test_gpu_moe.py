@@ -144,6 +144,23 @@ def test_20b_shape_decode_bit_exact(layer20b, m):
     assert_moe_equal(layer.forward(x), want)
 
 
+@pytest.mark.parametrize("experts,m", [(32, 1), (128, 1), (128, 4), (5, 4)])
+def test_one_launch_routing_bit_exact_and_repeatable(ctx, experts, m):
+    """Batches of at most 4 rows with a computed router take one launch for
+    the router, selection and dispatch (one work-group per expert, the last
+    to arrive selects). Three calls in a row, alternating with a 9-row batch
+    (two-launch path), all equal the oracle: the arrival counter resets."""
+    host = O.synthetic_layer(31, experts, experts=experts, hidden=256, intermediate=64, top_k=4)
+    layer = gpu_layer(ctx, host)
+    x = O.gen_hidden(31, m, m, 256)
+    x9 = O.gen_hidden(31, 9, 9, 256)
+    want, want9 = O.moe_batch(host, x), O.moe_batch(host, x9)
+    for _ in range(3):
+        assert_moe_equal(layer.forward(x), want)
+        assert_moe_equal(layer.forward(x9), want9)
+    close(layer)
+
+
 CHECK_THREADS = min(16, os.cpu_count() or 1)
 
 
@@ -366,17 +383,24 @@ def test_scratch_requirement_is_none_and_selftest_passes(ctx):
 
 
 def test_profiler_counts_every_stage(ctx):
+    """Every stage is timed once per call. Batches of at most 4 rows with a
+    computed router run the router, selection and dispatch as one launch,
+    counted under router_routing (dispatch then has no launch of its own)."""
     host = O.synthetic_layer(9, 0, experts=4, hidden=64, intermediate=32, top_k=2)
     layer = gpu_layer(ctx, host)
-    x = O.gen_hidden(9, 1, 4, 64)
-    ctx.profile(True)
-    ctx.profile_reset()
-    for _ in range(3):
-        layer.forward(x)
-    rec = ctx.profile_read()
-    ctx.profile(False)
-    for op in ("router_routing", "dispatch", "gate_up", "down", "weighting"):
-        assert rec[op]["launches"] == 3 and rec[op]["total_ms"] > 0.0
+    for m, fused in ((12, False), (4, True)):
+        x = O.gen_hidden(9, 1, m, 64)
+        ctx.profile(True)
+        ctx.profile_reset()
+        for _ in range(3):
+            layer.forward(x)
+        rec = ctx.profile_read()
+        ctx.profile(False)
+        for op in ("router_routing", "dispatch", "gate_up", "down", "weighting"):
+            if fused and op == "dispatch":
+                assert rec[op]["launches"] == 0
+            else:
+                assert rec[op]["launches"] == 3 and rec[op]["total_ms"] > 0.0, (m, op)
     close(layer)
 
 
