@@ -16,20 +16,34 @@ BASELINE.md's CPU figures). Inputs and weights are resident before timing.
   4  GPT-OSS-120B shape: 128 experts, all 36 layers resident (61 GB),
      decode batch 256 with Zipf(1.2) routing.
 
+  4 --prefill  the same 120B-shape layers, prefill of 4096 tokens with
+     near-uniform routing (MFMA roofline).
+
 Prints one JSON line. The per-kernel roofline uses the library's hipEvent
 profiler on the stream the kernels run on (the GEMM launches record their own
-start and stop events, so the interval is the kernel's execution); `cpu_baseline` times the oracle's
-faithful Auto lane (x8 AVX2 GEMV for single-row buckets, scalar matmul for
-multi-row buckets, one thread, as moe_batch runs it) on a bounded sample of
-layer 0 of the same batch after checking that the GPU's rows are
-bit-identical to it.
+start and stop events, so the interval is the kernel's execution). For the
+HBM-bound workloads roofline.traffic is measured in the same run: two child
+processes under rocprofv3 --pmc (FETCH_SIZE, then WRITE_SIZE) run a 1 GiB
+device copy, which calibrates each counter, and then the workload, before
+this process touches the GPU (--no-traffic skips them). `cpu_baseline` times
+the oracle's faithful Auto lane (x8 AVX2 GEMV for single-row buckets, scalar
+matmul for multi-row buckets, one thread, as moe_batch runs it) and its
+fastest forced panel lane on a bounded sample of layer 0 of the same batch,
+after checking that the GPU's rows are bit-identical to it (and the last
+layer's rows on the forced lane); the exit status is 1 if any bit differs.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
+import re
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -43,17 +57,15 @@ import synth  # noqa: E402
 METRIC = "MoE-layer tokens/s + achieved HBM GB/s (% of peak), 20B shape bs=1/64"
 HBM_PEAK_GBPS = 8000.0
 F16_MFMA_PEAK_TFLOPS = 2500.0     # dense f16 MFMA, the instruction the expert GEMM issues
+MXFP4_MFMA_PEAK_TFLOPS = 10100.0  # dense MXFP4 MFMA, the peak BASELINE.json's prefill target names
 HIDDEN = INTER = 2880
 BLOCKS = HIDDEN // 32
 GATE_UP_BYTES = 2 * INTER * BLOCKS * 17   # 8,812,800 B per expert
 DOWN_BYTES = HIDDEN * BLOCKS * 17         # 4,406,400 B per expert
 SEED = 20251201
 RMS_EPS = 1e-5  # GPT-OSS rms_norm_eps
-# HBM bytes per gate_up launch measured with rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE on each workload (FETCH KiB x 2.0 + WRITE KiB x 1.0, the factors
-# the counters read for a 1 GiB device copy; configs[1]: 166,485 x 2 + 3,242).
-# bench.py cannot read counters itself, so these are the profiled values.
-PMC_GATE_UP_TRAFFIC = {0: 35_101 * 1024, 1: 336_212 * 1024, 2: 3_381_431 * 1024, 4: 1_395_462 * 1024}
+COPY_PROBE_BYTES = 1 << 30  # device copy that calibrates the HBM byte counters
+GATE_UP_KERNEL = re.compile(r"gemm_kernel<.*>, 1, (true|false)>|gemv_kernel<1, \d+>")
 
 CONFIGS = {
     0: {"batch": 1, "layers": 12, "experts": 32, "routing": "router", "zipf": None, "roofline": "hbm",
@@ -73,6 +85,11 @@ CONFIGS = {
                     "Zipf({zipf}) injected routing, top-4 of 128 experts",
         "sample_rows": 32},
 }
+# configs[4]'s second workload (--config 4 --prefill).
+PREFILL_4 = {"batch": 4096, "layers": 36, "experts": 128, "routing": "uniform", "zipf": None, "roofline": "mfma",
+             "workload": "configs[4]: GPT-OSS-120B-shape MoE prefill, {batch} tokens, all {layers} layers resident, "
+                         "near-uniform injected routing, top-4 of 128 experts",
+             "sample_rows": 16}
 
 
 def stable_topk_sets(logits: np.ndarray, k: int) -> np.ndarray:
@@ -113,16 +130,25 @@ def build_workload(ctx, cfg: dict, rng):
     return x, x_dev, state
 
 
-def cpu_baseline(cfg: dict, x, st0, layer_out_gpu, threads: int):
-    """Oracle lanes on a bounded sample of layer 0's rows; checks GPU bits first."""
+def host_layer(O, cfg: dict, st, layer: int):
+    p = st["params"]
+    E = cfg["experts"]
+    return O.MoeLayerHost(p["router_weight"], p["router_bias"], O.gen_mxfp4(SEED, 16 * layer + 4, E, 2 * INTER, BLOCKS),
+                          p["gate_up_bias"], O.gen_mxfp4(SEED, 16 * layer + 5, E, HIDDEN, BLOCKS), p["down_bias"], E,
+                          HIDDEN, INTER, 4)
+
+
+def cpu_baseline(cfg: dict, x, state, threads: int):
+    """Oracle lanes on a bounded sample of rows: layer 0 on the Auto lane (one
+    thread, then all threads) and on the host's fastest forced panel lane, and
+    the last layer on the forced lane over all threads; each result is
+    checked bit for bit against the GPU's rows first."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
-    p = st0["params"]
-    E = cfg["experts"]
-    host = O.MoeLayerHost(p["router_weight"], p["router_bias"], O.gen_mxfp4(SEED, 4, E, 2 * INTER, BLOCKS),
-                          p["gate_up_bias"], O.gen_mxfp4(SEED, 5, E, HIDDEN, BLOCKS), p["down_bias"], E, HIDDEN,
-                          INTER, 4)
+    st0 = state[0]
+    layer_out_gpu = st0["out_dev"].cpu().numpy()
+    host = host_layer(O, cfg, st0, 0)
     n = min(cfg["sample_rows"], x.shape[0])
     rows = np.linspace(0, x.shape[0] - 1, n).astype(np.int64) if n < x.shape[0] else np.arange(n)
     xs = x[rows]
@@ -136,6 +162,21 @@ def cpu_baseline(cfg: dict, x, st0, layer_out_gpu, threads: int):
     ref_mt = O.moe_batch(host, xs, injected_logits=inj, auto_lane=True, threads=threads)
     t_all = time.perf_counter() - t0
     same_mt = bool((ref_mt["output"].view(np.uint32) == ref["output"].view(np.uint32)).all())
+    lane = O.fastest_lane()
+    lane_name = {O.LANE_AVX512_8X8: "avx512-vnni 8x8 panel", O.LANE_AVX2_4X8: "avx2 4x8 panel",
+                 O.LANE_SCALAR: "scalar"}[lane]
+    t0 = time.perf_counter()
+    ref_lane = O.moe_batch(host, xs, injected_logits=inj, lane=lane, threads=1)
+    t_lane = time.perf_counter() - t0
+    same_lane = bool((ref_lane["output"].view(np.uint32) == ref["output"].view(np.uint32)).all())
+    last = len(state) - 1
+    same_last = None
+    if last > 0:
+        stl = state[last]
+        inj_l = None if stl["logits"] is None else stl["logits"][rows]
+        ref_l = O.moe_batch(host_layer(O, cfg, stl, last), xs, injected_logits=inj_l, lane=lane, threads=threads)
+        same_last = bool((ref_l["output"].view(np.uint32) ==
+                          stl["out_dev"].cpu().numpy()[rows].view(np.uint32)).all())
     whole = "the whole batch" if n == x.shape[0] else f"{n} evenly spaced rows of the {x.shape[0]}-token batch"
     return {
         "value": n / t_auto, "unit": "layer-tokens/s", "cores": 1, "kind": "port",
@@ -143,7 +184,92 @@ def cpu_baseline(cfg: dict, x, st0, layer_out_gpu, threads: int):
                   f"scalar matmul for M>1 buckets, cpu_runner.rs:3409-3416), {t_auto:.1f} s",
         "gpu_bits_equal": same,
         "all_cores": {"value": n / t_all, "cores": threads, "seconds": round(t_all, 2), "bits_equal": same_mt},
+        "forced_lane": {"lane": lane_name, "value": n / t_lane, "cores": 1, "seconds": round(t_lane, 2),
+                        "bits_equal": same_lane,
+                        "source": "x86.rs:449-520 (AVX2 4x8), 660-732 (AVX-512-VNNI 8x8) restated in the oracle"},
+        "last_layer_bits_equal": same_last,
     }
+
+
+def probe_traffic(args) -> dict:
+    """HBM bytes per gate_up launch, measured in this run: two child processes
+    under rocprofv3 --pmc (FETCH_SIZE, then WRITE_SIZE: the counters do not
+    fit one pass), each running a 1 GiB device copy and then the workload
+    (--traffic-probe). Each counter is scaled by copy bytes / what it reads for
+    the copy; traffic = FETCH x that + WRITE x that, averaged over the gate_up
+    dispatches. Runs before this process touches the GPU."""
+    rp = shutil.which("rocprofv3")
+    if rp is None:
+        return {"traffic": None, "traffic_source": "not measured: rocprofv3 not found"}
+    env = dict(os.environ, TMPDIR="/tmp")
+    per = {}
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="gossmx_pmc_", dir="/tmp")
+        cmd = [rp, "--pmc", ctr, "--output-format", "csv", "-d", d, "-o", "p", "--", sys.executable,
+               os.path.abspath(__file__), "--traffic-probe", "--config", str(args.config)]
+        for key in ("layers", "batch", "zipf"):
+            if getattr(args, key) is not None:
+                cmd += [f"--{key}", str(getattr(args, key))]
+        if args.prefill:
+            cmd.append("--prefill")
+        try:
+            # rocprofv3 may end with a segmentation fault after the program's
+            # results are complete: the CSV decides.
+            subprocess.run(cmd, timeout=240, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, env=env,
+                           cwd="/tmp")
+        except subprocess.TimeoutExpired:
+            return {"traffic": None, "traffic_source": f"not measured: rocprofv3 --pmc {ctr} pass timed out"}
+        files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if not files:
+            return {"traffic": None, "traffic_source": f"not measured: rocprofv3 --pmc {ctr} wrote no counters"}
+        copy_kib, gate_up = 0.0, []
+        with open(files[0]) as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != ctr:
+                    continue
+                name, val = row.get("Kernel_Name", ""), float(row.get("Counter_Value", "nan"))
+                if "copyBuffer" in name:
+                    copy_kib = max(copy_kib, val)
+                elif GATE_UP_KERNEL.search(name):
+                    gate_up.append(val)
+        shutil.rmtree(d, ignore_errors=True)
+        if copy_kib <= 0 or not gate_up:
+            return {"traffic": None, "traffic_source": f"not measured: {ctr} rows for the copy or gate_up missing"}
+        per[ctr] = (float(np.mean(gate_up)), copy_kib, len(gate_up))
+    (fk, fc, n), (wk, wc, _) = per["FETCH_SIZE"], per["WRITE_SIZE"]
+    f_scale, w_scale = COPY_PROBE_BYTES / (fc * 1024), COPY_PROBE_BYTES / (wc * 1024)
+    traffic = fk * 1024 * f_scale + wk * 1024 * w_scale
+    return {"traffic": traffic,
+            "traffic_source": f"rocprofv3 --pmc FETCH_SIZE then WRITE_SIZE in this run, {n} gate_up dispatches: "
+                              f"{fk:.0f} KiB x {f_scale:.3f} + {wk:.0f} KiB x {w_scale:.3f} (scales from a 1 GiB "
+                              f"device copy: FETCH {fc:.0f} KiB, WRITE {wc:.0f} KiB)"}
+
+
+def run_traffic_probe(args, cfg: dict) -> int:
+    """Child of probe_traffic: a 1 GiB device copy, then one untimed pass and
+    one step of the workload (two layers at most), eager."""
+    import torch
+
+    torch.cuda.init()
+    src = torch.empty(COPY_PROBE_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    cfg = dict(cfg, layers=min(cfg["layers"], 2))
+    ctx = G.Context(0)
+    x, x_dev, state = build_workload(ctx, cfg, np.random.default_rng(SEED))
+    m = cfg["batch"]
+    for _ in range(2):
+        for st in state:
+            st["moe"].forward_device(x_dev, m, st["out_dev"], injected_logits=st["logits_dev"])
+    ctx.synchronize()
+    for st in state:
+        st["moe"].close()
+        st["gu"].close()
+        st["dn"].close()
+    ctx.close()
+    return 0
 
 
 def run_model(args) -> int:
@@ -254,6 +380,11 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a device-to-device copy of this many MiB (calibrates HBM byte counters)")
+    ap.add_argument("--prefill", action="store_true",
+                    help="with --config 4: the 4096-token prefill workload instead of decode 256")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the rocprofv3 --pmc passes that measure roofline.traffic")
+    ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.copy_probe_mib:
         import torch
@@ -270,11 +401,20 @@ def main() -> int:
         return 2
     if args.config == 3:
         return run_model(args)
-    cfg = dict(CONFIGS[args.config])
+    if args.prefill and args.config != 4:
+        print("--prefill applies to --config 4 only", file=sys.stderr)
+        return 2
+    cfg = dict(PREFILL_4 if args.prefill else CONFIGS[args.config])
     for key in ("layers", "batch", "zipf"):
         if getattr(args, key) is not None:
             cfg[key] = getattr(args, key)
     m, E, L = cfg["batch"], cfg["experts"], cfg["layers"]
+    if args.traffic_probe:
+        return run_traffic_probe(args, cfg)
+    # The counter passes run in child processes before this one touches the GPU.
+    probe = None
+    if cfg["roofline"] == "hbm" and not args.no_traffic and not args.residual:
+        probe = probe_traffic(args)
 
     import torch
 
@@ -370,22 +510,25 @@ def main() -> int:
     gu_avg_ms = gu["total_ms"] / max(gu["launches"], 1)
     gu_bytes_per_launch = touched * GATE_UP_BYTES / L
     gu_gbps = gu_bytes_per_launch / (gu_avg_ms * 1e-3) / 1e9
-    kernel = "gemm_kernel<kGateUp> (gate_up MXFP4 GEMM + SwiGLU + down-input quantization)"
+    if m <= 4:
+        kernel = (f"gemv_kernel<kGateUp, P={8 // (1 if m == 1 else 2 if m == 2 else 4)}> (block-packed small-batch "
+                  "MXFP4 GEMV + SwiGLU + down-input quantization)")
+    else:
+        kernel = "gemm_kernel<kGateUp> (gate_up MXFP4 GEMM + SwiGLU + down-input quantization)"
     if cfg["roofline"] == "hbm":
-        traffic = PMC_GATE_UP_TRAFFIC.get(args.config) if (args.layers, args.batch, args.zipf) == (None,) * 3 else None
         roofline = {"kernel": kernel, "bound": "hbm", "achieved": gu_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                    "frac": gu_gbps / HBM_PEAK_GBPS, "traffic": traffic, "avg_launch_ms": gu_avg_ms,
+                    "frac": gu_gbps / HBM_PEAK_GBPS, "traffic": None, "avg_launch_ms": gu_avg_ms,
                     "bytes_per_launch": gu_bytes_per_launch}
-        if traffic is not None:
-            roofline["traffic_source"] = "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE, profiles/gemm_decode64_pmc.md"
+        roofline.update(probe or {"traffic_source": "not measured (--no-traffic or --residual)"})
     else:
         flops = 2.0 * routes * (2 * INTER) * HIDDEN
         tflops = flops / (gu_avg_ms * 1e-3) / 1e12
         roofline = {"kernel": kernel, "bound": "mfma", "achieved": tflops, "peak": F16_MFMA_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": tflops / F16_MFMA_PEAK_TFLOPS, "traffic": None,
+                    "traffic_source": "not measured for the MFMA-bound workloads in bench.py",
+                    "frac_of_mxfp4_peak": tflops / MXFP4_MFMA_PEAK_TFLOPS, "mxfp4_peak": MXFP4_MFMA_PEAK_TFLOPS,
                     "avg_launch_ms": gu_avg_ms, "flops_per_launch": flops, "hbm_gbps": gu_gbps}
 
-    out0 = state[0]["out_dev"].cpu().numpy()
     result = {
         "metric": METRIC,
         "value": layer_tokens / (ms_step * 1e-3),
@@ -397,7 +540,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "mxfp4xq8->f32",
+        "dtype": "mxfp4 x residual-q8 (two integer dots per block) -> f32 holding bf16 values",
         "data": f"synthetic (seeded; random-init GPT-OSS-{'120B' if E == 128 else '20B'} MoE weights generated "
                 "on the device)",
         "config": {
@@ -423,8 +566,12 @@ def main() -> int:
             "steps": args.host_steps,
             "note": "GOSSMX_MEM_HOST calls: x and logits copied in, outputs copied out, synchronized per layer",
         }
+    bits_ok = True
     if not args.no_cpu_baseline and not args.residual:
-        result["cpu_baseline"] = cpu_baseline(cfg, x, state[0], out0, args.cpu_threads)
+        cb = cpu_baseline(cfg, x, state, args.cpu_threads)
+        result["cpu_baseline"] = cb
+        bits_ok = cb["gpu_bits_equal"] and cb["all_cores"]["bits_equal"] and cb["forced_lane"]["bits_equal"] and \
+            cb["last_layer_bits_equal"] is not False
     if graph is not None:
         graph.close()
     for st in state:
@@ -433,6 +580,9 @@ def main() -> int:
         st["dn"].close()
     ctx.close()
     print(json.dumps(result))
+    if not bits_ok:
+        print("GPU rows differ from the oracle's bits (cpu_baseline)", file=sys.stderr)
+        return 1
     return 0
 
 
