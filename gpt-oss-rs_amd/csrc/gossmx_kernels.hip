@@ -1540,9 +1540,6 @@ static_assert(kTinyMaxBlocks % kTinySuper == 0, "whole sets");
 
 __host__ __device__ constexpr int tiny_sets(int mp) { return kTinyMaxBlocks * mp / 8; }
 __host__ __device__ constexpr int tiny_image_bytes(int mp) { return tiny_sets(mp) * kTinySetBytes; }
-__host__ __device__ constexpr int tiny_lds_bytes(int mp) {
-  return tiny_image_bytes(mp) + tiny_sets(mp) * 64 + 4 * kTinyTermBufs * kTinyTermBytes;
-}
 
 // The geometry fields gemm_epilogue reads.
 struct GemmTinyCfg {
@@ -1567,21 +1564,36 @@ __device__ __forceinline__ void gemv_load(const GemvLoads& L, int q, u32x4& wn, 
   ws = __builtin_amdgcn_raw_buffer_load_b32(L.scl, L.vs, gi * 64, 0);
 }
 
-// The K loop of one wave for sets of P blocks (mp = 8 / P tokens), straight
-// line over all kTinyMaxBlocks blocks. Blocks past B contribute +0.0 terms,
-// which leave the running total unchanged (it is never -0.0). Their weights
-// are the last group's bytes (loads past the end are clamped to it) or the
-// plane slack: E2M1 codes and zeroed or stored scale bytes, all of which
-// convert to finite values, so the zero rows of the A operand keep every real
-// row exact (0 x finite = 0). With `fast` the conversion applies the tile's
-// scales (all in the exact range) and e8 is 1.0 (d * 1.0 is d); otherwise the
-// conversion is unscaled and e8 is e8m0_scale of the block.
+// The K loop of one wave over sets [S0, S1) of P blocks (mp = 8 / P tokens),
+// straight line, with a ring of R weight groups. Blocks past B contribute
+// +0.0 terms, which leave the running total unchanged (it is never -0.0).
+// Their weights are the last group's bytes (loads past the end are clamped
+// to it) or the plane slack: E2M1 codes and zeroed or stored scale bytes, all
+// of which convert to finite values, so the zero rows of the A operand keep
+// every real row exact (0 x finite = 0). With `fast` the conversion applies
+// the tile's scales (all in the exact range) and e8 is 1.0 (d * 1.0 is d);
+// otherwise the conversion is unscaled and e8 is e8m0_scale of the block.
+// STORE = false: set s's terms go to buffer s % kTinyTermBufs and the chain
+// of set s - 2 runs after set s is produced (its LDS round trip and adds
+// overlap the MFMAs of the sets in between). STORE = true: set s's terms go
+// to buffer s - S0 and no chain runs (another wave continues the chain).
 template <int P>
-__device__ __forceinline__ float gemv_sets(float tot, const GemvLoads& L, u32x4 (&wn)[tiny_ring(P)],
-                                           uint32_t (&ws)[tiny_ring(P)], const char* img, const float* scl,
-                                           float* terms, const int B, const int lane, const bool fast) {
-  constexpr int V = 16 / P, mp = 8 / P, R = tiny_ring(P);
-  constexpr int kSetsAll = kTinyMaxBlocks / P;
+__device__ __forceinline__ void gemv_chain_set(float& tot, const float* tb, const int n, const int t_read) {
+  constexpr int mp = 8 / P;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const float2 v = reinterpret_cast<const float2*>(tb)[(p * mp + t_read) * 16 + n];
+    tot = tot + v.x;
+    tot = tot + v.y;
+  }
+}
+
+template <int P, int R, int S0, int S1, bool STORE>
+__device__ __forceinline__ float gemv_sets(float tot, const GemvLoads& L, u32x4 (&wn)[R], uint32_t (&ws)[R],
+                                           const char* img, const float* scl, float* terms, const int B,
+                                           const int lane, const bool fast) {
+  constexpr int V = 16 / P, mp = 8 / P;
+  constexpr int G1 = S1 * P / 4;  // groups of this range end here
   const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
   const int G = lane >> 4, n = lane & 15;
   // A operand of MFMA p: lane (g = lane / 16, i = lane % 16) reads piece
@@ -1591,23 +1603,11 @@ __device__ __forceinline__ float gemv_sets(float tot, const GemvLoads& L, u32x4 
   for (int p = 0; p < P; ++p) off[p] = (n / V == p) ? (4 * n + G) * 16 : 1024;
   // Positions of this lane's result rows 4G, 4G+1 and 4G+2, 4G+3.
   const int pos_a = (4 * G) / V, pos_b = (4 * G + 2) / V;
-  // Chain lane 16 t + n reads entry p * mp + t of the term buffer (t past mp
+  // Chain lane 16 t + n reads entry p * mp + t of a term buffer (t past mp
   // folds onto a real token; its total is never stored).
   const int t_read = G & (mp - 1);
-  // Set s's terms go to buffer s % kTinyTermBufs; the chain of set s - 2
-  // runs after set s is produced, so its LDS round trip and the chain's adds
-  // overlap the MFMAs of the sets in between.
-  auto chain = [&](const int s) {
-    const float* tb = terms + (s % kTinyTermBufs) * (kTinyTermBytes / 4);
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const float2 v = reinterpret_cast<const float2*>(tb)[(p * mp + t_read) * 16 + n];
-      tot = tot + v.x;
-      tot = tot + v.y;
-    }
-  };
-#pragma unroll
-  for (int s = 0; s < kSetsAll; ++s) {
+  for (int s = S0; s < S1; ++s) {
     f32x4 d = zero;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -1635,7 +1635,7 @@ __device__ __forceinline__ float gemv_sets(float tot, const GemvLoads& L, u32x4 
     // Groups whose blocks are all converted take the group R ahead.
 #pragma unroll
     for (int q = (s * P) / 4; q < ((s + 1) * P) / 4; ++q)
-      if (q + R < kTinyGroups) gemv_load(L, q + R, wn[q % R], ws[q % R]);
+      if (q + R < G1) gemv_load(L, q + R, wn[q % R], ws[q % R]);
     const float4 sc = *reinterpret_cast<const float4*>(scl + s * 16 + 4 * G);
     // Terms of blocks past B become +0.0 by a bit mask (no branch).
     const uint32_t ma = s * P + pos_a < B ? ~0u : 0u, mb = s * P + pos_b < B ? ~0u : 0u;
@@ -1645,22 +1645,51 @@ __device__ __forceinline__ float gemv_sets(float tot, const GemvLoads& L, u32x4 
     t23.x = __uint_as_float(__float_as_uint((d[2] * e8b) * sc.z) & mb);
     t23.y = __uint_as_float(__float_as_uint((d[3] * e8b) * sc.w) & mb);
     // Rows 4G, 4G+1 are entry 2G, rows 4G+2, 4G+3 entry 2G+1 ([p][token]).
-    float* tb = terms + (s % kTinyTermBufs) * (kTinyTermBytes / 4);
+    float* tb = terms + (STORE ? s - S0 : s % kTinyTermBufs) * (kTinyTermBytes / 4);
     reinterpret_cast<float2*>(tb)[(2 * G) * 16 + n] = t01;
     reinterpret_cast<float2*>(tb)[(2 * G + 1) * 16 + n] = t23;
-    if (s >= 2) chain(s - 2);
+    if (!STORE && s >= S0 + 2)
+      gemv_chain_set<P>(tot, terms + ((s - 2) % kTinyTermBufs) * (kTinyTermBytes / 4), n, t_read);
   }
-  chain(kSetsAll - 2);
-  chain(kSetsAll - 1);
+  if (!STORE) {
+    gemv_chain_set<P>(tot, terms + ((S1 - 2) % kTinyTermBufs) * (kTinyTermBytes / 4), n, t_read);
+    gemv_chain_set<P>(tot, terms + ((S1 - 1) % kTinyTermBufs) * (kTinyTermBytes / 4), n, t_read);
+  }
   return tot;
 }
 
-template <int MODE, int P>
-__global__ __launch_bounds__(256, 2) void gemv_kernel(GemmArgs a) {
+// Geometry of a gemv_kernel launch: HALVES = 2 splits each tile's K range
+// over two waves (one token only): wave (half 0, tile t) produces and chains
+// the first half of the sets, wave (half 1, tile t) produces the second
+// half's terms into an LDS buffer, and after a barrier wave (0, t) continues
+// its chain through them; twice the waves keep the SIMDs busier where one
+// wave per SIMD would otherwise issue alone.
+template <int P, int HALVES>
+struct GemvGeom {
+  static constexpr int kMp = 8 / P;
+  static constexpr int kSets = kTinyMaxBlocks / P;
+  static constexpr int kHalfSets = kSets / HALVES;
+  static constexpr int kWaves = 4 * HALVES;
+  static constexpr int kThreads = 64 * kWaves;
+  // A half's first group is a multiple of the ring, so ring slots are
+  // compile-time in both halves.
+  static constexpr int kRing = HALVES == 2 ? 6 : tiny_ring(P);
+  // Per-wave term region: the chain's ring, or half 1's buffered sets.
+  static constexpr int kTermRegion = (HALVES == 2 ? (kHalfSets > kTinyTermBufs ? kHalfSets : kTinyTermBufs)
+                                                  : kTinyTermBufs) * kTinyTermBytes;
+  static constexpr int kLds = tiny_image_bytes(kMp) + tiny_sets(kMp) * 64 + kWaves * kTermRegion;
+  static_assert(kSets % HALVES == 0 && (kHalfSets * P) % 4 == 0, "halves end on whole groups");
+  static_assert(HALVES == 1 || ((kHalfSets * P) / 4) % kRing == 0, "a half starts on ring slot 0");
+};
+
+template <int MODE, int P, int HALVES>
+__global__ __launch_bounds__(64 * 4 * HALVES, 2) void gemv_kernel(GemmArgs a) {
   using C = GemmTinyCfg;
+  using Geo = GemvGeom<P, HALVES>;
   extern __shared__ __align__(16) char s_dyn[];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int half = wave >> 2, wt = wave & 3;  // K half, and the wave's tile within the work-group
   const int nl = lane & 15;
   int expert, start, count;
   if (MODE == kPlain) {
@@ -1676,9 +1705,9 @@ __global__ __launch_bounds__(256, 2) void gemv_kernel(GemmArgs a) {
     start = rec.y;
     count = rec.z;
   }
-  constexpr int mp = 8 / P, V = 2 * mp;  // every item of the launch holds at most mp tokens
+  constexpr int mp = Geo::kMp, V = 2 * mp;  // every item of the launch holds at most mp tokens
   const int rows = (int)a.w.rows, B = (int)a.w.blocks;
-  const int tile0 = blockIdx.x * C::kWaves + wave;
+  const int tile0 = blockIdx.x * C::kWaves + wt;
   const bool ok = tile0 < (int)a.w.tiles;
   const int safe_tile = ok ? tile0 : 0;  // tiles past the end stream tile 0 and discard it
   const int nq4 = (B + 3) >> 2;
@@ -1689,8 +1718,8 @@ __global__ __launch_bounds__(256, 2) void gemv_kernel(GemmArgs a) {
   float bias = 0.0f;
   if (a.bias != nullptr && ok && row < rows) bias = a.bias[(size_t)expert * a.bias_expert_stride + row];
 
-  // The first four weight groups, then the activation rows, then the rest of
-  // the ring: the weights need only the expert.
+  // The first four weight groups of the wave's range, then the activation
+  // rows, then the rest of the ring: the weights need only the expert.
   GemvLoads L;
   L.nib = buffer_rsrc(a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)safe_tile * 256 * B);
   L.scl = buffer_rsrc(a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)safe_tile * 64 * nq4);
@@ -1699,12 +1728,13 @@ __global__ __launch_bounds__(256, 2) void gemv_kernel(GemmArgs a) {
   L.vs = nl * 4;
   L.nq4 = nq4;
   L.nfull4 = B >> 2;
-  constexpr int R = tiny_ring(P);
+  constexpr int R = Geo::kRing;
+  const int g0 = HALVES == 2 ? half * (Geo::kHalfSets * P / 4) : 0;  // first group of the wave's range (slot 0)
   u32x4 wn[R];
   uint32_t ws[R];
   constexpr int kFirst = 4;
 #pragma unroll
-  for (int q = 0; q < kFirst; ++q) gemv_load(L, q, wn[q], ws[q]);
+  for (int q = 0; q < kFirst; ++q) gemv_load(L, g0 + q, wn[q], ws[q]);
 
   // Activation rows of the item's tokens (absent tokens read row 0: valid
   // memory whose products are never stored).
@@ -1715,8 +1745,8 @@ __global__ __launch_bounds__(256, 2) void gemv_kernel(GemmArgs a) {
 
   char* img = s_dyn;
   float* s_scl = reinterpret_cast<float*>(s_dyn + tiny_image_bytes(mp));
-  float* terms = reinterpret_cast<float*>(s_dyn + tiny_image_bytes(mp) + tiny_sets(mp) * 64) +
-                 wave * (kTinyTermBufs * kTinyTermBytes / 4);
+  float* term_base = reinterpret_cast<float*>(s_dyn + tiny_image_bytes(mp) + tiny_sets(mp) * 64);
+  float* terms = term_base + wave * (Geo::kTermRegion / 4);
   const int nsets = (B + P - 1) / P;
   const __amdgpu_buffer_rsrc_t act_codes = buffer_rsrc(a.actv), act_scl = buffer_rsrc(a.acts);
   {
@@ -1724,13 +1754,13 @@ __global__ __launch_bounds__(256, 2) void gemv_kernel(GemmArgs a) {
     // i % V), k-slice lane % 4.
     const int i = lane >> 2, g = lane & 3, v = i % V, t = v >> 1, part = v & 1;
     const int rt = t == 0 ? r[0] : (t == 1 ? r[1] : (t == 2 ? r[2] : r[3]));
-    for (int k = wave; k < nsets; k += C::kWaves) {  // uniform per wave
+    for (int k = wave; k < nsets; k += Geo::kWaves) {  // uniform per wave
       const int b = k * P + i / V;
       const int voff = (b < B && t < count) ? ((rt * B + b) * 2 + part) * 64 + g * 16 : 0;
       dma16(act_codes, img + k * kTinySetBytes, voff, 0);
     }
     // Scale f of the image: block f / (2 mp), token (f / 2) % mp, part f % 2.
-    for (int k = wave; k * 64 < nsets * 16; k += C::kWaves) {  // uniform per wave
+    for (int k = wave; k * 64 < nsets * 16; k += Geo::kWaves) {  // uniform per wave
       const int f = k * 64 + lane;
       const int b = f / (2 * mp), ts = (f >> 1) % mp, ps = f & 1;
       const int rs = ts == 0 ? r[0] : (ts == 1 ? r[1] : (ts == 2 ? r[2] : r[3]));
@@ -1738,9 +1768,10 @@ __global__ __launch_bounds__(256, 2) void gemv_kernel(GemmArgs a) {
       dma4(act_scl, reinterpret_cast<char*>(s_scl) + k * 256, voff, 0);
     }
   }
-  for (int k = tid; k < nsets; k += C::kThreads) *reinterpret_cast<u32x4*>(img + k * kTinySetBytes + 1024) = u32x4{};
+  for (int k = tid; k < nsets; k += Geo::kThreads)
+    *reinterpret_cast<u32x4*>(img + k * kTinySetBytes + 1024) = u32x4{};
 #pragma unroll
-  for (int q = kFirst; q < R; ++q) gemv_load(L, q, wn[q], ws[q]);
+  for (int q = kFirst; q < R; ++q) gemv_load(L, g0 + q, wn[q], ws[q]);
   // The DMA and the first groups have landed once at most the later groups'
   // loads are outstanding; then every wave's part is in.
   constexpr int kWait = 2 * (R - kFirst);
@@ -1749,7 +1780,22 @@ __global__ __launch_bounds__(256, 2) void gemv_kernel(GemmArgs a) {
   __syncthreads();
 
   float tot = bias + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
-  tot = gemv_sets<P>(tot, L, wn, ws, img, s_scl, terms, B, lane, fast);
+  if (HALVES == 1) {
+    tot = gemv_sets<P, R, 0, Geo::kSets, false>(tot, L, wn, ws, img, s_scl, terms, B, lane, fast);
+  } else if (half == 0) {
+    tot = gemv_sets<P, R, 0, Geo::kHalfSets, false>(tot, L, wn, ws, img, s_scl, terms, B, lane, fast);
+  } else {
+    gemv_sets<P, R, Geo::kHalfSets, Geo::kSets, true>(tot, L, wn, ws, img, s_scl, terms, B, lane, fast);
+  }
+  if (HALVES == 2) {
+    __syncthreads();  // the second half's terms are in LDS
+    if (half == 0) {
+      const float* tb2 = term_base + (wave + 4) * (Geo::kTermRegion / 4);
+      const int n = lane & 15, t_read = (lane >> 4) & (mp - 1);
+#pragma unroll
+      for (int s = 0; s < Geo::kHalfSets; ++s) gemv_chain_set<P>(tot, tb2 + s * (kTinyTermBytes / 4), n, t_read);
+    }
+  }
 
   // Lane 16 t + n holds (row n, token t); the epilogue's lane (G, n) holds
   // tokens 2G and 2G + 1.
@@ -1759,7 +1805,11 @@ __global__ __launch_bounds__(256, 2) void gemv_kernel(GemmArgs a) {
   acc[0][0][1] = __shfl(tot, ((2 * G + 1) * 16 + nl) & 63);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();  // every wave is done with the LDS image before the epilogue reuses it
-  gemm_epilogue<C, MODE, true>(a, acc, 1, count, start, tile0, reinterpret_cast<float*>(s_dyn));
+  if (half == 0) {
+    gemm_epilogue<C, MODE, true>(a, acc, 1, count, start, tile0, reinterpret_cast<float*>(s_dyn));
+  } else if (MODE == kGateUp) {
+    __syncthreads();  // gemm_epilogue's one barrier (gate_up), matched by the second half's waves
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -2250,22 +2300,24 @@ hipError_t launch_gemv(GemmMode mode, const GemmArgs& a, int rows_max, int grid_
   if (!a.residual) return hipErrorInvalidValue;
   const int mp_max = rows_max <= 1 ? 1 : (rows_max <= 2 ? 2 : 4);
   const dim3 grid((unsigned)((a.w.tiles + GemmTinyCfg::kWgTiles - 1) / GemmTinyCfg::kWgTiles), (unsigned)grid_work);
-  const dim3 block(GemmTinyCfg::kThreads);
-  const unsigned lds = (unsigned)tiny_lds_bytes(mp_max);
-  auto go = [&](auto kernel) {
-    if (start) hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, start, stop, 0, a);
-    else hipLaunchKernelGGL(kernel, grid, block, lds, stream, a);
+  auto go = [&](auto kernel, int threads, int lds) {
+    if (start) hipExtLaunchKernelGGL(kernel, grid, dim3(threads), (unsigned)lds, stream, start, stop, 0, a);
+    else hipLaunchKernelGGL(kernel, grid, dim3(threads), (unsigned)lds, stream, a);
   };
-  // Sets of P = 8 / mp_max blocks for every item of the launch.
+  // One token: sets of 8 blocks, each tile's K range over two waves; two
+  // tokens: sets of 4; three or four: sets of 2.
+  using G8 = GemvGeom<8, 2>;
+  using G4 = GemvGeom<4, 1>;
+  using G2 = GemvGeom<2, 1>;
   auto pick = [&](auto k8, auto k4, auto k2) {
-    if (mp_max == 1) go(k8);
-    else if (mp_max == 2) go(k4);
-    else go(k2);
+    if (mp_max == 1) go(k8, G8::kThreads, G8::kLds);
+    else if (mp_max == 2) go(k4, G4::kThreads, G4::kLds);
+    else go(k2, G2::kThreads, G2::kLds);
   };
   switch (mode) {
-    case kPlain: pick(gemv_kernel<kPlain, 8>, gemv_kernel<kPlain, 4>, gemv_kernel<kPlain, 2>); break;
-    case kGateUp: pick(gemv_kernel<kGateUp, 8>, gemv_kernel<kGateUp, 4>, gemv_kernel<kGateUp, 2>); break;
-    case kDown: pick(gemv_kernel<kDown, 8>, gemv_kernel<kDown, 4>, gemv_kernel<kDown, 2>); break;
+    case kPlain: pick(gemv_kernel<kPlain, 8, 2>, gemv_kernel<kPlain, 4, 1>, gemv_kernel<kPlain, 2, 1>); break;
+    case kGateUp: pick(gemv_kernel<kGateUp, 8, 2>, gemv_kernel<kGateUp, 4, 1>, gemv_kernel<kGateUp, 2, 1>); break;
+    case kDown: pick(gemv_kernel<kDown, 8, 2>, gemv_kernel<kDown, 4, 1>, gemv_kernel<kDown, 2, 1>); break;
   }
   return hipGetLastError();
 }
