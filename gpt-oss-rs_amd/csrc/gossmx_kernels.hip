@@ -623,71 +623,148 @@ __device__ __forceinline__ void select_quantize(const RouteArgs& r, int qwg) {
   }
 }
 
-// stable_top_k and the routing softmax of rows w, w + 16, ... by wave w of a
-// 1024-thread work-group (experts <= kMaxExperts): lane e holds the keys of
-// experts e and e + 64, and a key's rank is the number of larger keys among
-// all experts (keys are distinct, so ranks are too); ranks below K are the
-// selection in stable_top_k order. The softmax then follows
-// select_row_lanes's operations: max folded in rank order, each rank's
-// exponential, the sum folded in rank order from 0.0f.
-__device__ __forceinline__ void select_rows_ranked(const RouteArgs& r, const float* s_lg, int stride, int* s_sel,
-                                                   const uint64_t* tab) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int E = r.experts, K = r.top_k, M = r.m;
-  __shared__ uint64_t s_key[16][kMaxExperts];
-  __shared__ int s_pick[16][kMaxTopK];
-  __shared__ float s_ex[16][kMaxTopK];
-  for (int row = wave; row < M; row += 16) {  // uniform per wave
-    const float* lg = s_lg + row * stride;
-    const uint64_t k0 = lane < E ? route_key(lg[lane], lane) : 0;
-    const uint64_t k1 = lane + 64 < E ? route_key(lg[lane + 64], lane + 64) : 0;
-    s_key[wave][lane] = k0;
-    s_key[wave][lane + 64] = k1;
-    __builtin_amdgcn_wave_barrier();  // LDS of one wave is in order: the keys are in place
-    int r0 = 0, r1 = 0;
+// stable_top_k and the routing softmax of one row by one wave (experts <=
+// kMaxExperts): lane e holds the keys of experts e and e + 64, and a key's
+// rank is the number of larger keys among all experts (keys are distinct, so
+// ranks are too); ranks below K are the selection in stable_top_k order. The
+// softmax then follows select_row_lanes's operations: max folded in rank
+// order, each rank's exponential, the sum folded in rank order from 0.0f.
+// `ws`: this wave's LDS scratch (keys, picks, exponentials).
+struct RankScratch {
+  uint64_t key[kMaxExperts];
+  int pick[kMaxTopK];
+  float ex[kMaxTopK];
+};
+
+__device__ __forceinline__ void select_row_ranked(const RouteArgs& r, const float* lg, int row, int* s_sel,
+                                                  const uint64_t* tab, RankScratch& ws) {
+  const int lane = threadIdx.x & 63;
+  const int E = r.experts, K = r.top_k;
+  const uint64_t k0 = lane < E ? route_key(lg[lane], lane) : 0;
+  const uint64_t k1 = lane + 64 < E ? route_key(lg[lane + 64], lane + 64) : 0;
+  ws.key[lane] = k0;
+  ws.key[lane + 64] = k1;
+  __builtin_amdgcn_wave_barrier();  // LDS of one wave is in order: the keys are in place
+  int r0 = 0, r1 = 0;
 #pragma unroll 8
-    for (int f = 0; f < E; ++f) {
-      const uint64_t kf = s_key[wave][f];
-      r0 += kf > k0;
-      r1 += kf > k1;
-    }
-    if (lane < E && r0 < K) s_pick[wave][r0] = lane;
-    if (lane + 64 < E && r1 < K) s_pick[wave][r1] = lane + 64;
-    __builtin_amdgcn_wave_barrier();
-    float mx = -INFINITY;
-    for (int k = 0; k < K; ++k) mx = fmaxf(mx, lg[s_pick[wave][k]]);
-    const int my_e = s_pick[wave][lane < K ? lane : 0];
-    const float ex = expf_glibc(lg[my_e] - mx, tab);
-    if (lane < K) s_ex[wave][lane] = ex;
-    __builtin_amdgcn_wave_barrier();
-    float sum = 0.0f;
-    for (int k = 0; k < K; ++k) sum = sum + s_ex[wave][k];
-    if (lane < K) {
-      r.selected[(size_t)row * K + lane] = my_e;
-      r.weights[(size_t)row * K + lane] = bf16r(ex / sum);
-      s_sel[row * K + lane] = my_e;
-    }
-    __builtin_amdgcn_wave_barrier();  // the next row's key writes follow this row's reads
+  for (int f = 0; f < E; ++f) {
+    const uint64_t kf = ws.key[f];
+    r0 += kf > k0;
+    r1 += kf > k1;
   }
+  if (lane < E && r0 < K) ws.pick[r0] = lane;
+  if (lane + 64 < E && r1 < K) ws.pick[r1] = lane + 64;
+  __builtin_amdgcn_wave_barrier();
+  float mx = -INFINITY;
+  for (int k = 0; k < K; ++k) mx = fmaxf(mx, lg[ws.pick[k]]);
+  const int my_e = ws.pick[lane < K ? lane : 0];
+  const float ex = expf_glibc(lg[my_e] - mx, tab);
+  if (lane < K) ws.ex[lane] = ex;
+  __builtin_amdgcn_wave_barrier();
+  float sum = 0.0f;
+  for (int k = 0; k < K; ++k) sum = sum + ws.ex[k];
+  if (lane < K) {
+    r.selected[(size_t)row * K + lane] = my_e;
+    r.weights[(size_t)row * K + lane] = bf16r(ex / sum);
+    s_sel[row * K + lane] = my_e;
+  }
+  __builtin_amdgcn_wave_barrier();  // the next row's key writes follow this row's reads
+}
+
+// Selection and dispatch of m <= kFusedRouteRows rows by one wave, with no
+// work-group barrier (route_select_kernel's last router work-group). The
+// logits are read with device-scope atomic loads. Routes R = m * top_k and
+// every bucket holds at most m <= chunk routes, so each touched expert is one
+// partial work item, and dispatch_offsets's order reduces to descending size,
+// ties by expert. Route i of expert e goes to bucket_off[e] + #{j < i routed
+// to e} (stable_group_routes).
+__device__ __forceinline__ void select_dispatch_tiny(const RouteArgs& r, const DispatchArgs& d) {
+  const int lane = threadIdx.x & 63;
+  const int E = r.experts, K = r.top_k, M = r.m, R = M * K;
+  __shared__ float s_lg[kFusedRouteRows][kMaxExperts];
+  __shared__ int s_sel[kFusedRouteRows * kMaxTopK];
+  __shared__ int s_cnt[kMaxExperts], s_off[kMaxExperts], s_nz[kFusedRouteRows * kMaxTopK];
+  __shared__ uint64_t s_tab[32];
+  __shared__ RankScratch s_rank;
+  if (lane < 32) s_tab[lane] = kExp2Tab[lane];
+  for (int i = lane; i < M * E; i += 64) {
+    const float v = __hip_atomic_load(r.logits + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!isfinite(v)) atomicOr(r.err, kErrNonFiniteLogits);
+    s_lg[i / E][i % E] = v;
+  }
+  __builtin_amdgcn_wave_barrier();
+  for (int row = 0; row < M; ++row) select_row_ranked(r, s_lg[row], row, s_sel, s_tab, s_rank);
+  // Per-expert counts and their exclusive scan (experts lane and lane + 64).
+  int c0 = 0, c1 = 0;
+  for (int j = 0; j < R; ++j) {
+    const int e = s_sel[j];
+    c0 += e == lane;
+    c1 += e == lane + 64;
+  }
+  int i0 = c0, i1 = c1;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u0 = __shfl_up(i0, o), u1 = __shfl_up(i1, o);
+    if (lane >= o) {
+      i0 += u0;
+      i1 += u1;
+    }
+  }
+  const int total0 = __shfl(i0, 63);
+  const int off0 = i0 - c0, off1 = total0 + i1 - c1;
+  if (lane < E) {
+    s_cnt[lane] = c0;
+    s_off[lane] = off0;
+    d.bucket_off[lane] = off0;
+  }
+  if (lane + 64 < E) {
+    s_cnt[lane + 64] = c1;
+    s_off[lane + 64] = off1;
+    d.bucket_off[lane + 64] = off1;
+  }
+  if (lane == 0) d.bucket_off[E] = R;
+  // Touched experts in expert order (ballots over the two halves).
+  const unsigned long long m0 = __ballot(lane < E && c0 > 0), m1 = __ballot(lane + 64 < E && c1 > 0);
+  const unsigned long long below = (1ull << lane) - 1ull;
+  const int nz0 = __popcll(m0);
+  if (lane < E && c0 > 0) s_nz[__popcll(m0 & below)] = lane;
+  if (lane + 64 < E && c1 > 0) s_nz[nz0 + __popcll(m1 & below)] = lane + 64;
+  const int n_items = nz0 + __popcll(m1);
+  __builtin_amdgcn_wave_barrier();
+  // Route lane i: its rank among earlier routes of its expert, then its place.
+  if (lane < R) {
+    const int e = s_sel[lane];
+    int rank = 0;
+    for (int j = 0; j < lane; ++j) rank += s_sel[j] == e;
+    const int pos = s_off[e] + rank;
+    d.route_tok[pos] = lane / K;
+    d.route_slot[pos] = lane;
+  }
+  // Work item of touched expert lane (< n_items): records by descending
+  // size, ties by expert.
+  if (lane < n_items) {
+    const int e = s_nz[lane], c = s_cnt[e];
+    int before = 0;
+    for (int j = 0; j < n_items; ++j) {
+      const int f = s_nz[j], cf = s_cnt[f];
+      before += cf > c || (cf == c && f < e);
+    }
+    reinterpret_cast<int4*>(d.work)[before] = make_int4(e, s_off[e], c, 0);
+  }
+  if (lane == 0) *d.n_work = n_items;
 }
 
 // Top-k, softmax and dispatch of every row by one work-group of 1024 threads.
-// SMALL (route_select_kernel, m <= kFusedRouteRows): the logits were written
-// by other work-groups of this launch and are read with device-scope atomic
-// loads, and the selection is select_rows_ranked.
-template <bool SMALL>
 __device__ __forceinline__ void select_dispatch_body(const RouteArgs& r, const DispatchArgs& d) {
   const int tid = threadIdx.x;
   const int E = r.experts, K = r.top_k, M = r.m, stride = E + 1;
-  __shared__ float s_lg[SMALL ? kFusedRouteRows * (kMaxExperts + 1) : kSelectLds];
-  __shared__ int s_sel[SMALL ? kFusedRouteRows * kMaxTopK : kSelectMaxRoutes];
+  __shared__ float s_lg[kSelectLds];
+  __shared__ int s_sel[kSelectMaxRoutes];
   __shared__ uint64_t s_tab[32];
   if (tid < 32) s_tab[tid] = kExp2Tab[tid];
   for (int i = tid; i < M * E; i += 1024) {
     float v;
-    if (SMALL) {
-      v = __hip_atomic_load(r.logits + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else if (r.injected != nullptr) {
+    if (r.injected != nullptr) {
       v = bf16r(r.injected[i]);
       if (r.logits) r.logits[i] = v;
     } else {
@@ -703,8 +780,7 @@ __device__ __forceinline__ void select_dispatch_body(const RouteArgs& r, const D
   while (T > 1 && (T * M > 1024 || 4 * T > E)) T >>= 1;
   while (T < K) T <<= 1;
   const int rows_per_pass = 1024 / T;
-  if (SMALL) select_rows_ranked(r, s_lg, stride, s_sel, s_tab);
-  for (int base = 0; !SMALL && base < M; base += rows_per_pass) {  // uniform
+  for (int base = 0; base < M; base += rows_per_pass) {  // uniform
     // A row's T lanes share a wave: waves whose first row is past the batch
     // have nothing to select and skip (wave-uniform).
     if (base + (tid & ~63) / T >= M) continue;
@@ -724,7 +800,7 @@ __global__ __launch_bounds__(1024) void select_dispatch_kernel(RouteArgs r, Disp
     select_quantize(r, (int)blockIdx.x - 1);
     return;
   }
-  select_dispatch_body<false>(r, d);
+  select_dispatch_body(r, d);
 }
 
 // Router, selection and dispatch of a small batch (m <= kFusedRouteRows,
@@ -736,9 +812,9 @@ __global__ __launch_bounds__(1024) void select_dispatch_kernel(RouteArgs r, Disp
 // (cpu_runner.rs:2781-2783, 2829). Each work-group releases its logits
 // (device-scope release fence) and counts itself on `counter`; the last one
 // to arrive (it has seen every other count) reads them all with device-scope
-// atomic loads, resets the counter for the next launch and runs
-// select_dispatch_body. Work-groups past the experts quantize the gate_up
-// input (select_quantize).
+// atomic loads, resets the counter for the next launch and selects and
+// dispatches with one wave (select_dispatch_tiny). Work-groups past the
+// experts quantize the gate_up input (select_quantize).
 __global__ __launch_bounds__(1024) void route_select_kernel(RouteArgs r, DispatchArgs d, int* counter) {
   const int tid = threadIdx.x;
   const int E = r.experts, H = r.hidden, M = r.m;
@@ -814,7 +890,7 @@ __global__ __launch_bounds__(1024) void route_select_kernel(RouteArgs r, Dispatc
   __syncthreads();
   if (!s_last) return;
   if (tid == 0) atomicExch(counter, 0);
-  select_dispatch_body<true>(r, d);
+  if (tid < 64) select_dispatch_tiny(r, d);
 }
 
 // Selection and grouping of batches past the fused kernel's limits, in two
@@ -2249,9 +2325,9 @@ hipError_t launch_select_dispatch(const RouteArgs& r, const DispatchArgs& d, int
 }
 
 hipError_t launch_route_select(const RouteArgs& r, const DispatchArgs& d, int* counter, hipStream_t stream) {
+  // Every bucket must be one work item (at most m routes per expert).
   if (r.m < 1 || r.m > kFusedRouteRows || r.hidden > kFusedRouteHidden || r.hidden % 32 != 0 || r.injected != nullptr ||
-      r.m * (r.experts + 1) > kSelectLds || d.routes > kSelectMaxRoutes || r.top_k > kSelectTopK ||
-      r.experts > kMaxExperts)
+      r.top_k > kSelectTopK || r.experts > kMaxExperts || d.chunk < r.m || d.routes != r.m * r.top_k)
     return hipErrorInvalidValue;
   const size_t qblocks = r.quant ? (size_t)r.m * (r.hidden / kBlock) : 0;
   const unsigned grid = (unsigned)r.experts + (unsigned)((qblocks + kSelectQuantBlocks - 1) / kSelectQuantBlocks);
