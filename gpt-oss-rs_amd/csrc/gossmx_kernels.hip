@@ -483,6 +483,40 @@ __device__ __forceinline__ void dispatch_place(const DispatchArgs& a, const int*
   }
 }
 
+// The whole grouping in one work-group for at most kMaskRoutes routes (one
+// per thread): route i sets bit i of its expert's route mask in LDS; an
+// expert's count is its mask's popcount, and route i's place among its
+// expert's routes is the popcount of the mask's bits below i
+// (stable_group_routes's order), with no per-wave ballot loop.
+constexpr int kMaskRoutes = 1024;
+
+__device__ __forceinline__ void dispatch_body_masked(const DispatchArgs& a, const int* sel) {
+  const int tid = threadIdx.x, E = a.experts, R = a.routes;
+  const int nw = (R + 31) / 32;  // mask words in use
+  __shared__ uint32_t s_mask[kMaxExperts][kMaskRoutes / 32];
+  __shared__ int s_tot[kMaxExperts];
+  __shared__ int s_off[kMaxExperts];
+  for (int v = tid; v < E * nw; v += 1024) s_mask[v / nw][v % nw] = 0u;
+  __syncthreads();
+  const int e = tid < R ? sel[tid] : -1;
+  if (e >= 0) atomicOr(&s_mask[e][tid >> 5], 1u << (tid & 31));
+  __syncthreads();
+  if (tid < E) {
+    int c = 0;
+    for (int w = 0; w < nw; ++w) c += __popc(s_mask[tid][w]);
+    s_tot[tid] = c;
+  }
+  __syncthreads();
+  dispatch_offsets(a, s_tot, s_off, true);
+  if (e >= 0) {
+    int rank = __popc(s_mask[e][tid >> 5] & ((1u << (tid & 31)) - 1u));
+    for (int w = 0; w < (tid >> 5); ++w) rank += __popc(s_mask[e][w]);
+    const int pos = s_off[e] + rank;
+    a.route_tok[pos] = tid / a.top_k;
+    a.route_slot[pos] = tid;
+  }
+}
+
 // The whole grouping in one work-group; `sel` is the selected experts of
 // every route in route order (global memory or LDS).
 __device__ __forceinline__ void dispatch_body(const DispatchArgs& a, const int* sel) {
@@ -792,7 +826,8 @@ __device__ __forceinline__ void select_dispatch_body(const RouteArgs& r, const D
     select_row_lanes<kSelectTopK>(s_lg + rr * stride, has_row, j, T, E, K, sr, wr, s_sel + rr * K, s_tab);
   }
   __syncthreads();
-  dispatch_body(d, s_sel);
+  if (d.routes <= kMaskRoutes) dispatch_body_masked(d, s_sel);
+  else dispatch_body(d, s_sel);
 }
 
 __global__ __launch_bounds__(1024) void select_dispatch_kernel(RouteArgs r, DispatchArgs d) {
