@@ -161,6 +161,26 @@ def test_one_launch_routing_bit_exact_and_repeatable(ctx, experts, m):
     close(layer)
 
 
+@pytest.mark.parametrize("experts,top_k", [(40, 4), (7, 3), (100, 1), (128, 2)])
+def test_one_launch_routing_ties_and_signed_zeros(ctx, experts, top_k):
+    """Router weights of zero make every logit its bias: tied biases and
+    -0.0 / +0.0 force the ranked selection's tie rule (lower index first,
+    -0.0 equal to +0.0) for batches of 1..4 rows, against the oracle."""
+    host = O.synthetic_layer(33, experts, experts=experts, hidden=128, intermediate=64, top_k=top_k)
+    host.router_weight[:] = 0
+    rng = np.random.default_rng(experts)
+    bias = rng.choice(np.array([0.5, 0.25, -0.0, 0.0, -0.25], np.float32), experts)
+    bias[[1, experts - 2]] = 0.5  # ties at the top
+    host.router_bias[:] = bias
+    layer = gpu_layer(ctx, host)
+    for m in (1, 2, 3, 4):
+        x = O.gen_hidden(33, m, m, 128)
+        want = O.moe_batch(host, x)
+        assert want["status"] == O.OK
+        assert_moe_equal(layer.forward(x), want)
+    close(layer)
+
+
 CHECK_THREADS = min(16, os.cpu_count() or 1)
 
 
