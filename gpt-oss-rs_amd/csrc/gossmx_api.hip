@@ -189,14 +189,14 @@ struct OpScope {
   OpScope(gossmx_ctx* c, int o) : ctx(c), op(o) {
     if (ctx->profiling && !ctx->capturing) {
       start = take_event(ctx);
-      if (start) hipEventRecord(start, ctx->stream);
+      if (start) (void)hipEventRecord(start, ctx->stream);
     }
   }
   ~OpScope() {
     if (start) {
       hipEvent_t stop = take_event(ctx);
       if (stop) {
-        hipEventRecord(stop, ctx->stream);
+        (void)hipEventRecord(stop, ctx->stream);
         ctx->marks.push_back({op, start, stop});
       } else {
         ctx->event_pool.push_back(start);
@@ -336,9 +336,9 @@ int alloc_tiled(gossmx_ctx* ctx, size_t experts, size_t rows, size_t blocks, gos
                           ctx->stream);
   if (e == hipSuccess) e = launch_fill_tiled_padding(w->t, ctx->stream);
   if (e != hipSuccess) {
-    if (w->t.nib) hipFree(w->t.nib);
-    if (w->t.scl) hipFree(w->t.scl);
-    if (w->t.fast) hipFree(w->t.fast);
+    if (w->t.nib) (void)hipFree(w->t.nib);
+    if (w->t.scl) (void)hipFree(w->t.scl);
+    if (w->t.fast) (void)hipFree(w->t.fast);
     delete w;
     return hip_fail(e, "weights allocation");
   }
@@ -489,23 +489,23 @@ int gossmx_ctx_create(int device, void* stream, gossmx_ctx** out) {
 
 void gossmx_ctx_destroy(gossmx_ctx* ctx) {
   if (!ctx) return;
-  hipSetDevice(ctx->device);
-  if (ctx->stream) hipStreamSynchronize(ctx->stream);
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   for (auto& m : ctx->marks) {
-    hipEventDestroy(m.start);
-    hipEventDestroy(m.stop);
+    (void)hipEventDestroy(m.start);
+    (void)hipEventDestroy(m.stop);
   }
-  for (auto e : ctx->event_pool) hipEventDestroy(e);
+  for (auto e : ctx->event_pool) (void)hipEventDestroy(e);
   DevBuf* bufs[] = {&ctx->x, &ctx->injected, &ctx->logits, &ctx->selected, &ctx->weights, &ctx->act1v,
                     &ctx->act1s, &ctx->bucket, &ctx->route_tok, &ctx->route_slot, &ctx->work, &ctx->act2v,
                     &ctx->act2s, &ctx->y, &ctx->cnt, &ctx->normw, &ctx->next, &ctx->out,
                     &ctx->trace, &ctx->trace_gu, &ctx->trace_sw, &ctx->rec, &ctx->bias, &ctx->mout};
   for (DevBuf* b : bufs)
-    if (b->p) hipFree(b->p);
-  for (void* p : ctx->retired) hipFree(p);
-  if (ctx->err) hipFree(ctx->err);
-  if (ctx->sig_tab) hipFree(ctx->sig_tab);
-  if (ctx->own_stream && ctx->stream) hipStreamDestroy(ctx->stream);
+    if (b->p) (void)hipFree(b->p);
+  for (void* p : ctx->retired) (void)hipFree(p);
+  if (ctx->err) (void)hipFree(ctx->err);
+  if (ctx->sig_tab) (void)hipFree(ctx->sig_tab);
+  if (ctx->own_stream && ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
 
@@ -513,7 +513,7 @@ int gossmx_ctx_set_stream(gossmx_ctx* ctx, void* stream) {
   if (!ctx || !stream) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context or stream");
   HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
   if (int s = fold_profile(ctx)) return s;
-  if (ctx->own_stream) hipStreamDestroy(ctx->stream);
+  if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
   ctx->stream = static_cast<hipStream_t>(stream);
   ctx->own_stream = false;
   return GOSSMX_OK;
@@ -572,7 +572,7 @@ int gossmx_weights_upload(gossmx_ctx* ctx, const uint8_t* data, size_t len, size
   if (e == hipSuccess) e = launch_repack(static_cast<const uint8_t*>(staging), layout, w->t, ctx->stream);
   if (e == hipSuccess) e = launch_tile_flags(w->t, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-  if (staging) hipFree(staging);
+  if (staging) (void)hipFree(staging);
   if (e != hipSuccess) {
     gossmx_weights_destroy(w);
     return hip_fail(e, "weights upload");
@@ -606,7 +606,7 @@ int gossmx_weights_export(gossmx_ctx* ctx, const gossmx_weights* w, uint8_t* out
   hipError_t e = launch_export(w->t, static_cast<uint8_t*>(dev), ctx->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(out, dev, len, hipMemcpyDeviceToHost, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-  hipFree(dev);
+  (void)hipFree(dev);
   if (e != hipSuccess) return hip_fail(e, "weights export");
   return GOSSMX_OK;
 }
@@ -627,11 +627,11 @@ void gossmx_weights_destroy(gossmx_weights* w) {
   if (!w) return;
   // Work of any stream may still read the planes; the device-wide wait does
   // not need the context, which may already be gone.
-  hipSetDevice(w->device);
-  hipDeviceSynchronize();
-  if (w->t.nib) hipFree(w->t.nib);
-  if (w->t.scl) hipFree(w->t.scl);
-  if (w->t.fast) hipFree(w->t.fast);
+  (void)hipSetDevice(w->device);
+  (void)hipDeviceSynchronize();
+  if (w->t.nib) (void)hipFree(w->t.nib);
+  if (w->t.scl) (void)hipFree(w->t.scl);
+  if (w->t.fast) (void)hipFree(w->t.fast);
   delete w;
 }
 
@@ -787,12 +787,12 @@ int gossmx_layer_create(gossmx_ctx* ctx, const gossmx_moe_config* cfg, const uin
 
 void gossmx_layer_destroy(gossmx_layer* L) {
   if (!L) return;
-  hipSetDevice(L->device);
-  hipDeviceSynchronize();
-  if (L->router_w) hipFree(L->router_w);
-  if (L->router_b) hipFree(L->router_b);
-  if (L->gate_up_bias) hipFree(L->gate_up_bias);
-  if (L->down_bias) hipFree(L->down_bias);
+  (void)hipSetDevice(L->device);
+  (void)hipDeviceSynchronize();
+  if (L->router_w) (void)hipFree(L->router_w);
+  if (L->router_b) (void)hipFree(L->router_b);
+  if (L->gate_up_bias) (void)hipFree(L->gate_up_bias);
+  if (L->down_bias) (void)hipFree(L->down_bias);
   delete L;
 }
 
@@ -1160,12 +1160,12 @@ int gossmx_graph_launch(gossmx_ctx* ctx, const gossmx_graph* g) {
 
 void gossmx_graph_destroy(gossmx_graph* g) {
   if (!g) return;
-  hipSetDevice(g->device);
-  if (g->ctx) hipStreamSynchronize(g->ctx->stream);  // no replay still reads its buffers
-  if (g->exec) hipGraphExecDestroy(g->exec);
-  if (g->graph) hipGraphDestroy(g->graph);
+  (void)hipSetDevice(g->device);
+  if (g->ctx) (void)hipStreamSynchronize(g->ctx->stream);  // no replay still reads its buffers
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
   if (g->ctx && --g->ctx->live_graphs == 0) {
-    for (void* p : g->ctx->retired) hipFree(p);
+    for (void* p : g->ctx->retired) (void)hipFree(p);
     g->ctx->retired.clear();
   }
   delete g;
@@ -1195,7 +1195,7 @@ static int run_selftest(gossmx_ctx* ctx, bool* scaled_ok) {
   if (e == hipSuccess) e = hipMemcpyAsync(host.data(), dev, kSelftestFloats * sizeof(float), hipMemcpyDeviceToHost,
                                           ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-  hipFree(dev);
+  (void)hipFree(dev);
   if (e != hipSuccess) return hip_fail(e, "selftest");
   const float codes[16] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f,
                            -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};

@@ -1066,8 +1066,6 @@ __device__ __forceinline__ float e8m0_select(uint32_t s) {
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
-constexpr int kGemmMaxThreads = 512;        // largest GEMM work-group (8 waves)
-
 // Geometry of one GEMM instantiation. TILES 16-row weight tiles per wave,
 // work items of NTOK activation rows (NTOK / 8 MFMA token groups), K steps of
 // GROUPS 4-block groups, WAVES waves per work-group, and MIN_WAVES waves per
@@ -1354,7 +1352,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& t
     for (int i = 0; i < kPer; ++i) {
       const int item = hw + i * kHalfWaves;
       const int c = item / kBlocksPerWg, h = item % kBlocksPerWg;
-      live[i] = item < count * kBlocksPerWg && blockIdx.x * kBlocksPerWg + h < blocks_next;  // uniform per half wave
+      live[i] = item < count * kBlocksPerWg && (int)blockIdx.x * kBlocksPerWg + h < blocks_next;  // uniform per half wave
       v[i] = live[i] ? s_act[c * kActStride + h * kBlock + l32] : 0.0f;
       if (live[i] && !isfinite(v[i])) atomicOr(a.err, kErrNonFiniteInput);
     }
@@ -1638,8 +1636,6 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
 // activation scales [block][token][part] f32 (the 16 scales of set s at
 // 16 s); kTinyTermBufs term buffers of 1 KiB per wave.
 
-constexpr int kTinyGroups = kTinyMaxBlocks / 4;
-constexpr int kTinySuper = 8;  // blocks per set at one token
 // Weight groups in flight per wave (measured at one token: 8 and 16 groups
 // run alike, the whole K range at once is slower); fewer at four tokens,
 // whose sets hold more operands in registers.
@@ -1647,7 +1643,7 @@ __host__ __device__ constexpr int tiny_ring(int P) { return P == 2 ? 12 : 16; }
 constexpr int kTinySetBytes = 1024 + 16;                        // a set's 64 pieces and its zero piece
 constexpr int kTinyTermBytes = 1024;                            // [8 (position, token)][16 rows][2] f32
 constexpr int kTinyTermBufs = 4;                                // term buffers per wave (the chain lags 2 sets)
-static_assert(kTinyMaxBlocks % kTinySuper == 0, "whole sets");
+static_assert(kTinyMaxBlocks % 8 == 0, "whole sets at one token (8 blocks per set)");
 
 __host__ __device__ constexpr int tiny_sets(int mp) { return kTinyMaxBlocks * mp / 8; }
 __host__ __device__ constexpr int tiny_image_bytes(int mp) { return tiny_sets(mp) * kTinySetBytes; }
