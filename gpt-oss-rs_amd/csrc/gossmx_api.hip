@@ -996,6 +996,9 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   d.y = ybuf;
   d.trace_gu = d.trace_sw = nullptr;
   d.xin = g.act_next16;
+  // One row with at most four routes (one route per work item): the down
+  // projection's work-groups also run the combine.
+  const bool down_combine = proj != GOSSMX_PROJECTION_EXACT_BF16 && m == 1 && K <= 4 && use_gemv(m, B2, d.residual != 0);
   if (proj == GOSSMX_PROJECTION_EXACT_BF16) {
     {
       OpScope sc(ctx, GOSSMX_OP_GATE_UP);
@@ -1015,13 +1018,16 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
     }
     {
       KernelScope sc(ctx, GOSSMX_OP_DOWN);
-      if (use_gemv(m, B2, d.residual != 0))
+      if (down_combine)
+        HIP_TRY(launch_down_combine(d, weights, (int)K, output, trace, resid, next, ctx->stream, sc.start, sc.stop),
+                "down/combine launch");
+      else if (use_gemv(m, B2, d.residual != 0))
         HIP_TRY(launch_gemv(kDown, d, (int)m, (int)max_work, ctx->stream, sc.start, sc.stop), "down launch");
       else
         HIP_TRY(launch_gemm(kDown, d, chunk, (int)max_work, ctx->stream, sc.start, sc.stop), "down launch");
     }
   }
-  {
+  if (!down_combine) {
     OpScope sc(ctx, GOSSMX_OP_WEIGHTING);
     HIP_TRY(launch_combine(d.y, weights, (int)m, (int)K, (int)H, output, trace, resid, next, ctx->stream),
             "combine launch");

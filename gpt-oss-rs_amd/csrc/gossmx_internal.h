@@ -176,6 +176,13 @@ hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream);
 // to hold at most rows_max <= kTinyMaxRows rows and blocks <= kTinyMaxBlocks.
 hipError_t launch_gemv(GemmMode mode, const GemmArgs& a, int rows_max, int grid_work, hipStream_t stream,
                        hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+// Down projection + weighted combine of a one-row batch (residual-Q8, every
+// work item one route, top_k <= 4, blocks <= kTinyMaxBlocks): the outputs of
+// launch_gemv(kDown) followed by launch_combine with m = 1, without the y
+// buffer (d.y is not written).
+hipError_t launch_down_combine(const GemmArgs& d, const float* weights, int top_k, float* out, float* trace_down,
+                               const uint16_t* resid, uint16_t* next, hipStream_t stream,
+                               hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 // Exact-BF16 expert projection over the work list (mode kGateUp or kDown);
 // chunk <= kChunkMax.
 hipError_t launch_exact(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream);

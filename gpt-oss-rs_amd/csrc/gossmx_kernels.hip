@@ -1920,6 +1920,138 @@ __global__ __launch_bounds__(64 * 4 * HALVES, 2) void gemv_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Down projection and weighted combine of a one-row batch in one launch
+// (cpu_runner.rs:2933-2947 then :2959-2999 at m = 1). The row's top_k routes
+// go to top_k distinct experts, so the work list holds top_k items of one
+// route each. Work-group x covers 16-row tile x of the down output for every
+// item: wave (k, half) streams item k's expert over half of the K range
+// exactly as gemv_kernel<kDown, 8, 2> does (sets of 8 blocks, half 1's terms
+// buffered in LDS, half 0 continuing the ordered chain through them), from
+// item k's own activation image. The bf16 outputs of the items then meet in
+// LDS by rank, and 16 lanes run the combine of the tile's rows in rank order
+// from 0.0 (and the residual add), so no other launch reads them back.
+struct DownCombineGeom {
+  using Geo = GemvGeom<8, 2>;
+  static constexpr int kItems = 4;                         // routes of the row (top_k <= 4)
+  static constexpr int kWaves = 2 * kItems;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kImage = tiny_image_bytes(1);       // one item's activation sets
+  static constexpr int kScl = tiny_sets(1) * 64;           // one item's activation scales
+  static constexpr int kLds = kItems * (kImage + kScl) + kWaves * Geo::kTermRegion + kItems * kTileRows * 4;
+  static_assert(kLds <= 160 * 1024, "LDS of one work-group");
+};
+
+struct CombineArgs {
+  const float* weights;    // [top_k] routing weights by rank
+  int top_k;
+  float* out;              // [rows] f32 (bf16 values), or null
+  float* trace;            // [top_k][rows] down outputs by rank, or null
+  const uint16_t* resid;   // [rows] bf16 residual stream, or null
+  uint16_t* next;          // [rows] bf16(resid + out), or null
+};
+
+__global__ __launch_bounds__(DownCombineGeom::kThreads, 2) void gemv_down_combine_kernel(GemmArgs a, CombineArgs c) {
+  using DC = DownCombineGeom;
+  using Geo = DC::Geo;
+  constexpr int P = 8, V = 2, R = Geo::kRing;
+  __shared__ __align__(16) char s_img[DC::kItems * DC::kImage];
+  __shared__ __align__(16) float s_scl[DC::kItems * DC::kScl / 4];
+  __shared__ __align__(16) float s_terms[DC::kWaves * Geo::kTermRegion / 4];
+  __shared__ float s_y[DC::kItems * kTileRows];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int item = wave & 3, half = wave >> 2;
+  const int nl = lane & 15;
+  const int rows = (int)a.w.rows, B = (int)a.w.blocks;
+  const int tile = blockIdx.x;
+  const int row = tile * kTileRows + nl;
+  const int nw = *a.n_work;
+  const bool live = item < nw;  // uniform per wave
+  int expert = 0, start = 0, slot = 0;
+  if (live) {
+    const int4 rec = reinterpret_cast<const int4*>(a.work)[item];
+    expert = rec.x;
+    start = rec.y;
+    slot = a.route_slot[start];  // = rank (one row)
+  }
+  if (tid < DC::kItems * kTileRows) s_y[tid] = 0.0f;
+  const int nq4 = (B + 3) >> 2;
+  const bool fast = live && a.fast_ok && a.w.fast[(size_t)expert * a.w.tiles + tile] != 0;
+  float bias = 0.0f;
+  if (live && a.bias != nullptr && row < rows) bias = a.bias[(size_t)expert * a.bias_expert_stride + row];
+
+  GemvLoads L;
+  L.nib = buffer_rsrc(a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)tile * 256 * B);
+  L.scl = buffer_rsrc(a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)tile * 64 * nq4);
+  L.vl = lane * 16;
+  L.vl_tail = lane * (B & 3) * 4;
+  L.vs = nl * 4;
+  L.nq4 = nq4;
+  L.nfull4 = B >> 2;
+  const int g0 = half * (Geo::kHalfSets * P / 4);
+  u32x4 wn[R];
+  uint32_t ws[R];
+  constexpr int kFirst = 4;
+  char* img = s_img + item * DC::kImage;
+  float* scl = s_scl + item * (DC::kScl / 4);
+  float* terms = s_terms + wave * (Geo::kTermRegion / 4);
+  const int nsets = (B + P - 1) / P;
+  if (live) {
+#pragma unroll
+    for (int q = 0; q < kFirst; ++q) gemv_load(L, g0 + q, wn[q], ws[q]);
+    // The item's image: the two waves of the item take alternate sets. Piece
+    // `lane` of a set: row i = lane / 4 (block i / 2, part i % 2), k-slice lane % 4.
+    const __amdgpu_buffer_rsrc_t act_codes = buffer_rsrc(a.actv), act_scl = buffer_rsrc(a.acts);
+    const int i = lane >> 2, g = lane & 3, part = i & 1;
+    for (int k = half; k < nsets; k += 2) {
+      const int b = k * P + i / V;
+      dma16(act_codes, img + k * kTinySetBytes, b < B ? ((start * B + b) * 2 + part) * 64 + g * 16 : 0, 0);
+    }
+    // Scale f of the image: block f / 2, part f % 2.
+    for (int k = half; k * 64 < nsets * 16; k += 2) {
+      const int f = k * 64 + lane, b = f >> 1;
+      dma4(act_scl, reinterpret_cast<char*>(scl) + k * 256, b < B ? ((start * B + b) * 2 + (f & 1)) * 4 : 0, 0);
+    }
+    if (half == 0)
+      for (int k = lane; k < nsets; k += 64) *reinterpret_cast<u32x4*>(img + k * kTinySetBytes + 1024) = u32x4{};
+#pragma unroll
+    for (int q = kFirst; q < R; ++q) gemv_load(L, g0 + q, wn[q], ws[q]);
+  }
+  constexpr int kWait = 2 * (R - kFirst);
+  __builtin_amdgcn_s_waitcnt((kWait & 15) | ((kWait >> 4) << 14) | (7 << 4) | (15 << 8));
+  __syncthreads();
+
+  float tot = bias + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
+  if (live) {
+    if (half == 0)
+      tot = gemv_sets<P, R, 0, Geo::kHalfSets, false>(tot, L, wn, ws, img, scl, terms, B, lane, fast);
+    else
+      gemv_sets<P, R, Geo::kHalfSets, Geo::kSets, true>(tot, L, wn, ws, img, scl, terms, B, lane, fast);
+  }
+  __syncthreads();  // the second halves' terms are in LDS
+  if (live && half == 0) {
+    const float* tb2 = s_terms + (wave + 4) * (Geo::kTermRegion / 4);
+#pragma unroll
+    for (int s = 0; s < Geo::kHalfSets; ++s) gemv_chain_set<P>(tot, tb2 + s * (kTinyTermBytes / 4), nl, 0);
+    // Lane n < 16 holds (row n, the item's one token): the down output in bf16
+    // (cpu_runner.rs:2945-2947).
+    const float yv = bf16r(tot);
+    if (lane < kTileRows && slot < DC::kItems) {
+      s_y[slot * kTileRows + nl] = yv;
+      if (c.trace != nullptr && row < rows) c.trace[(size_t)slot * rows + row] = yv;
+    }
+  }
+  __syncthreads();
+  if (tid < kTileRows && row < rows) {
+    float acc = 0.0f;
+    for (int k = 0; k < c.top_k; ++k) acc = acc + s_y[k * kTileRows + nl] * c.weights[k];
+    const float o = bf16r(acc);
+    if (c.out != nullptr) c.out[row] = o;
+    if (c.next != nullptr) c.next[row] = bf16_bits(bf16_to_f32(c.resid[row]) + o);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Exact-BF16 expert projection (CpuExpertProjection::ExactBf16; project_mxfp4,
 // cpu_runner.rs:3497-3519): per output, total = bias; total += the 16 lane
 // sums folded 0..15 from -0.0. Lane l sums bf16(decode(code) * e8m0) * x over
@@ -2426,6 +2558,19 @@ hipError_t launch_gemv(GemmMode mode, const GemmArgs& a, int rows_max, int grid_
     case kGateUp: pick(gemv_kernel<kGateUp, 8, 2>, gemv_kernel<kGateUp, 4, 1>, gemv_kernel<kGateUp, 2, 1>); break;
     case kDown: pick(gemv_kernel<kDown, 8, 2>, gemv_kernel<kDown, 4, 1>, gemv_kernel<kDown, 2, 1>); break;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_down_combine(const GemmArgs& d, const float* weights, int top_k, float* out, float* trace_down,
+                               const uint16_t* resid, uint16_t* next, hipStream_t stream, hipEvent_t start,
+                               hipEvent_t stop) {
+  if (d.w.blocks > (size_t)kTinyMaxBlocks || !d.residual || top_k < 1 || top_k > DownCombineGeom::kItems ||
+      (next != nullptr && resid == nullptr))
+    return hipErrorInvalidValue;
+  CombineArgs c{weights, top_k, out, trace_down, resid, next};
+  const dim3 grid((unsigned)d.w.tiles), block(DownCombineGeom::kThreads);
+  if (start) hipExtLaunchKernelGGL(gemv_down_combine_kernel, grid, block, 0, stream, start, stop, 0, d, c);
+  else hipLaunchKernelGGL(gemv_down_combine_kernel, grid, block, 0, stream, d, c);
   return hipGetLastError();
 }
 

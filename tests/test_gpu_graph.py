@@ -10,10 +10,11 @@ import oracle as O
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("m", [3, 12])
+@pytest.mark.parametrize("m", [1, 3, 12])
 def test_captured_forward_replays_match_eager_and_oracle(m):
-    """m = 3 takes the one-launch router/selection kernel, whose arrival
-    counter must be back at zero after every launch, eager or replayed."""
+    """m = 1 and 3 take the one-launch router/selection kernel, whose arrival
+    counter must be back at zero after every launch, eager or replayed; m = 1
+    also the down projection with the combine in the same launch."""
     with G.Context(0) as ctx:
         E, H, I, K = 8, 128, 64, 4
         host = O.synthetic_layer(21, 0, experts=E, hidden=H, intermediate=I, top_k=K)

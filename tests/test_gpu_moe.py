@@ -53,7 +53,8 @@ def assert_moe_equal(got, want):
 
 
 @pytest.mark.parametrize("experts,hidden,inter,top_k,m", [(3, 64, 32, 2, 2), (4, 96, 64, 2, 5), (8, 128, 96, 4, 17),
-                                                           (32, 256, 128, 4, 70)])
+                                                           (32, 256, 128, 4, 70), (3, 64, 32, 2, 1),
+                                                           (8, 160, 96, 4, 1), (6, 96, 320, 3, 1)])
 def test_small_layers_bit_exact(ctx, experts, hidden, inter, top_k, m):
     host = O.synthetic_layer(11, 0, experts=experts, hidden=hidden, intermediate=inter, top_k=top_k)
     x = O.gen_hidden(11, 100, m, hidden)
@@ -72,7 +73,8 @@ PROJECTIONS = [G.PROJECTION_RESIDUAL_Q8, G.PROJECTION_Q8, G.PROJECTION_EXACT_BF1
 @pytest.mark.parametrize("projection", PROJECTIONS, ids=["residual-q8", "q8", "exact-bf16"])
 @pytest.mark.parametrize("experts,hidden,inter,top_k,m,inject", [(4, 96, 64, 2, 5, False), (8, 128, 96, 4, 17, True),
                                                                   (32, 256, 128, 4, 70, False),
-                                                                  (32, 64, 64, 4, 600, True)])
+                                                                  (32, 64, 64, 4, 600, True),
+                                                                  (8, 128, 96, 4, 1, False), (5, 96, 64, 3, 1, True)])
 def test_projection_modes_bit_exact_with_traces(ctx, projection, experts, hidden, inter, top_k, m, inject):
     """Every CpuExpertProjection (cpu_runner.rs:49-90) against the oracle's
     moe_batch in the same mode: outputs, routing and the gate_up / SwiGLU /
@@ -405,10 +407,12 @@ def test_scratch_requirement_is_none_and_selftest_passes(ctx):
 def test_profiler_counts_every_stage(ctx):
     """Every stage is timed once per call. Batches of at most 4 rows with a
     computed router run the router, selection and dispatch as one launch,
-    counted under router_routing (dispatch then has no launch of its own)."""
+    counted under router_routing (dispatch then has no launch of its own);
+    one-row batches also run the combine inside the down launch (weighting
+    has none)."""
     host = O.synthetic_layer(9, 0, experts=4, hidden=64, intermediate=32, top_k=2)
     layer = gpu_layer(ctx, host)
-    for m, fused in ((12, False), (4, True)):
+    for m, fused in ((12, False), (4, True), (1, True)):
         x = O.gen_hidden(9, 1, m, 64)
         ctx.profile(True)
         ctx.profile_reset()
@@ -417,8 +421,8 @@ def test_profiler_counts_every_stage(ctx):
         rec = ctx.profile_read()
         ctx.profile(False)
         for op in ("router_routing", "dispatch", "gate_up", "down", "weighting"):
-            if fused and op == "dispatch":
-                assert rec[op]["launches"] == 0
+            if (fused and op == "dispatch") or (m == 1 and op == "weighting"):
+                assert rec[op]["launches"] == 0, (m, op)
             else:
                 assert rec[op]["launches"] == 3 and rec[op]["total_ms"] > 0.0, (m, op)
     close(layer)
