@@ -946,7 +946,15 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   // Small batches with a computed router: router, selection and dispatch in
   // one launch (the route counter is the second int of the flags buffer).
   const bool route_fused = injected == nullptr && fused && m <= (size_t)kFusedRouteRows && H <= (size_t)kFusedRouteHidden;
-  if (route_fused) {
+  // One row (no gate_up / SwiGLU traces): a launch for the logits and the
+  // input quantization, then every gate_up work-group selects for itself in
+  // the gate_up launch.
+  const bool route_gemv = route_fused && m == 1 && E <= (size_t)kRouteGemvExperts && K <= (size_t)kSelectTopK &&
+                          proj == GOSSMX_PROJECTION_RESIDUAL_Q8 && use_gemv(m, B1, true) && !trace_gu && !trace_sw;
+  if (route_gemv) {
+    OpScope sc(ctx, GOSSMX_OP_ROUTER_ROUTING);
+    HIP_TRY(launch_route_logits(ra, ctx->stream), "router launch");
+  } else if (route_fused) {
     OpScope sc(ctx, GOSSMX_OP_ROUTER_ROUTING);
     HIP_TRY(launch_route_select(ra, da, ctx->err + 1, ctx->stream), "route/select launch");
   } else if (injected == nullptr) {
@@ -1011,7 +1019,9 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   } else {
     {
       KernelScope sc(ctx, GOSSMX_OP_GATE_UP);
-      if (use_gemv(m, B1, g.residual != 0))
+      if (route_gemv)
+        HIP_TRY(launch_route_gemv(ra, da, g, ctx->stream, sc.start, sc.stop), "route/gate_up launch");
+      else if (use_gemv(m, B1, g.residual != 0))
         HIP_TRY(launch_gemv(kGateUp, g, (int)m, (int)max_work, ctx->stream, sc.start, sc.stop), "gate_up launch");
       else
         HIP_TRY(launch_gemm(kGateUp, g, chunk, (int)max_work, ctx->stream, sc.start, sc.stop), "gate_up launch");

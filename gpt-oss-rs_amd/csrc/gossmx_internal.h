@@ -144,6 +144,8 @@ constexpr int kSelectTopK = 4;          // top_k (GPT-OSS routes to 4 experts)
 // the selection and the dispatch (route_select_kernel).
 constexpr int kFusedRouteRows = 4;
 constexpr int kFusedRouteHidden = 4096;
+// One-row batches select inside the gate_up launch up to this many experts.
+constexpr int kRouteGemvExperts = kMaxExperts;
 
 // Launchers (gossmx_kernels.hip). All are asynchronous on `stream`.
 // Router logits (bf16-rounded, into a.logits) and the gate_up input
@@ -176,6 +178,17 @@ hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream);
 // to hold at most rows_max <= kTinyMaxRows rows and blocks <= kTinyMaxBlocks.
 hipError_t launch_gemv(GemmMode mode, const GemmArgs& a, int rows_max, int grid_work, hipStream_t stream,
                        hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+// Router logits of m <= kFusedRouteRows rows only (route_select_kernel
+// without its arrival counter), and the gate_up input quantization when
+// r.quant.
+hipError_t launch_route_logits(const RouteArgs& r, hipStream_t stream);
+// Selection, dispatch and gate_up GEMV of a one-row batch in one launch,
+// after launch_route_logits with r.quant (computed router, experts <=
+// kRouteGemvExperts, top_k <= 4, residual-Q8, hidden <= kTinyMaxBlocks * 32,
+// no gate_up / SwiGLU traces): the outputs of launch_route_select followed by
+// launch_gemv(kGateUp).
+hipError_t launch_route_gemv(const RouteArgs& r, const DispatchArgs& d, const GemmArgs& g, hipStream_t stream,
+                             hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 // Down projection + weighted combine of a one-row batch (residual-Q8, every
 // work item one route, top_k <= 4, blocks <= kTinyMaxBlocks): the outputs of
 // launch_gemv(kDown) followed by launch_combine with m = 1, without the y

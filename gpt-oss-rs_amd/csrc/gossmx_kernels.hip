@@ -26,6 +26,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
 // Scalar helpers.
@@ -849,7 +850,8 @@ __global__ __launch_bounds__(1024) void select_dispatch_kernel(RouteArgs r, Disp
 // to arrive (it has seen every other count) reads them all with device-scope
 // atomic loads, resets the counter for the next launch and selects and
 // dispatches with one wave (select_dispatch_tiny). Work-groups past the
-// experts quantize the gate_up input (select_quantize).
+// experts quantize the gate_up input (select_quantize). With a null counter
+// the launch writes the logits only.
 __global__ __launch_bounds__(1024) void route_select_kernel(RouteArgs r, DispatchArgs d, int* counter) {
   const int tid = threadIdx.x;
   const int E = r.experts, H = r.hidden, M = r.m;
@@ -918,8 +920,9 @@ __global__ __launch_bounds__(1024) void route_select_kernel(RouteArgs r, Dispatc
     float sum = s_chain[tid][0];
     for (int j = 1; j < 16; ++j) sum = sum + s_chain[tid][j];
     r.logits[(size_t)tid * E + e] = bf16r(sum + r.router_b[e]);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // this row's logit reaches device scope before the count
+    if (counter != nullptr) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // the logit reaches device scope before the count
   }
+  if (counter == nullptr) return;  // logits only (route_gemv_kernel selects in the next launch)
   __syncthreads();
   if (tid == 0) s_last = atomicAdd(counter, 1) == E - 1;
   __syncthreads();
@@ -2052,6 +2055,203 @@ __global__ __launch_bounds__(DownCombineGeom::kThreads, 2) void gemv_down_combin
 }
 
 // ---------------------------------------------------------------------------
+// Selection, dispatch and the gate_up GEMV of a one-row batch in one launch
+// (the moe_batch routing loop, cpu_runner.rs:2808-2889, and the gate_up
+// projection with SwiGLU, :2893-2919, at m = 1), after route_select_kernel
+// has written the row's bf16 logits and quantized the row (launched without
+// its arrival counter). Every work-group selects for itself, so that no
+// cross-work-group signal or serial selection step separates the logits from
+// the weight stream: the activation image's DMA (the row does not depend on
+// the selection) and the logits are requested first; wave 0 ranks the keys
+// (stable_top_k, :3768-3778; experts e and e + 64 per lane, the keys read
+// 16 at a time from LDS); the selected experts in increasing index are the
+// work items (every bucket holds one route, so dispatch_offsets's order is
+// expert order). Work-group (x, y) then runs gemv_kernel<kGateUp, 8, 2>'s
+// tile group x for item y. Work-group (0, 0) also writes what the selection
+// kernels write for the down launch and the caller: the selection, the
+// softmax weights (select_row_ranked's operations), bucket offsets, route
+// order and the work list, and the non-finite flag.
+struct RouteGemvGeom {
+  using Geo = GemvGeom<8, 2>;
+  static constexpr int kThreads = Geo::kThreads;
+  static constexpr int kLds = Geo::kLds;
+};
+
+__global__ __launch_bounds__(RouteGemvGeom::kThreads, 4) void route_gemv_kernel(RouteArgs r, DispatchArgs d,
+                                                                                 GemmArgs a) {
+  using C = GemmTinyCfg;
+  using RG = RouteGemvGeom;
+  using Geo = RG::Geo;
+  constexpr int P = 8, V = 2, R = Geo::kRing;
+  __shared__ __align__(16) char s_dyn[RG::kLds];
+  __shared__ float s_lg[kMaxExperts];
+  __shared__ __align__(16) uint64_t s_key[kMaxExperts];
+  __shared__ int s_item[kSelectTopK], s_pick[kSelectTopK];
+  __shared__ float s_ex[kSelectTopK];
+  __shared__ uint64_t s_tab[32];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int E = r.experts, K = r.top_k;
+  const int B = (int)a.w.blocks;
+  const int nsets = (B + P - 1) / P;
+  const bool first = blockIdx.x == 0 && blockIdx.y == 0;  // writes the routing outputs
+  char* img = s_dyn;
+  float* s_scl = reinterpret_cast<float*>(s_dyn + tiny_image_bytes(1));
+  float* term_base = reinterpret_cast<float*>(s_dyn + tiny_image_bytes(1) + tiny_sets(1) * 64);
+  // The logits (0 past the experts: a key below every real one).
+  if (tid < 32) s_tab[tid] = kExp2Tab[tid];
+  if (tid < kMaxExperts) {
+    const float lg = tid < E ? r.logits[tid] : 0.0f;
+    s_lg[tid] = lg;
+    s_key[tid] = tid < E ? route_key(lg, tid) : 0;
+  }
+  for (int k = tid; k < nsets; k += Geo::kThreads) *reinterpret_cast<u32x4*>(img + k * kTinySetBytes + 1024) = u32x4{};
+  __syncthreads();
+
+  // Wave 0 selects: lane e's key ranks among all keys (16 per LDS round
+  // trip), experts e and e + 64 per lane.
+  int r0 = 0, r1 = 0, item0 = 0, item1 = 0;
+  bool sel0 = false, sel1 = false;
+  float lg0 = 0.0f, lg1 = 0.0f;
+  if (wave == 0) {
+    lg0 = s_lg[lane];
+    lg1 = s_lg[lane + 64];
+    const uint64_t k0 = s_key[lane], k1 = s_key[lane + 64];
+    for (int c = 0; c < E; c += 16) {  // uniform
+      u64x2 kk[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) kk[j] = reinterpret_cast<const u64x2*>(s_key + c)[j];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        r0 += (kk[j][0] > k0) + (kk[j][1] > k0);
+        r1 += (kk[j][0] > k1) + (kk[j][1] > k1);
+      }
+    }
+    sel0 = lane < E && r0 < K;
+    sel1 = lane + 64 < E && r1 < K;
+    const unsigned long long m0 = __ballot(sel0), m1 = __ballot(sel1), below = (1ull << lane) - 1ull;
+    item0 = __popcll(m0 & below);
+    item1 = __popcll(m0) + __popcll(m1 & below);
+    if (sel0) {
+      s_item[item0] = lane;
+      s_pick[r0] = lane;
+    }
+    if (sel1) {
+      s_item[item1] = lane + 64;
+      s_pick[r1] = lane + 64;
+    }
+  }
+  __syncthreads();
+
+  // The wave's weight ring (gemv_kernel<kGateUp, 8, 2>: tile group x, item y).
+  const int y = blockIdx.y;
+  const int expert = s_item[y];
+  const int half = wave >> 2, wt = wave & 3;
+  const int nl = lane & 15;
+  const int start = y, count = 1;
+  const int rows = (int)a.w.rows;
+  const int tile0 = blockIdx.x * C::kWaves + wt;
+  const bool ok = tile0 < (int)a.w.tiles;
+  const int safe_tile = ok ? tile0 : 0;
+  const int nq4 = (B + 3) >> 2;
+  GemvLoads L;
+  L.nib = buffer_rsrc(a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)safe_tile * 256 * B);
+  L.scl = buffer_rsrc(a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)safe_tile * 64 * nq4);
+  L.vl = lane * 16;
+  L.vl_tail = lane * (B & 3) * 4;
+  L.vs = nl * 4;
+  L.nq4 = nq4;
+  L.nfull4 = B >> 2;
+  const int g0 = half * (Geo::kHalfSets * P / 4);
+  // The image of row 0 (gemv_kernel's DMA at one token), the tile's
+  // fast-path flag and bias (branch-free, from valid addresses), then the
+  // ring: all in flight together.
+  {
+    const __amdgpu_buffer_rsrc_t act_codes = buffer_rsrc(a.actv), act_scl = buffer_rsrc(a.acts);
+    const int i = lane >> 2, g = lane & 3, part = i & 1;
+    for (int k = wave; k < nsets; k += Geo::kWaves) {  // uniform per wave
+      const int b = k * P + i / V;
+      dma16(act_codes, img + k * kTinySetBytes, b < B ? (b * 2 + part) * 64 + g * 16 : 0, 0);
+    }
+    for (int k = wave; k * 64 < nsets * 16; k += Geo::kWaves) {  // uniform per wave
+      const int f = k * 64 + lane, b = f >> 1;
+      dma4(act_scl, reinterpret_cast<char*>(s_scl) + k * 256, b < B ? (b * 2 + (f & 1)) * 4 : 0, 0);
+    }
+  }
+  const int row = tile0 * kTileRows + nl;
+  const uint8_t fast_raw = a.w.fast[(size_t)expert * a.w.tiles + safe_tile];
+  const float* bias_p =
+      a.bias != nullptr ? a.bias + (size_t)expert * a.bias_expert_stride + min(row, rows - 1) : r.router_b;
+  const float bias_raw = *bias_p;
+  u32x4 wn[R];
+  uint32_t ws[R];
+#pragma unroll
+  for (int q = 0; q < R; ++q) gemv_load(L, g0 + q, wn[q], ws[q]);
+  // This wave's DMA has landed once at most the flag, the bias and the ring
+  // are outstanding.
+  constexpr int kWait = 2 + 2 * R;
+  static_assert(kWait < 64, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((kWait & 15) | ((kWait >> 4) << 14) | (7 << 4) | (15 << 8));
+
+  // Work-group (0, 0), wave 0: the routing outputs.
+  if (first && wave == 0) {
+    if ((lane < E && !isfinite(lg0)) || (lane + 64 < E && !isfinite(lg1))) atomicOr(r.err, kErrNonFiniteLogits);
+    if (lane < E) d.bucket_off[lane] = item0;  // routes of the experts below
+    if (lane + 64 < E) d.bucket_off[lane + 64] = item1;
+    if (lane == 0) {
+      d.bucket_off[E] = K;
+      *d.n_work = K;
+    }
+    if (sel0) {
+      d.route_tok[item0] = 0;
+      d.route_slot[item0] = r0;
+      reinterpret_cast<int4*>(d.work)[item0] = make_int4(lane, item0, 1, 0);
+    }
+    if (sel1) {
+      d.route_tok[item1] = 0;
+      d.route_slot[item1] = r1;
+      reinterpret_cast<int4*>(d.work)[item1] = make_int4(lane + 64, item1, 1, 0);
+    }
+    float mx = -INFINITY;
+    for (int k = 0; k < K; ++k) mx = fmaxf(mx, s_lg[s_pick[k]]);
+    const int my_e = s_pick[lane < K ? lane : 0];
+    const float ex = expf_glibc(s_lg[my_e] - mx, s_tab);
+    if (lane < K) s_ex[lane] = ex;
+    __builtin_amdgcn_wave_barrier();
+    float sum = 0.0f;
+    for (int k = 0; k < K; ++k) sum = sum + s_ex[k];
+    if (lane < K) {
+      r.selected[lane] = my_e;
+      r.weights[lane] = bf16r(ex / sum);
+    }
+  }
+  __syncthreads();  // every wave's DMA is in
+  const bool fast = a.fast_ok && fast_raw != 0;
+  const float bias = (a.bias != nullptr && ok && row < rows) ? bias_raw : 0.0f;
+
+  float* terms = term_base + wave * (Geo::kTermRegion / 4);
+  float tot = bias + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
+  if (half == 0)
+    tot = gemv_sets<P, R, 0, Geo::kHalfSets, false>(tot, L, wn, ws, img, s_scl, terms, B, lane, fast);
+  else
+    gemv_sets<P, R, Geo::kHalfSets, Geo::kSets, true>(tot, L, wn, ws, img, s_scl, terms, B, lane, fast);
+  __syncthreads();  // the second half's terms are in LDS
+  if (half == 0) {
+    const float* tb2 = term_base + (wave + 4) * (Geo::kTermRegion / 4);
+#pragma unroll
+    for (int s = 0; s < Geo::kHalfSets; ++s) gemv_chain_set<P>(tot, tb2 + s * (kTinyTermBytes / 4), nl, 0);
+  }
+  const int G = lane >> 4;
+  Acc<C> acc;
+  acc[0][0][0] = __shfl(tot, ((2 * G) * 16 + nl) & 63);
+  acc[0][0][1] = __shfl(tot, ((2 * G + 1) * 16 + nl) & 63);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();  // every wave is done with the LDS image before the epilogue reuses it
+  if (half == 0) gemm_epilogue<C, kGateUp, true>(a, acc, 1, count, start, tile0, reinterpret_cast<float*>(s_dyn));
+  else __syncthreads();  // gemm_epilogue's one barrier (gate_up), matched by the second half's waves
+}
+
+// ---------------------------------------------------------------------------
 // Exact-BF16 expert projection (CpuExpertProjection::ExactBf16; project_mxfp4,
 // cpu_runner.rs:3497-3519): per output, total = bias; total += the 16 lane
 // sums folded 0..15 from -0.0. Lane l sums bf16(decode(code) * e8m0) * x over
@@ -2558,6 +2758,33 @@ hipError_t launch_gemv(GemmMode mode, const GemmArgs& a, int rows_max, int grid_
     case kGateUp: pick(gemv_kernel<kGateUp, 8, 2>, gemv_kernel<kGateUp, 4, 1>, gemv_kernel<kGateUp, 2, 1>); break;
     case kDown: pick(gemv_kernel<kDown, 8, 2>, gemv_kernel<kDown, 4, 1>, gemv_kernel<kDown, 2, 1>); break;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_route_logits(const RouteArgs& r, hipStream_t stream) {
+  if (r.m < 1 || r.m > kFusedRouteRows || r.hidden > kFusedRouteHidden || r.hidden % 32 != 0 || r.injected != nullptr ||
+      r.experts > kMaxExperts)
+    return hipErrorInvalidValue;
+  const size_t qblocks = r.quant ? (size_t)r.m * (r.hidden / kBlock) : 0;
+  const unsigned grid = (unsigned)r.experts + (unsigned)((qblocks + kSelectQuantBlocks - 1) / kSelectQuantBlocks);
+  hipLaunchKernelGGL(route_select_kernel, dim3(grid), dim3(1024), 0, stream, r, DispatchArgs{}, (int*)nullptr);
+  return hipGetLastError();
+}
+
+hipError_t launch_route_gemv(const RouteArgs& r, const DispatchArgs& d, const GemmArgs& g, hipStream_t stream,
+                             hipEvent_t start, hipEvent_t stop) {
+  // One row, its logits in r.logits and its residual-Q8 input in g.actv /
+  // g.acts; every selected expert is one work item of one route.
+  if (r.m != 1 || r.injected != nullptr || r.experts < 1 || r.experts > kRouteGemvExperts || r.top_k < 1 ||
+      r.top_k > kSelectTopK || r.top_k > r.experts || r.hidden % kBlock != 0 ||
+      g.w.blocks > (size_t)kTinyMaxBlocks || r.qmode != kProjResidualQ8 || !g.residual ||
+      g.w.blocks != (size_t)(r.hidden / kBlock) || g.trace_gu != nullptr || g.trace_sw != nullptr ||
+      d.routes != r.top_k)
+    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((g.w.tiles + GemmTinyCfg::kWgTiles - 1) / GemmTinyCfg::kWgTiles), (unsigned)r.top_k);
+  const dim3 block(RouteGemvGeom::kThreads);
+  if (start) hipExtLaunchKernelGGL(route_gemv_kernel, grid, block, 0, stream, start, stop, 0, r, d, g);
+  else hipLaunchKernelGGL(route_gemv_kernel, grid, block, 0, stream, r, d, g);
   return hipGetLastError();
 }
 

@@ -183,6 +183,39 @@ def test_one_launch_routing_ties_and_signed_zeros(ctx, experts, top_k):
     close(layer)
 
 
+@pytest.mark.parametrize("experts,hidden,top_k", [(32, 2880, 4), (5, 96, 2), (64, 352, 4), (65, 3072, 4),
+                                                   (128, 160, 3)])
+def test_one_row_selects_inside_the_gate_up_launch(ctx, experts, hidden, top_k):
+    """One-row batches with a computed router (no gate_up traces) take a
+    logits-only router launch, then every gate_up work-group quantizes the row
+    and selects for itself, and work-group (0, 0) writes the routing outputs.
+    Bit-exact against the oracle, repeated and alternating with a 2-row batch
+    (one-launch routing with the arrival counter), with the RMSNorm in front,
+    and with a non-finite input."""
+    host = O.synthetic_layer(41, experts, experts=experts, hidden=hidden, intermediate=64, top_k=top_k)
+    layer = gpu_layer(ctx, host)
+    x = O.gen_hidden(41, hidden, 1, hidden)
+    x2 = O.gen_hidden(41, hidden + 1, 2, hidden)
+    want, want2 = O.moe_batch(host, x), O.moe_batch(host, x2)
+    assert want["status"] == O.OK and want2["status"] == O.OK
+    for _ in range(2):
+        assert_moe_equal(layer.forward(x), want)
+        assert_moe_equal(layer.forward(x2), want2)
+    res = residual_stream(41, 1, hidden)
+    w = norm_weights(41, hidden)
+    want_r = O.moe_residual(host, res, w, 1e-5)
+    assert want_r["status"] == O.OK
+    assert_residual_equal(layer.forward_residual(res, w, 1e-5), want_r)
+    bad = x.copy()
+    bad[0, hidden - 1] = 0x7F80  # +inf bf16
+    with pytest.raises(G.GossmxError) as e:
+        layer.forward(bad)
+    assert e.value.status == G.ERR_NON_FINITE_LOGITS
+    assert O.moe_batch(host, bad)["status"] == O.NON_FINITE_LOGITS
+    assert_moe_equal(layer.forward(x), want)
+    close(layer)
+
+
 CHECK_THREADS = min(16, os.cpu_count() or 1)
 
 
@@ -408,8 +441,9 @@ def test_profiler_counts_every_stage(ctx):
     """Every stage is timed once per call. Batches of at most 4 rows with a
     computed router run the router, selection and dispatch as one launch,
     counted under router_routing (dispatch then has no launch of its own);
-    one-row batches also run the combine inside the down launch (weighting
-    has none)."""
+    one-row batches launch the router for the logits only, select inside the
+    gate_up launch and run the combine inside the down launch (weighting has
+    none)."""
     host = O.synthetic_layer(9, 0, experts=4, hidden=64, intermediate=32, top_k=2)
     layer = gpu_layer(ctx, host)
     for m, fused in ((12, False), (4, True), (1, True)):
