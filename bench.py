@@ -36,6 +36,7 @@ from __future__ import annotations
 
 import argparse
 import csv
+import gc
 import glob
 import json
 import os
@@ -65,7 +66,7 @@ DOWN_BYTES = HIDDEN * BLOCKS * 17         # 4,406,400 B per expert
 SEED = 20251201
 RMS_EPS = 1e-5  # GPT-OSS rms_norm_eps
 COPY_PROBE_BYTES = 1 << 30  # device copy that calibrates the HBM byte counters
-GATE_UP_KERNEL = re.compile(r"gemm_kernel<.*>, 1, (true|false)>|gemv_kernel<1, \d+>")
+GATE_UP_KERNEL = re.compile(r"gemm_kernel<.*>, 1, (true|false)>|gemv_kernel<1, \d+, \d+>|route_gemv_kernel")
 
 CONFIGS = {
     0: {"batch": 1, "layers": 12, "experts": 32, "routing": "router", "zipf": None, "roofline": "hbm",
@@ -481,15 +482,23 @@ def main() -> int:
     # Host-memory mode (GOSSMX_MEM_HOST, the direct drop-in for Rust slices):
     # every layer call copies x and the logits in and the outputs out, then
     # synchronizes. PCIe-inclusive, reported beside value, never as value.
+    # Python's cyclic collector is paused for the timed calls: a full
+    # collection of the interpreter's objects (torch's included) takes tens of
+    # ms and would land inside some call; a native caller has no such pause.
     host_ms = None
     if not args.residual and args.host_steps > 0:
         for st in state:  # one untimed pass (host staging buffers)
             st["moe"].forward(x, injected_logits=st["logits"])
-        t0 = time.perf_counter()
-        for _ in range(args.host_steps):
-            for st in state:
-                st["moe"].forward(x, injected_logits=st["logits"])
-        host_ms = (time.perf_counter() - t0) * 1e3 / args.host_steps
+        gc.collect()
+        gc.disable()
+        try:
+            t0 = time.perf_counter()
+            for _ in range(args.host_steps):
+                for st in state:
+                    st["moe"].forward(x, injected_logits=st["logits"])
+            host_ms = (time.perf_counter() - t0) * 1e3 / args.host_steps
+        finally:
+            gc.enable()
 
     sel = [st["sel_dev"].cpu().numpy() for st in state]
     if cfg["routing"] != "router":
@@ -510,7 +519,10 @@ def main() -> int:
     gu_avg_ms = gu["total_ms"] / max(gu["launches"], 1)
     gu_bytes_per_launch = touched * GATE_UP_BYTES / L
     gu_gbps = gu_bytes_per_launch / (gu_avg_ms * 1e-3) / 1e9
-    if m <= 4:
+    if m == 1 and cfg["routing"] == "router":
+        kernel = ("route_gemv_kernel (top-k selection per work-group + block-packed MXFP4 GEMV, P=8 + SwiGLU + "
+                  "down-input quantization)")
+    elif m <= 4:
         kernel = (f"gemv_kernel<kGateUp, P={8 // (1 if m == 1 else 2 if m == 2 else 4)}> (block-packed small-batch "
                   "MXFP4 GEMV + SwiGLU + down-input quantization)")
     else:
