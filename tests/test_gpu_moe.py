@@ -146,28 +146,37 @@ def test_20b_shape_decode_bit_exact(layer20b, m):
     assert_moe_equal(layer.forward(x), want)
 
 
-@pytest.mark.parametrize("experts,m", [(32, 1), (128, 1), (128, 4), (5, 4)])
-def test_one_launch_routing_bit_exact_and_repeatable(ctx, experts, m):
-    """Batches of at most 4 rows with a computed router take one launch for
-    the router, selection and dispatch (one work-group per expert, the last
-    to arrive selects). Three calls in a row, alternating with a 9-row batch
-    (two-launch path), all equal the oracle: the arrival counter resets."""
+@pytest.mark.parametrize("trace", [False, True], ids=["select-in-gate_up", "one-launch"])
+@pytest.mark.parametrize("experts,m", [(32, 1), (128, 1), (128, 4), (5, 4), (17, 3)])
+def test_small_batch_routing_bit_exact_and_repeatable(ctx, experts, m, trace):
+    """Batches of at most 4 rows with a computed router. One row without
+    traces: a logits launch, then every gate_up work-group selects for
+    itself. Two to four rows, or the gate_up / SwiGLU traces requested: one
+    launch for the router, selection and dispatch (one work-group per expert,
+    the last to arrive selects). Three calls in a row, alternating with a
+    9-row batch (two-launch path), all equal the oracle: the arrival counter
+    resets."""
     host = O.synthetic_layer(31, experts, experts=experts, hidden=256, intermediate=64, top_k=4)
     layer = gpu_layer(ctx, host)
     x = O.gen_hidden(31, m, m, 256)
     x9 = O.gen_hidden(31, 9, 9, 256)
-    want, want9 = O.moe_batch(host, x), O.moe_batch(host, x9)
+    want, want9 = O.moe_batch(host, x, trace=trace), O.moe_batch(host, x9)
     for _ in range(3):
-        assert_moe_equal(layer.forward(x), want)
+        got = layer.forward(x, trace=trace)
+        assert_moe_equal(got, want)
+        if trace:
+            assert_traces_equal(got, want)
         assert_moe_equal(layer.forward(x9), want9)
     close(layer)
 
 
+@pytest.mark.parametrize("trace", [False, True], ids=["select-in-gate_up", "one-launch"])
 @pytest.mark.parametrize("experts,top_k", [(40, 4), (7, 3), (100, 1), (128, 2)])
-def test_one_launch_routing_ties_and_signed_zeros(ctx, experts, top_k):
+def test_small_batch_routing_ties_and_signed_zeros(ctx, experts, top_k, trace):
     """Router weights of zero make every logit its bias: tied biases and
     -0.0 / +0.0 force the ranked selection's tie rule (lower index first,
-    -0.0 equal to +0.0) for batches of 1..4 rows, against the oracle."""
+    -0.0 equal to +0.0) for batches of 1..4 rows, on both small-batch routing
+    paths, against the oracle."""
     host = O.synthetic_layer(33, experts, experts=experts, hidden=128, intermediate=64, top_k=top_k)
     host.router_weight[:] = 0
     rng = np.random.default_rng(experts)
@@ -177,9 +186,12 @@ def test_one_launch_routing_ties_and_signed_zeros(ctx, experts, top_k):
     layer = gpu_layer(ctx, host)
     for m in (1, 2, 3, 4):
         x = O.gen_hidden(33, m, m, 128)
-        want = O.moe_batch(host, x)
+        want = O.moe_batch(host, x, trace=trace)
         assert want["status"] == O.OK
-        assert_moe_equal(layer.forward(x), want)
+        got = layer.forward(x, trace=trace)
+        assert_moe_equal(got, want)
+        if trace:
+            assert_traces_equal(got, want)
     close(layer)
 
 
@@ -187,11 +199,10 @@ def test_one_launch_routing_ties_and_signed_zeros(ctx, experts, top_k):
                                                    (128, 160, 3)])
 def test_one_row_selects_inside_the_gate_up_launch(ctx, experts, hidden, top_k):
     """One-row batches with a computed router (no gate_up traces) take a
-    logits-only router launch, then every gate_up work-group quantizes the row
-    and selects for itself, and work-group (0, 0) writes the routing outputs.
-    Bit-exact against the oracle, repeated and alternating with a 2-row batch
-    (one-launch routing with the arrival counter), with the RMSNorm in front,
-    and with a non-finite input."""
+    logits and quantization launch, then every gate_up work-group selects for
+    itself, and work-group (0, 0) writes the routing outputs. Bit-exact
+    against the oracle, repeated and alternating with a 2-row batch, with the
+    RMSNorm in front, and with a non-finite input."""
     host = O.synthetic_layer(41, experts, experts=experts, hidden=hidden, intermediate=64, top_k=top_k)
     layer = gpu_layer(ctx, host)
     x = O.gen_hidden(41, hidden, 1, hidden)
