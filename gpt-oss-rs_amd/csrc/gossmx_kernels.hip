@@ -790,24 +790,31 @@ __device__ __forceinline__ void select_dispatch_tiny(const RouteArgs& r, const D
 }
 
 // Top-k, softmax and dispatch of every row by one work-group of 1024 threads.
+// Every global store waits until after the last work-group barrier: a barrier
+// waits for the work-group's outstanding stores, so outputs written early
+// would each add a store round trip.
 __device__ __forceinline__ void select_dispatch_body(const RouteArgs& r, const DispatchArgs& d) {
   const int tid = threadIdx.x;
   const int E = r.experts, K = r.top_k, M = r.m, stride = E + 1;
   __shared__ float s_lg[kSelectLds];
   __shared__ int s_sel[kSelectMaxRoutes];
+  __shared__ float s_w[kSelectMaxRoutes];
   __shared__ uint64_t s_tab[32];
   if (tid < 32) s_tab[tid] = kExp2Tab[tid];
+  // Element i is (i / E, i % E), the quotient by a multiply-high (exact for
+  // i < 2^32 / E). Loops stay short and rolled: this code runs once per
+  // launch from a cold instruction cache.
+  const uint32_t inv_e = 0xffffffffu / (uint32_t)E + 1u;
+  bool bad = false;
+#pragma unroll 2
   for (int i = tid; i < M * E; i += 1024) {
-    float v;
-    if (r.injected != nullptr) {
-      v = bf16r(r.injected[i]);
-      if (r.logits) r.logits[i] = v;
-    } else {
-      v = r.logits[i];
-    }
-    if (!isfinite(v)) atomicOr(r.err, kErrNonFiniteLogits);
-    s_lg[(i / E) * stride + i % E] = v;
+    float v = r.injected != nullptr ? r.injected[i] : r.logits[i];
+    if (r.injected != nullptr) v = bf16r(v);
+    bad = bad || !isfinite(v);
+    const int row = (int)__umulhi((uint32_t)i, inv_e);
+    s_lg[row * stride + (i - row * E)] = v;
   }
+  if (bad) atomicOr(r.err, kErrNonFiniteLogits);
   __syncthreads();
   // T lanes per row: the largest power of two <= 64 with T * M <= 1024 and T
   // <= E / 4 (a few experts per lane), but at least top_k (<= 4).
@@ -822,13 +829,23 @@ __device__ __forceinline__ void select_dispatch_body(const RouteArgs& r, const D
     const int row = base + tid / T, j = tid % T;
     const bool has_row = row < M;
     const int rr = has_row ? row : 0;
-    float* const wr = r.weights + (size_t)rr * K;
-    int* const sr = r.selected + (size_t)rr * K;
-    select_row_lanes<kSelectTopK>(s_lg + rr * stride, has_row, j, T, E, K, sr, wr, s_sel + rr * K, s_tab);
+    select_row_lanes<kSelectTopK>(s_lg + rr * stride, has_row, j, T, E, K, s_sel + rr * K, s_w + rr * K,
+                                  s_sel + rr * K, s_tab);
   }
   __syncthreads();
   if (d.routes <= kMaskRoutes) dispatch_body_masked(d, s_sel);
   else dispatch_body(d, s_sel);
+  // No barrier follows: the selection, weights and (injected) logits.
+  for (int i = tid; i < M * K; i += 1024) {
+    r.selected[i] = s_sel[i];
+    r.weights[i] = s_w[i];
+  }
+  if (r.injected != nullptr && r.logits != nullptr) {
+    for (int i = tid; i < M * E; i += 1024) {
+      const int row = (int)__umulhi((uint32_t)i, inv_e);
+      r.logits[i] = s_lg[row * stride + (i - row * E)];
+    }
+  }
 }
 
 __global__ __launch_bounds__(1024) void select_dispatch_kernel(RouteArgs r, DispatchArgs d) {
