@@ -2104,6 +2104,7 @@ __global__ __launch_bounds__(RouteGemvGeom::kThreads, 4) void route_gemv_kernel(
   __shared__ float s_lg[kMaxExperts];
   __shared__ __align__(16) uint64_t s_key[kMaxExperts];
   __shared__ int s_item[kSelectTopK], s_pick[kSelectTopK];
+  __shared__ int s_rank[kMaxExperts], s_slot[kMaxExperts];  // each expert's rank and item (or route) index
   __shared__ float s_ex[kSelectTopK];
   __shared__ uint64_t s_tab[32];
   const int tid = threadIdx.x;
@@ -2127,12 +2128,8 @@ __global__ __launch_bounds__(RouteGemvGeom::kThreads, 4) void route_gemv_kernel(
 
   // Wave 0 selects: lane e's key ranks among all keys (16 per LDS round
   // trip), experts e and e + 64 per lane.
-  int r0 = 0, r1 = 0, item0 = 0, item1 = 0;
-  bool sel0 = false, sel1 = false;
-  float lg0 = 0.0f, lg1 = 0.0f;
   if (wave == 0) {
-    lg0 = s_lg[lane];
-    lg1 = s_lg[lane + 64];
+    int r0 = 0, r1 = 0;
     const uint64_t k0 = s_key[lane], k1 = s_key[lane + 64];
     for (int c = 0; c < E; c += 16) {  // uniform
       u64x2 kk[8];
@@ -2144,11 +2141,9 @@ __global__ __launch_bounds__(RouteGemvGeom::kThreads, 4) void route_gemv_kernel(
         r1 += (kk[j][0] > k1) + (kk[j][1] > k1);
       }
     }
-    sel0 = lane < E && r0 < K;
-    sel1 = lane + 64 < E && r1 < K;
+    const bool sel0 = lane < E && r0 < K, sel1 = lane + 64 < E && r1 < K;
     const unsigned long long m0 = __ballot(sel0), m1 = __ballot(sel1), below = (1ull << lane) - 1ull;
-    item0 = __popcll(m0 & below);
-    item1 = __popcll(m0) + __popcll(m1 & below);
+    const int item0 = __popcll(m0 & below), item1 = __popcll(m0) + __popcll(m1 & below);
     if (sel0) {
       s_item[item0] = lane;
       s_pick[r0] = lane;
@@ -2157,6 +2152,10 @@ __global__ __launch_bounds__(RouteGemvGeom::kThreads, 4) void route_gemv_kernel(
       s_item[item1] = lane + 64;
       s_pick[r1] = lane + 64;
     }
+    s_rank[lane] = r0;
+    s_rank[lane + 64] = r1;
+    s_slot[lane] = item0;
+    s_slot[lane + 64] = item1;
   }
   __syncthreads();
 
@@ -2210,38 +2209,6 @@ __global__ __launch_bounds__(RouteGemvGeom::kThreads, 4) void route_gemv_kernel(
   static_assert(kWait < 64, "vmcnt field");
   __builtin_amdgcn_s_waitcnt((kWait & 15) | ((kWait >> 4) << 14) | (7 << 4) | (15 << 8));
 
-  // Work-group (0, 0), wave 0: the routing outputs.
-  if (first && wave == 0) {
-    if ((lane < E && !isfinite(lg0)) || (lane + 64 < E && !isfinite(lg1))) atomicOr(r.err, kErrNonFiniteLogits);
-    if (lane < E) d.bucket_off[lane] = item0;  // routes of the experts below
-    if (lane + 64 < E) d.bucket_off[lane + 64] = item1;
-    if (lane == 0) {
-      d.bucket_off[E] = K;
-      *d.n_work = K;
-    }
-    if (sel0) {
-      d.route_tok[item0] = 0;
-      d.route_slot[item0] = r0;
-      reinterpret_cast<int4*>(d.work)[item0] = make_int4(lane, item0, 1, 0);
-    }
-    if (sel1) {
-      d.route_tok[item1] = 0;
-      d.route_slot[item1] = r1;
-      reinterpret_cast<int4*>(d.work)[item1] = make_int4(lane + 64, item1, 1, 0);
-    }
-    float mx = -INFINITY;
-    for (int k = 0; k < K; ++k) mx = fmaxf(mx, s_lg[s_pick[k]]);
-    const int my_e = s_pick[lane < K ? lane : 0];
-    const float ex = expf_glibc(s_lg[my_e] - mx, s_tab);
-    if (lane < K) s_ex[lane] = ex;
-    __builtin_amdgcn_wave_barrier();
-    float sum = 0.0f;
-    for (int k = 0; k < K; ++k) sum = sum + s_ex[k];
-    if (lane < K) {
-      r.selected[lane] = my_e;
-      r.weights[lane] = bf16r(ex / sum);
-    }
-  }
   __syncthreads();  // every wave's DMA is in
   const bool fast = a.fast_ok && fast_raw != 0;
   const float bias = (a.bias != nullptr && ok && row < rows) ? bias_raw : 0.0f;
@@ -2264,8 +2231,46 @@ __global__ __launch_bounds__(RouteGemvGeom::kThreads, 4) void route_gemv_kernel(
   acc[0][0][1] = __shfl(tot, ((2 * G + 1) * 16 + nl) & 63);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();  // every wave is done with the LDS image before the epilogue reuses it
-  if (half == 0) gemm_epilogue<C, kGateUp, true>(a, acc, 1, count, start, tile0, reinterpret_cast<float*>(s_dyn));
-  else __syncthreads();  // gemm_epilogue's one barrier (gate_up), matched by the second half's waves
+  if (half == 0) {
+    gemm_epilogue<C, kGateUp, true>(a, acc, 1, count, start, tile0, reinterpret_cast<float*>(s_dyn));
+  } else {
+    __syncthreads();  // gemm_epilogue's one barrier (gate_up), matched by the second half's waves
+    // Work-group (0, 0): the routing outputs, written by a wave without an
+    // epilogue after the last barrier (a barrier would wait for the stores).
+    if (first && wave == 4) {
+      const int e0 = lane, e1 = lane + 64;
+      const bool sel0 = e0 < E && s_rank[e0] < K, sel1 = e1 < E && s_rank[e1] < K;
+      if ((e0 < E && !isfinite(s_lg[e0])) || (e1 < E && !isfinite(s_lg[e1]))) atomicOr(r.err, kErrNonFiniteLogits);
+      if (e0 < E) d.bucket_off[e0] = s_slot[e0];  // routes of the experts below
+      if (e1 < E) d.bucket_off[e1] = s_slot[e1];
+      if (lane == 0) {
+        d.bucket_off[E] = K;
+        *d.n_work = K;
+      }
+      if (sel0) {
+        d.route_tok[s_slot[e0]] = 0;
+        d.route_slot[s_slot[e0]] = s_rank[e0];
+        reinterpret_cast<int4*>(d.work)[s_slot[e0]] = make_int4(e0, s_slot[e0], 1, 0);
+      }
+      if (sel1) {
+        d.route_tok[s_slot[e1]] = 0;
+        d.route_slot[s_slot[e1]] = s_rank[e1];
+        reinterpret_cast<int4*>(d.work)[s_slot[e1]] = make_int4(e1, s_slot[e1], 1, 0);
+      }
+      float mx = -INFINITY;
+      for (int k = 0; k < K; ++k) mx = fmaxf(mx, s_lg[s_pick[k]]);
+      const int my_e = s_pick[lane < K ? lane : 0];
+      const float ex = expf_glibc(s_lg[my_e] - mx, s_tab);
+      if (lane < K) s_ex[lane] = ex;
+      __builtin_amdgcn_wave_barrier();
+      float sum = 0.0f;
+      for (int k = 0; k < K; ++k) sum = sum + s_ex[k];
+      if (lane < K) {
+        r.selected[lane] = my_e;
+        r.weights[lane] = bf16r(ex / sum);
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
