@@ -409,32 +409,37 @@ __device__ __forceinline__ void dispatch_offsets(const DispatchArgs& a, const in
     if (lane == 63) { s_scan[2 * wave] = sc; s_scan[2 * wave + 1] = sf; }
   }
   __syncthreads();
+  int off = 0, full_before = 0, total_full = 0, part = 0, parts = 0, before = 0;
   if (wave < 2) {
     if (wave == 1) { sc += s_scan[0]; sf += s_scan[1]; }
-    const int total_full = s_scan[1] + s_scan[3];
-    const int off = sc - c, full_before = sf - full;
+    total_full = s_scan[1] + s_scan[3];
+    off = sc - c;
+    full_before = sf - full;
     if (tid < E) {
       s_off[tid] = off;
       if (meta) {
-        a.bucket_off[tid] = off;
-        int4* const rec = reinterpret_cast<int4*>(a.work);
-        for (int i = 0; i < full; ++i) rec[full_before + i] = make_int4(tid, off + i * a.chunk, a.chunk, 0);
-        const int part = s_part[tid];
-        int parts = 0, before = 0;
+        part = s_part[tid];
         for (int f = 0; f < E; ++f) {
           const int pf = s_part[f];
           parts += pf > 0;
           before += pf > part || (pf == part && f < tid);
         }
-        if (part > 0) rec[total_full + before] = make_int4(tid, off + full * a.chunk, part, 0);
-        if (tid == 0) {
-          *a.n_work = total_full + parts;
-          a.bucket_off[E] = s_scan[0] + s_scan[2];
-        }
       }
     }
   }
   __syncthreads();
+  // The offsets, work list and item count after the barrier (a barrier waits
+  // for the work-group's outstanding stores).
+  if (meta && wave < 2 && tid < E) {
+    a.bucket_off[tid] = off;
+    int4* const rec = reinterpret_cast<int4*>(a.work);
+    for (int i = 0; i < full; ++i) rec[full_before + i] = make_int4(tid, off + i * a.chunk, a.chunk, 0);
+    if (part > 0) rec[total_full + before] = make_int4(tid, off + full * a.chunk, part, 0);
+    if (tid == 0) {
+      *a.n_work = total_full + parts;
+      a.bucket_off[E] = s_scan[0] + s_scan[2];
+    }
+  }
 }
 
 // Places routes [begin, end) of `sel` (global memory or LDS) in route order:
