@@ -2405,10 +2405,21 @@ __global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* y, const 
   float acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  // The first kCombineBatch ranks' rows and weights are requested together
+  // (one memory round trip), then added in rank order.
+  constexpr int kCombineBatch = 4;
+  u32x4 pb[kCombineBatch];
+  float wb[kCombineBatch];
+#pragma unroll
+  for (int k = 0; k < kCombineBatch; ++k) {
+    const size_t slot = (size_t)r * top_k + (k < top_k ? k : 0);
+    pb[k] = *reinterpret_cast<const u32x4*>(y + slot * hidden + h);
+    wb[k] = w[slot];
+  }
   for (int k = 0; k < top_k; ++k) {
     const size_t slot = (size_t)r * top_k + k;
-    const u32x4 p = *reinterpret_cast<const u32x4*>(y + slot * hidden + h);
-    const float wk = w[slot];
+    const u32x4 p = k < kCombineBatch ? pb[k < kCombineBatch ? k : 0] : *reinterpret_cast<const u32x4*>(y + slot * hidden + h);
+    const float wk = k < kCombineBatch ? wb[k < kCombineBatch ? k : 0] : w[slot];
     float v[8];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
