@@ -98,9 +98,30 @@ __device__ float expf_glibc(float x, const uint64_t* tab = kExp2Tab) {
 
 // The SwiGLU sigmoid bf16(1 / (1 + expf(-s))) of gpt_oss_swiglu
 // (cpu_runner.rs:3819-3820) for every bf16 value s = bits << 16.
-__device__ __forceinline__ uint16_t sigmoid_bf16(uint32_t bits) {
+__device__ __forceinline__ uint16_t sigmoid_bf16(uint32_t bits, const uint64_t* tab = kExp2Tab) {
   const float scaled = bf16_to_f32((uint16_t)bits);
-  return bf16_bits(1.0f / (1.0f + expf_glibc(-scaled)));
+  return bf16_bits(1.0f / (1.0f + expf_glibc(-scaled, tab)));
+}
+
+// kExp2Tab copied into LDS by every kernel that runs the gate_up epilogue
+// (its first 32 threads, before the K loop's barriers), so that the epilogue
+// computes each sigmoid with LDS lookups instead of a dependent global gather.
+__shared__ uint64_t s_exp2_tab[32];
+__device__ __forceinline__ void stage_exp2_tab() {
+  if (threadIdx.x < 32) s_exp2_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+}
+
+// gpt_oss_swiglu for one (gate, up) pair with the sigmoid computed as
+// sigmoid_bf16 (the function the table of swiglu_one holds); the same bits.
+__device__ __forceinline__ float swiglu_one_lds(float g, float u, float alpha, float limit) {
+  const float gate = fminf(g, limit);
+  float up = u;
+  if (up < -limit) up = -limit;
+  if (up > limit) up = limit;
+  const float sig = bf16_to_f32(sigmoid_bf16(bf16_bits(gate * alpha), s_exp2_tab));
+  const float glu = bf16r(gate * sig);
+  const float lin = bf16r(up + 1.0f);
+  return bf16r(glu * lin);
 }
 
 // gpt_oss_swiglu for one (gate, up) pair, cpu_runner.rs:3797-3826: gate =
@@ -1352,7 +1373,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& t
             }
           }
           if (c < count) {
-            const float act = swiglu_one(gate, up, a.alpha, a.limit, a.sig_tab);
+            const float act = swiglu_one_lds(gate, up, a.alpha, a.limit);
             s_act[c * kActStride + (wave * C::kWaveTiles + t) * 8 + (nl >> 1)] = act;
             if (a.trace_sw != nullptr && row < rows)  // CpuExpertTrace::swiglu
               a.trace_sw[(size_t)a.route_slot[start + c] * (rows / 2) + (row >> 1)] = act;
@@ -1511,6 +1532,7 @@ __device__ __forceinline__ void k_loop(const KLoop<C>& k, Acc<C>& tot, char* c0,
 template <class C, int MODE, bool RESIDUAL>
 __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArgs a) {
   const int tid = threadIdx.x;
+  if (MODE == kGateUp) stage_exp2_tab();
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int nl = lane & 15, G = lane >> 4;
   int expert, start, count;
@@ -1815,11 +1837,12 @@ struct GemvGeom {
 };
 
 template <int MODE, int P, int HALVES>
-__global__ __launch_bounds__(64 * 4 * HALVES, 2) void gemv_kernel(GemmArgs a) {
+__global__ __launch_bounds__(64 * 4 * HALVES, HALVES == 2 ? 4 : 2) void gemv_kernel(GemmArgs a) {
   using C = GemmTinyCfg;
   using Geo = GemvGeom<P, HALVES>;
   extern __shared__ __align__(16) char s_dyn[];
   const int tid = threadIdx.x;
+  if (MODE == kGateUp) stage_exp2_tab();
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int half = wave >> 2, wt = wave & 3;  // K half, and the wave's tile within the work-group
   const int nl = lane & 15;
@@ -2111,7 +2134,6 @@ __global__ __launch_bounds__(RouteGemvGeom::kThreads, 4) void route_gemv_kernel(
   __shared__ int s_item[kSelectTopK], s_pick[kSelectTopK];
   __shared__ int s_rank[kMaxExperts], s_slot[kMaxExperts];  // each expert's rank and item (or route) index
   __shared__ float s_ex[kSelectTopK];
-  __shared__ uint64_t s_tab[32];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int E = r.experts, K = r.top_k;
@@ -2122,7 +2144,7 @@ __global__ __launch_bounds__(RouteGemvGeom::kThreads, 4) void route_gemv_kernel(
   float* s_scl = reinterpret_cast<float*>(s_dyn + tiny_image_bytes(1));
   float* term_base = reinterpret_cast<float*>(s_dyn + tiny_image_bytes(1) + tiny_sets(1) * 64);
   // The logits (0 past the experts: a key below every real one).
-  if (tid < 32) s_tab[tid] = kExp2Tab[tid];
+  stage_exp2_tab();
   if (tid < kMaxExperts) {
     const float lg = tid < E ? r.logits[tid] : 0.0f;
     s_lg[tid] = lg;
@@ -2265,7 +2287,7 @@ __global__ __launch_bounds__(RouteGemvGeom::kThreads, 4) void route_gemv_kernel(
       float mx = -INFINITY;
       for (int k = 0; k < K; ++k) mx = fmaxf(mx, s_lg[s_pick[k]]);
       const int my_e = s_pick[lane < K ? lane : 0];
-      const float ex = expf_glibc(s_lg[my_e] - mx, s_tab);
+      const float ex = expf_glibc(s_lg[my_e] - mx, s_exp2_tab);
       if (lane < K) s_ex[lane] = ex;
       __builtin_amdgcn_wave_barrier();
       float sum = 0.0f;
