@@ -110,6 +110,12 @@ __shared__ uint64_t s_exp2_tab[32];
 __device__ __forceinline__ void stage_exp2_tab() {
   if (threadIdx.x < 32) s_exp2_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
 }
+// The same in two halves: the load early, the LDS store once other loads are
+// in flight (the store waits for its data).
+__device__ __forceinline__ uint64_t load_exp2_entry() { return threadIdx.x < 32 ? kExp2Tab[threadIdx.x] : 0ull; }
+__device__ __forceinline__ void store_exp2_entry(uint64_t v) {
+  if (threadIdx.x < 32) s_exp2_tab[threadIdx.x] = v;
+}
 
 // gpt_oss_swiglu for one (gate, up) pair with the sigmoid computed as
 // sigmoid_bf16 (the function the table of swiglu_one holds); the same bits.
@@ -1532,7 +1538,7 @@ __device__ __forceinline__ void k_loop(const KLoop<C>& k, Acc<C>& tot, char* c0,
 template <class C, int MODE, bool RESIDUAL>
 __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArgs a) {
   const int tid = threadIdx.x;
-  if (MODE == kGateUp) stage_exp2_tab();
+  const uint64_t exp2_entry = MODE == kGateUp ? load_exp2_entry() : 0ull;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int nl = lane & 15, G = lane >> 4;
   int expert, start, count;
@@ -1543,10 +1549,12 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
   } else {
     const int wi = blockIdx.y;
     // The item count and the item's record in one round trip (records past
-    // the count are in bounds and ignored).
+    // the count are in bounds and ignored). A real item has an expert and a
+    // start >= 0 and at least one row; testing all three keeps the whole
+    // record's load ahead of the branch.
     const int nw = *a.n_work;
     const int4 rec = reinterpret_cast<const int4*>(a.work)[wi];
-    if (wi >= nw) return;  // uniform over the work-group
+    if ((wi >= nw) | (min(min(rec.x, rec.y), rec.z - 1) < 0)) return;  // uniform over the work-group
     expert = rec.x;
     start = rec.y;  // grouped index of the item's first route
     count = rec.z;
@@ -1556,8 +1564,16 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
   const int n_tg = (count + 7) >> 3;
   const int nq4 = (B + 3) >> 2;
 
-  // Per-tile state first: its loads (fast-path flags, biases) only need the
-  // expert, so they are in flight together with the row indices below.
+  // Everything that needs only the item goes out in one round trip: the
+  // activation row indices, the tiles' fast-path flags and biases
+  // (branch-free, from valid addresses; read after the barrier).
+  __shared__ int s_row[C::kChunk];
+  int row_idx = -1;
+  if (tid < C::kChunk && tid < count) {
+    if (MODE == kPlain) row_idx = start + tid;
+    else if (MODE == kGateUp) row_idx = a.route_tok[start + tid];
+    else row_idx = start + tid;
+  }
   KLoop<C> k;
   k.B = B;
   k.nsteps = (B + C::kStep - 1) / C::kStep;
@@ -1570,8 +1586,8 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
   k.vl = lane * 16;
   k.vl_tail = lane * (B & 3) * 4;
   k.vs = nl * 4;
-  bool fast = true;
-  float b0[C::kWaveTiles];
+  uint8_t fast_raw[C::kWaveTiles];
+  float bias_raw[C::kWaveTiles];
 #pragma unroll
   for (int t = 0; t < C::kWaveTiles; ++t) {
     const int tile = tile0 + t;
@@ -1582,34 +1598,40 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
     const uint8_t* scl = a.w.scl + (size_t)expert * a.w.scl_stride + (size_t)safe_tile * 64 * nq4;
     k.nib[t] = buffer_rsrc(nib);
     k.scl[t] = buffer_rsrc(scl);
-    const uint8_t tile_fast = a.w.fast[(size_t)expert * a.w.tiles + safe_tile];
-    fast = fast && (!ok || tile_fast != 0) && a.fast_ok;
-    const int row = tile * kTileRows + nl;
-    float bias = 0.0f;
-    if (a.bias != nullptr && ok && row < rows) bias = a.bias[(size_t)expert * a.bias_expert_stride + row];
-    b0[t] = bias + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
+  }
+#pragma unroll
+  for (int t = 0; t < C::kWaveTiles; ++t) {
+    const int tile = tile0 + t;
+    const int safe_tile = tile < (int)a.w.tiles ? tile : 0;
+    fast_raw[t] = a.w.fast[(size_t)expert * a.w.tiles + safe_tile];
+    // Without a bias the load reads the first word of the scales instead
+    // (discarded).
+    const int row = min(tile * kTileRows + nl, rows - 1);
+    const float* bp = a.bias != nullptr ? a.bias + (size_t)expert * a.bias_expert_stride + row
+                                        : reinterpret_cast<const float*>(a.w.scl);
+    bias_raw[t] = *bp;
   }
 
   // LDS ring of three steps, filled by DMA two steps ahead.
   __shared__ __align__(16) char s_codes0[C::kSlotBytes], s_codes1[C::kSlotBytes], s_codes2[C::kSlotBytes];
   __shared__ __align__(16) float s_scl0[C::kSclSlot], s_scl1[C::kSclSlot], s_scl2[C::kSclSlot];
-  __shared__ int s_row[C::kChunk];
-  if (tid < C::kChunk) {
-    int r = -1;
-    if (tid < count) {
-      if (MODE == kPlain) r = start + tid;
-      else if (MODE == kGateUp) r = a.route_tok[start + tid];
-      else r = start + tid;
-    }
-    s_row[tid] = r;
-  }
+  if (tid < C::kChunk) s_row[tid] = row_idx;
+  if (MODE == kGateUp) store_exp2_entry(exp2_entry);
   __syncthreads();
 
+  bool fast = a.fast_ok != 0;
   Acc<C> tot;
 #pragma unroll
-  for (int t = 0; t < C::kWaveTiles; ++t)
+  for (int t = 0; t < C::kWaveTiles; ++t) {
+    const int tile = tile0 + t;
+    const bool ok = tile < (int)a.w.tiles;
+    fast = fast && (!ok || fast_raw[t] != 0);
+    const int row = tile * kTileRows + nl;
+    // A -0.0 bias becomes +0.0, as the reference's first add does.
+    const float b0 = (a.bias != nullptr && ok && row < rows ? bias_raw[t] : 0.0f) + 0.0f;
 #pragma unroll
-    for (int tg = 0; tg < C::kNtg; ++tg) { tot[t][tg][0] = b0[t]; tot[t][tg][1] = b0[t]; }
+    for (int tg = 0; tg < C::kNtg; ++tg) { tot[t][tg][0] = b0; tot[t][tg][1] = b0; }
+  }
 
   // DMA lane map, the same for every step. Code piece i of this wave fills
   // slot bytes c * 16 with c = (i * C::kWaves + wave) * 64 + lane, i.e. block j,
