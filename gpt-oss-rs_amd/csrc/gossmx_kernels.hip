@@ -1875,9 +1875,13 @@ __global__ __launch_bounds__(64 * 4 * HALVES, HALVES == 2 ? 4 : 2) void gemv_ker
     count = min(kTinyMaxRows, a.plain_m - start);
   } else {
     const int wi = blockIdx.y;
+    // The item count and the item's record in one round trip (records past
+    // the count are in bounds and ignored). A real item has an expert and a
+    // start >= 0 and at least one row; testing all three keeps the whole
+    // record's load ahead of the branch.
     const int nw = *a.n_work;
     const int4 rec = reinterpret_cast<const int4*>(a.work)[wi];
-    if (wi >= nw) return;  // uniform over the work-group
+    if ((wi >= nw) | (min(min(rec.x, rec.y), rec.z - 1) < 0)) return;  // uniform over the work-group
     expert = rec.x;
     start = rec.y;
     count = rec.z;
@@ -1889,11 +1893,12 @@ __global__ __launch_bounds__(64 * 4 * HALVES, HALVES == 2 ? 4 : 2) void gemv_ker
   const int safe_tile = ok ? tile0 : 0;  // tiles past the end stream tile 0 and discard it
   const int nq4 = (B + 3) >> 2;
 
-  // Per-tile state first (fast-path flag, bias).
-  const bool fast = a.fast_ok && a.w.fast[(size_t)expert * a.w.tiles + safe_tile] != 0;
+  // Per-tile state first (fast-path flag, bias), branch-free and read after
+  // the barrier (without a bias, the first word of the scales, discarded).
+  const uint8_t fast_raw = a.w.fast[(size_t)expert * a.w.tiles + safe_tile];
   const int row = tile0 * kTileRows + nl;
-  float bias = 0.0f;
-  if (a.bias != nullptr && ok && row < rows) bias = a.bias[(size_t)expert * a.bias_expert_stride + row];
+  const float bias_raw = *(a.bias != nullptr ? a.bias + (size_t)expert * a.bias_expert_stride + min(row, rows - 1)
+                                             : reinterpret_cast<const float*>(a.w.scl));
 
   // The first four weight groups of the wave's range, then the activation
   // rows, then the rest of the ring: the weights need only the expert.
@@ -1956,7 +1961,9 @@ __global__ __launch_bounds__(64 * 4 * HALVES, HALVES == 2 ? 4 : 2) void gemv_ker
   __builtin_amdgcn_s_waitcnt((kWait & 15) | ((kWait >> 4) << 14) | (7 << 4) | (15 << 8));
   __syncthreads();
 
-  float tot = bias + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
+  const bool fast = a.fast_ok && fast_raw != 0;
+  // A -0.0 bias becomes +0.0, as the reference's first add does.
+  float tot = (a.bias != nullptr && ok && row < rows ? bias_raw : 0.0f) + 0.0f;
   if (HALVES == 1) {
     tot = gemv_sets<P, R, 0, Geo::kSets, false>(tot, L, wn, ws, img, s_scl, terms, B, lane, fast);
   } else if (half == 0) {
@@ -2035,20 +2042,22 @@ __global__ __launch_bounds__(DownCombineGeom::kThreads, 2) void gemv_down_combin
   const int rows = (int)a.w.rows, B = (int)a.w.blocks;
   const int tile = blockIdx.x;
   const int row = tile * kTileRows + nl;
+  // The item count and the wave's record in one round trip: records
+  // 0 .. top_k - 1 exist (the work list holds more than top_k), so the read
+  // is clamped to them and discarded for an item past the count.
   const int nw = *a.n_work;
+  const int4 rec = reinterpret_cast<const int4*>(a.work)[min(item, c.top_k - 1)];
   const bool live = item < nw;  // uniform per wave
-  int expert = 0, start = 0, slot = 0;
-  if (live) {
-    const int4 rec = reinterpret_cast<const int4*>(a.work)[item];
-    expert = rec.x;
-    start = rec.y;
-    slot = a.route_slot[start];  // = rank (one row)
-  }
+  const int expert = live ? rec.x : 0, start = live ? rec.y : 0;
+  // What needs only the record goes out together, branch-free, and is read
+  // later: the route's rank (one row: slot = rank), the tile's fast-path flag
+  // and bias (without a bias, the first word of the scales, discarded).
+  const int slot = a.route_slot[start];
+  const uint8_t fast_raw = a.w.fast[(size_t)expert * a.w.tiles + tile];
+  const float bias_raw = *(a.bias != nullptr ? a.bias + (size_t)expert * a.bias_expert_stride + min(row, rows - 1)
+                                             : reinterpret_cast<const float*>(a.w.scl));
   if (tid < DC::kItems * kTileRows) s_y[tid] = 0.0f;
   const int nq4 = (B + 3) >> 2;
-  const bool fast = live && a.fast_ok && a.w.fast[(size_t)expert * a.w.tiles + tile] != 0;
-  float bias = 0.0f;
-  if (live && a.bias != nullptr && row < rows) bias = a.bias[(size_t)expert * a.bias_expert_stride + row];
 
   GemvLoads L;
   L.nib = buffer_rsrc(a.w.nib + (size_t)expert * a.w.nib_stride + (size_t)tile * 256 * B);
@@ -2091,7 +2100,9 @@ __global__ __launch_bounds__(DownCombineGeom::kThreads, 2) void gemv_down_combin
   __builtin_amdgcn_s_waitcnt((kWait & 15) | ((kWait >> 4) << 14) | (7 << 4) | (15 << 8));
   __syncthreads();
 
-  float tot = bias + 0.0f;  // a -0.0 bias becomes +0.0, as the reference's first add does
+  const bool fast = live && a.fast_ok && fast_raw != 0;
+  // A -0.0 bias becomes +0.0, as the reference's first add does.
+  float tot = (live && a.bias != nullptr && row < rows ? bias_raw : 0.0f) + 0.0f;
   if (live) {
     if (half == 0)
       tot = gemv_sets<P, R, 0, Geo::kHalfSets, false>(tot, L, wn, ws, img, scl, terms, B, lane, fast);
