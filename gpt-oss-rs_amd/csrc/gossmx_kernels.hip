@@ -106,12 +106,9 @@ __device__ __forceinline__ uint16_t sigmoid_bf16(uint32_t bits, const uint64_t* 
 // kExp2Tab copied into LDS by every kernel that runs the gate_up epilogue
 // (its first 32 threads, before the K loop's barriers), so that the epilogue
 // computes each sigmoid with LDS lookups instead of a dependent global gather.
+// In two halves: the load with the kernel's first requests, the LDS store once
+// they are in flight (the store waits for its data).
 __shared__ uint64_t s_exp2_tab[32];
-__device__ __forceinline__ void stage_exp2_tab() {
-  if (threadIdx.x < 32) s_exp2_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
-}
-// The same in two halves: the load early, the LDS store once other loads are
-// in flight (the store waits for its data).
 __device__ __forceinline__ uint64_t load_exp2_entry() { return threadIdx.x < 32 ? kExp2Tab[threadIdx.x] : 0ull; }
 __device__ __forceinline__ void store_exp2_entry(uint64_t v) {
   if (threadIdx.x < 32) s_exp2_tab[threadIdx.x] = v;
@@ -1864,7 +1861,7 @@ __global__ __launch_bounds__(64 * 4 * HALVES, HALVES == 2 ? 4 : 2) void gemv_ker
   using Geo = GemvGeom<P, HALVES>;
   extern __shared__ __align__(16) char s_dyn[];
   const int tid = threadIdx.x;
-  if (MODE == kGateUp) stage_exp2_tab();
+  const uint64_t exp2_entry = MODE == kGateUp ? load_exp2_entry() : 0ull;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int half = wave >> 2, wt = wave & 3;  // K half, and the wave's tile within the work-group
   const int nl = lane & 15;
@@ -1952,6 +1949,7 @@ __global__ __launch_bounds__(64 * 4 * HALVES, HALVES == 2 ? 4 : 2) void gemv_ker
   }
   for (int k = tid; k < nsets; k += Geo::kThreads)
     *reinterpret_cast<u32x4*>(img + k * kTinySetBytes + 1024) = u32x4{};
+  if (MODE == kGateUp) store_exp2_entry(exp2_entry);
 #pragma unroll
   for (int q = kFirst; q < R; ++q) gemv_load(L, g0 + q, wn[q], ws[q]);
   // The DMA and the first groups have landed once at most the later groups'
@@ -2176,14 +2174,16 @@ __global__ __launch_bounds__(RouteGemvGeom::kThreads, 4) void route_gemv_kernel(
   char* img = s_dyn;
   float* s_scl = reinterpret_cast<float*>(s_dyn + tiny_image_bytes(1));
   float* term_base = reinterpret_cast<float*>(s_dyn + tiny_image_bytes(1) + tiny_sets(1) * 64);
-  // The logits (0 past the experts: a key below every real one).
-  stage_exp2_tab();
+  // The logits (0 past the experts: a key below every real one), requested
+  // together with the exp2 table's entries.
+  const uint64_t exp2_entry = load_exp2_entry();
+  const float lg = tid < E ? r.logits[tid] : 0.0f;
+  for (int k = tid; k < nsets; k += Geo::kThreads) *reinterpret_cast<u32x4*>(img + k * kTinySetBytes + 1024) = u32x4{};
   if (tid < kMaxExperts) {
-    const float lg = tid < E ? r.logits[tid] : 0.0f;
     s_lg[tid] = lg;
     s_key[tid] = tid < E ? route_key(lg, tid) : 0;
   }
-  for (int k = tid; k < nsets; k += Geo::kThreads) *reinterpret_cast<u32x4*>(img + k * kTinySetBytes + 1024) = u32x4{};
+  store_exp2_entry(exp2_entry);
   __syncthreads();
 
   // Wave 0 selects: lane e's key ranks among all keys (16 per LDS round
