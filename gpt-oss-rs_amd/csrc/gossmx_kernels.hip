@@ -452,8 +452,8 @@ __device__ __forceinline__ void dispatch_offsets(const DispatchArgs& a, const in
     }
   }
   __syncthreads();
-  // The offsets, work list and item count after the barrier (a barrier waits
-  // for the work-group's outstanding stores).
+  // The offsets, work list and item count after the last barrier, so that
+  // their stores are off the path to it.
   if (meta && wave < 2 && tid < E) {
     a.bucket_off[tid] = off;
     int4* const rec = reinterpret_cast<int4*>(a.work);
@@ -819,9 +819,8 @@ __device__ __forceinline__ void select_dispatch_tiny(const RouteArgs& r, const D
 }
 
 // Top-k, softmax and dispatch of every row by one work-group of 1024 threads.
-// Every global store waits until after the last work-group barrier: a barrier
-// waits for the work-group's outstanding stores, so outputs written early
-// would each add a store round trip.
+// The outputs are stored after the last work-group barrier, from LDS, so that
+// no store's address and data computation sits between the phases.
 __device__ __forceinline__ void select_dispatch_body(const RouteArgs& r, const DispatchArgs& d) {
   const int tid = threadIdx.x;
   const int E = r.experts, K = r.top_k, M = r.m, stride = E + 1;
@@ -2295,8 +2294,8 @@ __global__ __launch_bounds__(RouteGemvGeom::kThreads, 4) void route_gemv_kernel(
     gemm_epilogue<C, kGateUp, true>(a, acc, 1, count, start, tile0, reinterpret_cast<float*>(s_dyn));
   } else {
     __syncthreads();  // gemm_epilogue's one barrier (gate_up), matched by the second half's waves
-    // Work-group (0, 0): the routing outputs, written by a wave without an
-    // epilogue after the last barrier (a barrier would wait for the stores).
+    // Work-group (0, 0): the routing outputs, written after the last barrier
+    // by a wave that has no epilogue work.
     if (first && wave == 4) {
       const int e0 = lane, e1 = lane + 64;
       const bool sel0 = e0 < E && s_rank[e0] < K, sel1 = e1 < E && s_rank[e1] < K;
