@@ -251,6 +251,7 @@ int check_device_errors(gossmx_ctx* ctx) {
   if (flags == 0) return GOSSMX_OK;
   HIP_TRY(launch_clear_ints(ctx->err, 1, ctx->stream), "clear error flags");
   HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  if (flags & kErrWorkOrder) return fail(GOSSMX_ERR_DEVICE, "internal: work list not in the order a kernel relies on");
   if (flags & kErrNonFiniteLogits) return fail(GOSSMX_ERR_NON_FINITE_LOGITS, "router produced non-finite logits");
   return fail(GOSSMX_ERR_NON_FINITE_INPUT, "kernel input contains a non-finite value");
 }

@@ -29,6 +29,7 @@ constexpr int kNormMaxHidden = 8192;  // hidden sizes the fused post-attention R
 // Device error flags (sticky until the host reads them).
 constexpr int kErrNonFiniteLogits = 1;
 constexpr int kErrNonFiniteInput = 2;
+constexpr int kErrWorkOrder = 4;  // a kernel found the work list in an order it relies on not holding
 
 // Resident layout v3 of one [experts][rows][blocks] MXFP4 tensor.
 //  tiles = ceil(rows / 16). Per expert and tile t:

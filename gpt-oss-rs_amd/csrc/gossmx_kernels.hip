@@ -2041,21 +2041,47 @@ __global__ __launch_bounds__(DownCombineGeom::kThreads, 2) void gemv_down_combin
   const int rows = (int)a.w.rows, B = (int)a.w.blocks;
   const int tile = blockIdx.x;
   const int row = tile * kTileRows + nl;
+  const int nsets = (B + P - 1) / P;
+  char* img = s_img + item * DC::kImage;
+  float* scl = s_scl + item * (DC::kScl / 4);
+  // LDS stores first (none may follow the DMA into the same arrays).
+  if (tid < DC::kItems * kTileRows) s_y[tid] = 0.0f;
+  if (half == 0)
+    for (int k = lane; k < nsets; k += 64) *reinterpret_cast<u32x4*>(img + k * kTinySetBytes + 1024) = u32x4{};
   // The item count and the wave's record in one round trip: records
   // 0 .. top_k - 1 exist (the work list holds more than top_k), so the read
   // is clamped to them and discarded for an item past the count.
   const int nw = *a.n_work;
   const int4 rec = reinterpret_cast<const int4*>(a.work)[min(item, c.top_k - 1)];
+  // With one row every item is one route, and the routes are grouped in item
+  // order, so item k's down input is route row k: its image moves into LDS
+  // while the record is on its way (the two waves of the item take alternate
+  // sets; piece `lane` of a set: row i = lane / 4 (block i / 2, part i % 2),
+  // k-slice lane % 4).
+  if (item < c.top_k) {
+    const __amdgpu_buffer_rsrc_t act_codes = buffer_rsrc(a.actv), act_scl = buffer_rsrc(a.acts);
+    const int i = lane >> 2, g = lane & 3, part = i & 1;
+    for (int k = half; k < nsets; k += 2) {
+      const int b = k * P + i / V;
+      dma16(act_codes, img + k * kTinySetBytes, b < B ? ((item * B + b) * 2 + part) * 64 + g * 16 : 0, 0);
+    }
+    // Scale f of the image: block f / 2, part f % 2.
+    for (int k = half; k * 64 < nsets * 16; k += 2) {
+      const int f = k * 64 + lane, b = f >> 1;
+      dma4(act_scl, reinterpret_cast<char*>(scl) + k * 256, b < B ? ((item * B + b) * 2 + (f & 1)) * 4 : 0, 0);
+    }
+  }
   const bool live = item < nw;  // uniform per wave
   const int expert = live ? rec.x : 0, start = live ? rec.y : 0;
+  if (live && start != item && lane == 0) atomicOr(a.err, kErrWorkOrder);
   // What needs only the record goes out together, branch-free, and is read
-  // later: the route's rank (one row: slot = rank), the tile's fast-path flag
-  // and bias (without a bias, the first word of the scales, discarded).
-  const int slot = a.route_slot[start];
+  // after the barrier: the tile's fast-path flag and bias (without a bias,
+  // the first word of the scales, discarded), the weight ring, and the
+  // route's rank (one row: slot = rank; requested last, as its first use
+  // would otherwise wait for the image DMA issued before it).
   const uint8_t fast_raw = a.w.fast[(size_t)expert * a.w.tiles + tile];
   const float bias_raw = *(a.bias != nullptr ? a.bias + (size_t)expert * a.bias_expert_stride + min(row, rows - 1)
                                              : reinterpret_cast<const float*>(a.w.scl));
-  if (tid < DC::kItems * kTileRows) s_y[tid] = 0.0f;
   const int nq4 = (B + 3) >> 2;
 
   GemvLoads L;
@@ -2069,34 +2095,13 @@ __global__ __launch_bounds__(DownCombineGeom::kThreads, 2) void gemv_down_combin
   const int g0 = half * (Geo::kHalfSets * P / 4);
   u32x4 wn[R];
   uint32_t ws[R];
-  constexpr int kFirst = R < 4 ? R : 4;
-  char* img = s_img + item * DC::kImage;
-  float* scl = s_scl + item * (DC::kScl / 4);
   float* terms = s_terms + wave * (Geo::kTermRegion / 4);
-  const int nsets = (B + P - 1) / P;
   if (live) {
 #pragma unroll
-    for (int q = 0; q < kFirst; ++q) gemv_load(L, g0 + q, wn[q], ws[q]);
-    // The item's image: the two waves of the item take alternate sets. Piece
-    // `lane` of a set: row i = lane / 4 (block i / 2, part i % 2), k-slice lane % 4.
-    const __amdgpu_buffer_rsrc_t act_codes = buffer_rsrc(a.actv), act_scl = buffer_rsrc(a.acts);
-    const int i = lane >> 2, g = lane & 3, part = i & 1;
-    for (int k = half; k < nsets; k += 2) {
-      const int b = k * P + i / V;
-      dma16(act_codes, img + k * kTinySetBytes, b < B ? ((start * B + b) * 2 + part) * 64 + g * 16 : 0, 0);
-    }
-    // Scale f of the image: block f / 2, part f % 2.
-    for (int k = half; k * 64 < nsets * 16; k += 2) {
-      const int f = k * 64 + lane, b = f >> 1;
-      dma4(act_scl, reinterpret_cast<char*>(scl) + k * 256, b < B ? ((start * B + b) * 2 + (f & 1)) * 4 : 0, 0);
-    }
-    if (half == 0)
-      for (int k = lane; k < nsets; k += 64) *reinterpret_cast<u32x4*>(img + k * kTinySetBytes + 1024) = u32x4{};
-#pragma unroll
-    for (int q = kFirst; q < R; ++q) gemv_load(L, g0 + q, wn[q], ws[q]);
+    for (int q = 0; q < R; ++q) gemv_load(L, g0 + q, wn[q], ws[q]);
   }
-  constexpr int kWait = 2 * (R - kFirst);
-  __builtin_amdgcn_s_waitcnt((kWait & 15) | ((kWait >> 4) << 14) | (7 << 4) | (15 << 8));
+  const int slot = a.route_slot[start];
+  __builtin_amdgcn_s_waitcnt(0);  // the image and the ring are in
   __syncthreads();
 
   const bool fast = live && a.fast_ok && fast_raw != 0;
