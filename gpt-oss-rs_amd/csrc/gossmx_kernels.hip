@@ -1147,10 +1147,10 @@ struct GemmCfg {
   // scale dword) per tile; activations kCodeDma code pieces + 1 scale dword.
   static constexpr int kLoadsW = 2 * GROUPS * TILES;
   static constexpr int kLoadsD = kCodeDma + 1;
-  // s_waitcnt immediate for "the DMA of step q has landed": issued after it
-  // are W(q+1), D(q+1), W(q+2) (see k_loop). expcnt and lgkmcnt are not
-  // waited on.
-  static constexpr int kWaitVm = 2 * kLoadsW + kLoadsD;
+  // s_waitcnt immediate for "the DMA and the weights of step q have landed":
+  // issued after them are D(q+1) and W(q+1) (see k_loop). expcnt and lgkmcnt
+  // are not waited on.
+  static constexpr int kWaitVm = kLoadsW + kLoadsD;
   static constexpr int kWaitDma = (kWaitVm & 15) | ((kWaitVm >> 4) << 14) | (7 << 4) | (15 << 8);
   static_assert(kSlotBytes == kCodeDma * 16 * kThreads, "code DMA covers a slot exactly");
   static_assert(kStep * NTOK * 2 <= kSclSlot, "one dword DMA per lane covers a step's scales");
@@ -1489,10 +1489,12 @@ __device__ __forceinline__ void step_update(const KLoop<C>& k, Acc<C>& tot, cons
 
 // The K loop. Vector-memory issue order per wave, fixed so that one
 // immediate wait covers every step:
-//   prologue W(0) D(0) W(1) D(1) W(2); step q: wait(D(q)) barrier
-//   D(q+2) compute(q) W(q+3).
-// After D(q) come W(q+1), D(q+1), W(q+2) = kWaitVm instructions, and W(q)
-// was issued before D(q), so the wait also covers the weights of step q.
+//   prologue W(0) D(0) W(1) D(1); step q: wait(D(q), W(q)) barrier
+//   D(q+2) compute(q) W(q+2).
+// At step q's wait the requests after D(q) and W(q) are D(q+1) and W(q+1)
+// = kWaitVm instructions. The weights run two steps ahead, like the DMA (a
+// third step in flight queued more requests ahead of each step's own and ran
+// 1% slower), so one of the three register slots is free at any time.
 template <class C, bool RESIDUAL, int NTG, bool FAST>
 __device__ __forceinline__ void k_loop(const KLoop<C>& k, Acc<C>& tot, char* c0, char* c1, char* c2, float* s0,
                                        float* s1, float* s2) {
@@ -1506,9 +1508,7 @@ __device__ __forceinline__ void k_loop(const KLoop<C>& k, Acc<C>& tot, char* c0,
   __builtin_amdgcn_sched_barrier(0);
   issue_dma<C>(k, 1, c1, s1);
   __builtin_amdgcn_sched_barrier(0);
-  w2 = load_wstep(k, 2);
-  __builtin_amdgcn_sched_barrier(0);
-#define GOSSMX_STEP(QV, SLOT, CODES, SCL, NCODES, NSCL)                                              \
+#define GOSSMX_STEP(QV, SLOT, CODES, SCL, NCODES, NSCL, NSLOT)                                       \
   {                                                                                                  \
     const int q = (QV);                                                                              \
     __builtin_amdgcn_sched_barrier(0);                                                               \
@@ -1519,14 +1519,14 @@ __device__ __forceinline__ void k_loop(const KLoop<C>& k, Acc<C>& tot, char* c0,
     __builtin_amdgcn_sched_barrier(0);                                                               \
     if (k.wave_ok && q < k.nsteps) step_update<C, RESIDUAL, NTG, FAST>(k, tot, CODES, SCL, SLOT, q); \
     __builtin_amdgcn_sched_barrier(0);                                                               \
-    SLOT = load_wstep(k, q + 3);                                                                     \
+    NSLOT = load_wstep(k, q + 2);                                                                    \
     __builtin_amdgcn_sched_barrier(0);                                                               \
   }
   const int n_pad = (k.nsteps + 2) / 3 * 3;
   for (int q0 = 0; q0 < n_pad; q0 += 3) {
-    GOSSMX_STEP(q0, w0, c0, s0, c2, s2)
-    GOSSMX_STEP(q0 + 1, w1, c1, s1, c0, s0)
-    GOSSMX_STEP(q0 + 2, w2, c2, s2, c1, s1)
+    GOSSMX_STEP(q0, w0, c0, s0, c2, s2, w2)
+    GOSSMX_STEP(q0 + 1, w1, c1, s1, c0, s0, w0)
+    GOSSMX_STEP(q0 + 2, w2, c2, s2, c1, s1, w1)
   }
 #undef GOSSMX_STEP
 }
