@@ -1128,7 +1128,7 @@ typedef __attribute__((address_space(3))) void* lds_ptr;
 //  GemmHuge (2 tiles, 32 rows, 4 blocks, 8 waves) serves prefill-sized
 //    batches, where the FP4->f16 conversion of a weight block is shared by
 //    four token groups.
-template <int TILES, int NTOK, int GROUPS, int WAVES = 8, int MIN_WAVES = 4>
+template <int TILES, int NTOK, int GROUPS, int WAVES = 8, int MIN_WAVES = 4, int WLEAD = 2>
 struct GemmCfg {
   static constexpr int kWaves = WAVES;                    // waves per work-group
   static constexpr int kThreads = 64 * WAVES;
@@ -1147,21 +1147,25 @@ struct GemmCfg {
   // scale dword) per tile; activations kCodeDma code pieces + 1 scale dword.
   static constexpr int kLoadsW = 2 * GROUPS * TILES;
   static constexpr int kLoadsD = kCodeDma + 1;
+  // Steps by which the weight requests lead their use (1 or 2; the DMA leads
+  // by 2).
+  static constexpr int kWLead = WLEAD;
   // s_waitcnt immediate for "the DMA and the weights of step q have landed":
-  // issued after them are D(q+1) and W(q+1) (see k_loop). expcnt and lgkmcnt
-  // are not waited on.
-  static constexpr int kWaitVm = kLoadsW + kLoadsD;
+  // issued after them are D(q+1) and, with a two-step lead, W(q+1) (see
+  // k_loop). expcnt and lgkmcnt are not waited on.
+  static constexpr int kWaitVm = (WLEAD == 2 ? kLoadsW : 0) + kLoadsD;
   static constexpr int kWaitDma = (kWaitVm & 15) | ((kWaitVm >> 4) << 14) | (7 << 4) | (15 << 8);
   static_assert(kSlotBytes == kCodeDma * 16 * kThreads, "code DMA covers a slot exactly");
   static_assert(kStep * NTOK * 2 <= kSclSlot, "one dword DMA per lane covers a step's scales");
   static_assert(NTOK % 8 == 0 && NTOK <= kChunkMax, "token groups of 8");
   static_assert(kGemmRows % 64 == 0, "a work-group's gate_up rows make whole 32-value down-input blocks");
   static_assert(kWaitVm < 64, "vmcnt field");
+  static_assert(WLEAD == 1 || WLEAD == 2, "weight lead");
   static_assert((kStep - 1) * 2 * kBlock * 2 <= (int)kActSlack, "a last partial step reads inside the slack");
 };
 using GemmBig = GemmCfg<2, 16, 1, 4, 5>;
 using GemmSmall = GemmCfg<1, 8, 2, 4, 5>;
-using GemmHuge = GemmCfg<2, 32, 1>;
+using GemmHuge = GemmCfg<2, 32, 1, 8, 4, 1>;
 static_assert(GemmBig::kChunk == kChunk && GemmSmall::kChunk == kSmallChunk && GemmHuge::kChunk == kHugeChunk,
               "work item sizes");
 constexpr int kBufferFlags = 0x00020000;    // raw 32-bit buffer resource, gfx9 family
@@ -1488,13 +1492,17 @@ __device__ __forceinline__ void step_update(const KLoop<C>& k, Acc<C>& tot, cons
 }
 
 // The K loop. Vector-memory issue order per wave, fixed so that one
-// immediate wait covers every step:
+// immediate wait covers every step. With a two-step weight lead:
 //   prologue W(0) D(0) W(1) D(1); step q: wait(D(q), W(q)) barrier
-//   D(q+2) compute(q) W(q+2).
-// At step q's wait the requests after D(q) and W(q) are D(q+1) and W(q+1)
-// = kWaitVm instructions. The weights run two steps ahead, like the DMA (a
-// third step in flight queued more requests ahead of each step's own and ran
-// 1% slower), so one of the three register slots is free at any time.
+//   D(q+2) compute(q) W(q+2);
+// at step q's wait the requests after D(q) and W(q) are D(q+1) and W(q+1)
+// = kWaitVm instructions. With a one-step lead:
+//   prologue W(0) D(0) D(1); step q: wait(D(q), W(q)) barrier
+//   W(q+1) D(q+2) compute(q);
+// at step q's wait only D(q+1) follows W(q). A three-step weight lead queued
+// more requests ahead of each step's own and ran 1% slower on decode batches;
+// prefill, with four token groups of compute per step, runs 1-2% faster with
+// a one-step lead, decode 0.5% slower.
 template <class C, bool RESIDUAL, int NTG, bool FAST>
 __device__ __forceinline__ void k_loop(const KLoop<C>& k, Acc<C>& tot, char* c0, char* c1, char* c2, float* s0,
                                        float* s1, float* s2) {
@@ -1504,29 +1512,31 @@ __device__ __forceinline__ void k_loop(const KLoop<C>& k, Acc<C>& tot, char* c0,
   __builtin_amdgcn_sched_barrier(0);
   issue_dma<C>(k, 0, c0, s0);
   __builtin_amdgcn_sched_barrier(0);
-  w1 = load_wstep(k, 1);
+  if (C::kWLead == 2) w1 = load_wstep(k, 1);
   __builtin_amdgcn_sched_barrier(0);
   issue_dma<C>(k, 1, c1, s1);
   __builtin_amdgcn_sched_barrier(0);
-#define GOSSMX_STEP(QV, SLOT, CODES, SCL, NCODES, NSCL, NSLOT)                                       \
+#define GOSSMX_STEP(QV, SLOT, CODES, SCL, NCODES, NSCL, NEXT1, NEXT2)                               \
   {                                                                                                  \
     const int q = (QV);                                                                              \
     __builtin_amdgcn_sched_barrier(0);                                                               \
-    __builtin_amdgcn_s_waitcnt(C::kWaitDma); /* this wave's DMA for step q has landed */            \
+    __builtin_amdgcn_s_waitcnt(C::kWaitDma); /* this wave's DMA and weights for step q have landed */\
     __builtin_amdgcn_s_barrier();         /* ... and every other wave's; the slot of q-1 is free */  \
+    __builtin_amdgcn_sched_barrier(0);                                                               \
+    if (C::kWLead == 1) NEXT1 = load_wstep(k, q + 1);                                                \
     __builtin_amdgcn_sched_barrier(0);                                                               \
     issue_dma<C>(k, q + 2, NCODES, NSCL);                                                            \
     __builtin_amdgcn_sched_barrier(0);                                                               \
     if (k.wave_ok && q < k.nsteps) step_update<C, RESIDUAL, NTG, FAST>(k, tot, CODES, SCL, SLOT, q); \
     __builtin_amdgcn_sched_barrier(0);                                                               \
-    NSLOT = load_wstep(k, q + 2);                                                                    \
+    if (C::kWLead == 2) NEXT2 = load_wstep(k, q + 2);                                                \
     __builtin_amdgcn_sched_barrier(0);                                                               \
   }
   const int n_pad = (k.nsteps + 2) / 3 * 3;
   for (int q0 = 0; q0 < n_pad; q0 += 3) {
-    GOSSMX_STEP(q0, w0, c0, s0, c2, s2, w2)
-    GOSSMX_STEP(q0 + 1, w1, c1, s1, c0, s0, w0)
-    GOSSMX_STEP(q0 + 2, w2, c2, s2, c1, s1, w1)
+    GOSSMX_STEP(q0, w0, c0, s0, c2, s2, w1, w2)
+    GOSSMX_STEP(q0 + 1, w1, c1, s1, c0, s0, w2, w0)
+    GOSSMX_STEP(q0 + 2, w2, c2, s2, c1, s1, w0, w1)
   }
 #undef GOSSMX_STEP
 }
