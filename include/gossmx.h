@@ -70,7 +70,7 @@ typedef enum gossmx_status {
   GOSSMX_ERR_INVALID_DIMENSIONS = 3,  /* KernelError::InvalidDimensions */
   GOSSMX_ERR_NON_FINITE_INPUT = 4,    /* KernelError::NonFiniteInput */
   GOSSMX_ERR_UNAVAILABLE_BACKEND = 5, /* KernelError::UnavailableMatmulBackend (no gfx950 device) */
-  GOSSMX_ERR_DEVICE = 6,              /* HIP runtime error */
+  GOSSMX_ERR_DEVICE = 6,              /* HIP runtime error, or a kernel's internal consistency check */
   GOSSMX_ERR_OUT_OF_MEMORY = 7,
   GOSSMX_ERR_NON_FINITE_LOGITS = 8,   /* "CPU router produced non-finite logits" */
   GOSSMX_ERR_INJECTED_FAULT = 9,      /* gossmx_inject_fault test hook fired */
