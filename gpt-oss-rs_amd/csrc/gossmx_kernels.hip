@@ -2153,13 +2153,15 @@ __global__ __launch_bounds__(DownCombineGeom::kThreads, 2) void gemv_down_combin
 // has written the row's bf16 logits and quantized the row (launched without
 // its arrival counter). Every work-group selects for itself, so that no
 // cross-work-group signal or serial selection step separates the logits from
-// the weight stream: the activation image's DMA (the row does not depend on
-// the selection) and the logits are requested first; wave 0 ranks the keys
+// the weight stream: the logits are requested first; wave 0 ranks the keys
 // (stable_top_k, :3768-3778; experts e and e + 64 per lane, the keys read
 // 16 at a time from LDS); the selected experts in increasing index are the
 // work items (every bucket holds one route, so dispatch_offsets's order is
-// expert order). Work-group (x, y) then runs gemv_kernel<kGateUp, 8, 2>'s
-// tile group x for item y. Work-group (0, 0) also writes what the selection
+// expert order). Work-group (x, y) then requests the row's activation image
+// (DMA into LDS), its tiles' flags and biases and its weight ring together,
+// and runs gemv_kernel<kGateUp, 8, 2>'s tile group x for item y. (The DMA
+// cannot go out before the selection: the compiler waits for LDS DMA before
+// the selection's LDS accesses.) Work-group (0, 0) also writes what the selection
 // kernels write for the down launch and the caller: the selection, the
 // softmax weights (select_row_ranked's operations), bucket offsets, route
 // order and the work list, and the non-finite flag.
