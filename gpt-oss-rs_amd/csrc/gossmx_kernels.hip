@@ -2207,6 +2207,22 @@ __global__ __launch_bounds__(RouteGemvGeom::kThreads, 4) void route_gemv_kernel(
   store_exp2_entry(exp2_entry);
   __syncthreads();
 
+  // Waves 1-7 request the row's activation image (DMA into LDS; the row does
+  // not depend on the selection) and wait for it while wave 0 selects, so
+  // the image is complete at the selection's barrier.
+  if (wave != 0) {
+    const __amdgpu_buffer_rsrc_t act_codes = buffer_rsrc(a.actv), act_scl = buffer_rsrc(a.acts);
+    const int i = lane >> 2, g = lane & 3, part = i & 1;
+    for (int k = wave - 1; k < nsets; k += Geo::kWaves - 1) {  // uniform per wave
+      const int b = k * P + i / V;
+      dma16(act_codes, img + k * kTinySetBytes, b < B ? (b * 2 + part) * 64 + g * 16 : 0, 0);
+    }
+    for (int k = wave - 1; k * 64 < nsets * 16; k += Geo::kWaves - 1) {  // uniform per wave
+      const int f = k * 64 + lane, b = f >> 1;
+      dma4(act_scl, reinterpret_cast<char*>(s_scl) + k * 256, b < B ? (b * 2 + (f & 1)) * 4 : 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's share of the image is in LDS
+  }
   // Wave 0 selects: lane e's key ranks among all keys (16 per LDS round
   // trip), experts e and e + 64 per lane.
   if (wave == 0) {
@@ -2260,21 +2276,8 @@ __global__ __launch_bounds__(RouteGemvGeom::kThreads, 4) void route_gemv_kernel(
   L.nq4 = nq4;
   L.nfull4 = B >> 2;
   const int g0 = half * (Geo::kHalfSets * P / 4);
-  // The image of row 0 (gemv_kernel's DMA at one token), the tile's
-  // fast-path flag and bias (branch-free, from valid addresses), then the
-  // ring: all in flight together.
-  {
-    const __amdgpu_buffer_rsrc_t act_codes = buffer_rsrc(a.actv), act_scl = buffer_rsrc(a.acts);
-    const int i = lane >> 2, g = lane & 3, part = i & 1;
-    for (int k = wave; k < nsets; k += Geo::kWaves) {  // uniform per wave
-      const int b = k * P + i / V;
-      dma16(act_codes, img + k * kTinySetBytes, b < B ? (b * 2 + part) * 64 + g * 16 : 0, 0);
-    }
-    for (int k = wave; k * 64 < nsets * 16; k += Geo::kWaves) {  // uniform per wave
-      const int f = k * 64 + lane, b = f >> 1;
-      dma4(act_scl, reinterpret_cast<char*>(s_scl) + k * 256, b < B ? (b * 2 + (f & 1)) * 4 : 0, 0);
-    }
-  }
+  // The tile's fast-path flag and bias (branch-free, from valid addresses),
+  // then the ring: all in flight together.
   const int row = tile0 * kTileRows + nl;
   const uint8_t fast_raw = a.w.fast[(size_t)expert * a.w.tiles + safe_tile];
   const float* bias_p =
@@ -2284,13 +2287,7 @@ __global__ __launch_bounds__(RouteGemvGeom::kThreads, 4) void route_gemv_kernel(
   uint32_t ws[R];
 #pragma unroll
   for (int q = 0; q < R; ++q) gemv_load(L, g0 + q, wn[q], ws[q]);
-  // This wave's DMA has landed once at most the flag, the bias and the ring
-  // are outstanding.
-  constexpr int kWait = 2 + 2 * R;
-  static_assert(kWait < 64, "vmcnt field");
-  __builtin_amdgcn_s_waitcnt((kWait & 15) | ((kWait >> 4) << 14) | (7 << 4) | (15 << 8));
 
-  __syncthreads();  // every wave's DMA is in
   const bool fast = a.fast_ok && fast_raw != 0;
   const float bias = (a.bias != nullptr && ok && row < rows) ? bias_raw : 0.0f;
 
