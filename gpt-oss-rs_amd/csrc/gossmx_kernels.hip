@@ -148,14 +148,37 @@ __global__ void build_sigmoid_table_kernel(uint16_t* tab) {
   if (i < 65536u) tab[i] = sigmoid_bf16(i);
 }
 
+// The partner lane of a butterfly round over groups of 2 O lanes, taken in
+// increasing O: O = 1 and 2 swap lanes i ^ O (DPP quad permutes, no LDS
+// round trip); O = 4 and 8 take lane i's mirror within its 8- or 16-lane row
+// (DPP row_half_mirror, row_mirror), a lane of the other half whose value the
+// earlier rounds made equal to its whole half's; O = 16 swaps i ^ 16
+// (ds_swizzle), O = 32 i ^ 32 (ds_bpermute). After the rounds up to O every
+// lane of a 2 O-lane group holds the same result of an order-free operation
+// (max, top-k of distinct keys). Every lane of the group must execute it.
+template <int O>
+__device__ __forceinline__ uint32_t lane_partner(uint32_t v) {
+  if constexpr (O == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+  else if constexpr (O == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+  else if constexpr (O == 4) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false);
+  else if constexpr (O == 8) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false);
+  else if constexpr (O == 16) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401F);
+  else return __shfl_xor(v, 32);
+}
+__device__ __forceinline__ float half_wave_max(float m) {
+  m = fmaxf(m, __uint_as_float(lane_partner<1>(__float_as_uint(m))));
+  m = fmaxf(m, __uint_as_float(lane_partner<2>(__float_as_uint(m))));
+  m = fmaxf(m, __uint_as_float(lane_partner<4>(__float_as_uint(m))));
+  m = fmaxf(m, __uint_as_float(lane_partner<8>(__float_as_uint(m))));
+  return fmaxf(m, __uint_as_float(lane_partner<16>(__float_as_uint(m))));
+}
+
 // quantize_q8_block (lib.rs:1051-1065) for the 32 values held by a 32-lane
 // half wave (lane l32 holds value l32): scale = max|v| / 127, inverse =
 // 1 / scale (0 when scale is 0), q = clamp(round_half_away(v * inverse)).
 // max is order-free, so the butterfly gives the reference's fold.
 __device__ __forceinline__ void q8_half_wave(float v, float& q, float& scale) {
-  float mx = fabsf(v);
-#pragma unroll
-  for (int o = 16; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  const float mx = half_wave_max(fabsf(v));
   scale = mx / 127.0f;
   const float inv = scale == 0.0f ? 0.0f : 1.0f / scale;
   q = fminf(fmaxf(roundf(v * inv), -127.0f), 127.0f);
@@ -198,11 +221,7 @@ __device__ __forceinline__ void residual_q8_store_n(const float (&v)[N], const b
                                                     int first_blk, ActBuffers act) {
   float mx[N], q[N], s[N], r[N], rq[N], rs[N];
 #pragma unroll
-  for (int i = 0; i < N; ++i) mx[i] = fabsf(v[i]);
-#pragma unroll
-  for (int o = 16; o >= 1; o >>= 1)
-#pragma unroll
-    for (int i = 0; i < N; ++i) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], o));
+  for (int i = 0; i < N; ++i) mx[i] = half_wave_max(fabsf(v[i]));
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     s[i] = mx[i] / 127.0f;
@@ -212,9 +231,7 @@ __device__ __forceinline__ void residual_q8_store_n(const float (&v)[N], const b
     mx[i] = fabsf(r[i]);
   }
 #pragma unroll
-  for (int o = 16; o >= 1; o >>= 1)
-#pragma unroll
-    for (int i = 0; i < N; ++i) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], o));
+  for (int i = 0; i < N; ++i) mx[i] = half_wave_max(mx[i]);
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     rs[i] = mx[i] / 127.0f;
@@ -1367,7 +1384,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& t
       for (int tg = 0; tg < C::kNtg; ++tg) {
         if (tg < n_tg) {
           const float own0 = bf16r(tot[t][tg][0]), own1 = bf16r(tot[t][tg][1]);
-          const float recv = __shfl_xor(odd ? own0 : own1, 1);
+          const float recv = __uint_as_float(lane_partner<1>(__float_as_uint(odd ? own0 : own1)));
           const float gate = odd ? recv : own0;
           const float up = odd ? own1 : recv;
           const int c = tg * 8 + 2 * G + (odd ? 1 : 0);
