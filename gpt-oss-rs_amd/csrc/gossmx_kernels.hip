@@ -433,13 +433,17 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
 __device__ __forceinline__ void dispatch_offsets(const DispatchArgs& a, const int* s_tot, int* s_off, bool meta) {
   const int E = a.experts;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  __shared__ int s_part[kMaxExperts];
   __shared__ int s_scan[4];
-  int c = 0, full = 0, sc = 0, sf = 0;
+  __shared__ int s_parts[2];
+  // Per wave w and partial-chunk size v: experts of the wave with a larger
+  // partial chunk (s_gt) and with this size (s_eq), for the other wave's
+  // ranking.
+  __shared__ int s_gt[2][kChunkMax], s_eq[2][kChunkMax];
+  int c = 0, full = 0, sc = 0, sf = 0, part = 0, rank_in_wave = 0;
   if (wave < 2) {
     c = tid < E ? s_tot[tid] : 0;
     full = c / a.chunk;
-    s_part[tid] = c % a.chunk;
+    part = c % a.chunk;
     sc = c;
     sf = full;
 #pragma unroll
@@ -448,9 +452,29 @@ __device__ __forceinline__ void dispatch_offsets(const DispatchArgs& a, const in
       if (lane >= o) { sc += u; sf += v; }
     }
     if (lane == 63) { s_scan[2 * wave] = sc; s_scan[2 * wave + 1] = sf; }
+    if (meta) {
+      // Partial chunks are ranked by descending size, ties by expert: within
+      // the wave, by one ballot per size (lanes past E hold size 0 and never
+      // count).
+      const unsigned long long lt = (1ull << lane) - 1ull;
+      int gt_lane = 0, eq_lane = 0;  // for lane l < chunk: the wave's experts with a partial chunk > l, == l
+      for (int v = 1; v < a.chunk; ++v) {  // uniform
+        const unsigned long long m = __ballot(part == v);
+        const int n = __popcll(m);
+        rank_in_wave += (v > part ? n : 0) + (v == part ? __popcll(m & lt) : 0);
+        gt_lane += v > lane ? n : 0;
+        eq_lane = v == lane ? n : eq_lane;
+      }
+      const int n_parts = __popcll(__ballot(part > 0));
+      if (lane < a.chunk) {
+        s_gt[wave][lane] = gt_lane;
+        s_eq[wave][lane] = eq_lane;
+      }
+      if (lane == 0) s_parts[wave] = n_parts;
+    }
   }
   __syncthreads();
-  int off = 0, full_before = 0, total_full = 0, part = 0, parts = 0, before = 0;
+  int off = 0, full_before = 0, total_full = 0, parts = 0, before = 0;
   if (wave < 2) {
     if (wave == 1) { sc += s_scan[0]; sf += s_scan[1]; }
     total_full = s_scan[1] + s_scan[3];
@@ -459,12 +483,9 @@ __device__ __forceinline__ void dispatch_offsets(const DispatchArgs& a, const in
     if (tid < E) {
       s_off[tid] = off;
       if (meta) {
-        part = s_part[tid];
-        for (int f = 0; f < E; ++f) {
-          const int pf = s_part[f];
-          parts += pf > 0;
-          before += pf > part || (pf == part && f < tid);
-        }
+        parts = s_parts[0] + s_parts[1];
+        // Wave 0's experts all come before wave 1's.
+        before = rank_in_wave + (wave == 0 ? s_gt[1][part] : s_gt[0][part] + s_eq[0][part]);
       }
     }
   }
