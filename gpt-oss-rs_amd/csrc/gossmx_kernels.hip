@@ -1038,6 +1038,8 @@ __global__ __launch_bounds__(1024) void select_count_kernel(RouteArgs r, int row
   __shared__ uint64_t s_tab[32];
   if (tid < 32) s_tab[tid] = kExp2Tab[tid];
   if (tid < kMaxExperts) s_cnt[tid] = 0;
+  // Unrolled so that a thread's loads go out together.
+#pragma unroll 4
   for (int i = tid; i < nrows * E; i += 1024) {
     const size_t gi = (size_t)r0 * E + i;
     float v;
@@ -1071,12 +1073,19 @@ __global__ __launch_bounds__(1024) void place_kernel(DispatchArgs a, int routes_
   __shared__ int s_off[kMaxExperts];
   if (tid < kMaxExperts) {
     int tot = 0, pre = 0;
-    if (tid < E)
-      for (int v = 0; v < n_sel; ++v) {
-        const int c = cnt[(size_t)v * E + tid];
-        tot += c;
-        if (v < w) pre += c;
+    if (tid < E) {
+      // Eight selection work-groups' counts requested at a time.
+      for (int v0 = 0; v0 < n_sel; v0 += 8) {  // uniform
+        int cv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) cv[i] = v0 + i < n_sel ? cnt[(size_t)(v0 + i) * E + tid] : 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          tot += cv[i];
+          if (v0 + i < w) pre += cv[i];
+        }
       }
+    }
     s_tot[tid] = tot;
     s_pre[tid] = pre;
   }
