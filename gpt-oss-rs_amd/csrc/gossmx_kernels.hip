@@ -1364,10 +1364,12 @@ __device__ __forceinline__ void group_update_pipelined(Acc<C>& tot, const char* 
 // Shared GEMM epilogue: plain f32 stores, the down projection's bf16 rows,
 // or gate_up's SwiGLU and down-input quantization. `s_act` is LDS scratch of
 // at least count * (kGemmRows / 2 + 1) floats, free for reuse. Rows of tiles
-// past the end (row >= rows) are never stored.
+// past the end (row >= rows) are never stored. `s_slot` (kDown, nullable):
+// the item's route slots already in LDS (else they are read from route_slot).
 template <class C, int MODE, bool RESIDUAL>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& tot, const int n_tg, const int count,
-                                              const int start, const int tile0, float* s_act) {
+                                              const int start, const int tile0, float* s_act,
+                                              const int* s_slot = nullptr) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int nl = lane & 15, G = lane >> 4;
@@ -1387,7 +1389,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& t
               if (MODE == kPlain) {
                 a.out[(size_t)(start + c) * a.out_stride + row] = tot[t][tg][u];
               } else {
-                const int slot = a.route_slot[start + c];
+                const int slot = s_slot != nullptr ? s_slot[c] : a.route_slot[start + c];
                 a.y[(size_t)slot * rows + row] = bf16_bits(tot[t][tg][u]);  // bf16 (cpu_runner.rs:2945-2947)
               }
             }
@@ -1621,11 +1623,13 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
   // activation row indices, the tiles' fast-path flags and biases
   // (branch-free, from valid addresses; read after the barrier).
   __shared__ int s_row[C::kChunk];
-  int row_idx = -1;
+  __shared__ int s_slot[C::kChunk];  // kDown: the item's route slots, for the epilogue's stores
+  int row_idx = -1, slot_idx = -1;
   if (tid < C::kChunk && tid < count) {
     if (MODE == kPlain) row_idx = start + tid;
     else if (MODE == kGateUp) row_idx = a.route_tok[start + tid];
     else row_idx = start + tid;
+    if (MODE == kDown) slot_idx = a.route_slot[start + tid];
   }
   KLoop<C> k;
   k.B = B;
@@ -1669,6 +1673,7 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
   __shared__ __align__(16) char s_codes0[C::kSlotBytes], s_codes1[C::kSlotBytes], s_codes2[C::kSlotBytes];
   __shared__ __align__(16) float s_scl0[C::kSclSlot], s_scl1[C::kSclSlot], s_scl2[C::kSclSlot];
   if (tid < C::kChunk) s_row[tid] = row_idx;
+  if (MODE == kDown && tid < C::kChunk) s_slot[tid] = slot_idx;
   if (MODE == kGateUp) store_exp2_entry(exp2_entry);
   __syncthreads();
 
@@ -1722,7 +1727,8 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
   // work-group ends.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  gemm_epilogue<C, MODE, RESIDUAL>(a, tot, n_tg, count, start, tile0, reinterpret_cast<float*>(s_codes0));
+  gemm_epilogue<C, MODE, RESIDUAL>(a, tot, n_tg, count, start, tile0, reinterpret_cast<float*>(s_codes0),
+                                   MODE == kDown ? s_slot : nullptr);
 }
 
 // ---------------------------------------------------------------------------
