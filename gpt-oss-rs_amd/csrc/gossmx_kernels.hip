@@ -1174,8 +1174,19 @@ typedef __attribute__((address_space(3))) void* lds_ptr;
 //    count per expert), 73 VGPRs, 5 work-groups per CU.
 //  GemmHuge (2 tiles, 32 rows, 4 blocks, 8 waves) serves prefill-sized
 //    batches, where the FP4->f16 conversion of a weight block is shared by
-//    four token groups.
-template <int TILES, int NTOK, int GROUPS, int WAVES = 8, int MIN_WAVES = 4, int WLEAD = 2>
+//    four token groups. Its gate_up grid pins weight tiles to XCDs (PIN_XCD).
+//
+// PIN_XCD: work-groups reach the eight XCDs round-robin in launch order, so
+// with a grid row of n_x work-groups the chunks of one expert (consecutive
+// rows) would read the same tile through different L2s whenever n_x is not a
+// multiple of 8. A pinned gate_up grid pads its rows to a multiple of 8
+// (padding work-groups return at once) and rotates each row by the item's
+// expert, so tile column x of expert e always runs on XCD (x + e) mod 8: the
+// later chunks of a popular expert hit the L2 the first one filled, and the
+// XCDs that get one column fewer differ from expert to expert. It pays when
+// experts have many chunks (prefill); with one or two chunks per expert the
+// padding's imbalance costs more than the L2 hits save.
+template <int TILES, int NTOK, int GROUPS, int WAVES = 8, int MIN_WAVES = 4, int WLEAD = 2, bool PIN_XCD = false>
 struct GemmCfg {
   static constexpr int kWaves = WAVES;                    // waves per work-group
   static constexpr int kThreads = 64 * WAVES;
@@ -1197,6 +1208,7 @@ struct GemmCfg {
   // Steps by which the weight requests lead their use (1 or 2; the DMA leads
   // by 2).
   static constexpr int kWLead = WLEAD;
+  static constexpr bool kPinXcd = PIN_XCD;  // gate_up grid rows pinned to XCDs (above)
   // s_waitcnt immediate for "the DMA and the weights of step q have landed":
   // issued after them are D(q+1) and, with a two-step lead, W(q+1) (see
   // k_loop). expcnt and lgkmcnt are not waited on.
@@ -1212,7 +1224,7 @@ struct GemmCfg {
 };
 using GemmBig = GemmCfg<2, 16, 1, 4, 5>;
 using GemmSmall = GemmCfg<1, 8, 2, 4, 5>;
-using GemmHuge = GemmCfg<2, 32, 1, 8, 4, 1>;
+using GemmHuge = GemmCfg<2, 32, 1, 8, 4, 1, true>;
 static_assert(GemmBig::kChunk == kChunk && GemmSmall::kChunk == kSmallChunk && GemmHuge::kChunk == kHugeChunk,
               "work item sizes");
 constexpr int kBufferFlags = 0x00020000;    // raw 32-bit buffer resource, gfx9 family
@@ -1369,7 +1381,8 @@ __device__ __forceinline__ void group_update_pipelined(Acc<C>& tot, const char* 
 template <class C, int MODE, bool RESIDUAL>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& tot, const int n_tg, const int count,
                                               const int start, const int tile0, float* s_act,
-                                              const int* s_slot = nullptr) {
+                                              const int* s_slot = nullptr, int wg_x = -1) {
+  if (wg_x < 0) wg_x = (int)blockIdx.x;  // the work-group's tile column
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int nl = lane & 15, G = lane >> 4;
@@ -1453,12 +1466,12 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& t
     for (int i = 0; i < kPer; ++i) {
       const int item = hw + i * kHalfWaves;
       const int c = item / kBlocksPerWg, h = item % kBlocksPerWg;
-      live[i] = item < count * kBlocksPerWg && (int)blockIdx.x * kBlocksPerWg + h < blocks_next;  // uniform per half wave
+      live[i] = item < count * kBlocksPerWg && wg_x * kBlocksPerWg + h < blocks_next;  // uniform per half wave
       v[i] = live[i] ? s_act[c * kActStride + h * kBlock + l32] : 0.0f;
       if (live[i] && !isfinite(v[i])) atomicOr(a.err, kErrNonFiniteInput);
     }
     residual_q8_store_n<kPer, RESIDUAL>(v, live, l32, hw, kHalfWaves, kBlocksPerWg, (size_t)start, blocks_next,
-                                        (int)blockIdx.x * kBlocksPerWg, nx);
+                                        wg_x * kBlocksPerWg, nx);
   }
 }
 
@@ -1615,7 +1628,14 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
     count = rec.z;
   }
   const int rows = (int)a.w.rows, B = (int)a.w.blocks;
-  const int tile0 = (blockIdx.x * C::kWaves + wave) * C::kWaveTiles;
+  int wg_x = (int)blockIdx.x;  // tile column
+  if (C::kPinXcd && MODE == kGateUp) {
+    const int n_x = ((int)a.w.tiles + C::kWgTiles - 1) / C::kWgTiles;
+    const int p_x = (int)gridDim.x;  // n_x padded to a multiple of 8
+    wg_x = ((int)blockIdx.x + p_x - (expert & 7)) % p_x;
+    if (wg_x >= n_x) return;  // padding; uniform over the work-group
+  }
+  const int tile0 = (wg_x * C::kWaves + wave) * C::kWaveTiles;
   const int n_tg = (count + 7) >> 3;
   const int nq4 = (B + 3) >> 2;
 
@@ -1728,7 +1748,7 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   gemm_epilogue<C, MODE, RESIDUAL>(a, tot, n_tg, count, start, tile0, reinterpret_cast<float*>(s_codes0),
-                                   MODE == kDown ? s_slot : nullptr);
+                                   MODE == kDown ? s_slot : nullptr, wg_x);
 }
 
 // ---------------------------------------------------------------------------
@@ -2869,7 +2889,9 @@ hipError_t launch_route_select(const RouteArgs& r, const DispatchArgs& d, int* c
 template <class C>
 static hipError_t launch_gemm_cfg(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream,
                                   hipEvent_t start, hipEvent_t stop) {
-  const dim3 grid((unsigned)((a.w.tiles + C::kWgTiles - 1) / C::kWgTiles), (unsigned)grid_work);
+  const unsigned n_x = (unsigned)((a.w.tiles + C::kWgTiles - 1) / C::kWgTiles);
+  const bool pin = C::kPinXcd && mode == kGateUp;
+  const dim3 grid(pin ? (n_x + 7) & ~7u : n_x, (unsigned)grid_work);
   const dim3 block(C::kThreads);
   auto go = [&](auto kernel) {
     if (start) hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, start, stop, 0, a);
