@@ -383,6 +383,8 @@ namespace gossmx {
 int set_error(int status, const char* message) { return fail(status, "%s", message); }
 
 const gossmx_moe_config* layer_config(const gossmx_layer* layer) { return layer ? &layer->cfg : nullptr; }
+int context_device(const gossmx_ctx* ctx) { return ctx->device; }
+hipStream_t context_stream(const gossmx_ctx* ctx) { return ctx->stream; }
 
 void tiled_image_bytes(size_t experts, size_t rows, size_t blocks, size_t* nib_bytes, size_t* scl_bytes) {
   const TiledWeights t = make_tiled(experts, rows, blocks);

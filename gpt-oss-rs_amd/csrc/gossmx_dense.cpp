@@ -1,13 +1,15 @@
-// The dense path around the MoE block, on the host CPU: the rest of a GPT-OSS
-// decoder step as CpuModel::prepare_step runs it (crates/gpt-oss-model-runner/
-// src/cpu_runner.rs:2103-2333, forward_layer_batch :2335-2586), with each
-// layer's MoE half (post-attention RMSNorm, moe_batch, residual add) on the GPU
-// through gossmx_moe_forward_residual.
+// The dense path around the MoE block: the rest of a GPT-OSS decoder step as
+// CpuModel::prepare_step runs it (crates/gpt-oss-model-runner/src/
+// cpu_runner.rs:2103-2333, forward_layer_batch :2335-2586). Norms, RoPE,
+// attention and the KV cache run on the host; the projections and each
+// layer's MoE half (post-attention RMSNorm, moe_batch, residual add, through
+// gossmx_moe_forward_residual) on the GPU.
 //
 // - bf16 projections: Kernels::bf16_matvec (gpt-oss-cpu-kernels lib.rs:314-341)
 //   with its 16 fixed reduction lanes, multiply then add, lanes folded 0..15
-//   (scalar_bf16_dot lib.rs:1007-1029; the AVX2 and AVX-512 lanes keep the same
-//   16 logical lanes), then += bias (project_bf16[_batch] cpu_runner.rs:2689-2792).
+//   (scalar_bf16_dot lib.rs:1007-1029), then += bias (project_bf16[_batch]
+//   cpu_runner.rs:2689-2792): dense_proj_kernel, over copies of the Q/K/V/O
+//   weights and lm_head made in HBM when the model is created.
 // - RMSNorm boundaries: norm_boundary (:2680-2687) over Kernels::rms_norm
 //   (lib.rs:699-730, the same 16-lane sum of squares).
 // - YaRN RoPE (YarnRope :3927-4013) with its bf16 boundaries.
@@ -54,138 +56,6 @@ inline uint16_t bf16_bits(float f) {
 }
 inline float bf16_f32(uint16_t b) { return u2f((uint32_t)b << 16); }
 inline float bf16_round(float f) { return bf16_f32(bf16_bits(f)); }
-
-// ---------------------------------------------------------------------------
-// 16-lane bf16 dot products. One weight row against NX input rows at once, so
-// the weight row is read once per NX outputs. Lane l of every variant holds
-// the products of elements i = l (mod 16) in increasing i, exactly as the
-// reference's lanes do; the multiply and the add are separate roundings (no
-// FMA: this file builds with -ffp-contract=off, so the products and sums
-// below are never contracted).
-
-typedef float f32x8 __attribute__((vector_size(32)));
-typedef uint32_t u32x8 __attribute__((vector_size(32)));
-typedef uint16_t u16x8 __attribute__((vector_size(16)));
-
-// 8 bf16 values -> f32 (the bits shifted into the high half).
-__attribute__((target("avx2"), always_inline)) inline f32x8 widen(const uint16_t* p) {
-  u16x8 h;
-  std::memcpy(&h, p, 16);
-  const u32x8 u = __builtin_convertvector(h, u32x8) << 16;
-  f32x8 f;
-  std::memcpy(&f, &u, 32);
-  return f;
-}
-
-template <int NX>
-__attribute__((target("avx2"))) void dots_avx2(const uint16_t* w, const uint16_t* const* x, size_t n, float* out) {
-  f32x8 lo[NX], hi[NX];
-  for (int r = 0; r < NX; ++r) lo[r] = hi[r] = f32x8{0, 0, 0, 0, 0, 0, 0, 0};
-  size_t i = 0;
-  for (; i + 16 <= n; i += 16) {
-    const f32x8 wl = widen(w + i), wh = widen(w + i + 8);
-    for (int r = 0; r < NX; ++r) {
-      const f32x8 pl = wl * widen(x[r] + i);
-      const f32x8 ph = wh * widen(x[r] + i + 8);
-      lo[r] = lo[r] + pl;
-      hi[r] = hi[r] + ph;
-    }
-  }
-  for (int r = 0; r < NX; ++r) {
-    float lanes[16];
-    std::memcpy(lanes, &lo[r], 32);
-    std::memcpy(lanes + 8, &hi[r], 32);
-    for (size_t j = i, l = 0; j < n; ++j, ++l) lanes[l] += bf16_f32(w[j]) * bf16_f32(x[r][j]);
-    float s = 0.0f;
-    for (int l = 0; l < 16; ++l) s += lanes[l];
-    out[r] = s;
-  }
-}
-
-// The same 16 lanes as one 512-bit vector.
-typedef float f32x16 __attribute__((vector_size(64)));
-typedef uint32_t u32x16 __attribute__((vector_size(64)));
-typedef uint16_t u16x16 __attribute__((vector_size(32)));
-
-__attribute__((target("avx512f"), always_inline)) inline f32x16 widen16(const uint16_t* p) {
-  u16x16 h;
-  std::memcpy(&h, p, 32);
-  const u32x16 u = __builtin_convertvector(h, u32x16) << 16;
-  f32x16 f;
-  std::memcpy(&f, &u, 64);
-  return f;
-}
-
-template <int NX>
-__attribute__((target("avx512f"))) void dots_avx512(const uint16_t* w, const uint16_t* const* x, size_t n,
-                                                    float* out) {
-  f32x16 acc[NX];
-  for (int r = 0; r < NX; ++r) acc[r] = f32x16{};
-  size_t i = 0;
-  for (; i + 16 <= n; i += 16) {
-    const f32x16 wv = widen16(w + i);
-    for (int r = 0; r < NX; ++r) {
-      const f32x16 p = wv * widen16(x[r] + i);
-      acc[r] = acc[r] + p;
-    }
-  }
-  for (int r = 0; r < NX; ++r) {
-    float lanes[16];
-    std::memcpy(lanes, &acc[r], 64);
-    for (size_t j = i, l = 0; j < n; ++j, ++l) lanes[l] += bf16_f32(w[j]) * bf16_f32(x[r][j]);
-    float s = 0.0f;
-    for (int l = 0; l < 16; ++l) s += lanes[l];
-    out[r] = s;
-  }
-}
-
-float dot_scalar(const uint16_t* w, const uint16_t* x, size_t n) {
-  float lanes[16] = {0};
-  size_t i = 0;
-  for (; i + 16 <= n; i += 16)
-    for (int l = 0; l < 16; ++l) lanes[l] += bf16_f32(w[i + l]) * bf16_f32(x[i + l]);
-  for (size_t l = 0; i < n; ++i, ++l) lanes[l] += bf16_f32(w[i]) * bf16_f32(x[i]);
-  float s = 0.0f;
-  for (int l = 0; l < 16; ++l) s += lanes[l];
-  return s;
-}
-
-// 2: AVX-512F, 1: AVX2, 0: neither (the host's widest vector unit).
-int vector_level() {
-  static const int level = [] {
-    __builtin_cpu_init();
-    if (__builtin_cpu_supports("avx512f")) return 2;
-    return __builtin_cpu_supports("avx2") ? 1 : 0;
-  }();
-  return level;
-}
-
-// out[r] = dot(w, x[r]) for r < nx.
-void dots(const uint16_t* w, const uint16_t* const* x, size_t nx, size_t n, float* out) {
-  if (vector_level() == 2) {
-    size_t r = 0;
-    for (; r + 4 <= nx; r += 4) dots_avx512<4>(w, x + r, n, out + r);
-    switch (nx - r) {
-      case 3: dots_avx512<3>(w, x + r, n, out + r); break;
-      case 2: dots_avx512<2>(w, x + r, n, out + r); break;
-      case 1: dots_avx512<1>(w, x + r, n, out + r); break;
-      default: break;
-    }
-    return;
-  }
-  if (vector_level() == 0) {
-    for (size_t r = 0; r < nx; ++r) out[r] = dot_scalar(w, x[r], n);
-    return;
-  }
-  size_t r = 0;
-  for (; r + 4 <= nx; r += 4) dots_avx2<4>(w, x + r, n, out + r);
-  switch (nx - r) {
-    case 3: dots_avx2<3>(w, x + r, n, out + r); break;
-    case 2: dots_avx2<2>(w, x + r, n, out + r); break;
-    case 1: dots_avx2<1>(w, x + r, n, out + r); break;
-    default: break;
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Worker pool: run(n, fn) calls fn(i) for every i < n on the pool's threads
@@ -252,28 +122,6 @@ class Pool {
   uint64_t generation_ = 0;
   bool stop_ = false;
 };
-
-// out[r][o] = dot(w[o], x[r]) (+ bias[o]) for r < m, o < rows: project_bf16_batch.
-// Work items are blocks of output rows; each weight row meets every input row
-// while it is in cache.
-void project(Pool& pool, const uint16_t* w, size_t rows, size_t cols, const uint16_t* x, size_t m,
-             const float* bias, float* out) {
-  constexpr size_t kRowsPerItem = 32;
-  std::vector<const uint16_t*> xs(m);
-  for (size_t r = 0; r < m; ++r) xs[r] = x + r * cols;
-  const size_t items = (rows + kRowsPerItem - 1) / kRowsPerItem;
-  pool.run(items, [&](size_t item) {
-    float d[64];
-    const size_t lo = item * kRowsPerItem, hi = std::min(rows, lo + kRowsPerItem);
-    for (size_t o = lo; o < hi; ++o) {
-      for (size_t r0 = 0; r0 < m; r0 += 64) {
-        const size_t nr = std::min<size_t>(64, m - r0);
-        dots(w + o * cols, xs.data() + r0, nr, cols, d);
-        for (size_t r = 0; r < nr; ++r) out[(r0 + r) * rows + o] = bias ? d[r] + bias[o] : d[r];
-      }
-    }
-  });
-}
 
 // norm_boundary: bf16 -> f32, rms_norm, -> bf16.
 void norm_boundary(const uint16_t* x, const float* w, size_t n, float eps, uint16_t* out) {
@@ -430,6 +278,31 @@ int check_config(const gossmx_model_config* c) {
 
 }  // namespace
 
+// The model's device side: the projection weights and lm_head copied to HBM,
+// and grow-only f32 staging for the projections' inputs and outputs (device
+// buffers, and pinned host buffers for the copies).
+struct DenseDevice {
+  struct Layer {
+    const uint16_t *q, *k, *v, *o;
+    const float *qb, *kb, *vb, *ob;
+  };
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::vector<void*> weights;  // device allocations of the copies
+  std::vector<Layer> layers;
+  const uint16_t* lm_head = nullptr;
+  float *d_in = nullptr, *d_out = nullptr, *h_in = nullptr, *h_out = nullptr;
+  size_t in_cap = 0, out_cap = 0;  // floats
+  ~DenseDevice() {
+    (void)hipSetDevice(device);
+    for (void* p : weights) (void)hipFree(p);
+    (void)hipFree(d_in);
+    (void)hipFree(d_out);
+    (void)hipHostFree(h_in);
+    (void)hipHostFree(h_out);
+  }
+};
+
 struct gossmx_model {
   gossmx_ctx* ctx = nullptr;
   gossmx_model_config cfg{};
@@ -441,10 +314,85 @@ struct gossmx_model {
   std::vector<KvCache> caches;
   size_t position = 0;
   std::unique_ptr<Pool> pool;
+  DenseDevice dev;
   double dense_seconds = 0.0, moe_seconds = 0.0;
 };
 
 namespace {
+
+int hip_err(hipError_t e, const char* what) {
+  char msg[256];
+  std::snprintf(msg, sizeof msg, "%s: %s", what, hipGetErrorString(e));
+  return err(e == hipErrorOutOfMemory ? GOSSMX_ERR_OUT_OF_MEMORY : GOSSMX_ERR_DEVICE, msg);
+}
+
+#define DENSE_HIP(expr, what)                        \
+  do {                                               \
+    const hipError_t e_ = (expr);                    \
+    if (e_ != hipSuccess) return hip_err(e_, what);  \
+  } while (0)
+
+// A copy of n elements of T in device memory, owned by the model.
+template <class T>
+int upload(DenseDevice& D, const T* src, size_t n, const T** dst) {
+  void* p = nullptr;
+  DENSE_HIP(hipMalloc(&p, n * sizeof(T)), "model weights allocation");
+  D.weights.push_back(p);
+  DENSE_HIP(hipMemcpy(p, src, n * sizeof(T), hipMemcpyHostToDevice), "model weights upload");
+  *dst = static_cast<const T*>(p);
+  return GOSSMX_OK;
+}
+
+int grow(float** dev, float** host, size_t* cap, size_t n) {
+  if (n <= *cap) return GOSSMX_OK;
+  (void)hipFree(*dev);
+  (void)hipHostFree(*host);
+  *dev = *host = nullptr;
+  *cap = 0;
+  DENSE_HIP(hipMalloc(dev, n * sizeof(float)), "projection buffer");
+  DENSE_HIP(hipHostMalloc(host, n * sizeof(float)), "projection staging");
+  *cap = n;
+  return GOSSMX_OK;
+}
+
+// One projection of the rows `in` (m x cols bf16) by w ([rows][cols] bf16 in
+// HBM) + bias, into out (m x rows f32, host).
+struct Projection {
+  const uint16_t* w;
+  const float* bias;
+  size_t rows;
+  float* out;
+};
+
+// Runs the projections of one input on the GPU (project_bf16_batch): one copy
+// in, one launch each, one copy out, one synchronization.
+int gpu_project(gossmx_model* M, const uint16_t* in, size_t m, size_t cols, const Projection* p, size_t count) {
+  DenseDevice& D = M->dev;
+  size_t total = 0;
+  for (size_t i = 0; i < count; ++i) total += m * p[i].rows;
+  DENSE_HIP(hipSetDevice(D.device), "hipSetDevice");
+  if (int st = grow(&D.d_in, &D.h_in, &D.in_cap, m * cols)) return st;
+  if (int st = grow(&D.d_out, &D.h_out, &D.out_cap, total)) return st;
+  for (size_t i = 0; i < m * cols; ++i) D.h_in[i] = bf16_f32(in[i]);
+  DENSE_HIP(hipMemcpyAsync(D.d_in, D.h_in, m * cols * sizeof(float), hipMemcpyHostToDevice, D.stream),
+            "projection input copy");
+  size_t off = 0;
+  for (size_t i = 0; i < count; ++i) {
+    DENSE_HIP(gossmx::launch_dense_proj(p[i].w, p[i].bias, D.d_in, (int)p[i].rows, (int)cols, (int)m, D.d_out + off,
+                                        D.stream),
+              "projection launch");
+    off += m * p[i].rows;
+  }
+  DENSE_HIP(hipMemcpyAsync(D.h_out, D.d_out, total * sizeof(float), hipMemcpyDeviceToHost, D.stream),
+            "projection output copy");
+  DENSE_HIP(hipStreamSynchronize(D.stream), "projection");
+  off = 0;
+  for (size_t i = 0; i < count; ++i) {
+    std::memcpy(p[i].out, D.h_out + off, m * p[i].rows * sizeof(float));
+    off += m * p[i].rows;
+  }
+  return GOSSMX_OK;
+}
 
 // One layer-major step over m rows at positions model->position + r
 // (prepare_step with every row in one sequence). Writes the last row's logits.
@@ -466,11 +414,11 @@ int run_step(gossmx_model* M, const uint32_t* tokens, size_t m, float* logits) {
   Pool& pool = *M->pool;
   for (size_t li = 0; li < c.layers; ++li) {
     const gossmx_dense_layer& L = M->layers[li];
+    const DenseDevice::Layer& DL = M->dev.layers[li];
     const KvCache& cache = M->caches[li];
     pool.run(m, [&](size_t r) { norm_boundary(&hidden[r * H], L.input_norm, H, c.rms_norm_eps, &normalized[r * H]); });
-    project(pool, L.q_weight, QW, H, normalized.data(), m, L.q_bias, q.data());
-    project(pool, L.k_weight, KW, H, normalized.data(), m, L.k_bias, k.data());
-    project(pool, L.v_weight, KW, H, normalized.data(), m, L.v_bias, v.data());
+    const Projection qkv[3] = {{DL.q, DL.qb, QW, q.data()}, {DL.k, DL.kb, KW, k.data()}, {DL.v, DL.vb, KW, v.data()}};
+    if (int st = gpu_project(M, normalized.data(), m, H, qkv, 3)) return st;
     uint16_t* sk = &staged_k[li * m * KW];
     uint16_t* sv = &staged_v[li * m * KW];
     // Rows are independent once staged: row r attends to the committed rows and
@@ -511,7 +459,8 @@ int run_step(gossmx_model* M, const uint32_t* tokens, size_t m, float* logits) {
       attention(&q[r * QW], visible, key, value, L.sinks, c.heads, c.kv_heads, c.head_dim, ctx.data(), sc);
       for (size_t i = 0; i < QW; ++i) attn[r * QW + i] = bf16_bits(ctx[i]);
     });
-    project(pool, L.o_weight, H, QW, attn.data(), m, L.o_bias, proj.data());
+    const Projection o_proj = {DL.o, DL.ob, H, proj.data()};
+    if (int st = gpu_project(M, attn.data(), m, QW, &o_proj, 1)) return st;
     pool.run(m, [&](size_t r) {
       for (size_t i = 0; i < H; ++i)
         after[r * H + i] = bf16_bits(bf16_f32(hidden[r * H + i]) + bf16_round(proj[r * H + i]));
@@ -531,7 +480,8 @@ int run_step(gossmx_model* M, const uint32_t* tokens, size_t m, float* logits) {
   // Final norm and lm_head for the last row (the only row whose logits are required).
   std::vector<uint16_t> fin(H);
   norm_boundary(&hidden[(m - 1) * H], M->final_norm, H, c.rms_norm_eps, fin.data());
-  project(pool, M->lm_head, c.vocab, H, fin.data(), 1, nullptr, logits);
+  const Projection head = {M->dev.lm_head, nullptr, c.vocab, logits};
+  if (int st = gpu_project(M, fin.data(), 1, H, &head, 1)) return st;
   bool finite = true;
   for (size_t i = 0; i < c.vocab; ++i) {
     logits[i] = bf16_round(logits[i]);
@@ -592,6 +542,30 @@ int gossmx_model_create(gossmx_ctx* ctx, const gossmx_model_config* config, cons
   if (!threads) threads = std::max(1u, std::thread::hardware_concurrency());
   M->pool.reset(new Pool(std::min<size_t>(threads, 64)));
   reset_caches(M);
+  // The projection weights and lm_head go to the context's GPU.
+  const size_t H = config->hidden, QW = config->heads * config->head_dim, KW = config->kv_heads * config->head_dim;
+  DenseDevice& D = M->dev;
+  D.device = gossmx::context_device(ctx);
+  D.stream = gossmx::context_stream(ctx);
+  int st = hipSetDevice(D.device) == hipSuccess ? GOSSMX_OK : err(GOSSMX_ERR_DEVICE, "hipSetDevice failed");
+  D.layers.resize(config->layers);
+  for (size_t li = 0; li < config->layers && st == GOSSMX_OK; ++li) {
+    const gossmx_dense_layer& L = layers[li];
+    DenseDevice::Layer& DL = D.layers[li];
+    if (!st) st = upload(D, L.q_weight, QW * H, &DL.q);
+    if (!st) st = upload(D, L.k_weight, KW * H, &DL.k);
+    if (!st) st = upload(D, L.v_weight, KW * H, &DL.v);
+    if (!st) st = upload(D, L.o_weight, H * QW, &DL.o);
+    if (!st) st = upload(D, L.q_bias, QW, &DL.qb);
+    if (!st) st = upload(D, L.k_bias, KW, &DL.kb);
+    if (!st) st = upload(D, L.v_bias, KW, &DL.vb);
+    if (!st) st = upload(D, L.o_bias, H, &DL.ob);
+  }
+  if (!st) st = upload(D, lm_head, config->vocab * H, &D.lm_head);
+  if (st) {
+    delete M;
+    return st;
+  }
   *out = M;
   return GOSSMX_OK;
 }

@@ -219,6 +219,11 @@ constexpr int kSelftestCodes = 8;
 constexpr int kSelftestDirty = 5 * 4 * 6;  // exponents x byte positions x neighbour patterns
 constexpr int kSelftestFloats = kSelftestCodes + 256 + kSelftestCodes + 16 * kSelftestDirty;
 hipError_t launch_selftest(float* out, hipStream_t stream);
+// The model's dense bf16 projections (16-lane dot order): out[r * rows + o] =
+// dot(w[o], x[r]) (+ bias[o]) for r < m, o < rows; w bf16 [rows][cols], x f32
+// [m][cols], bias f32 [rows] or null.
+hipError_t launch_dense_proj(const uint16_t* w, const float* bias, const float* x, int rows, int cols, int m,
+                             float* out, hipStream_t stream);
 
 }  // namespace gossmx
 
@@ -233,6 +238,8 @@ struct gossmx_moe_config;
 namespace gossmx {
 int set_error(int status, const char* message);
 const gossmx_moe_config* layer_config(const gossmx_layer* layer);
+int context_device(const gossmx_ctx* ctx);
+hipStream_t context_stream(const gossmx_ctx* ctx);
 void tiled_image_bytes(size_t experts, size_t rows, size_t blocks, size_t* nib_bytes, size_t* scl_bytes);
 int tiled_image_read(gossmx_ctx* ctx, const gossmx_weights* w, uint8_t* nib, uint8_t* scl);
 int tiled_image_create(gossmx_ctx* ctx, size_t experts, size_t rows, size_t blocks, const uint8_t* nib,

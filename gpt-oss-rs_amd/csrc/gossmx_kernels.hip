@@ -3065,4 +3065,134 @@ hipError_t launch_selftest(float* out, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Dense bf16 projections of the model around the block: the attention's
+// Q/K/V/O projections and lm_head (Kernels::bf16_matvec, gpt-oss-cpu-kernels
+// lib.rs:314-341, through project_bf16[_batch] cpu_runner.rs:2689-2792):
+// out[r * rows + o] = dot(w[o], x[r]) (+ bias[o]).
+//
+// dot keeps the reference's 16 reduction lanes (scalar_bf16_dot lib.rs:
+// 1007-1029): lane l sums w[k] * x[k] over k = l, l + 16, ... in increasing k,
+// from 0.0, each product and each sum rounded to f32 (no fma); the lanes then
+// fold as 0.0 + lane 0 + lane 1 + ... + lane 15. x arrives as f32 (the exact
+// values of the bf16 inputs).
+//
+// A work-group is kDenseRows weight rows x 16 lanes: thread tid runs lane
+// tid % 16 of row kDenseRows * blockIdx.x + tid / 16 for the TOK rows of x of
+// group blockIdx.y. K moves through LDS in chunks of kDenseKc values (a
+// multiple of 16, so a lane's elements stay in order), the next chunk's loads
+// in flight while the current chunk is summed. At one token the kernel streams
+// the weights (lm_head: 201,088 x 2,880 bf16, 1.16 GB per call).
+constexpr int kDenseRows = 16;
+constexpr int kDenseKc = 256;
+constexpr int kDenseWStride = kDenseKc + 8;  // LDS row stride (u16): consecutive rows start 4 banks apart
+
+template <int TOK>
+struct DenseChunk {
+  static constexpr int kXPieces = (TOK * kDenseKc / 4 + 255) / 256;  // float4 pieces per thread
+  u32x4 w[2];  // pieces tid and tid + 256 of the 16 x kDenseKc weight chunk (8 values each)
+  float4 x[kXPieces];
+};
+
+template <int TOK>
+__device__ __forceinline__ void dense_load(DenseChunk<TOK>& c, const uint16_t* w, const float* x, int rows, int cols,
+                                           int m, int o0, int r0, int k0, int tid) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int p = tid + 256 * q, o = o0 + (p >> 5), k = k0 + (p & 31) * 8;
+    if (o < rows && (cols & 7) == 0 && k + 8 <= cols) {
+      c.w[q] = *reinterpret_cast<const u32x4*>(w + (size_t)o * cols + k);
+    } else {  // ragged edge: values past the matrix read as zero and are never summed
+      uint32_t v[4] = {0u, 0u, 0u, 0u};
+      for (int e = 0; e < 8; ++e)
+        if (o < rows && k + e < cols) v[e >> 1] |= (uint32_t)w[(size_t)o * cols + k + e] << (16 * (e & 1));
+      c.w[q] = u32x4{v[0], v[1], v[2], v[3]};
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < DenseChunk<TOK>::kXPieces; ++q) {
+    const int p = tid + 256 * q, r = r0 + (p >> 6), k = k0 + (p & 63) * 4;
+    if (p < TOK * kDenseKc / 4 && r < m && (cols & 3) == 0 && k + 4 <= cols) {
+      c.x[q] = *reinterpret_cast<const float4*>(x + (size_t)r * cols + k);
+    } else {
+      float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int e = 0; e < 4; ++e)
+        if (p < TOK * kDenseKc / 4 && r < m && k + e < cols) v[e] = x[(size_t)r * cols + k + e];
+      c.x[q] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+  }
+}
+
+template <int TOK>
+__global__ __launch_bounds__(256) void dense_proj_kernel(const uint16_t* __restrict__ w, const float* __restrict__ bias,
+                                                         const float* __restrict__ x, int rows, int cols, int m,
+                                                         float* __restrict__ out) {
+  static_assert(kDenseRows * 16 == 256 && kDenseKc % 16 == 0 && TOK <= 16, "thread map");
+  __shared__ __align__(16) uint16_t s_w[kDenseRows * kDenseWStride];
+  __shared__ __align__(16) float s_x[TOK * kDenseKc];  // also the fold buffer: [row][token][lane]
+  const int tid = threadIdx.x, i = tid >> 4, l = tid & 15;
+  const int o0 = blockIdx.x * kDenseRows, r0 = blockIdx.y * TOK;
+  float acc[TOK];
+#pragma unroll
+  for (int t = 0; t < TOK; ++t) acc[t] = 0.0f;
+  DenseChunk<TOK> c;
+  dense_load<TOK>(c, w, x, rows, cols, m, o0, r0, 0, tid);
+  for (int k0 = 0; k0 < cols; k0 += kDenseKc) {
+    __syncthreads();  // every lane has summed the previous chunk
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int p = tid + 256 * q;
+      *reinterpret_cast<u32x4*>(&s_w[(p >> 5) * kDenseWStride + (p & 31) * 8]) = c.w[q];
+    }
+#pragma unroll
+    for (int q = 0; q < DenseChunk<TOK>::kXPieces; ++q) {
+      const int p = tid + 256 * q;
+      if (p < TOK * kDenseKc / 4) *reinterpret_cast<float4*>(&s_x[(p >> 6) * kDenseKc + (p & 63) * 4]) = c.x[q];
+    }
+    __syncthreads();
+    if (k0 + kDenseKc < cols) dense_load<TOK>(c, w, x, rows, cols, m, o0, r0, k0 + kDenseKc, tid);
+    const int kc = min(kDenseKc, cols - k0);
+#pragma unroll 4
+    for (int j = 0; j < kDenseKc / 16; ++j) {
+      const int k = j * 16 + l;
+      if (k < kc) {
+        const float wv = __uint_as_float((uint32_t)s_w[i * kDenseWStride + k] << 16);
+#pragma unroll
+        for (int t = 0; t < TOK; ++t) acc[t] = acc[t] + wv * s_x[t * kDenseKc + k];
+      }
+    }
+  }
+  // The 16 lanes of each (row, token) fold in lane order, from 0.0.
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < TOK; ++t) s_x[(i * TOK + t) * 16 + l] = acc[t];
+  __syncthreads();
+  if (tid < kDenseRows * TOK) {
+    const int fi = tid / TOK, ft = tid % TOK;
+    const int o = o0 + fi, r = r0 + ft;
+    if (o < rows && r < m) {
+      const float* v = &s_x[(fi * TOK + ft) * 16];
+      float s = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) s = s + v[q];
+      if (bias != nullptr) s = s + bias[o];
+      out[(size_t)r * rows + o] = s;
+    }
+  }
+}
+
+hipError_t launch_dense_proj(const uint16_t* w, const float* bias, const float* x, int rows, int cols, int m,
+                             float* out, hipStream_t stream) {
+  if (rows <= 0 || cols <= 0 || m <= 0) return hipSuccess;
+  const unsigned gx = (unsigned)((rows + kDenseRows - 1) / kDenseRows);
+  if (m == 1)
+    hipLaunchKernelGGL(dense_proj_kernel<1>, dim3(gx, 1), dim3(256), 0, stream, w, bias, x, rows, cols, m, out);
+  else if (m <= 4)
+    hipLaunchKernelGGL(dense_proj_kernel<4>, dim3(gx, 1), dim3(256), 0, stream, w, bias, x, rows, cols, m, out);
+  else
+    hipLaunchKernelGGL(dense_proj_kernel<16>, dim3(gx, (unsigned)((m + 15) / 16)), dim3(256), 0, stream, w, bias, x,
+                       rows, cols, m, out);
+  return hipGetLastError();
+}
+
 }  // namespace gossmx
