@@ -281,8 +281,9 @@ def run_traffic_probe(args, cfg: dict) -> int:
 
 def run_model(args) -> int:
     """the random-init GPT-OSS-20B forward, a 63-token prefill and 8
-    greedy decode steps, on the dense CPU path (gossmx_model_*, host threads)
-    with every layer's MoE block on the GPU. Times whole generations and splits
+    greedy decode steps through gossmx_model_*: norms, RoPE, attention and the
+    KV cache on host threads, the Q/K/V/O projections, lm_head and every
+    layer's MoE block on the GPU. Times whole generations and splits
     them into dense and MoE wall time; the CPU baseline is the oracle's
     whole-model run (dense path and MoE on the host) on the same weights, whose
     tokens and logits bits must equal the product's."""
@@ -329,10 +330,10 @@ def run_model(args) -> int:
         "metric": "configs[3] GPT-OSS-20B forward: token forwards/s (63-token prefill + 8 greedy decodes)",
         "value": forwards / wall, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": wall * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16 dense path (host) + MXFP4 x residual-Q8 MoE (GPU)",
+        "dtype": "bf16 projections and lm_head (GPU), bf16 attention (host) + MXFP4 x residual-Q8 MoE (GPU)",
         "data": "synthetic (random-init weights, random prompt)",
         "config": {"workload": f"configs[3]: random-init GPT-OSS-20B, {layers} layers, 63-token prefill + "
-                               f"{decode_steps} greedy decode steps, dense path on {args.cpu_threads} host threads",
+                               f"{decode_steps} greedy decode steps, projections on the GPU, attention on {args.cpu_threads} host threads",
                    "layers": layers, "prompt": int(prompt.size), "decode_steps": decode_steps},
         "dense_s": dense_s, "moe_s": moe_s, "moe_share": moe_s / wall, "greedy_tokens": tokens.tolist(),
         "roofline": None, "cpu_baseline": None,

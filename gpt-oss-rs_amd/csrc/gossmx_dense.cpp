@@ -206,15 +206,17 @@ void rope_apply(const Rope& r, float* v, size_t heads, size_t position) {
 // Attention for one query over `tokens` visible key/value rows, oldest first
 // (attention_one_staged): bf16 QK dot, bf16 scale, softmax with the sink in
 // the denominator, bf16 probabilities, f32 accumulation, bf16 output.
-// key(t) / value(t) return the row of visible token t (all kv heads).
+// key(t) / value(t) return the row of visible token t (all kv heads). Heads
+// are independent: this computes heads [h_begin, h_end) of out.
 
 template <class KeyRow, class ValueRow>
 void attention(const float* q_all, size_t tokens, const KeyRow& key, const ValueRow& value, const float* sinks,
-               size_t heads, size_t kv_heads, size_t head_dim, float* out, std::vector<float>& scores) {
+               size_t heads, size_t kv_heads, size_t head_dim, float* out, std::vector<float>& scores,
+               size_t h_begin, size_t h_end) {
   const size_t groups = heads / kv_heads;
   const float scale = 1.0f / std::sqrt((float)head_dim);
   scores.resize(tokens);
-  for (size_t h = 0; h < heads; ++h) {
+  for (size_t h = h_begin; h < h_end; ++h) {
     const float* q = q_all + h * head_dim;
     const size_t kvh = h / groups;
     for (size_t t = 0; t < tokens; ++t) {
@@ -408,7 +410,7 @@ int run_step(gossmx_model* M, const uint32_t* tokens, size_t m, float* logits) {
   double moe = 0.0;
   const size_t base = M->position;
   std::vector<uint16_t> hidden(m * H), normalized(m * H), after(m * H), attn(m * QW);
-  std::vector<float> q(m * QW), k(m * KW), v(m * KW), proj(m * H), scores;
+  std::vector<float> q(m * QW), k(m * KW), v(m * KW), proj(m * H), attn_f(m * QW), scores;
   std::vector<uint16_t> staged_k(c.layers * m * KW), staged_v(c.layers * m * KW);
   for (size_t r = 0; r < m; ++r) std::memcpy(&hidden[r * H], M->embedding + (size_t)tokens[r] * H, H * 2);
   Pool& pool = *M->pool;
@@ -435,9 +437,15 @@ int run_step(gossmx_model* M, const uint32_t* tokens, size_t m, float* logits) {
         sv[r * KW + i] = bf16_bits(v[r * KW + i]);
       }
     });
-    pool.run(m, [&](size_t r) {
+    // Tasks of (row, block of heads): a one-row step still spreads over the
+    // pool.
+    const size_t head_blocks = std::min<size_t>(c.heads, m >= 16 ? 1 : (32 + m - 1) / m);
+    const size_t per_block = (c.heads + head_blocks - 1) / head_blocks;
+    pool.run(m * head_blocks, [&](size_t task) {
       thread_local std::vector<float> sc;
-      thread_local std::vector<float> ctx;
+      const size_t r = task / head_blocks, hb = task % head_blocks;
+      const size_t h_begin = hb * per_block, h_end = std::min(c.heads, h_begin + per_block);
+      if (h_begin >= h_end) return;
       // Positions below `base` are committed (slot p % capacity of the ring),
       // the others are this step's staged rows.
       const size_t combined = cache.len + r + 1;
@@ -455,9 +463,9 @@ int run_step(gossmx_model* M, const uint32_t* tokens, size_t m, float* logits) {
         const size_t p = first + t;
         return p < base ? cv + (p % cap) * KW : rv + (p - base) * KW;
       };
-      ctx.resize(QW);
-      attention(&q[r * QW], visible, key, value, L.sinks, c.heads, c.kv_heads, c.head_dim, ctx.data(), sc);
-      for (size_t i = 0; i < QW; ++i) attn[r * QW + i] = bf16_bits(ctx[i]);
+      float* ctx = &attn_f[r * QW];
+      attention(&q[r * QW], visible, key, value, L.sinks, c.heads, c.kv_heads, c.head_dim, ctx, sc, h_begin, h_end);
+      for (size_t i = h_begin * c.head_dim; i < h_end * c.head_dim; ++i) attn[r * QW + i] = bf16_bits(ctx[i]);
     });
     const Projection o_proj = {DL.o, DL.ob, H, proj.data()};
     if (int st = gpu_project(M, attn.data(), m, QW, &o_proj, 1)) return st;
@@ -647,7 +655,8 @@ int gossmx_attention(const float* query, const uint16_t* keys, const uint16_t* v
   const size_t visible = std::min(tokens, window), first = tokens - visible, KW = kv_heads * head_dim;
   std::vector<float> scores;
   attention(query, visible, [&](size_t t) { return keys + (first + t) * KW; },
-            [&](size_t t) { return values + (first + t) * KW; }, sinks, heads, kv_heads, head_dim, out, scores);
+            [&](size_t t) { return values + (first + t) * KW; }, sinks, heads, kv_heads, head_dim, out, scores, 0,
+            heads);
   return GOSSMX_OK;
 }
 

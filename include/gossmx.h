@@ -395,12 +395,15 @@ int gossmx_inject_fault(gossmx_ctx* ctx, int armed);
 int gossmx_selftest(gossmx_ctx* ctx);
 
 /* ---------------------------------------------------------------------------
- * The dense path around the block, on the host CPU (crates/gpt-oss-model-runner/
- * src/cpu_runner.rs): a GPT-OSS model whose attention, RoPE, dense projections,
- * norms and lm_head run as the reference's CPU runner runs them, bit for bit,
- * and whose MoE halves run on the GPU through gossmx_moe_forward_residual
- * (host memory). Weights are host memory, borrowed (they and the MoE layers must
- * outlive the model). A model holds one sequence's KV caches. */
+ * The dense path around the block (crates/gpt-oss-model-runner/src/
+ * cpu_runner.rs): a GPT-OSS model that computes what the reference's CPU runner
+ * computes, bit for bit. Attention, RoPE, norms and the KV caches run on host
+ * threads. The Q/K/V/O projections and lm_head run on the context's GPU with the
+ * reference's 16-lane dot order, over copies of those matrices made in HBM by
+ * gossmx_model_create (about 2.4 GB for GPT-OSS-20B). The MoE halves run on
+ * the GPU through gossmx_moe_forward_residual (host memory). The embedding,
+ * the norm weights, the sinks and the MoE layers stay borrowed and must outlive
+ * the model. A model holds one sequence's KV caches. */
 typedef struct gossmx_model gossmx_model;
 
 /* CpuGptOssConfig (cpu_runner.rs:252-291) and the sequence's context cap
