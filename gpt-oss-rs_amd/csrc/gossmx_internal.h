@@ -224,6 +224,17 @@ hipError_t launch_selftest(float* out, hipStream_t stream);
 // [m][cols], bias f32 [rows] or null.
 hipError_t launch_dense_proj(const uint16_t* w, const float* bias, const float* x, int rows, int cols, int m,
                              float* out, hipStream_t stream);
+// One token through up to three projections of the same input in one launch
+// (count <= 3; cols a multiple of 8, at most 4096); the same dot order.
+// wg_begin is filled by the launcher.
+struct DenseSet {
+  const uint16_t* w[3];
+  const float* bias[3];
+  float* out[3];
+  int rows[3];
+  int wg_begin[4];
+};
+hipError_t launch_dense_gemv(const DenseSet& set, int count, const float* x, int cols, hipStream_t stream);
 
 }  // namespace gossmx
 

@@ -3181,6 +3181,86 @@ __global__ __launch_bounds__(256) void dense_proj_kernel(const uint16_t* __restr
   }
 }
 
+// One token, up to three projections of the same input in one launch (Q, K
+// and V): the same dot, with the work-group's 16 weight rows for the whole K
+// range staged in LDS by loads that are all in flight at once, so the
+// work-group waits for one memory round trip instead of one per K chunk.
+// Work-groups [wg_begin[i], wg_begin[i + 1]) serve projection i. cols is a
+// multiple of 8 and at most kDenseGemvMaxCols.
+constexpr int kDenseGemvMaxCols = 4096;
+constexpr int kDenseGemvPieces = kDenseRows * kDenseGemvMaxCols / 8 / 256;  // 16-byte weight pieces per thread
+
+__global__ __launch_bounds__(256) void dense_gemv_kernel(DenseSet set, const float* __restrict__ x, int cols) {
+  extern __shared__ __align__(16) char s_dyn[];
+  __shared__ float s_fold[kDenseRows * 16];
+  const int stride = cols + 8;  // u16 per LDS row
+  uint16_t* s_w = reinterpret_cast<uint16_t*>(s_dyn);
+  float* s_x = reinterpret_cast<float*>(s_dyn + (size_t)kDenseRows * stride * 2);
+  const int tid = threadIdx.x, i = tid >> 4, l = tid & 15;
+  const int b = (int)blockIdx.x;
+  const int pi = b >= set.wg_begin[2] ? 2 : (b >= set.wg_begin[1] ? 1 : 0);
+  const uint16_t* w = set.w[pi];
+  const int rows = set.rows[pi], o0 = (b - set.wg_begin[pi]) * kDenseRows;
+  const int per_row = cols >> 3, n_w = kDenseRows * per_row;
+  u32x4 v[kDenseGemvPieces];
+#pragma unroll
+  for (int q = 0; q < kDenseGemvPieces; ++q) {
+    const int p = tid + 256 * q;
+    const int r = p / per_row, k = (p - r * per_row) * 8;
+    v[q] = u32x4{0u, 0u, 0u, 0u};
+    if (p < n_w && o0 + r < rows) v[q] = *reinterpret_cast<const u32x4*>(w + (size_t)(o0 + r) * cols + k);
+  }
+  float4 xv[kDenseGemvMaxCols / 4 / 256];
+#pragma unroll
+  for (int q = 0; q < kDenseGemvMaxCols / 4 / 256; ++q) {
+    const int p = tid + 256 * q;
+    xv[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (p * 4 < cols) xv[q] = *reinterpret_cast<const float4*>(x + p * 4);
+  }
+#pragma unroll
+  for (int q = 0; q < kDenseGemvPieces; ++q) {
+    const int p = tid + 256 * q;
+    const int r = p / per_row, k = (p - r * per_row) * 8;
+    if (p < n_w) *reinterpret_cast<u32x4*>(&s_w[r * stride + k]) = v[q];
+  }
+#pragma unroll
+  for (int q = 0; q < kDenseGemvMaxCols / 4 / 256; ++q) {
+    const int p = tid + 256 * q;
+    if (p * 4 < cols) *reinterpret_cast<float4*>(&s_x[p * 4]) = xv[q];
+  }
+  __syncthreads();
+  float acc = 0.0f;
+  const uint16_t* wr = &s_w[i * stride];
+#pragma unroll 8
+  for (int k = l; k < cols; k += 16) acc = acc + __uint_as_float((uint32_t)wr[k] << 16) * s_x[k];
+  s_fold[i * 16 + l] = acc;
+  __syncthreads();
+  if (tid < kDenseRows && o0 + tid < rows) {
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) s = s + s_fold[tid * 16 + q];
+    if (set.bias[pi] != nullptr) s = s + set.bias[pi][o0 + tid];
+    set.out[pi][o0 + tid] = s;
+  }
+}
+
+size_t dense_gemv_lds(int cols) { return (size_t)kDenseRows * (cols + 8) * 2 + (size_t)cols * 4; }
+
+hipError_t launch_dense_gemv(const DenseSet& set, int count, const float* x, int cols, hipStream_t stream) {
+  if (count <= 0 || count > 3 || cols <= 0 || cols % 8 != 0 || cols > kDenseGemvMaxCols) return hipErrorInvalidValue;
+  DenseSet s = set;
+  int wg = 0;
+  for (int i = 0; i < 3; ++i) {
+    s.wg_begin[i] = wg;
+    if (i < count) wg += (s.rows[i] + kDenseRows - 1) / kDenseRows;
+  }
+  s.wg_begin[3] = wg;
+  if (wg == 0) return hipSuccess;
+  hipLaunchKernelGGL(dense_gemv_kernel, dim3((unsigned)wg), dim3(256), (unsigned)dense_gemv_lds(cols), stream, s, x,
+                     cols);
+  return hipGetLastError();
+}
+
 hipError_t launch_dense_proj(const uint16_t* w, const float* bias, const float* x, int rows, int cols, int m,
                              float* out, hipStream_t stream) {
   if (rows <= 0 || cols <= 0 || m <= 0) return hipSuccess;
