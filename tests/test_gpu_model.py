@@ -77,6 +77,33 @@ def test_small_model_matches_oracle(tiny):
     assert dense > 0 and moe > 0
 
 
+# Projection shapes off the fast paths: Q width 18 (O's input is not a
+# multiple of 8 values, so the K-chunked kernel's element-wise loads run), Q/K/V
+# and vocab row counts that are not multiples of the 16-row work-group, and a
+# 20-token prompt (a full and a partial 16-row input group).
+RAGGED = dict(vocab=301, hidden=64, layers=2, heads=3, kv_heads=1, head_dim=6, sliding_window=5, context_cap=64,
+              rms_norm_eps=1e-5, **ROPE_20B)
+
+
+def test_ragged_projection_shapes_match_oracle(ctx):
+    cfg = dict(RAGGED)
+    w = synth.model_weights(cfg, synth.numpy_normal(np.random.default_rng(7)))
+    hosts = [O.synthetic_layer(7, i, experts=4, hidden=64, intermediate=32, top_k=2) for i in range(cfg["layers"])]
+    for L, h in zip(w["layers"], hosts):
+        L["moe_host"] = h
+    model, keep = build(ctx, cfg, w, hosts)
+    try:
+        oracle = O.ModelHost(cfg, w["embedding"], w["final_norm"], w["lm_head"], w["layers"])
+        prompt = (np.arange(20, dtype=np.uint32) * 13) % 301
+        st, want_tokens, want_logits = O.model_generate(oracle, prompt, 4, threads=4)
+        assert st == O.OK
+        tokens, logits = model.generate(prompt, 4)
+        assert (tokens == want_tokens).all()
+        assert_bits(logits, want_logits)
+    finally:
+        release(model, keep)
+
+
 def test_small_model_chunked_prefill(tiny):
     cfg, model, oracle = tiny
     _, _, want = O.model_generate(oracle, PROMPT, 0, threads=4)
