@@ -19,7 +19,7 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
 ]
-# Host-only sources (.cpp: the store and the dense CPU path) build as plain C++
+# Host-only sources (.cpp: the store and the dense path's host side) build as plain C++
 # with the HIP runtime headers.
 HOST_FLAGS = [
     "-x", "c++", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", "-O3", "-std=c++17", "-fPIC",

@@ -671,7 +671,7 @@ class MoeLayer:
 
 
 class Model:
-    """A GPT-OSS model on the dense CPU path with GPU MoE layers (gossmx_model_*).
+    """A GPT-OSS model (gossmx_model_*): attention on host threads, projections, lm_head and MoE layers on the GPU.
 
     `layers` is a list of dicts with the gossmx_dense_layer tensors (numpy
     arrays: norms, biases and sinks f32, matrices bf16 bits as uint16), the

@@ -1,4 +1,4 @@
-"""A GPT-OSS model on the dense CPU path with its MoE blocks on the GPU
+"""A GPT-OSS model with its attention on the host and its projections and MoE blocks on the GPU
 (gossmx_model_*) against the oracle's whole-model restatement
 (oracle_model_generate): greedy tokens and every logits bit, for a small model
 and for configs[3], the random-init GPT-OSS-20B forward (63-token prefill,
