@@ -185,14 +185,21 @@ Rope make_rope(const gossmx_model_config& c) {
   return r;
 }
 
+// The bf16 cosine and sine of a position depend on (position, i) only: they
+// are computed once per call and shared by every head.
 void rope_apply(const Rope& r, float* v, size_t heads, size_t position) {
   const size_t half = r.head_dim / 2;
+  thread_local std::vector<float> table;
+  table.resize(2 * half);
+  for (size_t i = 0; i < half; ++i) {
+    const float angle = (float)position * r.inv_freq[i];
+    table[i] = bf16_round(cosf(angle) * r.attention_scale);
+    table[half + i] = bf16_round(sinf(angle) * r.attention_scale);
+  }
   for (size_t h = 0; h < heads; ++h) {
     float* p = v + h * r.head_dim;
     for (size_t i = 0; i < half; ++i) {
-      const float angle = (float)position * r.inv_freq[i];
-      const float cosine = bf16_round(cosf(angle) * r.attention_scale);
-      const float sine = bf16_round(sinf(angle) * r.attention_scale);
+      const float cosine = table[i], sine = table[half + i];
       const float left = bf16_round(p[i]), right = bf16_round(p[half + i]);
       const float left_cosine = bf16_round(left * cosine), right_sine = bf16_round(right * sine);
       const float right_cosine = bf16_round(right * cosine), left_sine = bf16_round(left * sine);
