@@ -93,6 +93,10 @@ struct gossmx_ctx {
   std::vector<hipEvent_t> event_pool;
   double op_ms[GOSSMX_OP_COUNT] = {0};
   uint64_t op_launches[GOSSMX_OP_COUNT] = {0};
+  // Pinned host staging of the host-memory calls' outputs and the error flags,
+  // read back by one synchronization (grow-only).
+  char* h_stage = nullptr;
+  size_t stage_cap = 0;
   // scratch
   DevBuf x, injected, logits, selected, weights, act1v, act1s, bucket, route_tok, route_slot, work, act2v, act2s, y,
       cnt, normw, next,
@@ -243,17 +247,22 @@ int fold_profile(gossmx_ctx* ctx) {
   return GOSSMX_OK;
 }
 
-// Reads and clears the sticky device error flags (synchronizes).
-int check_device_errors(gossmx_ctx* ctx) {
-  int flags = 0;
-  HIP_TRY(hipMemcpyAsync(&flags, ctx->err, sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "read error flags");
-  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
-  if (flags == 0) return GOSSMX_OK;
+// Clears the sticky device error flags after a read that found `flags` set,
+// and returns the error they name.
+int device_flags_fail(gossmx_ctx* ctx, int flags) {
   HIP_TRY(launch_clear_ints(ctx->err, 1, ctx->stream), "clear error flags");
   HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
   if (flags & kErrWorkOrder) return fail(GOSSMX_ERR_DEVICE, "internal: work list not in the order a kernel relies on");
   if (flags & kErrNonFiniteLogits) return fail(GOSSMX_ERR_NON_FINITE_LOGITS, "router produced non-finite logits");
   return fail(GOSSMX_ERR_NON_FINITE_INPUT, "kernel input contains a non-finite value");
+}
+
+// Reads and clears the sticky device error flags (synchronizes).
+int check_device_errors(gossmx_ctx* ctx) {
+  int flags = 0;
+  HIP_TRY(hipMemcpyAsync(&flags, ctx->err, sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "read error flags");
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  return flags == 0 ? GOSSMX_OK : device_flags_fail(ctx, flags);
 }
 
 int set_device(int device) {
@@ -508,6 +517,7 @@ void gossmx_ctx_destroy(gossmx_ctx* ctx) {
   for (void* p : ctx->retired) (void)hipFree(p);
   if (ctx->err) (void)hipFree(ctx->err);
   if (ctx->sig_tab) (void)hipFree(ctx->sig_tab);
+  if (ctx->h_stage) (void)hipHostFree(ctx->h_stage);
   if (ctx->own_stream && ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -1046,7 +1056,33 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
             "combine launch");
   }
 
-  if (host) {
+  const bool rows_only = !io->router_logits && !io->selected && !io->routing_weights && !io->route_order &&
+                         !io->trace_down && !io->trace_gate_up && !io->trace_swiglu;
+  if (host && rows_only) {
+    // The error flags and the output rows come back in one stream sequence
+    // into pinned staging and one synchronization; the caller's buffers are
+    // written only when the flags are clear.
+    const size_t out_bytes = io->output ? m * H * 4 : 0, next_bytes = residual ? m * H * 2 : 0;
+    const size_t need = 16 + out_bytes + next_bytes;
+    if (need > ctx->stage_cap) {
+      if (ctx->h_stage) HIP_TRY(hipHostFree(ctx->h_stage), "hipHostFree");
+      ctx->h_stage = nullptr;
+      ctx->stage_cap = 0;
+      HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ctx->h_stage), need), "pinned staging");
+      ctx->stage_cap = need;
+    }
+    int* flags = reinterpret_cast<int*>(ctx->h_stage);
+    HIP_TRY(hipMemcpyAsync(flags, ctx->err, sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "read error flags");
+    if (out_bytes)
+      HIP_TRY(hipMemcpyAsync(ctx->h_stage + 16, output, out_bytes, hipMemcpyDeviceToHost, ctx->stream), "D2H output");
+    if (next_bytes)
+      HIP_TRY(hipMemcpyAsync(ctx->h_stage + 16 + out_bytes, next, next_bytes, hipMemcpyDeviceToHost, ctx->stream),
+              "D2H next");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (*flags != 0) return device_flags_fail(ctx, *flags);
+    if (out_bytes) std::memcpy(io->output, ctx->h_stage + 16, out_bytes);
+    if (next_bytes) std::memcpy(next_residual, ctx->h_stage + 16 + out_bytes, next_bytes);
+  } else if (host) {
     if ((s = check_device_errors(ctx))) return s;
     if (io->output)
       HIP_TRY(hipMemcpyAsync(io->output, output, m * H * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H output");
