@@ -385,29 +385,23 @@ int gpu_project(gossmx_model* M, const uint16_t* in, size_t m, size_t cols, cons
   for (size_t i = 0; i < m * cols; ++i) D.h_in[i] = bf16_f32(in[i]);
   DENSE_HIP(hipMemcpyAsync(D.d_in, D.h_in, m * cols * sizeof(float), hipMemcpyHostToDevice, D.stream),
             "projection input copy");
-  // One token through small matrices (Q/K/V, O): one launch whose work-groups
-  // stage their whole K range at once. lm_head and batches: the K-chunked
-  // kernel, one launch per projection.
-  const bool one_launch = m == 1 && count <= 3 && cols % 8 == 0 && cols <= 4096 && total <= 65536;
+  // One launch per group. One token through small matrices (Q/K/V, O):
+  // work-groups stage their whole K range at once; lm_head and batches: the
+  // K-chunked kernel.
+  if (count > 3) return err(GOSSMX_ERR_INVALID_ARGUMENT, "internal: more than three projections in a group");
+  gossmx::DenseSet set{};
   size_t off = 0;
-  if (one_launch) {
-    gossmx::DenseSet set{};
-    for (size_t i = 0; i < count; ++i) {
-      set.w[i] = p[i].w;
-      set.bias[i] = p[i].bias;
-      set.out[i] = D.d_out + off;
-      set.rows[i] = (int)p[i].rows;
-      off += p[i].rows;
-    }
-    DENSE_HIP(gossmx::launch_dense_gemv(set, (int)count, D.d_in, (int)cols, D.stream), "projection launch");
-  } else {
-    for (size_t i = 0; i < count; ++i) {
-      DENSE_HIP(gossmx::launch_dense_proj(p[i].w, p[i].bias, D.d_in, (int)p[i].rows, (int)cols, (int)m,
-                                          D.d_out + off, D.stream),
-                "projection launch");
-      off += m * p[i].rows;
-    }
+  for (size_t i = 0; i < count; ++i) {
+    set.w[i] = p[i].w;
+    set.bias[i] = p[i].bias;
+    set.out[i] = D.d_out + off;
+    set.rows[i] = (int)p[i].rows;
+    off += m * p[i].rows;
   }
+  const bool whole_k = m == 1 && cols % 8 == 0 && cols <= 4096 && total <= 65536;
+  DENSE_HIP(whole_k ? gossmx::launch_dense_gemv(set, (int)count, D.d_in, (int)cols, D.stream)
+                    : gossmx::launch_dense_proj(set, (int)count, D.d_in, (int)cols, (int)m, D.stream),
+            "projection launch");
   DENSE_HIP(hipMemcpyAsync(D.h_out, D.d_out, total * sizeof(float), hipMemcpyDeviceToHost, D.stream),
             "projection output copy");
   DENSE_HIP(hipStreamSynchronize(D.stream), "projection");

@@ -219,14 +219,10 @@ constexpr int kSelftestCodes = 8;
 constexpr int kSelftestDirty = 5 * 4 * 6;  // exponents x byte positions x neighbour patterns
 constexpr int kSelftestFloats = kSelftestCodes + 256 + kSelftestCodes + 16 * kSelftestDirty;
 hipError_t launch_selftest(float* out, hipStream_t stream);
-// The model's dense bf16 projections (16-lane dot order): out[r * rows + o] =
-// dot(w[o], x[r]) (+ bias[o]) for r < m, o < rows; w bf16 [rows][cols], x f32
-// [m][cols], bias f32 [rows] or null.
-hipError_t launch_dense_proj(const uint16_t* w, const float* bias, const float* x, int rows, int cols, int m,
-                             float* out, hipStream_t stream);
-// One token through up to three projections of the same input in one launch
-// (count <= 3; cols a multiple of 8, at most 4096); the same dot order.
-// wg_begin is filled by the launcher.
+// The model's dense bf16 projections (16-lane dot order), up to three of the
+// same input in one launch: out_p[r * rows_p + o] = dot(w_p[o], x[r])
+// (+ bias_p[o]) for r < m, o < rows_p; w bf16 [rows][cols], x f32 [m][cols],
+// bias f32 [rows] or null. wg_begin is filled by the launchers.
 struct DenseSet {
   const uint16_t* w[3];
   const float* bias[3];
@@ -234,6 +230,9 @@ struct DenseSet {
   int rows[3];
   int wg_begin[4];
 };
+hipError_t launch_dense_proj(const DenseSet& set, int count, const float* x, int cols, int m, hipStream_t stream);
+// One token through up to three projections with the whole K range of a
+// work-group staged at once (cols a multiple of 8, at most 4096).
 hipError_t launch_dense_gemv(const DenseSet& set, int count, const float* x, int cols, hipStream_t stream);
 
 }  // namespace gossmx

@@ -3123,15 +3123,21 @@ __device__ __forceinline__ void dense_load(DenseChunk<TOK>& c, const uint16_t* w
   }
 }
 
+// Work-group columns [wg_begin[p], wg_begin[p + 1]) serve projection p of
+// `set` (up to three projections of the same input in one launch).
 template <int TOK>
-__global__ __launch_bounds__(256) void dense_proj_kernel(const uint16_t* __restrict__ w, const float* __restrict__ bias,
-                                                         const float* __restrict__ x, int rows, int cols, int m,
-                                                         float* __restrict__ out) {
+__global__ __launch_bounds__(256) void dense_proj_kernel(DenseSet set, const float* __restrict__ x, int cols, int m) {
   static_assert(kDenseRows * 16 == 256 && kDenseKc % 16 == 0 && TOK <= 16, "thread map");
   __shared__ __align__(16) uint16_t s_w[kDenseRows * kDenseWStride];
   __shared__ __align__(16) float s_x[TOK * kDenseKc];  // also the fold buffer: [row][token][lane]
   const int tid = threadIdx.x, i = tid >> 4, l = tid & 15;
-  const int o0 = blockIdx.x * kDenseRows, r0 = blockIdx.y * TOK;
+  const int b = (int)blockIdx.x;
+  const int pi = b >= set.wg_begin[2] ? 2 : (b >= set.wg_begin[1] ? 1 : 0);
+  const uint16_t* w = set.w[pi];
+  const float* bias = set.bias[pi];
+  float* out = set.out[pi];
+  const int rows = set.rows[pi];
+  const int o0 = (b - set.wg_begin[pi]) * kDenseRows, r0 = blockIdx.y * TOK;
   float acc[TOK];
 #pragma unroll
   for (int t = 0; t < TOK; ++t) acc[t] = 0.0f;
@@ -3168,7 +3174,7 @@ __global__ __launch_bounds__(256) void dense_proj_kernel(const uint16_t* __restr
   for (int t = 0; t < TOK; ++t) s_x[(i * TOK + t) * 16 + l] = acc[t];
   __syncthreads();
   if (tid < kDenseRows * TOK) {
-    const int fi = tid / TOK, ft = tid % TOK;
+    const int fi = tid % kDenseRows, ft = tid / kDenseRows;  // consecutive threads: consecutive outputs
     const int o = o0 + fi, r = r0 + ft;
     if (o < rows && r < m) {
       const float* v = &s_x[(fi * TOK + ft) * 16];
@@ -3261,17 +3267,23 @@ hipError_t launch_dense_gemv(const DenseSet& set, int count, const float* x, int
   return hipGetLastError();
 }
 
-hipError_t launch_dense_proj(const uint16_t* w, const float* bias, const float* x, int rows, int cols, int m,
-                             float* out, hipStream_t stream) {
-  if (rows <= 0 || cols <= 0 || m <= 0) return hipSuccess;
-  const unsigned gx = (unsigned)((rows + kDenseRows - 1) / kDenseRows);
+hipError_t launch_dense_proj(const DenseSet& set, int count, const float* x, int cols, int m, hipStream_t stream) {
+  if (count <= 0 || count > 3 || cols <= 0 || m <= 0) return hipErrorInvalidValue;
+  DenseSet s = set;
+  int wg = 0;
+  for (int i = 0; i < 3; ++i) {
+    s.wg_begin[i] = wg;
+    if (i < count) wg += (s.rows[i] + kDenseRows - 1) / kDenseRows;
+  }
+  s.wg_begin[3] = wg;
+  if (wg == 0) return hipSuccess;
   if (m == 1)
-    hipLaunchKernelGGL(dense_proj_kernel<1>, dim3(gx, 1), dim3(256), 0, stream, w, bias, x, rows, cols, m, out);
+    hipLaunchKernelGGL(dense_proj_kernel<1>, dim3((unsigned)wg, 1), dim3(256), 0, stream, s, x, cols, m);
   else if (m <= 4)
-    hipLaunchKernelGGL(dense_proj_kernel<4>, dim3(gx, 1), dim3(256), 0, stream, w, bias, x, rows, cols, m, out);
+    hipLaunchKernelGGL(dense_proj_kernel<4>, dim3((unsigned)wg, 1), dim3(256), 0, stream, s, x, cols, m);
   else
-    hipLaunchKernelGGL(dense_proj_kernel<16>, dim3(gx, (unsigned)((m + 15) / 16)), dim3(256), 0, stream, w, bias, x,
-                       rows, cols, m, out);
+    hipLaunchKernelGGL(dense_proj_kernel<16>, dim3((unsigned)wg, (unsigned)((m + 15) / 16)), dim3(256), 0, stream, s,
+                       x, cols, m);
   return hipGetLastError();
 }
 
