@@ -294,6 +294,7 @@ struct DenseDevice {
   struct Layer {
     const uint16_t *q, *k, *v, *o;
     const float *qb, *kb, *vb, *ob;
+    const float* post_norm;  // post_attention_norm, for the MoE call in device memory
   };
   int device = 0;
   hipStream_t stream = nullptr;
@@ -302,13 +303,19 @@ struct DenseDevice {
   const uint16_t* lm_head = nullptr;
   float *d_in = nullptr, *d_out = nullptr, *h_in = nullptr, *h_out = nullptr;
   size_t in_cap = 0, out_cap = 0;  // floats
+  // The residual rows around the MoE call: device hidden, after and next
+  // (m x hidden bf16 each) and their pinned staging, as floats' worth of bytes.
+  float *d_rows = nullptr, *h_rows = nullptr;
+  size_t rows_cap = 0;
   ~DenseDevice() {
     (void)hipSetDevice(device);
     for (void* p : weights) (void)hipFree(p);
     (void)hipFree(d_in);
     (void)hipFree(d_out);
+    (void)hipFree(d_rows);
     (void)hipHostFree(h_in);
     (void)hipHostFree(h_out);
+    (void)hipHostFree(h_rows);
   }
 };
 
@@ -413,6 +420,55 @@ int gpu_project(gossmx_model* M, const uint16_t* in, size_t m, size_t cols, cons
   return GOSSMX_OK;
 }
 
+// The rest of a layer after attention, in one round trip: the O projection of
+// attn (m x QW bf16), the residual add with hidden, and the MoE half
+// (post-attention norm, block, residual add) in device memory; hidden
+// (m x H bf16) becomes the next layer's rows. The MoE time is added to *moe.
+int gpu_o_residual_moe(gossmx_model* M, const gossmx_dense_layer& L, const DenseDevice::Layer& DL,
+                       const uint16_t* attn, size_t m, uint16_t* hidden, double* moe) {
+  DenseDevice& D = M->dev;
+  const size_t H = M->cfg.hidden, QW = M->cfg.heads * M->cfg.head_dim, n = m * H;
+  DENSE_HIP(hipSetDevice(D.device), "hipSetDevice");
+  if (int st = grow(&D.d_in, &D.h_in, &D.in_cap, m * QW)) return st;
+  if (int st = grow(&D.d_out, &D.h_out, &D.out_cap, n)) return st;
+  if (int st = grow(&D.d_rows, &D.h_rows, &D.rows_cap, (3 * n + 1) / 2)) return st;
+  uint16_t* d_hidden = reinterpret_cast<uint16_t*>(D.d_rows);
+  uint16_t *d_after = d_hidden + n, *d_next = d_hidden + 2 * n;
+  uint16_t* h_rows = reinterpret_cast<uint16_t*>(D.h_rows);
+  for (size_t i = 0; i < m * QW; ++i) D.h_in[i] = bf16_f32(attn[i]);
+  std::memcpy(h_rows, hidden, n * 2);
+  DENSE_HIP(hipMemcpyAsync(D.d_in, D.h_in, m * QW * sizeof(float), hipMemcpyHostToDevice, D.stream),
+            "projection input copy");
+  DENSE_HIP(hipMemcpyAsync(d_hidden, h_rows, n * 2, hipMemcpyHostToDevice, D.stream), "residual rows copy");
+  gossmx::DenseSet set{};
+  set.w[0] = DL.o;
+  set.bias[0] = DL.ob;
+  set.out[0] = D.d_out;
+  set.rows[0] = (int)H;
+  const bool whole_k = m == 1 && QW % 8 == 0 && QW <= 4096;
+  DENSE_HIP(whole_k ? gossmx::launch_dense_gemv(set, 1, D.d_in, (int)QW, D.stream)
+                    : gossmx::launch_dense_proj(set, 1, D.d_in, (int)QW, (int)m, D.stream),
+            "projection launch");
+  DENSE_HIP(gossmx::launch_residual_add(d_hidden, D.d_out, d_after, n, D.stream), "residual add launch");
+  const auto t_moe = std::chrono::steady_clock::now();
+  gossmx_moe_io io{};
+  io.x = d_after;
+  io.m = m;
+  io.memory = GOSSMX_MEM_DEVICE;
+  int st = gossmx_moe_forward_residual(M->ctx, L.moe, &io, DL.post_norm, M->cfg.rms_norm_eps, d_next);
+  if (st == GOSSMX_OK) {
+    const hipError_t e = hipMemcpyAsync(h_rows + n, d_next, n * 2, hipMemcpyDeviceToHost, D.stream);
+    st = e == hipSuccess ? gossmx_synchronize(M->ctx) : hip_err(e, "next rows copy");
+  }
+  *moe += seconds_since(t_moe);
+  if (st != GOSSMX_OK) {
+    (void)hipStreamSynchronize(D.stream);  // the staging buffers' copies end before the next step reuses them
+    return st;
+  }
+  std::memcpy(hidden, h_rows + n, n * 2);
+  return GOSSMX_OK;
+}
+
 // One layer-major step over m rows at positions model->position + r
 // (prepare_step with every row in one sequence). Writes the last row's logits.
 // The caches change only when the step succeeds.
@@ -426,8 +482,8 @@ int run_step(gossmx_model* M, const uint32_t* tokens, size_t m, float* logits) {
   const auto t_step = std::chrono::steady_clock::now();
   double moe = 0.0;
   const size_t base = M->position;
-  std::vector<uint16_t> hidden(m * H), normalized(m * H), after(m * H), attn(m * QW);
-  std::vector<float> q(m * QW), k(m * KW), v(m * KW), proj(m * H), attn_f(m * QW), scores;
+  std::vector<uint16_t> hidden(m * H), normalized(m * H), attn(m * QW);
+  std::vector<float> q(m * QW), k(m * KW), v(m * KW), attn_f(m * QW), scores;
   std::vector<uint16_t> staged_k(c.layers * m * KW), staged_v(c.layers * m * KW);
   for (size_t r = 0; r < m; ++r) std::memcpy(&hidden[r * H], M->embedding + (size_t)tokens[r] * H, H * 2);
   Pool& pool = *M->pool;
@@ -484,22 +540,9 @@ int run_step(gossmx_model* M, const uint32_t* tokens, size_t m, float* logits) {
       attention(&q[r * QW], visible, key, value, L.sinks, c.heads, c.kv_heads, c.head_dim, ctx, sc, h_begin, h_end);
       for (size_t i = h_begin * c.head_dim; i < h_end * c.head_dim; ++i) attn[r * QW + i] = bf16_bits(ctx[i]);
     });
-    const Projection o_proj = {DL.o, DL.ob, H, proj.data()};
-    if (int st = gpu_project(M, attn.data(), m, QW, &o_proj, 1)) return st;
-    pool.run(m, [&](size_t r) {
-      for (size_t i = 0; i < H; ++i)
-        after[r * H + i] = bf16_bits(bf16_f32(hidden[r * H + i]) + bf16_round(proj[r * H + i]));
-    });
-    // The MoE half on the GPU: norm_boundary(after, post_attention_norm), moe_batch,
-    // add_residual(after, moe) -> the next layer's hidden rows.
-    const auto t_moe = std::chrono::steady_clock::now();
-    gossmx_moe_io io{};
-    io.x = after.data();
-    io.m = m;
-    io.memory = GOSSMX_MEM_HOST;
-    const int st = gossmx_moe_forward_residual(M->ctx, L.moe, &io, L.post_attention_norm, c.rms_norm_eps,
-                                               hidden.data());
-    moe += seconds_since(t_moe);
+    // O projection, residual add and the MoE half (norm_boundary(after,
+    // post_attention_norm), moe_batch, add_residual) -> the next layer's rows.
+    const int st = gpu_o_residual_moe(M, L, DL, attn.data(), m, hidden.data(), &moe);
     if (st != GOSSMX_OK) return st;
   }
   // Final norm and lm_head for the last row (the only row whose logits are required).
@@ -585,6 +628,7 @@ int gossmx_model_create(gossmx_ctx* ctx, const gossmx_model_config* config, cons
     if (!st) st = upload(D, L.k_bias, KW, &DL.kb);
     if (!st) st = upload(D, L.v_bias, KW, &DL.vb);
     if (!st) st = upload(D, L.o_bias, H, &DL.ob);
+    if (!st) st = upload(D, L.post_attention_norm, H, &DL.post_norm);
   }
   if (!st) st = upload(D, lm_head, config->vocab * H, &D.lm_head);
   if (st) {

@@ -234,6 +234,9 @@ hipError_t launch_dense_proj(const DenseSet& set, int count, const float* x, int
 // One token through up to three projections with the whole K range of a
 // work-group staged at once (cols a multiple of 8, at most 4096).
 hipError_t launch_dense_gemv(const DenseSet& set, int count, const float* x, int cols, hipStream_t stream);
+// after[i] = bf16(hidden[i] + bf16(proj[i])) for i < n (bf16 bits).
+hipError_t launch_residual_add(const uint16_t* hidden, const float* proj, uint16_t* after, size_t n,
+                               hipStream_t stream);
 
 }  // namespace gossmx
 

@@ -3267,6 +3267,23 @@ hipError_t launch_dense_gemv(const DenseSet& set, int count, const float* x, int
   return hipGetLastError();
 }
 
+// The attention half's residual add (add_residual, cpu_runner.rs:3732-3738,
+// after the O projection's bf16 round trip): after = bf16(hidden + bf16(proj)).
+__global__ __launch_bounds__(256) void residual_add_kernel(const uint16_t* __restrict__ hidden,
+                                                           const float* __restrict__ proj, uint16_t* __restrict__ after,
+                                                           size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) after[i] = bf16_bits(bf16_to_f32(hidden[i]) + bf16r(proj[i]));
+}
+
+hipError_t launch_residual_add(const uint16_t* hidden, const float* proj, uint16_t* after, size_t n,
+                               hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, hidden, proj, after,
+                     n);
+  return hipGetLastError();
+}
+
 hipError_t launch_dense_proj(const DenseSet& set, int count, const float* x, int cols, int m, hipStream_t stream) {
   if (count <= 0 || count > 3 || cols <= 0 || m <= 0) return hipErrorInvalidValue;
   DenseSet s = set;
