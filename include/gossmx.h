@@ -400,10 +400,12 @@ int gossmx_selftest(gossmx_ctx* ctx);
  * computes, bit for bit. Attention, RoPE, norms and the KV caches run on host
  * threads. The Q/K/V/O projections and lm_head run on the context's GPU with the
  * reference's 16-lane dot order, over copies of those matrices made in HBM by
- * gossmx_model_create (about 2.4 GB for GPT-OSS-20B). The MoE halves run on
- * the GPU through gossmx_moe_forward_residual (host memory). The embedding,
- * the norm weights, the sinks and the MoE layers stay borrowed and must outlive
- * the model. A model holds one sequence's KV caches. */
+ * gossmx_model_create (about 2.4 GB for GPT-OSS-20B, with the post-attention
+ * norm weights). The MoE halves run on the GPU through
+ * gossmx_moe_forward_residual (device memory, one round trip per layer with the
+ * O projection). The embedding, the input and final norm weights, the sinks and
+ * the MoE layers stay borrowed and must outlive the model. A model holds one
+ * sequence's KV caches. */
 typedef struct gossmx_model gossmx_model;
 
 /* CpuGptOssConfig (cpu_runner.rs:252-291) and the sequence's context cap
