@@ -208,7 +208,7 @@ def probe_traffic(args, config=None) -> dict:
     if rp is None:
         return {"traffic": None, "traffic_source": "not measured: rocprofv3 not found"}
     env = dict(os.environ, TMPDIR="/tmp")
-    per = {}
+    per, codes = {}, {}
     for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
         d = tempfile.mkdtemp(prefix="gossmx_pmc_", dir="/tmp")
         cmd = [rp, "--pmc", ctr, "--output-format", "csv", "-d", d, "-o", "p", "--", sys.executable,
@@ -220,15 +220,19 @@ def probe_traffic(args, config=None) -> dict:
             if args.prefill:
                 cmd.append("--prefill")
         try:
-            # rocprofv3 may end with a segmentation fault after the program's
-            # results are complete: the CSV decides.
-            subprocess.run(cmd, timeout=240, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, env=env,
-                           cwd="/tmp")
+            # The child prints "probe done" as its last line; its exit status
+            # and that line are recorded in traffic_source.
+            proc = subprocess.run(cmd, timeout=240, stdout=subprocess.PIPE, stderr=subprocess.DEVNULL, env=env,
+                                  cwd="/tmp", text=True)
         except subprocess.TimeoutExpired:
             return {"traffic": None, "traffic_source": f"not measured: rocprofv3 --pmc {ctr} pass timed out"}
+        finished = "probe done" in (proc.stdout or "")
+        codes[ctr] = f"exit {proc.returncode}" + ("" if finished else ", the workload did not finish")
         files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
-        if not files:
-            return {"traffic": None, "traffic_source": f"not measured: rocprofv3 --pmc {ctr} wrote no counters"}
+        if not files or not finished:
+            return {"traffic": None,
+                    "traffic_source": f"not measured: rocprofv3 --pmc {ctr} ({codes[ctr]}) wrote no counters"
+                    if not files else f"not measured: rocprofv3 --pmc {ctr} ({codes[ctr]})"}
         copy_kib, gate_up = 0.0, []
         with open(files[0]) as f:
             for row in csv.DictReader(f):
@@ -249,7 +253,8 @@ def probe_traffic(args, config=None) -> dict:
     return {"traffic": traffic,
             "traffic_source": f"rocprofv3 --pmc FETCH_SIZE then WRITE_SIZE in this run, {n} gate_up dispatches: "
                               f"{fk:.0f} KiB x {f_scale:.3f} + {wk:.0f} KiB x {w_scale:.3f} (scales from a 1 GiB "
-                              f"device copy: FETCH {fc:.0f} KiB, WRITE {wc:.0f} KiB)"}
+                              f"device copy: FETCH {fc:.0f} KiB, WRITE {wc:.0f} KiB); profiler children: "
+                              f"FETCH {codes['FETCH_SIZE']}, WRITE {codes['WRITE_SIZE']}"}
 
 
 def run_traffic_probe(args, cfg: dict) -> int:
@@ -276,7 +281,20 @@ def run_traffic_probe(args, cfg: dict) -> int:
         st["gu"].close()
         st["dn"].close()
     ctx.close()
+    release_torch()
+    print("probe done", flush=True)
     return 0
+
+
+def release_torch():
+    """Ends the process's GPU work before the interpreter exits: waits for the
+    device and returns torch's cached blocks, so that nothing of this program
+    is in flight or cached while the runtime (and a profiler's library, when
+    one is loaded) tears down."""
+    import torch
+
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
 
 
 def run_model(args) -> int:
@@ -357,13 +375,14 @@ def run_model(args) -> int:
             "greedy_match": bool(st == 0 and (want_tokens == tokens).all()),
             "logits_bits_equal": bool(st == 0 and (want_logits.view(np.uint32) == logits.view(np.uint32)).all()),
         }
-    print(json.dumps(line))
     model.close()
     for gu, dn, moe, _ in keep:
         moe.close()
         gu.close()
         dn.close()
     ctx.close()
+    release_torch()
+    print(json.dumps(line))
     return 0
 
 
@@ -597,7 +616,9 @@ def main() -> int:
             result["host_memory"] = {
                 "ms_per_step": host_ms, "value": layer_tokens / (host_ms * 1e-3), "unit": "layer-tokens/s",
                 "steps": host_steps,
-                "note": "GOSSMX_MEM_HOST calls: x and logits copied in, outputs copied out, synchronized per layer",
+                "note": ("GOSSMX_MEM_HOST calls (eager launches): x and logits copied in; every CpuMoeStep output "
+                         "(router logits, selection, routing weights, route order, output rows) and the device "
+                         "error flags copied out in one synchronization per layer"),
             }
         return result, x, state, graph
 
@@ -631,6 +652,7 @@ def main() -> int:
             "roofline": r0["roofline"], "stage_ms_per_step": r0["stage_ms_per_step"],
         }
     ctx.close()
+    release_torch()
     print(json.dumps(result))
     if not bits_ok:
         print("GPU rows differ from the oracle's bits (cpu_baseline)", file=sys.stderr)

@@ -298,6 +298,13 @@ int projection_gate(gossmx_ctx* ctx) {
   ctx->fault_armed = 0;
   if (mode == 1) return fail(GOSSMX_ERR_INJECTED_FAULT, "injected fault before launch");
   if (mode == 2) return fail(GOSSMX_ERR_DEVICE, "injected device fault before launch");
+  if (mode == 3) {
+    // The call runs, and the device's work-order flag is raised ahead of its
+    // kernels in stream order (a host-sourced copy, no kernel faults), so the
+    // failure surfaces where the call's device flags are next read.
+    static const int kRaised = kErrWorkOrder;
+    HIP_TRY(hipMemcpyAsync(ctx->err, &kRaised, sizeof(int), hipMemcpyHostToDevice, ctx->stream), "raise flag");
+  }
   return GOSSMX_OK;
 }
 
@@ -394,6 +401,7 @@ int set_error(int status, const char* message) { return fail(status, "%s", messa
 const gossmx_moe_config* layer_config(const gossmx_layer* layer) { return layer ? &layer->cfg : nullptr; }
 int context_device(const gossmx_ctx* ctx) { return ctx->device; }
 hipStream_t context_stream(const gossmx_ctx* ctx) { return ctx->stream; }
+int run_time_result(gossmx_ctx* ctx, int status) { return projection_result(ctx, status); }
 
 void tiled_image_bytes(size_t experts, size_t rows, size_t blocks, size_t* nib_bytes, size_t* scl_bytes) {
   const TiledWeights t = make_tiled(experts, rows, blocks);
@@ -537,8 +545,11 @@ void* gossmx_ctx_stream(gossmx_ctx* ctx) { return ctx ? (void*)ctx->stream : nul
 int gossmx_synchronize(gossmx_ctx* ctx) {
   if (!ctx) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context");
   if (int s = set_device(ctx->device)) return s;
-  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
-  return check_device_errors(ctx);
+  // Device-memory calls report their run-time failures here, so a device
+  // fault found here opens the circuit breaker as inside a call.
+  const hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return projection_result(ctx, hip_fail(e, "hipStreamSynchronize"));
+  return projection_result(ctx, check_device_errors(ctx));
 }
 
 int gossmx_malloc(gossmx_ctx* ctx, size_t bytes, void** out) {
@@ -1056,14 +1067,28 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
             "combine launch");
   }
 
-  const bool rows_only = !io->router_logits && !io->selected && !io->routing_weights && !io->route_order &&
-                         !io->trace_down && !io->trace_gate_up && !io->trace_swiglu;
-  if (host && rows_only) {
-    // The error flags and the output rows come back in one stream sequence
-    // into pinned staging and one synchronization; the caller's buffers are
-    // written only when the flags are clear.
-    const size_t out_bytes = io->output ? m * H * 4 : 0, next_bytes = residual ? m * H * 2 : 0;
-    const size_t need = 16 + out_bytes + next_bytes;
+  if (host) {
+    // Every requested output and the error flags come back in one stream
+    // sequence into pinned staging and one synchronization; the caller's
+    // buffers are written only when the flags are clear.
+    struct Piece {
+      const void* src;
+      void* dst;
+      size_t bytes;
+    };
+    const Piece pieces[] = {
+        {output, io->output, io->output ? m * H * 4 : 0},
+        {next, next_residual, residual ? m * H * 2 : 0},
+        {logits, io->router_logits, io->router_logits ? m * E * 4 : 0},
+        {selected, io->selected, io->selected ? R * 4 : 0},
+        {weights, io->routing_weights, io->routing_weights ? R * 4 : 0},
+        {da.route_slot, io->route_order, io->route_order ? R * 4 : 0},
+        {trace, io->trace_down, io->trace_down ? R * H * 4 : 0},
+        {trace_gu, io->trace_gate_up, io->trace_gate_up ? R * 2 * I * 4 : 0},
+        {trace_sw, io->trace_swiglu, io->trace_swiglu ? R * I * 4 : 0},
+    };
+    size_t need = 16;
+    for (const Piece& pc : pieces) need += (pc.bytes + 15) / 16 * 16;
     if (need > ctx->stage_cap) {
       if (ctx->h_stage) HIP_TRY(hipHostFree(ctx->h_stage), "hipHostFree");
       ctx->h_stage = nullptr;
@@ -1073,38 +1098,20 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
     }
     int* flags = reinterpret_cast<int*>(ctx->h_stage);
     HIP_TRY(hipMemcpyAsync(flags, ctx->err, sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "read error flags");
-    if (out_bytes)
-      HIP_TRY(hipMemcpyAsync(ctx->h_stage + 16, output, out_bytes, hipMemcpyDeviceToHost, ctx->stream), "D2H output");
-    if (next_bytes)
-      HIP_TRY(hipMemcpyAsync(ctx->h_stage + 16 + out_bytes, next, next_bytes, hipMemcpyDeviceToHost, ctx->stream),
-              "D2H next");
+    size_t off = 16;
+    for (const Piece& pc : pieces) {
+      if (!pc.bytes) continue;
+      HIP_TRY(hipMemcpyAsync(ctx->h_stage + off, pc.src, pc.bytes, hipMemcpyDeviceToHost, ctx->stream), "D2H output");
+      off += (pc.bytes + 15) / 16 * 16;
+    }
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     if (*flags != 0) return device_flags_fail(ctx, *flags);
-    if (out_bytes) std::memcpy(io->output, ctx->h_stage + 16, out_bytes);
-    if (next_bytes) std::memcpy(next_residual, ctx->h_stage + 16 + out_bytes, next_bytes);
-  } else if (host) {
-    if ((s = check_device_errors(ctx))) return s;
-    if (io->output)
-      HIP_TRY(hipMemcpyAsync(io->output, output, m * H * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H output");
-    if (residual)
-      HIP_TRY(hipMemcpyAsync(next_residual, next, m * H * 2, hipMemcpyDeviceToHost, ctx->stream), "D2H next");
-    if (io->router_logits)
-      HIP_TRY(hipMemcpyAsync(io->router_logits, logits, m * E * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H logits");
-    if (io->selected)
-      HIP_TRY(hipMemcpyAsync(io->selected, selected, R * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H selected");
-    if (io->routing_weights)
-      HIP_TRY(hipMemcpyAsync(io->routing_weights, weights, R * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H weights");
-    if (io->route_order)
-      HIP_TRY(hipMemcpyAsync(io->route_order, da.route_slot, R * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H order");
-    if (io->trace_down)
-      HIP_TRY(hipMemcpyAsync(io->trace_down, trace, R * H * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H trace");
-    if (io->trace_gate_up)
-      HIP_TRY(hipMemcpyAsync(io->trace_gate_up, trace_gu, R * 2 * I * 4, hipMemcpyDeviceToHost, ctx->stream),
-              "D2H gate_up trace");
-    if (io->trace_swiglu)
-      HIP_TRY(hipMemcpyAsync(io->trace_swiglu, trace_sw, R * I * 4, hipMemcpyDeviceToHost, ctx->stream),
-              "D2H SwiGLU trace");
-    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    off = 16;
+    for (const Piece& pc : pieces) {
+      if (!pc.bytes) continue;
+      std::memcpy(pc.dst, ctx->h_stage + off, pc.bytes);
+      off += (pc.bytes + 15) / 16 * 16;
+    }
   } else {
     if (io->selected)
       HIP_TRY(hipMemcpyAsync(io->selected, selected, R * 4, hipMemcpyDeviceToDevice, ctx->stream), "D2D selected");
@@ -1228,7 +1235,7 @@ void gossmx_graph_destroy(gossmx_graph* g) {
 
 int gossmx_inject_fault(gossmx_ctx* ctx, int armed) {
   if (!ctx) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context");
-  if (armed < 0 || armed > 2) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "unknown fault mode %d", armed);
+  if (armed < 0 || armed > 3) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "unknown fault mode %d", armed);
   ctx->fault_armed = armed;
   return GOSSMX_OK;
 }

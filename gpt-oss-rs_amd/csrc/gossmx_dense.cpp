@@ -297,7 +297,6 @@ struct DenseDevice {
     const float* post_norm;  // post_attention_norm, for the MoE call in device memory
   };
   int device = 0;
-  hipStream_t stream = nullptr;
   std::vector<void*> weights;  // device allocations of the copies
   std::vector<Layer> layers;
   const uint16_t* lm_head = nullptr;
@@ -382,15 +381,19 @@ struct Projection {
 
 // Runs the projections of one input on the GPU (project_bf16_batch): one copy
 // in, one launch each, one copy out, one synchronization.
-int gpu_project(gossmx_model* M, const uint16_t* in, size_t m, size_t cols, const Projection* p, size_t count) {
+int gpu_project_impl(gossmx_model* M, const uint16_t* in, size_t m, size_t cols, const Projection* p,
+                     size_t count) {
   DenseDevice& D = M->dev;
+  // The context's stream is read on every call: gossmx_ctx_set_stream may
+  // have replaced it since the model was created.
+  const hipStream_t stream = gossmx::context_stream(M->ctx);
   size_t total = 0;
   for (size_t i = 0; i < count; ++i) total += m * p[i].rows;
   DENSE_HIP(hipSetDevice(D.device), "hipSetDevice");
   if (int st = grow(&D.d_in, &D.h_in, &D.in_cap, m * cols)) return st;
   if (int st = grow(&D.d_out, &D.h_out, &D.out_cap, total)) return st;
   for (size_t i = 0; i < m * cols; ++i) D.h_in[i] = bf16_f32(in[i]);
-  DENSE_HIP(hipMemcpyAsync(D.d_in, D.h_in, m * cols * sizeof(float), hipMemcpyHostToDevice, D.stream),
+  DENSE_HIP(hipMemcpyAsync(D.d_in, D.h_in, m * cols * sizeof(float), hipMemcpyHostToDevice, stream),
             "projection input copy");
   // One launch per group. One token through small matrices (Q/K/V, O):
   // work-groups stage their whole K range at once; lm_head and batches: the
@@ -406,12 +409,12 @@ int gpu_project(gossmx_model* M, const uint16_t* in, size_t m, size_t cols, cons
     off += m * p[i].rows;
   }
   const bool whole_k = m == 1 && cols % 8 == 0 && cols <= 4096 && total <= 65536;
-  DENSE_HIP(whole_k ? gossmx::launch_dense_gemv(set, (int)count, D.d_in, (int)cols, D.stream)
-                    : gossmx::launch_dense_proj(set, (int)count, D.d_in, (int)cols, (int)m, D.stream),
+  DENSE_HIP(whole_k ? gossmx::launch_dense_gemv(set, (int)count, D.d_in, (int)cols, stream)
+                    : gossmx::launch_dense_proj(set, (int)count, D.d_in, (int)cols, (int)m, stream),
             "projection launch");
-  DENSE_HIP(hipMemcpyAsync(D.h_out, D.d_out, total * sizeof(float), hipMemcpyDeviceToHost, D.stream),
+  DENSE_HIP(hipMemcpyAsync(D.h_out, D.d_out, total * sizeof(float), hipMemcpyDeviceToHost, stream),
             "projection output copy");
-  DENSE_HIP(hipStreamSynchronize(D.stream), "projection");
+  DENSE_HIP(hipStreamSynchronize(stream), "projection");
   off = 0;
   for (size_t i = 0; i < count; ++i) {
     std::memcpy(p[i].out, D.h_out + off, m * p[i].rows * sizeof(float));
@@ -420,13 +423,20 @@ int gpu_project(gossmx_model* M, const uint16_t* in, size_t m, size_t cols, cons
   return GOSSMX_OK;
 }
 
+// A run-time failure of the round trip (HIP error, out of memory) opens the
+// circuit breaker, as a failed projection call does.
+int gpu_project(gossmx_model* M, const uint16_t* in, size_t m, size_t cols, const Projection* p, size_t count) {
+  return gossmx::run_time_result(M->ctx, gpu_project_impl(M, in, m, cols, p, count));
+}
+
 // The rest of a layer after attention, in one round trip: the O projection of
 // attn (m x QW bf16), the residual add with hidden, and the MoE half
 // (post-attention norm, block, residual add) in device memory; hidden
 // (m x H bf16) becomes the next layer's rows. The MoE time is added to *moe.
-int gpu_o_residual_moe(gossmx_model* M, const gossmx_dense_layer& L, const DenseDevice::Layer& DL,
-                       const uint16_t* attn, size_t m, uint16_t* hidden, double* moe) {
+int gpu_o_residual_moe_impl(gossmx_model* M, const gossmx_dense_layer& L, const DenseDevice::Layer& DL,
+                            const uint16_t* attn, size_t m, uint16_t* hidden, double* moe) {
   DenseDevice& D = M->dev;
+  const hipStream_t stream = gossmx::context_stream(M->ctx);
   const size_t H = M->cfg.hidden, QW = M->cfg.heads * M->cfg.head_dim, n = m * H;
   DENSE_HIP(hipSetDevice(D.device), "hipSetDevice");
   if (int st = grow(&D.d_in, &D.h_in, &D.in_cap, m * QW)) return st;
@@ -437,19 +447,19 @@ int gpu_o_residual_moe(gossmx_model* M, const gossmx_dense_layer& L, const Dense
   uint16_t* h_rows = reinterpret_cast<uint16_t*>(D.h_rows);
   for (size_t i = 0; i < m * QW; ++i) D.h_in[i] = bf16_f32(attn[i]);
   std::memcpy(h_rows, hidden, n * 2);
-  DENSE_HIP(hipMemcpyAsync(D.d_in, D.h_in, m * QW * sizeof(float), hipMemcpyHostToDevice, D.stream),
+  DENSE_HIP(hipMemcpyAsync(D.d_in, D.h_in, m * QW * sizeof(float), hipMemcpyHostToDevice, stream),
             "projection input copy");
-  DENSE_HIP(hipMemcpyAsync(d_hidden, h_rows, n * 2, hipMemcpyHostToDevice, D.stream), "residual rows copy");
+  DENSE_HIP(hipMemcpyAsync(d_hidden, h_rows, n * 2, hipMemcpyHostToDevice, stream), "residual rows copy");
   gossmx::DenseSet set{};
   set.w[0] = DL.o;
   set.bias[0] = DL.ob;
   set.out[0] = D.d_out;
   set.rows[0] = (int)H;
   const bool whole_k = m == 1 && QW % 8 == 0 && QW <= 4096;
-  DENSE_HIP(whole_k ? gossmx::launch_dense_gemv(set, 1, D.d_in, (int)QW, D.stream)
-                    : gossmx::launch_dense_proj(set, 1, D.d_in, (int)QW, (int)m, D.stream),
+  DENSE_HIP(whole_k ? gossmx::launch_dense_gemv(set, 1, D.d_in, (int)QW, stream)
+                    : gossmx::launch_dense_proj(set, 1, D.d_in, (int)QW, (int)m, stream),
             "projection launch");
-  DENSE_HIP(gossmx::launch_residual_add(d_hidden, D.d_out, d_after, n, D.stream), "residual add launch");
+  DENSE_HIP(gossmx::launch_residual_add(d_hidden, D.d_out, d_after, n, stream), "residual add launch");
   const auto t_moe = std::chrono::steady_clock::now();
   gossmx_moe_io io{};
   io.x = d_after;
@@ -457,16 +467,22 @@ int gpu_o_residual_moe(gossmx_model* M, const gossmx_dense_layer& L, const Dense
   io.memory = GOSSMX_MEM_DEVICE;
   int st = gossmx_moe_forward_residual(M->ctx, L.moe, &io, DL.post_norm, M->cfg.rms_norm_eps, d_next);
   if (st == GOSSMX_OK) {
-    const hipError_t e = hipMemcpyAsync(h_rows + n, d_next, n * 2, hipMemcpyDeviceToHost, D.stream);
+    // gossmx_synchronize reports the device error flags.
+    const hipError_t e = hipMemcpyAsync(h_rows + n, d_next, n * 2, hipMemcpyDeviceToHost, stream);
     st = e == hipSuccess ? gossmx_synchronize(M->ctx) : hip_err(e, "next rows copy");
   }
   *moe += seconds_since(t_moe);
   if (st != GOSSMX_OK) {
-    (void)hipStreamSynchronize(D.stream);  // the staging buffers' copies end before the next step reuses them
+    (void)hipStreamSynchronize(stream);  // the staging buffers' copies end before the next step reuses them
     return st;
   }
   std::memcpy(hidden, h_rows + n, n * 2);
   return GOSSMX_OK;
+}
+
+int gpu_o_residual_moe(gossmx_model* M, const gossmx_dense_layer& L, const DenseDevice::Layer& DL,
+                       const uint16_t* attn, size_t m, uint16_t* hidden, double* moe) {
+  return gossmx::run_time_result(M->ctx, gpu_o_residual_moe_impl(M, L, DL, attn, m, hidden, moe));
 }
 
 // One layer-major step over m rows at positions model->position + r
@@ -614,7 +630,6 @@ int gossmx_model_create(gossmx_ctx* ctx, const gossmx_model_config* config, cons
   const size_t H = config->hidden, QW = config->heads * config->head_dim, KW = config->kv_heads * config->head_dim;
   DenseDevice& D = M->dev;
   D.device = gossmx::context_device(ctx);
-  D.stream = gossmx::context_stream(ctx);
   int st = hipSetDevice(D.device) == hipSuccess ? GOSSMX_OK : err(GOSSMX_ERR_DEVICE, "hipSetDevice failed");
   D.layers.resize(config->layers);
   for (size_t li = 0; li < config->layers && st == GOSSMX_OK; ++li) {

@@ -253,6 +253,9 @@ int set_error(int status, const char* message);
 const gossmx_moe_config* layer_config(const gossmx_layer* layer);
 int context_device(const gossmx_ctx* ctx);
 hipStream_t context_stream(const gossmx_ctx* ctx);
+// A GPU round trip's status: GOSSMX_ERR_DEVICE or GOSSMX_ERR_OUT_OF_MEMORY
+// drains the context's stream and opens the process-wide circuit breaker.
+int run_time_result(gossmx_ctx* ctx, int status);
 void tiled_image_bytes(size_t experts, size_t rows, size_t blocks, size_t* nib_bytes, size_t* scl_bytes);
 int tiled_image_read(gossmx_ctx* ctx, const gossmx_weights* w, uint8_t* nib, uint8_t* scl);
 int tiled_image_create(gossmx_ctx* ctx, size_t experts, size_t rows, size_t blocks, const uint8_t* nib,

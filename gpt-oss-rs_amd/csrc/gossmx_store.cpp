@@ -214,6 +214,28 @@ class JsonReader {
     }
     return true;
   }
+  // One UTF-8 sequence in a string's raw bytes, from its lead byte c (the
+  // input must be valid UTF-8, as serde_json::from_slice requires: no
+  // overlong forms, no surrogates, nothing above U+10FFFF).
+  bool raw_utf8(std::string& s, unsigned char c) {
+    int n;
+    uint32_t cp, min;
+    if (c >= 0xC2 && c <= 0xDF) n = 1, cp = c & 0x1F, min = 0x80;
+    else if (c >= 0xE0 && c <= 0xEF) n = 2, cp = c & 0x0F, min = 0x800;
+    else if (c >= 0xF0 && c <= 0xF4) n = 3, cp = c & 0x07, min = 0x10000;
+    else return false;
+    if (end_ - p_ < n) return false;
+    for (int i = 0; i < n; ++i) {
+      const unsigned char b = (unsigned char)p_[i];
+      if ((b & 0xC0) != 0x80) return false;
+      cp = (cp << 6) | (b & 0x3F);
+    }
+    if (cp < min || cp > 0x10FFFF || (cp >= 0xD800 && cp < 0xE000)) return false;
+    s += (char)c;
+    s.append(p_, (size_t)n);
+    p_ += n;
+    return true;
+  }
   bool string(std::string& s) {
     if (p_ >= end_ || *p_ != '"') return false;
     ++p_;
@@ -221,6 +243,10 @@ class JsonReader {
       const char c = *p_++;
       if (c == '"') return true;
       if ((unsigned char)c < 0x20) return false;
+      if ((unsigned char)c >= 0x80) {
+        if (!raw_utf8(s, (unsigned char)c)) return false;
+        continue;
+      }
       if (c != '\\') {
         s += c;
         continue;

@@ -20,7 +20,9 @@ from dataclasses import dataclass
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libgossmx.so")
+# GOSSMX_LIB names another build of the library (the host-sanitized test
+# build, for instance); by default the in-tree libgossmx.so.
+LIB_PATH = os.environ.get("GOSSMX_LIB") or os.path.join(HERE, "libgossmx.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "gossmx.h")
 
 OK = 0
@@ -39,6 +41,7 @@ ERR_CIRCUIT_OPEN = 11
 FAULT_NONE = 0
 FAULT_INJECTED = 1   # GOSSMX_ERR_INJECTED_FAULT, the breaker stays closed
 FAULT_DEVICE = 2     # GOSSMX_ERR_DEVICE, opens the breaker
+FAULT_FLAG = 3       # the call runs; its device error flag is raised, reported where the flags are read
 
 LAYOUT_CANONICAL_V1 = 1
 LAYOUT_X8_SPLIT_V2 = 2
@@ -228,7 +231,7 @@ def load():
 
 def _check(status: int):
     if status != OK:
-        raise GossmxError(status, load().gossmx_last_error().decode())
+        raise GossmxError(status, load().gossmx_last_error().decode(errors="replace"))
 
 
 def _ptr(a):
@@ -284,7 +287,9 @@ class Context:
     def inject_fault(self, armed: bool | int = True):
         """Arms the fault hook of the next projection call: True or
         FAULT_INJECTED (a model error), FAULT_DEVICE (a device fault that
-        opens the circuit breaker), False or FAULT_NONE (disarm)."""
+        opens the circuit breaker), FAULT_FLAG (the call runs with its device
+        error flag raised: GOSSMX_ERR_DEVICE where the flags are next read),
+        False or FAULT_NONE (disarm)."""
         mode = int(armed) if not isinstance(armed, bool) else (FAULT_INJECTED if armed else FAULT_NONE)
         _check(load().gossmx_inject_fault(self._h, mode))
 

@@ -110,8 +110,14 @@ int gossmx_ctx_create(int device, void* stream, gossmx_ctx** out);
 /* 1 when the context's GEMMs may take the scaled-conversion fast path. */
 int gossmx_ctx_fast_path(const gossmx_ctx* ctx, int* enabled);
 void gossmx_ctx_destroy(gossmx_ctx* ctx);
+/* Replaces the context's stream (after draining the old one). Every later
+ * call, including a model's steps, runs on the new stream. */
 int gossmx_ctx_set_stream(gossmx_ctx* ctx, void* stream);
 void* gossmx_ctx_stream(gossmx_ctx* ctx);
+/* Waits for the context's stream and reads the device error flags. A
+ * run-time failure found here (GOSSMX_ERR_DEVICE, GOSSMX_ERR_OUT_OF_MEMORY:
+ * what a device-memory call reports only when it is waited for) opens the
+ * circuit breaker, as it does inside a call. */
 int gossmx_synchronize(gossmx_ctx* ctx);
 
 /* Device memory helpers (so non-PyTorch callers can stage device buffers). */
@@ -383,7 +389,11 @@ void gossmx_graph_destroy(gossmx_graph* graph);
  * and before it launches anything (outputs untouched): armed = 1 fails it with
  * GOSSMX_ERR_INJECTED_FAULT (a model error, like CpuExecutionFailurePoint);
  * armed = 2 fails it as a device fault, GOSSMX_ERR_DEVICE, which opens the
- * circuit breaker; 0 disarms. */
+ * circuit breaker; armed = 3 lets the call run and raises the device's
+ * work-order error flag ahead of its kernels (a host-sourced copy), so the
+ * failure (GOSSMX_ERR_DEVICE, breaker opened) surfaces where the flags are
+ * next read: inside a host-memory call, at gossmx_synchronize after a
+ * device-memory one, or in the model step that made the call; 0 disarms. */
 int gossmx_inject_fault(gossmx_ctx* ctx, int armed);
 
 /* Device self-test of what the GEMM relies on: the FP4 -> f16 conversion order,

@@ -13,7 +13,9 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libgossmx_oracle.so")
+# ORACLE_LIB names another build (the sanitized test build); by default the
+# in-tree library.
+LIB_PATH = os.environ.get("ORACLE_LIB") or os.path.join(HERE, "libgossmx_oracle.so")
 
 # numpy views of the reference's Q8Block / ResidualQ8Block (lib.rs:732-742):
 # f32 scale + 32 x i8 values, 36 bytes, no padding.

@@ -146,6 +146,62 @@ def test_small_model_moe_failure_mid_step_changes_nothing(ctx, tiny):
     assert_bits(model.decode(want_tokens[0]), want_logits[1])
 
 
+def test_small_model_device_flag_failure_opens_the_breaker(ctx, tiny):
+    # The first MoE call of the step runs with its device error flag raised
+    # (FAULT_FLAG, a host-sourced write, no kernel faults); the step finds it
+    # when it synchronizes, fails with GOSSMX_ERR_DEVICE, opens the circuit
+    # breaker and commits nothing. While the breaker is open the next step
+    # fails fast; after the reset it matches the oracle.
+    cfg, model, oracle = tiny
+    _, want_tokens, want_logits = O.model_generate(oracle, PROMPT, 1, threads=4)
+    model.prefill(PROMPT)
+    before = [model.cache(i) for i in range(cfg["layers"])]
+    try:
+        ctx.inject_fault(G.FAULT_FLAG)
+        with pytest.raises(G.GossmxError) as e:
+            model.decode(want_tokens[0])
+        assert e.value.status == G.ERR_DEVICE
+        assert G.circuit_is_open()
+        with pytest.raises(G.GossmxError) as e:
+            model.decode(want_tokens[0])
+        assert e.value.status == G.ERR_CIRCUIT_OPEN
+        assert model.position == PROMPT.size and [model.cache(i) for i in range(cfg["layers"])] == before
+    finally:
+        G.circuit_reset()
+    assert_bits(model.decode(want_tokens[0]), want_logits[1])
+
+
+def test_small_model_follows_a_replaced_stream():
+    # gossmx_ctx_set_stream between generations (the context's own stream is
+    # destroyed): the model's copies, launches and MoE calls run on the new
+    # stream, and tokens and logits bits still equal the oracle's.
+    import torch
+    c = G.Context(0)
+    cfg = dict(TINY)
+    w = synth.model_weights(cfg, synth.numpy_normal(np.random.default_rng(6)))
+    hosts = [O.synthetic_layer(6, i, experts=4, hidden=64, intermediate=32, top_k=2) for i in range(cfg["layers"])]
+    for L, h in zip(w["layers"], hosts):
+        L["moe_host"] = h
+    model, keep = build(c, cfg, w, hosts)
+    stream = torch.cuda.Stream(device=0)
+    try:
+        oracle = O.ModelHost(cfg, w["embedding"], w["final_norm"], w["lm_head"], w["layers"])
+        st, want_tokens, want_logits = O.model_generate(oracle, PROMPT, 4, threads=4)
+        assert st == O.OK
+        tokens, logits = model.generate(PROMPT, 4)
+        assert (tokens == want_tokens).all()
+        assert_bits(logits, want_logits)
+        c.set_stream(stream.cuda_stream)
+        assert c.stream() == stream.cuda_stream
+        model.reset()
+        tokens, logits = model.generate(PROMPT, 4)
+        assert (tokens == want_tokens).all()
+        assert_bits(logits, want_logits)
+    finally:
+        release(model, keep)
+        c.close()
+
+
 def hash_normal(seed):
     """normal(n, std) for model_weights: the oracle's counter-hash Gaussian,
     one stream per tensor, generated on 16 host threads."""

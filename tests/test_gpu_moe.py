@@ -331,6 +331,133 @@ def test_120b_shape_prefill_4096_uniform_all_rows(layer120b):
     assert_full_batch_equal(host, x, got, logits)
 
 
+# --- order pins: inputs on which the plausible other float orders give other
+# bits (test_oracle derives each expected value by hand and checks that the
+# alternatives differ); each router and selection path is run by row count:
+# one row (selection inside the gate_up launch), 2-4 rows (route_select_kernel
+# with its arrival counter), more rows (route_kernel, then the selection
+# kernels) and, with injected logits, the one-work-group and two-launch
+# selections ---
+
+@pytest.mark.parametrize("m", [1, 3, 8])
+@pytest.mark.parametrize("hidden,offset", [(64, 0), (2880, 1424)])
+def test_router_dot_order_pins(ctx, hidden, offset, m):
+    """test_oracle's 16-lane router pin (scalar_bf16_dot, lib.rs:1007-1029):
+    logits 15 and 0 on the pinned rows, where sequential, pairwise, tree-folded,
+    reversed and other lane counts give 0, 14 or 16. At hidden 2880 the
+    construction straddles the router kernels' staging chunks."""
+    from test_oracle import router_pin_case
+    w, bias, x = router_pin_case(hidden, offset)
+    host = O.MoeLayerHost(w, bias, O.gen_mxfp4(1, 1, 4, 64, hidden // 32), np.zeros(4 * 64, np.float32),
+                          O.gen_mxfp4(1, 2, 4, hidden, 1), np.zeros(4 * hidden, np.float32), 4, hidden, 32, 2)
+    xs = np.repeat(x[None, :], m, axis=0)
+    want = O.moe_batch(host, xs)
+    assert want["status"] == O.OK
+    layer = gpu_layer(ctx, host)
+    got = layer.forward(xs)
+    assert (got["router_logits"][:, :2] == [15.0, 0.0]).all()
+    assert_moe_equal(got, want)
+    close(layer)
+
+
+def _softmax_pin_layer(router_bias=None):
+    host = O.synthetic_layer(41, 0, experts=8, hidden=64, intermediate=32, top_k=4)
+    if router_bias is not None:  # computed router: zero weights, so the logits are the bias
+        host = O.MoeLayerHost(np.zeros_like(host.router_weight), router_bias, host.gate_up, host.gate_up_bias,
+                              host.down, host.down_bias, 8, 64, 32, 4)
+    return host
+
+
+@pytest.mark.parametrize("repeat", [1, 300], ids=["one-work-group", "two-launch"])
+def test_softmax_order_pins_injected(ctx, repeat):
+    """Injected rows whose bf16 routing weights depend on the softmax
+    denominator's rank order (test_oracle.SOFTMAX_PIN_ROWS,
+    cpu_runner.rs:3784-3795): reversed, pairwise and float64 sums give other
+    weights."""
+    from test_oracle import SOFTMAX_PIN_ROWS
+    rows = len(SOFTMAX_PIN_ROWS) * repeat
+    logits = np.full((rows, 8), -20.0, np.float32)
+    for r in range(rows):
+        logits[r, [5, 1, 6, 2]] = SOFTMAX_PIN_ROWS[r % len(SOFTMAX_PIN_ROWS)]
+    host = _softmax_pin_layer()
+    x = O.gen_hidden(41, 1, rows, 64)
+    want = O.moe_batch(host, x, injected_logits=logits)
+    assert want["status"] == O.OK
+    for r, row in enumerate(SOFTMAX_PIN_ROWS):
+        assert (want["routing_weights"][r] == O.bf16_round_array(O.softmax(np.array(row, np.float32)))).all()
+    layer = gpu_layer(ctx, host)
+    got = layer.forward(x, injected_logits=logits)
+    assert (got["selected"] == [[5, 1, 6, 2]] * rows).all()
+    assert_moe_equal(got, want)
+    close(layer)
+
+
+@pytest.mark.parametrize("m", [1, 3, 8])
+@pytest.mark.parametrize("pin", [0, 1])
+def test_softmax_order_pins_computed_router(ctx, pin, m):
+    """The same pin through a computed router (zero router weights, the pin
+    row as the bias), on each router/selection path."""
+    from test_oracle import SOFTMAX_PIN_ROWS
+    bias = np.full(8, -20.0, np.float32)
+    bias[[5, 1, 6, 2]] = SOFTMAX_PIN_ROWS[pin]
+    host = _softmax_pin_layer(bias)
+    x = O.gen_hidden(41, 2, m, 64)
+    want = O.moe_batch(host, x)
+    assert want["status"] == O.OK
+    assert (want["routing_weights"] == O.bf16_round_array(O.softmax(np.array(SOFTMAX_PIN_ROWS[pin], np.float32)))).all()
+    layer = gpu_layer(ctx, host)
+    got = layer.forward(x)
+    assert (got["selected"] == [[5, 1, 6, 2]] * m).all()
+    assert_moe_equal(got, want)
+    close(layer)
+
+
+# Combine pin (cpu_runner.rs:2959-2999: weighted = y * w, the ranks added in
+# rank order from 0.0, then bf16). Four equal logits give every rank the weight
+# 0.25 (expf(0) = 1, 1/4) and rank k = expert k; all-zero down codes make each
+# expert's down output its bias. Column 0 takes 4 * [1, 2^24, 1, -2^24]:
+# weighted [1, 2^24, 1, -2^24], in rank order 1 + 2^24 ties to 2^24, + 1 ties
+# to 2^24 again, - 2^24 = 0. Column 1 takes 4 * [2^24, 1, -2^24, 1]: 2^24 + 1
+# ties to 2^24, - 2^24 = 0, + 1 = 1. Reversed order gives 2 and 2, pairwise
+# 1 and 1, float64 2 and 2.
+B24 = float(2 ** 24)
+COMBINE_PIN = {0: ([1.0, B24, 1.0, -B24], 0.0), 1: ([B24, 1.0, -B24, 1.0], 1.0)}
+
+
+def _combine_pin_layer():
+    host = O.synthetic_layer(43, 0, experts=4, hidden=64, intermediate=32, top_k=4)
+    down = np.zeros((4, 64, 1, 17), np.uint8)
+    down[..., 0] = 127  # E8M0 scale 1.0, every code 0 (value 0.0)
+    down_bias = host.down_bias.copy().reshape(4, 64)
+    for col, (weighted, _) in COMBINE_PIN.items():
+        down_bias[:, col] = [4.0 * v for v in weighted]
+    return O.MoeLayerHost(np.zeros_like(host.router_weight), np.zeros(4, np.float32), host.gate_up,
+                          host.gate_up_bias, down.ravel(), down_bias.ravel(), 4, 64, 32, 4)
+
+
+@pytest.mark.parametrize("inject", [False, True], ids=["computed", "injected"])
+@pytest.mark.parametrize("m", [1, 3, 70])
+def test_combine_order_pins(ctx, m, inject):
+    from test_oracle import _fold
+    F = np.float32
+    for col, (weighted, expected) in COMBINE_PIN.items():
+        alts = [_fold(weighted[::-1], 0.0), F(F(weighted[0] + weighted[1]) + F(weighted[2] + weighted[3])),
+                F(np.sum(np.asarray(weighted, np.float64)))]
+        assert _fold(weighted, 0.0) == expected and expected not in alts
+    host = _combine_pin_layer()
+    x = O.gen_hidden(43, 1, m, 64)
+    logits = np.zeros((m, 4), np.float32) if inject else None
+    want = O.moe_batch(host, x, injected_logits=logits)
+    assert want["status"] == O.OK
+    layer = gpu_layer(ctx, host)
+    got = layer.forward(x, injected_logits=logits)
+    assert (got["selected"] == [[0, 1, 2, 3]] * m).all() and (got["routing_weights"] == 0.25).all()
+    for col, (_, expected) in COMBINE_PIN.items():
+        assert (got["output"][:, col] == expected).all(), col
+    assert_moe_equal(got, want)
+    close(layer)
+
+
 def test_all_experts_selected(ctx):
     host = O.synthetic_layer(5, 0, experts=4, hidden=64, intermediate=64, top_k=4)
     x = O.gen_hidden(5, 1, 9, 64)
@@ -432,6 +559,34 @@ def test_device_fault_opens_the_circuit_breaker(ctx):
         layer.forward(x)
     assert e.value.status == G.ERR_INJECTED_FAULT
     assert not G.circuit_is_open()
+    # a device error flag raised during the call (mode 3): a host-memory call
+    # reports it itself, a device-memory call at gossmx_synchronize; both open
+    # the breaker, and the flag is cleared once reported
+    dx, dout = ctx.malloc(x.nbytes), ctx.malloc(2 * 64 * 4)
+    ctx.h2d(dx, x)
+    try:
+        ctx.inject_fault(G.FAULT_FLAG)
+        with pytest.raises(G.GossmxError) as e:
+            layer.forward(x)
+        assert e.value.status == G.ERR_DEVICE
+        assert G.circuit_is_open()
+        G.circuit_reset()
+        ctx.inject_fault(G.FAULT_FLAG)
+        layer.forward_device(dx, 2, dout)
+        with pytest.raises(G.GossmxError) as e:
+            ctx.synchronize()
+        assert e.value.status == G.ERR_DEVICE
+        assert G.circuit_is_open()
+    finally:
+        G.circuit_reset()
+    layer.forward_device(dx, 2, dout)
+    ctx.synchronize()
+    got = np.empty((2, 64), np.float32)
+    ctx.d2h(got, dout)
+    assert (got.view(np.uint32) == want["output"].view(np.uint32)).all()
+    ctx.free(dx)
+    ctx.free(dout)
+    assert_moe_equal(layer.forward(x), want)
     close(layer)
 
 
