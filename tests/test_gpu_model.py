@@ -174,8 +174,10 @@ def test_small_model_device_flag_failure_opens_the_breaker(ctx, tiny):
 def test_small_model_follows_a_replaced_stream():
     # gossmx_ctx_set_stream between generations (the context's own stream is
     # destroyed): the model's copies, launches and MoE calls run on the new
-    # stream, and tokens and logits bits still equal the oracle's.
-    import torch
+    # stream (a plain HIP stream at the default priority), and tokens and
+    # logits bits still equal the oracle's.
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so")
     c = G.Context(0)
     cfg = dict(TINY)
     w = synth.model_weights(cfg, synth.numpy_normal(np.random.default_rng(6)))
@@ -183,7 +185,8 @@ def test_small_model_follows_a_replaced_stream():
     for L, h in zip(w["layers"], hosts):
         L["moe_host"] = h
     model, keep = build(c, cfg, w, hosts)
-    stream = torch.cuda.Stream(device=0)
+    stream = C.c_void_p()
+    assert hip.hipStreamCreate(C.byref(stream)) == 0
     try:
         oracle = O.ModelHost(cfg, w["embedding"], w["final_norm"], w["lm_head"], w["layers"])
         st, want_tokens, want_logits = O.model_generate(oracle, PROMPT, 4, threads=4)
@@ -191,8 +194,8 @@ def test_small_model_follows_a_replaced_stream():
         tokens, logits = model.generate(PROMPT, 4)
         assert (tokens == want_tokens).all()
         assert_bits(logits, want_logits)
-        c.set_stream(stream.cuda_stream)
-        assert c.stream() == stream.cuda_stream
+        c.set_stream(stream.value)
+        assert c.stream == stream.value
         model.reset()
         tokens, logits = model.generate(PROMPT, 4)
         assert (tokens == want_tokens).all()
@@ -200,6 +203,7 @@ def test_small_model_follows_a_replaced_stream():
     finally:
         release(model, keep)
         c.close()
+        assert hip.hipStreamDestroy(stream) == 0
 
 
 def hash_normal(seed):

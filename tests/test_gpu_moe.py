@@ -418,8 +418,9 @@ def test_softmax_order_pins_computed_router(ctx, pin, m):
 # expert's down output its bias. Column 0 takes 4 * [1, 2^24, 1, -2^24]:
 # weighted [1, 2^24, 1, -2^24], in rank order 1 + 2^24 ties to 2^24, + 1 ties
 # to 2^24 again, - 2^24 = 0. Column 1 takes 4 * [2^24, 1, -2^24, 1]: 2^24 + 1
-# ties to 2^24, - 2^24 = 0, + 1 = 1. Reversed order gives 2 and 2, pairwise
-# 1 and 1, float64 2 and 2.
+# ties to 2^24, - 2^24 = 0, + 1 = 1. Reversed order gives 2 on both columns,
+# pairwise 1 on both (2^24 + 1 ties down, 1 - 2^24 is exact), float64 2 on
+# both: every alternative differs on column 0.
 B24 = float(2 ** 24)
 COMBINE_PIN = {0: ([1.0, B24, 1.0, -B24], 0.0), 1: ([B24, 1.0, -B24, 1.0], 1.0)}
 
@@ -440,10 +441,13 @@ def _combine_pin_layer():
 def test_combine_order_pins(ctx, m, inject):
     from test_oracle import _fold
     F = np.float32
+    alternatives = {"reversed": lambda p: _fold(p[::-1], 0.0),
+                    "pairwise": lambda p: F(F(p[0] + p[1]) + F(p[2] + p[3])),
+                    "float64": lambda p: F(np.sum(np.asarray(p, np.float64)))}
     for col, (weighted, expected) in COMBINE_PIN.items():
-        alts = [_fold(weighted[::-1], 0.0), F(F(weighted[0] + weighted[1]) + F(weighted[2] + weighted[3])),
-                F(np.sum(np.asarray(weighted, np.float64)))]
-        assert _fold(weighted, 0.0) == expected and expected not in alts
+        assert _fold(weighted, 0.0) == expected
+    for name, fn in alternatives.items():
+        assert any(fn(w) != e for w, e in COMBINE_PIN.values()), name
     host = _combine_pin_layer()
     x = O.gen_hidden(43, 1, m, 64)
     logits = np.zeros((m, 4), np.float32) if inject else None
