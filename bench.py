@@ -26,8 +26,9 @@ configs[1] measurement; `value` stays configs[1]'s.
 
 Prints one JSON line. The per-kernel roofline uses the library's hipEvent
 profiler on the stream the kernels run on (the GEMM launches record their own
-start and stop events, so the interval is the kernel's execution). For the
-HBM-bound workloads roofline.traffic is measured in the same run: two child
+start and stop events, so the interval is the kernel's execution). For every
+workload roofline.traffic (HBM bytes per gate_up launch) is measured in the
+same run: two child
 processes under rocprofv3 --pmc (FETCH_SIZE, then WRITE_SIZE) run a 1 GiB
 device copy, which calibrates each counter, and then the workload, before
 this process touches the GPU (--no-traffic skips them). `cpu_baseline` times
@@ -446,7 +447,7 @@ def main() -> int:
         return run_traffic_probe(args, cfg)
     # The counter passes run in child processes before this one touches the GPU.
     probe = probe0 = None
-    if cfg["roofline"] == "hbm" and not args.no_traffic and not args.residual:
+    if not args.no_traffic and not args.residual:
         probe = probe_traffic(args)
         if both:
             probe0 = probe_traffic(args, config=0)
@@ -577,9 +578,10 @@ def main() -> int:
             tflops = flops / (gu_avg_ms * 1e-3) / 1e12
             roofline = {"kernel": kernel, "bound": "mfma", "achieved": tflops, "peak": F16_MFMA_PEAK_TFLOPS,
                         "unit": "TFLOP/s", "frac": tflops / F16_MFMA_PEAK_TFLOPS, "traffic": None,
-                        "traffic_source": "not measured for the MFMA-bound workloads in bench.py",
                         "frac_of_mxfp4_peak": tflops / MXFP4_MFMA_PEAK_TFLOPS, "mxfp4_peak": MXFP4_MFMA_PEAK_TFLOPS,
-                        "avg_launch_ms": gu_avg_ms, "flops_per_launch": flops, "hbm_gbps": gu_gbps}
+                        "avg_launch_ms": gu_avg_ms, "flops_per_launch": flops, "hbm_gbps": gu_gbps,
+                        "weight_bytes_per_launch": gu_bytes_per_launch}
+            roofline.update(probe or {"traffic_source": "not measured (--no-traffic or --residual)"})
 
         result = {
             "metric": METRIC,

@@ -114,33 +114,29 @@ __device__ __forceinline__ void store_exp2_entry(uint64_t v) {
   if (threadIdx.x < 32) s_exp2_tab[threadIdx.x] = v;
 }
 
-// gpt_oss_swiglu for one (gate, up) pair with the sigmoid computed as
-// sigmoid_bf16 (the function the table of swiglu_one holds); the same bits.
-__device__ __forceinline__ float swiglu_one_lds(float g, float u, float alpha, float limit) {
-  const float gate = fminf(g, limit);
-  float up = u;
-  if (up < -limit) up = -limit;
-  if (up > limit) up = limit;
-  const float sig = bf16_to_f32(sigmoid_bf16(bf16_bits(gate * alpha), s_exp2_tab));
-  const float glu = bf16r(gate * sig);
-  const float lin = bf16r(up + 1.0f);
-  return bf16r(glu * lin);
-}
-
 // gpt_oss_swiglu for one (gate, up) pair, cpu_runner.rs:3797-3826: gate =
 // min(g, limit) (NaN-ignoring like f32::min), up = clamp(u, -limit, limit)
 // (NaN kept), then bf16 after every tensor operation. The sigmoid's input is
 // a bf16 value, so it is read from `sig_tab`, the 65,536 values of
 // sigmoid_bf16 computed by the same code (build_sigmoid_table).
-__device__ __forceinline__ float swiglu_one(float g, float u, float alpha, float limit, const uint16_t* sig_tab) {
+// The table index of a pair's sigmoid: the bf16 bits of min(g, limit) * alpha.
+__device__ __forceinline__ uint32_t swiglu_sigmoid_index(float g, float alpha, float limit) {
+  return bf16_bits(fminf(g, limit) * alpha);
+}
+
+// The rest of gpt_oss_swiglu once the pair's bf16 sigmoid value is known.
+__device__ __forceinline__ float swiglu_finish(float g, float u, float limit, float sig) {
   const float gate = fminf(g, limit);
   float up = u;
   if (up < -limit) up = -limit;
   if (up > limit) up = limit;
-  const float sig = bf16_to_f32(sig_tab[bf16_bits(gate * alpha)]);
   const float glu = bf16r(gate * sig);
   const float lin = bf16r(up + 1.0f);
   return bf16r(glu * lin);
+}
+
+__device__ __forceinline__ float swiglu_one(float g, float u, float alpha, float limit, const uint16_t* sig_tab) {
+  return swiglu_finish(g, u, limit, bf16_to_f32(sig_tab[swiglu_sigmoid_index(g, alpha, limit)]));
 }
 
 __global__ void build_sigmoid_table_kernel(uint16_t* tab) {
@@ -1378,7 +1374,11 @@ __device__ __forceinline__ void group_update_pipelined(Acc<C>& tot, const char* 
 // at least count * (kGemmRows / 2 + 1) floats, free for reuse. Rows of tiles
 // past the end (row >= rows) are never stored. `s_slot` (kDown, nullable):
 // the item's route slots already in LDS (else they are read from route_slot).
-template <class C, int MODE, bool RESIDUAL>
+// TABLE: the SwiGLU sigmoids are gathered from a.sig_tab (one global round
+// trip, few instructions: the tiled GEMM, whose waves are VALU-bound);
+// otherwise each is computed from the LDS copy of kExp2Tab (no round trip:
+// the latency-bound small-batch GEMVs). Both give sigmoid_bf16's bits.
+template <class C, int MODE, bool RESIDUAL, bool TABLE = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& tot, const int n_tg, const int count,
                                               const int start, const int tile0, float* s_act,
                                               const int* s_slot = nullptr, int wg_x = -1) {
@@ -1422,7 +1422,11 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& t
     static_assert(C::kChunk * kActStride * 4 <= C::kSlotBytes, "SwiGLU values fit one code slot");
     // Lane pairs (even = gate row, odd = up row) hold both values for tokens
     // t0 = 2G and t1 = 2G + 1; the even lane finishes t0 and the odd lane t1.
+    // Two passes: every pair's sigmoid is gathered from the table first (one
+    // round trip for all of them), then the pairs are finished.
     const bool odd = (nl & 1) != 0;
+    float gate_v[C::kWaveTiles][C::kNtg], up_v[C::kWaveTiles][C::kNtg];
+    uint16_t sig_v[C::kWaveTiles][C::kNtg];
 #pragma unroll
     for (int t = 0; t < C::kWaveTiles; ++t)
 #pragma unroll
@@ -1430,9 +1434,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& t
         if (tg < n_tg) {
           const float own0 = bf16r(tot[t][tg][0]), own1 = bf16r(tot[t][tg][1]);
           const float recv = __uint_as_float(lane_partner<1>(__float_as_uint(odd ? own0 : own1)));
-          const float gate = odd ? recv : own0;
-          const float up = odd ? own1 : recv;
-          const int c = tg * 8 + 2 * G + (odd ? 1 : 0);
+          gate_v[t][tg] = odd ? recv : own0;
+          up_v[t][tg] = odd ? own1 : recv;
+          sig_v[t][tg] = TABLE ? a.sig_tab[swiglu_sigmoid_index(gate_v[t][tg], a.alpha, a.limit)]
+                               : sigmoid_bf16(swiglu_sigmoid_index(gate_v[t][tg], a.alpha, a.limit), s_exp2_tab);
           const int row = (tile0 + t) * kTileRows + nl;
           if (a.trace_gu != nullptr && row < rows) {  // CpuExpertTrace::gate_up_projection (bf16 values)
             for (int u = 0; u < 2; ++u) {
@@ -1440,12 +1445,19 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const Acc<C>& t
               if (cu < count) a.trace_gu[(size_t)a.route_slot[start + cu] * rows + row] = u ? own1 : own0;
             }
           }
-          if (c < count) {
-            const float act = swiglu_one_lds(gate, up, a.alpha, a.limit);
-            s_act[c * kActStride + (wave * C::kWaveTiles + t) * 8 + (nl >> 1)] = act;
-            if (a.trace_sw != nullptr && row < rows)  // CpuExpertTrace::swiglu
-              a.trace_sw[(size_t)a.route_slot[start + c] * (rows / 2) + (row >> 1)] = act;
-          }
+        }
+      }
+#pragma unroll
+    for (int t = 0; t < C::kWaveTiles; ++t)
+#pragma unroll
+      for (int tg = 0; tg < C::kNtg; ++tg) {
+        const int c = tg * 8 + 2 * G + (odd ? 1 : 0);
+        if (tg < n_tg && c < count) {
+          const float act = swiglu_finish(gate_v[t][tg], up_v[t][tg], a.limit, bf16_to_f32(sig_v[t][tg]));
+          s_act[c * kActStride + (wave * C::kWaveTiles + t) * 8 + (nl >> 1)] = act;
+          const int row = (tile0 + t) * kTileRows + nl;
+          if (a.trace_sw != nullptr && row < rows)  // CpuExpertTrace::swiglu
+            a.trace_sw[(size_t)a.route_slot[start + c] * (rows / 2) + (row >> 1)] = act;
         }
       }
     __syncthreads();
@@ -1606,7 +1618,6 @@ __device__ __forceinline__ void k_loop(const KLoop<C>& k, Acc<C>& tot, char* c0,
 template <class C, int MODE, bool RESIDUAL>
 __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArgs a) {
   const int tid = threadIdx.x;
-  const uint64_t exp2_entry = MODE == kGateUp ? load_exp2_entry() : 0ull;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int nl = lane & 15, G = lane >> 4;
   int expert, start, count;
@@ -1694,7 +1705,6 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
   __shared__ __align__(16) float s_scl0[C::kSclSlot], s_scl1[C::kSclSlot], s_scl2[C::kSclSlot];
   if (tid < C::kChunk) s_row[tid] = row_idx;
   if (MODE == kDown && tid < C::kChunk) s_slot[tid] = slot_idx;
-  if (MODE == kGateUp) store_exp2_entry(exp2_entry);
   __syncthreads();
 
   bool fast = a.fast_ok != 0;
@@ -1747,7 +1757,7 @@ __global__ __launch_bounds__(C::kThreads, C::kMinWaves) void gemm_kernel(GemmArg
   // work-group ends.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  gemm_epilogue<C, MODE, RESIDUAL>(a, tot, n_tg, count, start, tile0, reinterpret_cast<float*>(s_codes0),
+  gemm_epilogue<C, MODE, RESIDUAL, true>(a, tot, n_tg, count, start, tile0, reinterpret_cast<float*>(s_codes0),
                                    MODE == kDown ? s_slot : nullptr, wg_x);
 }
 
