@@ -597,21 +597,22 @@ class MoeLayer:
     def forward(self, x_bf16: np.ndarray, injected_logits: np.ndarray | None = None, trace: bool = False) -> dict:
         """All outputs as arrays: router_logits, selected, routing_weights,
         output, route_order (+ trace_down, trace_gate_up, trace_swiglu: the
-        CpuExpertTrace vectors of every (row, rank))."""
+        CpuExpertTrace vectors of every (row, rank)). The arrays are allocated
+        uninitialized: a successful call writes every element."""
         x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
         m = x.shape[0]
         E, K, H = self.experts, self.top_k, self.hidden
         res = {
-            "router_logits": np.zeros((m, E), np.float32),
-            "selected": np.zeros((m, K), np.uint32),
-            "routing_weights": np.zeros((m, K), np.float32),
-            "output": np.zeros((m, H), np.float32),
-            "route_order": np.zeros(m * K, np.uint32),
+            "router_logits": np.empty((m, E), np.float32),
+            "selected": np.empty((m, K), np.uint32),
+            "routing_weights": np.empty((m, K), np.float32),
+            "output": np.empty((m, H), np.float32),
+            "route_order": np.empty(m * K, np.uint32),
         }
         if trace:
-            res["trace_down"] = np.zeros((m, K, H), np.float32)
-            res["trace_gate_up"] = np.zeros((m, K, 2 * self.intermediate), np.float32)
-            res["trace_swiglu"] = np.zeros((m, K, self.intermediate), np.float32)
+            res["trace_down"] = np.empty((m, K, H), np.float32)
+            res["trace_gate_up"] = np.empty((m, K, 2 * self.intermediate), np.float32)
+            res["trace_swiglu"] = np.empty((m, K, self.intermediate), np.float32)
         inj = None if injected_logits is None else np.ascontiguousarray(injected_logits, dtype=np.float32)
         io = MoeIo(_ptr(x), m, _ptr(inj), _ptr(res["router_logits"]), _ptr(res["selected"]),
                    _ptr(res["routing_weights"]), _ptr(res["output"]), _ptr(res["route_order"]),
@@ -632,14 +633,14 @@ class MoeLayer:
         m = x.shape[0]
         E, K, H = self.experts, self.top_k, self.hidden
         res = {
-            "router_logits": np.zeros((m, E), np.float32),
-            "selected": np.zeros((m, K), np.uint32),
-            "routing_weights": np.zeros((m, K), np.float32),
-            "route_order": np.zeros(m * K, np.uint32),
-            "next_residual": np.zeros((m, H), np.uint16),
+            "router_logits": np.empty((m, E), np.float32),
+            "selected": np.empty((m, K), np.uint32),
+            "routing_weights": np.empty((m, K), np.float32),
+            "route_order": np.empty(m * K, np.uint32),
+            "next_residual": np.empty((m, H), np.uint16),
         }
         if want_output:
-            res["output"] = np.zeros((m, H), np.float32)
+            res["output"] = np.empty((m, H), np.float32)
         inj = None if injected_logits is None else np.ascontiguousarray(injected_logits, dtype=np.float32)
         io = MoeIo(_ptr(x), m, _ptr(inj), _ptr(res["router_logits"]), _ptr(res["selected"]),
                    _ptr(res["routing_weights"]), _ptr(res.get("output")), _ptr(res["route_order"]), None, MEM_HOST)
