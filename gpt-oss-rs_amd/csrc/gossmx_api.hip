@@ -40,6 +40,17 @@ int g_scratch_state[kMaxDevices] = {};  // 0: not looked up, 1: found, -1: looku
 // until gossmx_circuit_reset().
 std::atomic<bool> g_circuit_open{false};
 
+// Process-wide accounting (gossmx_stats_read): projection results, transfer
+// bytes by direction, and the resident bytes of live weights and layers with
+// their optional cap.
+struct Stats {
+  std::atomic<uint64_t> ok{0}, failed{0}, refused{0}, rejected{0};
+  std::atomic<uint64_t> transfer[3] = {};  // TransferDirection
+  std::atomic<uint64_t> resident{0}, high_water{0}, cap{0}, cap_refusals{0};
+  std::atomic<uint64_t> cache_hits{0}, cache_misses{0};
+};
+Stats g_stats;
+
 int fail(int status, const char* fmt, ...) {
   char buf[512];
   va_list ap;
@@ -67,9 +78,24 @@ struct DevBuf {
   size_t cap = 0;
 };
 
+// What a profiled stage records beside its events: the stage's shape and
+// kernel family, and the call it belongs to.
+struct StageInfo {
+  int role = GOSSMX_ROLE_NONE;
+  int kernel = GOSSMX_KERNEL_ROUTE;
+  uint32_t n = 0, k = 0, rows_per_item = 0;
+};
+struct CallInfo {
+  int layer = -1, phase = GOSSMX_PHASE_UNKNOWN, memory = GOSSMX_MEM_DEVICE;
+  uint32_t m = 0, routes = 0;
+  uint64_t scratch_bytes = 0, resident_bytes = 0;
+};
+
 struct ProfileMark {
   int op;
   hipEvent_t start, stop;
+  StageInfo stage;
+  CallInfo call;
 };
 
 }  // namespace
@@ -93,6 +119,14 @@ struct gossmx_ctx {
   std::vector<hipEvent_t> event_pool;
   double op_ms[GOSSMX_OP_COUNT] = {0};
   uint64_t op_launches[GOSSMX_OP_COUNT] = {0};
+  // Per-stage records (gossmx_profile_events): at most
+  // GOSSMX_PROFILE_CAPACITY between resets, timed from `prof_base`, the
+  // first recorded stage's start event (kept out of the pool until a reset).
+  std::vector<gossmx_profile_event> events;
+  uint64_t events_dropped = 0, events_seq = 0;
+  hipEvent_t prof_base = nullptr;
+  int tag_layer = -1, tag_phase = GOSSMX_PHASE_UNKNOWN;
+  CallInfo call;  // the profiled call in progress
   // Pinned host staging of the host-memory calls' outputs and the error flags,
   // read back by one synchronization (grow-only).
   char* h_stage = nullptr;
@@ -100,12 +134,20 @@ struct gossmx_ctx {
   // scratch
   DevBuf x, injected, logits, selected, weights, act1v, act1s, bucket, route_tok, route_slot, work, act2v, act2s, y,
       cnt, normw, next,
-      out, trace, trace_gu, trace_sw, rec, bias, mout;
+      out, trace, trace_gu, trace_sw, rec, bias, mout, unrounded;
+  template <class F>
+  void each_buf(F f) {
+    for (DevBuf* b : {&x, &injected, &logits, &selected, &weights, &act1v, &act1s, &bucket, &route_tok, &route_slot,
+                      &work, &act2v, &act2s, &y, &cnt, &normw, &next, &out, &trace, &trace_gu, &trace_sw, &rec,
+                      &bias, &mout, &unrounded})
+      f(*b);
+  }
 };
 
 struct gossmx_weights {
   int device = 0;
   TiledWeights t;
+  uint64_t resident = 0;  // bytes taken from the resident budget
 };
 
 struct gossmx_graph {
@@ -124,6 +166,7 @@ struct gossmx_layer {
   float* router_b = nullptr;
   float* gate_up_bias = nullptr;
   float* down_bias = nullptr;
+  uint64_t resident = 0;  // bytes taken from the resident budget
 };
 
 namespace {
@@ -189,8 +232,9 @@ hipEvent_t take_event(gossmx_ctx* ctx) {
 struct OpScope {
   gossmx_ctx* ctx;
   int op;
+  StageInfo info;
   hipEvent_t start = nullptr;
-  OpScope(gossmx_ctx* c, int o) : ctx(c), op(o) {
+  OpScope(gossmx_ctx* c, int o, StageInfo i = {}) : ctx(c), op(o), info(i) {
     if (ctx->profiling && !ctx->capturing) {
       start = take_event(ctx);
       if (start) (void)hipEventRecord(start, ctx->stream);
@@ -201,7 +245,7 @@ struct OpScope {
       hipEvent_t stop = take_event(ctx);
       if (stop) {
         (void)hipEventRecord(stop, ctx->stream);
-        ctx->marks.push_back({op, start, stop});
+        ctx->marks.push_back({op, start, stop, info, ctx->call});
       } else {
         ctx->event_pool.push_back(start);
       }
@@ -215,8 +259,9 @@ struct OpScope {
 struct KernelScope {
   gossmx_ctx* ctx;
   int op;
+  StageInfo info;
   hipEvent_t start = nullptr, stop = nullptr;
-  KernelScope(gossmx_ctx* c, int o) : ctx(c), op(o) {
+  KernelScope(gossmx_ctx* c, int o, StageInfo i = {}) : ctx(c), op(o), info(i) {
     if (ctx->profiling && !ctx->capturing) {
       start = take_event(ctx);
       stop = start ? take_event(ctx) : nullptr;
@@ -227,24 +272,109 @@ struct KernelScope {
     }
   }
   ~KernelScope() {
-    if (start) ctx->marks.push_back({op, start, stop});
+    if (start) ctx->marks.push_back({op, start, stop, info, ctx->call});
   }
 };
 
+// Folds the recorded stages into the per-operation totals and the per-stage
+// records (synchronizes the stream).
 int fold_profile(gossmx_ctx* ctx) {
   if (ctx->marks.empty()) return GOSSMX_OK;
   HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  if (!ctx->prof_base) ctx->prof_base = ctx->marks.front().start;
   for (const ProfileMark& m : ctx->marks) {
-    float ms = 0.0f;
+    float ms = 0.0f, at = 0.0f;
     if (hipEventElapsedTime(&ms, m.start, m.stop) == hipSuccess) {
       ctx->op_ms[m.op] += ms;
       ctx->op_launches[m.op] += 1;
+      if (ctx->events.size() < GOSSMX_PROFILE_CAPACITY) {
+        if (hipEventElapsedTime(&at, ctx->prof_base, m.start) != hipSuccess) at = 0.0f;
+        gossmx_profile_event ev{};
+        ev.sequence = ctx->events_seq;
+        ev.op = m.op;
+        ev.role = m.stage.role;
+        ev.kernel = m.stage.kernel;
+        ev.layer = m.call.layer;
+        ev.phase = m.call.phase;
+        ev.memory = m.call.memory;
+        ev.m = m.call.m;
+        ev.n = m.stage.n;
+        ev.k = m.stage.k;
+        ev.routes = m.call.routes;
+        ev.rows_per_item = m.stage.rows_per_item;
+        ev.start_ns = (uint64_t)std::llround(std::max(0.0, (double)at * 1e6));
+        ev.duration_ns = (uint64_t)std::llround(std::max(0.0, (double)ms * 1e6));
+        ev.scratch_bytes = m.call.scratch_bytes;
+        ev.resident_bytes = m.call.resident_bytes;
+        ctx->events.push_back(ev);
+      } else {
+        ctx->events_dropped += 1;
+      }
+      ctx->events_seq += 1;
     }
-    ctx->event_pool.push_back(m.start);
+    if (m.start != ctx->prof_base) ctx->event_pool.push_back(m.start);
     ctx->event_pool.push_back(m.stop);
   }
   ctx->marks.clear();
   return GOSSMX_OK;
+}
+
+// The call about to be profiled: its shape, memory and scratch, and the
+// caller's layer / phase tag.
+void begin_call(gossmx_ctx* ctx, size_t m, size_t routes, int memory, uint64_t scratch_bytes) {
+  if (!ctx->profiling) return;
+  CallInfo& c = ctx->call;
+  c.layer = ctx->tag_layer;
+  c.phase = ctx->tag_phase;
+  c.memory = memory;
+  c.m = (uint32_t)std::min<size_t>(m, UINT32_MAX);
+  c.routes = (uint32_t)std::min<size_t>(routes, UINT32_MAX);
+  c.scratch_bytes = scratch_bytes;
+  c.resident_bytes = g_stats.resident.load(std::memory_order_relaxed);
+}
+
+uint64_t context_scratch_bytes(gossmx_ctx* ctx) {
+  uint64_t total = 0;
+  ctx->each_buf([&](DevBuf& b) { total += b.cap; });
+  return total;
+}
+
+void raise_high_water(uint64_t v) {
+  uint64_t hw = g_stats.high_water.load();
+  while (v > hw && !g_stats.high_water.compare_exchange_weak(hw, v)) {
+  }
+}
+
+// Takes `bytes` of the resident budget before an allocation; past the cap
+// the creation fails (and counts a capacity refusal).
+int reserve_resident(uint64_t bytes, const char* what) {
+  const uint64_t cap = g_stats.cap.load();
+  uint64_t cur = g_stats.resident.load();
+  for (;;) {
+    if (cap != 0 && (cur > cap || bytes > cap - cur)) {
+      g_stats.cap_refusals.fetch_add(1);
+      return fail(GOSSMX_ERR_OUT_OF_MEMORY, "%s of %llu bytes would pass the resident cap (%llu of %llu bytes held)",
+                  what, (unsigned long long)bytes, (unsigned long long)cur, (unsigned long long)cap);
+    }
+    if (g_stats.resident.compare_exchange_weak(cur, cur + bytes)) break;
+  }
+  raise_high_water(cur + bytes);
+  return GOSSMX_OK;
+}
+
+void release_resident(uint64_t bytes) { g_stats.resident.fetch_sub(bytes); }
+
+// Counts a projection call by its result.
+int count_projection(int status) {
+  switch (status) {
+    case GOSSMX_OK: g_stats.ok.fetch_add(1, std::memory_order_relaxed); break;
+    case GOSSMX_ERR_CIRCUIT_OPEN: g_stats.refused.fetch_add(1, std::memory_order_relaxed); break;
+    case GOSSMX_ERR_DEVICE:
+    case GOSSMX_ERR_OUT_OF_MEMORY:
+    case GOSSMX_ERR_INJECTED_FAULT: g_stats.failed.fetch_add(1, std::memory_order_relaxed); break;
+    default: g_stats.rejected.fetch_add(1, std::memory_order_relaxed); break;
+  }
+  return status;
 }
 
 // Clears the sticky device error flags after a read that found `flags` set,
@@ -342,9 +472,16 @@ int alloc_tiled(gossmx_ctx* ctx, size_t experts, size_t rows, size_t blocks, gos
     delete w;
     return fail(GOSSMX_ERR_UNSUPPORTED, "expert of %zu x %zu blocks too large for this build", rows, blocks);
   }
-  hipError_t e = hipMalloc(&w->t.nib, experts * w->t.nib_stride + kPlaneSlack);
-  if (e == hipSuccess) e = hipMalloc(&w->t.scl, experts * w->t.scl_stride + kPlaneSlack);
-  if (e == hipSuccess) e = hipMalloc(&w->t.fast, experts * w->t.tiles);
+  const size_t nib_bytes = experts * w->t.nib_stride + kPlaneSlack, scl_bytes = experts * w->t.scl_stride + kPlaneSlack,
+               fast_bytes = experts * w->t.tiles;
+  if (int s = reserve_resident(nib_bytes + scl_bytes + fast_bytes, "MXFP4 weights")) {
+    delete w;
+    return s;
+  }
+  w->resident = nib_bytes + scl_bytes + fast_bytes;
+  hipError_t e = hipMalloc(&w->t.nib, nib_bytes);
+  if (e == hipSuccess) e = hipMalloc(&w->t.scl, scl_bytes);
+  if (e == hipSuccess) e = hipMalloc(&w->t.fast, fast_bytes);
   // The scale bytes of the blocks past the last one in a compact last group
   // are never stored: zero them (E8M0 2^-127), so that every byte of the
   // plane converts to finite values (gemv_kernel converts whole groups).
@@ -356,6 +493,7 @@ int alloc_tiled(gossmx_ctx* ctx, size_t experts, size_t rows, size_t blocks, gos
     if (w->t.nib) (void)hipFree(w->t.nib);
     if (w->t.scl) (void)hipFree(w->t.scl);
     if (w->t.fast) (void)hipFree(w->t.fast);
+    release_resident(w->resident);
     delete w;
     return hip_fail(e, "weights allocation");
   }
@@ -403,6 +541,12 @@ int context_device(const gossmx_ctx* ctx) { return ctx->device; }
 hipStream_t context_stream(const gossmx_ctx* ctx) { return ctx->stream; }
 int run_time_result(gossmx_ctx* ctx, int status) { return projection_result(ctx, status); }
 
+void count_transfer(int direction, size_t bytes) {
+  if (direction >= 0 && direction < 3) g_stats.transfer[direction].fetch_add(bytes, std::memory_order_relaxed);
+}
+
+void count_repack_cache(bool hit) { (hit ? g_stats.cache_hits : g_stats.cache_misses).fetch_add(1); }
+
 void tiled_image_bytes(size_t experts, size_t rows, size_t blocks, size_t* nib_bytes, size_t* scl_bytes) {
   const TiledWeights t = make_tiled(experts, rows, blocks);
   *nib_bytes = experts * t.nib_stride;
@@ -425,6 +569,7 @@ int tiled_image_create(gossmx_ctx* ctx, size_t experts, size_t rows, size_t bloc
                        const uint8_t* scl, gossmx_weights** out) {
   gossmx_weights* w = nullptr;
   if (int s = alloc_tiled(ctx, experts, rows, blocks, &w)) return s;
+  count_transfer(kTransferUpload, experts * (w->t.nib_stride + w->t.scl_stride));
   hipError_t e = hipMemcpyAsync(w->t.nib, nib, experts * w->t.nib_stride, hipMemcpyHostToDevice, ctx->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(w->t.scl, scl, experts * w->t.scl_stride, hipMemcpyHostToDevice, ctx->stream);
   if (e == hipSuccess) e = launch_tile_flags(w->t, ctx->stream);
@@ -516,12 +661,10 @@ void gossmx_ctx_destroy(gossmx_ctx* ctx) {
     (void)hipEventDestroy(m.stop);
   }
   for (auto e : ctx->event_pool) (void)hipEventDestroy(e);
-  DevBuf* bufs[] = {&ctx->x, &ctx->injected, &ctx->logits, &ctx->selected, &ctx->weights, &ctx->act1v,
-                    &ctx->act1s, &ctx->bucket, &ctx->route_tok, &ctx->route_slot, &ctx->work, &ctx->act2v,
-                    &ctx->act2s, &ctx->y, &ctx->cnt, &ctx->normw, &ctx->next, &ctx->out,
-                    &ctx->trace, &ctx->trace_gu, &ctx->trace_sw, &ctx->rec, &ctx->bias, &ctx->mout};
-  for (DevBuf* b : bufs)
-    if (b->p) (void)hipFree(b->p);
+  if (ctx->prof_base) (void)hipEventDestroy(ctx->prof_base);
+  ctx->each_buf([](DevBuf& b) {
+    if (b.p) (void)hipFree(b.p);
+  });
   for (void* p : ctx->retired) (void)hipFree(p);
   if (ctx->err) (void)hipFree(ctx->err);
   if (ctx->sig_tab) (void)hipFree(ctx->sig_tab);
@@ -592,6 +735,7 @@ int gossmx_weights_upload(gossmx_ctx* ctx, const uint8_t* data, size_t len, size
   if (int s = alloc_tiled(ctx, experts, rows, blocks, &w)) return s;
   void* staging = nullptr;
   hipError_t e = hipMalloc(&staging, len);
+  count_transfer(kTransferUpload, len);
   if (e == hipSuccess) e = hipMemcpyAsync(staging, data, len, hipMemcpyHostToDevice, ctx->stream);
   if (e == hipSuccess) e = launch_repack(static_cast<const uint8_t*>(staging), layout, w->t, ctx->stream);
   if (e == hipSuccess) e = launch_tile_flags(w->t, ctx->stream);
@@ -656,6 +800,7 @@ void gossmx_weights_destroy(gossmx_weights* w) {
   if (w->t.nib) (void)hipFree(w->t.nib);
   if (w->t.scl) (void)hipFree(w->t.scl);
   if (w->t.fast) (void)hipFree(w->t.fast);
+  release_resident(w->resident);
   delete w;
 }
 
@@ -697,6 +842,7 @@ static int matmul_impl(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
   const uint8_t* rec = static_cast<const uint8_t*>(p->activations);
   if (p->memory == GOSSMX_MEM_HOST) {
     if (int s = ensure(ctx, ctx->rec, rec_count * rsz)) return s;
+    count_transfer(kTransferActivation, rec_count * rsz);
     HIP_TRY(hipMemcpyAsync(ctx->rec.p, rec, rec_count * rsz, hipMemcpyHostToDevice, ctx->stream), "H2D activations");
     rec = static_cast<const uint8_t*>(ctx->rec.p);
   }
@@ -708,6 +854,7 @@ static int matmul_impl(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
   const float* bias = p->bias;
   if (bias && p->memory == GOSSMX_MEM_HOST) {
     if (int s = ensure(ctx, ctx->bias, rows * sizeof(float))) return s;
+    count_transfer(kTransferUpload, rows * sizeof(float));
     HIP_TRY(hipMemcpyAsync(ctx->bias.p, p->bias, rows * sizeof(float), hipMemcpyHostToDevice, ctx->stream), "H2D bias");
     bias = static_cast<const float*>(ctx->bias.p);
   }
@@ -731,9 +878,13 @@ static int matmul_impl(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
   g.out_stride = out_stride;
   g.err = ctx->err;
   g.bias_expert_stride = 0;  // this problem's single bias vector
+  begin_call(ctx, m, m, p->memory, context_scratch_bytes(ctx));
   {
-    KernelScope scope(ctx, GOSSMX_OP_MATMUL);
-    if (use_gemv(m, B, g.residual != 0)) {
+    const bool gemv = use_gemv(m, B, g.residual != 0);
+    KernelScope scope(ctx, GOSSMX_OP_MATMUL,
+                      {GOSSMX_ROLE_NONE, gemv ? GOSSMX_KERNEL_GEMV : GOSSMX_KERNEL_GEMM, (uint32_t)rows,
+                       (uint32_t)(B * kBlock), gemv ? 0u : (uint32_t)gemm_chunk(m)});
+    if (gemv) {
       HIP_TRY(launch_gemv(kPlain, g, (int)m, 1, ctx->stream, scope.start, scope.stop), "matmul launch");
     } else {
       const int chunk = gemm_chunk(m);
@@ -742,6 +893,7 @@ static int matmul_impl(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
     }
   }
   if (p->memory == GOSSMX_MEM_HOST) {
+    count_transfer(kTransferOutput, m * rows * sizeof(float));
     HIP_TRY(hipMemcpy2DAsync(p->output, p->output_stride * sizeof(float), out, rows * sizeof(float),
                              rows * sizeof(float), m, hipMemcpyDeviceToHost, ctx->stream),
             "D2H output");
@@ -751,7 +903,7 @@ static int matmul_impl(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
 }
 
 int gossmx_mxfp4_matmul(gossmx_ctx* ctx, const gossmx_matmul_problem* p) {
-  return projection_result(ctx, matmul_impl(ctx, p));
+  return count_projection(projection_result(ctx, matmul_impl(ctx, p)));
 }
 
 int gossmx_mxfp4_scratch_requirement(const gossmx_matmul_problem* p, size_t* size, size_t* alignment) {
@@ -788,11 +940,15 @@ int gossmx_layer_create(gossmx_ctx* ctx, const gossmx_moe_config* cfg, const uin
     return fail(GOSSMX_ERR_INVALID_DIMENSIONS, "expert tensors do not match [%zu, %zu, %zu] / [%zu, %zu, %zu]", E, 2 * I,
                 H / kBlock, E, H, I / kBlock);
   if (int s = set_device(ctx->device)) return s;
+  const uint64_t bytes = E * H * 2 + E * 4 + E * 2 * I * 4 + E * H * 4;
+  if (int s = reserve_resident(bytes, "MoE layer")) return s;
   auto* L = new gossmx_layer();
   L->device = ctx->device;
   L->cfg = *cfg;
   L->gate_up = gate_up;
   L->down = down;
+  L->resident = bytes;
+  count_transfer(kTransferUpload, bytes);
   hipError_t e = hipMalloc(&L->router_w, E * H * 2);
   if (e == hipSuccess) e = hipMalloc(&L->router_b, E * 4);
   if (e == hipSuccess) e = hipMalloc(&L->gate_up_bias, E * 2 * I * 4);
@@ -817,6 +973,7 @@ void gossmx_layer_destroy(gossmx_layer* L) {
   if (L->router_b) (void)hipFree(L->router_b);
   if (L->gate_up_bias) (void)hipFree(L->gate_up_bias);
   if (L->down_bias) (void)hipFree(L->down_bias);
+  release_resident(L->resident);
   delete L;
 }
 
@@ -889,13 +1046,16 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   float* trace = io->trace_down;
   float* trace_gu = io->trace_gate_up;
   float* trace_sw = io->trace_swiglu;
+  float* unrounded = io->output_unrounded;
   float* logits = (!host && io->router_logits) ? io->router_logits : logits_buf;
   if (host) {
     if ((s = ensure(ctx, ctx->x, m * H * 2)) || (s = ensure(ctx, ctx->out, m * H * 4))) return s;
+    count_transfer(kTransferActivation, m * H * 2);
     HIP_TRY(hipMemcpyAsync(ctx->x.p, io->x, m * H * 2, hipMemcpyHostToDevice, ctx->stream), "H2D x");
     x = static_cast<const uint16_t*>(ctx->x.p);
     if (injected) {
       if ((s = ensure(ctx, ctx->injected, m * E * 4))) return s;
+      count_transfer(kTransferActivation, m * E * 4);
       HIP_TRY(hipMemcpyAsync(ctx->injected.p, io->injected_logits, m * E * 4, hipMemcpyHostToDevice, ctx->stream),
               "H2D logits");
       injected = static_cast<const float*>(ctx->injected.p);
@@ -913,6 +1073,10 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
       if ((s = ensure(ctx, ctx->trace_sw, R * I * 4))) return s;
       trace_sw = static_cast<float*>(ctx->trace_sw.p);
     }
+    if (unrounded) {
+      if ((s = ensure(ctx, ctx->unrounded, m * H * 4))) return s;
+      unrounded = static_cast<float*>(ctx->unrounded.p);
+    }
   }
   // Post-attention RMSNorm: the block runs on the normalized rows, the
   // residual add reads the rows as given.
@@ -924,6 +1088,7 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
     next = next_residual;
     if (host) {
       if ((s = ensure(ctx, ctx->normw, H * 4)) || (s = ensure(ctx, ctx->next, m * H * 2))) return s;
+      count_transfer(kTransferActivation, H * 4);
       HIP_TRY(hipMemcpyAsync(ctx->normw.p, norm_weight, H * 4, hipMemcpyHostToDevice, ctx->stream), "H2D norm");
       nw = static_cast<const float*>(ctx->normw.p);
       next = static_cast<uint16_t*>(ctx->next.p);
@@ -975,20 +1140,22 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   // the gate_up launch.
   const bool route_gemv = route_fused && m == 1 && E <= (size_t)kRouteGemvExperts && K <= (size_t)kSelectTopK &&
                           proj == GOSSMX_PROJECTION_RESIDUAL_Q8 && use_gemv(m, B1, true) && !trace_gu && !trace_sw;
+  begin_call(ctx, m, R, io->memory, arena ? arena->used : context_scratch_bytes(ctx));
+  const StageInfo router_stage{GOSSMX_ROLE_ROUTER, GOSSMX_KERNEL_ROUTE, (uint32_t)E, (uint32_t)H, 0};
   if (route_gemv) {
-    OpScope sc(ctx, GOSSMX_OP_ROUTER_ROUTING);
+    OpScope sc(ctx, GOSSMX_OP_ROUTER_ROUTING, router_stage);
     HIP_TRY(launch_route_logits(ra, ctx->stream), "router launch");
   } else if (route_fused) {
-    OpScope sc(ctx, GOSSMX_OP_ROUTER_ROUTING);
+    OpScope sc(ctx, GOSSMX_OP_ROUTER_ROUTING, router_stage);
     HIP_TRY(launch_route_select(ra, da, ctx->err + 1, ctx->stream), "route/select launch");
   } else if (injected == nullptr) {
-    OpScope sc(ctx, GOSSMX_OP_ROUTER_ROUTING);
+    OpScope sc(ctx, GOSSMX_OP_ROUTER_ROUTING, router_stage);
     HIP_TRY(launch_route(ra, ctx->stream), "route launch");
   }
   if (!route_fused) {
     // This stage also holds top-k, softmax and (with injected logits) the
     // gate_up input quantization.
-    OpScope sc(ctx, GOSSMX_OP_DISPATCH);
+    OpScope sc(ctx, GOSSMX_OP_DISPATCH, {GOSSMX_ROLE_NONE, GOSSMX_KERNEL_ROUTE, 0, (uint32_t)E, 0});
     const int quantize = (injected != nullptr && ra.quant) ? 1 : 0;
     if (fused) {
       HIP_TRY(launch_select_dispatch(ra, da, quantize, ctx->stream), "select/dispatch launch");
@@ -1031,18 +1198,22 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   // One row with at most four routes (one route per work item): the down
   // projection's work-groups also run the combine.
   const bool down_combine = proj != GOSSMX_PROJECTION_EXACT_BF16 && m == 1 && K <= 4 && use_gemv(m, B2, d.residual != 0);
+  const uint32_t n_gu = (uint32_t)(2 * I), n_down = (uint32_t)H;
   if (proj == GOSSMX_PROJECTION_EXACT_BF16) {
     {
-      OpScope sc(ctx, GOSSMX_OP_GATE_UP);
+      OpScope sc(ctx, GOSSMX_OP_GATE_UP, {GOSSMX_ROLE_GATE_UP, GOSSMX_KERNEL_EXACT, n_gu, (uint32_t)H, 0});
       HIP_TRY(launch_exact(kGateUp, g, (int)max_work, ctx->stream), "exact gate_up launch");
     }
     {
-      OpScope sc(ctx, GOSSMX_OP_DOWN);
+      OpScope sc(ctx, GOSSMX_OP_DOWN, {GOSSMX_ROLE_DOWN, GOSSMX_KERNEL_EXACT, n_down, (uint32_t)I, 0});
       HIP_TRY(launch_exact(kDown, d, (int)max_work, ctx->stream), "exact down launch");
     }
   } else {
     {
-      KernelScope sc(ctx, GOSSMX_OP_GATE_UP);
+      const bool gemv = route_gemv || use_gemv(m, B1, g.residual != 0);
+      KernelScope sc(ctx, GOSSMX_OP_GATE_UP,
+                     {GOSSMX_ROLE_GATE_UP, gemv ? GOSSMX_KERNEL_GEMV : GOSSMX_KERNEL_GEMM, n_gu, (uint32_t)H,
+                      gemv ? 0u : (uint32_t)chunk});
       if (route_gemv)
         HIP_TRY(launch_route_gemv(ra, da, g, ctx->stream, sc.start, sc.stop), "route/gate_up launch");
       else if (use_gemv(m, B1, g.residual != 0))
@@ -1051,9 +1222,13 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
         HIP_TRY(launch_gemm(kGateUp, g, chunk, (int)max_work, ctx->stream, sc.start, sc.stop), "gate_up launch");
     }
     {
-      KernelScope sc(ctx, GOSSMX_OP_DOWN);
+      const bool gemv = down_combine || use_gemv(m, B2, d.residual != 0);
+      KernelScope sc(ctx, GOSSMX_OP_DOWN,
+                     {GOSSMX_ROLE_DOWN, gemv ? GOSSMX_KERNEL_GEMV : GOSSMX_KERNEL_GEMM, n_down, (uint32_t)I,
+                      gemv ? 0u : (uint32_t)chunk});
       if (down_combine)
-        HIP_TRY(launch_down_combine(d, weights, (int)K, output, trace, resid, next, ctx->stream, sc.start, sc.stop),
+        HIP_TRY(launch_down_combine(d, weights, (int)K, output, trace, resid, next, unrounded, ctx->stream, sc.start,
+                                    sc.stop),
                 "down/combine launch");
       else if (use_gemv(m, B2, d.residual != 0))
         HIP_TRY(launch_gemv(kDown, d, (int)m, (int)max_work, ctx->stream, sc.start, sc.stop), "down launch");
@@ -1062,8 +1237,8 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
     }
   }
   if (!down_combine) {
-    OpScope sc(ctx, GOSSMX_OP_WEIGHTING);
-    HIP_TRY(launch_combine(d.y, weights, (int)m, (int)K, (int)H, output, trace, resid, next, ctx->stream),
+    OpScope sc(ctx, GOSSMX_OP_WEIGHTING, {GOSSMX_ROLE_NONE, GOSSMX_KERNEL_COMBINE, n_down, (uint32_t)K, 0});
+    HIP_TRY(launch_combine(d.y, weights, (int)m, (int)K, (int)H, output, trace, resid, next, unrounded, ctx->stream),
             "combine launch");
   }
 
@@ -1086,9 +1261,14 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
         {trace, io->trace_down, io->trace_down ? R * H * 4 : 0},
         {trace_gu, io->trace_gate_up, io->trace_gate_up ? R * 2 * I * 4 : 0},
         {trace_sw, io->trace_swiglu, io->trace_swiglu ? R * I * 4 : 0},
+        {unrounded, io->output_unrounded, io->output_unrounded ? m * H * 4 : 0},
     };
-    size_t need = 16;
-    for (const Piece& pc : pieces) need += (pc.bytes + 15) / 16 * 16;
+    size_t need = 16, payload = 0;
+    for (const Piece& pc : pieces) {
+      need += (pc.bytes + 15) / 16 * 16;
+      payload += pc.bytes;
+    }
+    count_transfer(kTransferOutput, payload);
     if (need > ctx->stage_cap) {
       if (ctx->h_stage) HIP_TRY(hipHostFree(ctx->h_stage), "hipHostFree");
       ctx->h_stage = nullptr;
@@ -1124,16 +1304,16 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
 }
 
 int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_io* io) {
-  return projection_result(ctx, moe_forward_impl(ctx, L, io, nullptr, 0.0f, nullptr));
+  return count_projection(projection_result(ctx, moe_forward_impl(ctx, L, io, nullptr, 0.0f, nullptr)));
 }
 
 int gossmx_moe_forward_residual(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_io* io,
                                 const float* norm_weight, float epsilon, uint16_t* next_residual) {
   if (!norm_weight) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
-  return projection_result(ctx, moe_forward_impl(ctx, L, io, norm_weight, epsilon, next_residual));
+  return count_projection(projection_result(ctx, moe_forward_impl(ctx, L, io, norm_weight, epsilon, next_residual)));
 }
 
-int gossmx_moe_forward_noalloc(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_io* io) {
+static int moe_forward_noalloc_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_io* io) {
   if (!ctx || !L || !io) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
   if (io->memory != GOSSMX_MEM_DEVICE)
     return fail(GOSSMX_ERR_INVALID_ARGUMENT, "gossmx_moe_forward_noalloc takes device memory only");
@@ -1149,6 +1329,10 @@ int gossmx_moe_forward_noalloc(gossmx_ctx* ctx, const gossmx_layer* L, const gos
   const int s = moe_forward_impl(ctx, L, io, nullptr, 0.0f, nullptr, &arena);
   ctx->profiling = profiling;
   return projection_result(ctx, s);
+}
+
+int gossmx_moe_forward_noalloc(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx_moe_io* io) {
+  return count_projection(moe_forward_noalloc_impl(ctx, L, io));
 }
 
 // --- profiling, fault hook, self-test -------------------------------------------
@@ -1179,6 +1363,66 @@ int gossmx_profile_reset(gossmx_ctx* ctx) {
     ctx->op_ms[i] = 0.0;
     ctx->op_launches[i] = 0;
   }
+  ctx->events.clear();
+  ctx->events_dropped = 0;
+  ctx->events_seq = 0;
+  if (ctx->prof_base) ctx->event_pool.push_back(ctx->prof_base);
+  ctx->prof_base = nullptr;
+  return GOSSMX_OK;
+}
+
+int gossmx_profile_tag(gossmx_ctx* ctx, int layer, int phase) {
+  if (!ctx) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null context");
+  if (layer < -1) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "layer tag %d below -1", layer);
+  if (phase != GOSSMX_PHASE_UNKNOWN && phase != GOSSMX_PHASE_PREFILL && phase != GOSSMX_PHASE_DECODE)
+    return fail(GOSSMX_ERR_INVALID_ARGUMENT, "unknown phase %d", phase);
+  ctx->tag_layer = layer;
+  ctx->tag_phase = phase;
+  return GOSSMX_OK;
+}
+
+int gossmx_profile_events(gossmx_ctx* ctx, gossmx_profile_event* out, size_t capacity, size_t* written,
+                          size_t* available, uint64_t* dropped) {
+  if (!ctx || !written || (capacity && !out)) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+  if (int s = fold_profile(ctx)) return s;
+  const size_t n = std::min(capacity, ctx->events.size());
+  if (n) std::memcpy(out, ctx->events.data(), n * sizeof(gossmx_profile_event));
+  *written = n;
+  if (available) *available = ctx->events.size();
+  if (dropped) *dropped = ctx->events_dropped;
+  return GOSSMX_OK;
+}
+
+int gossmx_stats_read(gossmx_stats* out) {
+  if (!out) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null output");
+  *out = gossmx_stats{};
+  out->projections_ok = g_stats.ok.load();
+  out->projections_failed = g_stats.failed.load();
+  out->projections_refused = g_stats.refused.load();
+  out->projections_rejected = g_stats.rejected.load();
+  out->weights_bias_uploaded_bytes = g_stats.transfer[kTransferUpload].load();
+  out->activation_bytes = g_stats.transfer[kTransferActivation].load();
+  out->output_bytes = g_stats.transfer[kTransferOutput].load();
+  out->resident_bytes = g_stats.resident.load();
+  out->resident_high_water_bytes = g_stats.high_water.load();
+  out->resident_cap_bytes = g_stats.cap.load();
+  out->capacity_refusals = g_stats.cap_refusals.load();
+  out->repack_cache_hits = g_stats.cache_hits.load();
+  out->repack_cache_misses = g_stats.cache_misses.load();
+  out->circuit_open = g_circuit_open.load() ? 1 : 0;
+  return GOSSMX_OK;
+}
+
+void gossmx_stats_reset(void) {
+  for (std::atomic<uint64_t>* c : {&g_stats.ok, &g_stats.failed, &g_stats.refused, &g_stats.rejected,
+                                   &g_stats.transfer[0], &g_stats.transfer[1], &g_stats.transfer[2],
+                                   &g_stats.cap_refusals, &g_stats.cache_hits, &g_stats.cache_misses})
+    c->store(0);
+  g_stats.high_water.store(g_stats.resident.load());
+}
+
+int gossmx_set_resident_cap(uint64_t bytes) {
+  g_stats.cap.store(bytes);
   return GOSSMX_OK;
 }
 

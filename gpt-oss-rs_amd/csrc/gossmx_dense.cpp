@@ -353,6 +353,7 @@ int upload(DenseDevice& D, const T* src, size_t n, const T** dst) {
   void* p = nullptr;
   DENSE_HIP(hipMalloc(&p, n * sizeof(T)), "model weights allocation");
   D.weights.push_back(p);
+  gossmx::count_transfer(gossmx::kTransferUpload, n * sizeof(T));
   DENSE_HIP(hipMemcpy(p, src, n * sizeof(T), hipMemcpyHostToDevice), "model weights upload");
   *dst = static_cast<const T*>(p);
   return GOSSMX_OK;
@@ -393,6 +394,7 @@ int gpu_project_impl(gossmx_model* M, const uint16_t* in, size_t m, size_t cols,
   if (int st = grow(&D.d_in, &D.h_in, &D.in_cap, m * cols)) return st;
   if (int st = grow(&D.d_out, &D.h_out, &D.out_cap, total)) return st;
   for (size_t i = 0; i < m * cols; ++i) D.h_in[i] = bf16_f32(in[i]);
+  gossmx::count_transfer(gossmx::kTransferActivation, m * cols * sizeof(float));
   DENSE_HIP(hipMemcpyAsync(D.d_in, D.h_in, m * cols * sizeof(float), hipMemcpyHostToDevice, stream),
             "projection input copy");
   // One launch per group. One token through small matrices (Q/K/V, O):
@@ -412,6 +414,7 @@ int gpu_project_impl(gossmx_model* M, const uint16_t* in, size_t m, size_t cols,
   DENSE_HIP(whole_k ? gossmx::launch_dense_gemv(set, (int)count, D.d_in, (int)cols, stream)
                     : gossmx::launch_dense_proj(set, (int)count, D.d_in, (int)cols, (int)m, stream),
             "projection launch");
+  gossmx::count_transfer(gossmx::kTransferOutput, total * sizeof(float));
   DENSE_HIP(hipMemcpyAsync(D.h_out, D.d_out, total * sizeof(float), hipMemcpyDeviceToHost, stream),
             "projection output copy");
   DENSE_HIP(hipStreamSynchronize(stream), "projection");
@@ -447,6 +450,7 @@ int gpu_o_residual_moe_impl(gossmx_model* M, const gossmx_dense_layer& L, const 
   uint16_t* h_rows = reinterpret_cast<uint16_t*>(D.h_rows);
   for (size_t i = 0; i < m * QW; ++i) D.h_in[i] = bf16_f32(attn[i]);
   std::memcpy(h_rows, hidden, n * 2);
+  gossmx::count_transfer(gossmx::kTransferActivation, m * QW * sizeof(float) + n * 2);
   DENSE_HIP(hipMemcpyAsync(D.d_in, D.h_in, m * QW * sizeof(float), hipMemcpyHostToDevice, stream),
             "projection input copy");
   DENSE_HIP(hipMemcpyAsync(d_hidden, h_rows, n * 2, hipMemcpyHostToDevice, stream), "residual rows copy");
@@ -466,8 +470,10 @@ int gpu_o_residual_moe_impl(gossmx_model* M, const gossmx_dense_layer& L, const 
   io.m = m;
   io.memory = GOSSMX_MEM_DEVICE;
   int st = gossmx_moe_forward_residual(M->ctx, L.moe, &io, DL.post_norm, M->cfg.rms_norm_eps, d_next);
+  (void)gossmx_profile_tag(M->ctx, -1, GOSSMX_PHASE_UNKNOWN);
   if (st == GOSSMX_OK) {
     // gossmx_synchronize reports the device error flags.
+    gossmx::count_transfer(gossmx::kTransferOutput, n * 2);
     const hipError_t e = hipMemcpyAsync(h_rows + n, d_next, n * 2, hipMemcpyDeviceToHost, stream);
     st = e == hipSuccess ? gossmx_synchronize(M->ctx) : hip_err(e, "next rows copy");
   }
@@ -558,6 +564,8 @@ int run_step(gossmx_model* M, const uint32_t* tokens, size_t m, float* logits) {
     });
     // O projection, residual add and the MoE half (norm_boundary(after,
     // post_attention_norm), moe_batch, add_residual) -> the next layer's rows.
+    // The MoE block's profile records carry the layer and the phase.
+    (void)gossmx_profile_tag(M->ctx, (int)li, base == 0 || m > 1 ? GOSSMX_PHASE_PREFILL : GOSSMX_PHASE_DECODE);
     const int st = gpu_o_residual_moe(M, L, DL, attn.data(), m, hidden.data(), &moe);
     if (st != GOSSMX_OK) return st;
   }

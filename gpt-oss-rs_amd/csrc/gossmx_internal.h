@@ -195,14 +195,15 @@ hipError_t launch_route_gemv(const RouteArgs& r, const DispatchArgs& d, const Ge
 // launch_gemv(kDown) followed by launch_combine with m = 1, without the y
 // buffer (d.y is not written).
 hipError_t launch_down_combine(const GemmArgs& d, const float* weights, int top_k, float* out, float* trace_down,
-                               const uint16_t* resid, uint16_t* next, hipStream_t stream,
+                               const uint16_t* resid, uint16_t* next, float* unrounded, hipStream_t stream,
                                hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 // Exact-BF16 expert projection over the work list (mode kGateUp or kDown);
 // chunk <= kChunkMax.
 hipError_t launch_exact(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream);
 
 hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int top_k, int hidden, float* out,
-                          float* trace_down, const uint16_t* resid, uint16_t* next, hipStream_t stream);
+                          float* trace_down, const uint16_t* resid, uint16_t* next, float* unrounded,
+                          hipStream_t stream);
 hipError_t launch_prep_records(const uint8_t* records, int kind, size_t m, size_t blocks, size_t row_stride,
                                ActBuffers act, int* err, hipStream_t stream);
 hipError_t launch_repack(const uint8_t* src, int layout, TiledWeights w, hipStream_t stream);
@@ -256,6 +257,11 @@ hipStream_t context_stream(const gossmx_ctx* ctx);
 // A GPU round trip's status: GOSSMX_ERR_DEVICE or GOSSMX_ERR_OUT_OF_MEMORY
 // drains the context's stream and opens the process-wide circuit breaker.
 int run_time_result(gossmx_ctx* ctx, int status);
+// Process-wide accounting of host<->device copies (gossmx_stats).
+enum TransferDirection { kTransferUpload = 0, kTransferActivation = 1, kTransferOutput = 2 };
+void count_transfer(int direction, size_t bytes);
+// gossmx_weights_open_or_create's repack cache: a valid repack was found.
+void count_repack_cache(bool hit);
 void tiled_image_bytes(size_t experts, size_t rows, size_t blocks, size_t* nib_bytes, size_t* scl_bytes);
 int tiled_image_read(gossmx_ctx* ctx, const gossmx_weights* w, uint8_t* nib, uint8_t* scl);
 int tiled_image_create(gossmx_ctx* ctx, size_t experts, size_t rows, size_t blocks, const uint8_t* nib,

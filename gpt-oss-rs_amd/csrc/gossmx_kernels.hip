@@ -2117,6 +2117,7 @@ struct CombineArgs {
   float* trace;            // [top_k][rows] down outputs by rank, or null
   const uint16_t* resid;   // [rows] bf16 residual stream, or null
   uint16_t* next;          // [rows] bf16(resid + out), or null
+  float* unrounded;        // [rows] the weighted sum before its bf16 round trip, or null
 };
 
 __global__ __launch_bounds__(DownCombineGeom::kThreads, 2) void gemv_down_combine_kernel(GemmArgs a, CombineArgs c) {
@@ -2225,6 +2226,7 @@ __global__ __launch_bounds__(DownCombineGeom::kThreads, 2) void gemv_down_combin
     for (int k = 0; k < c.top_k; ++k) acc = acc + s_y[k * kTileRows + nl] * c.weights[k];
     const float o = bf16r(acc);
     if (c.out != nullptr) c.out[row] = o;
+    if (c.unrounded != nullptr) c.unrounded[row] = acc;
     if (c.next != nullptr) c.next[row] = bf16_bits(bf16_to_f32(c.resid[row]) + o);
   }
 }
@@ -2554,7 +2556,7 @@ __global__ __launch_bounds__(256) void tile_flags_kernel(TiledWeights w) {
 // bf16(resid + out). `out` may be null when only `next` is wanted.
 __global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* y, const float* w, int top_k, int hidden,
                                                       float* out, float* trace, const uint16_t* resid,
-                                                      uint16_t* next) {
+                                                      uint16_t* next, float* unrounded) {
   const int r = blockIdx.y;
   const int h = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
   if (h >= hidden) return;
@@ -2590,6 +2592,11 @@ __global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* y, const 
       t[1] = make_float4(v[4], v[5], v[6], v[7]);
     }
   }
+  if (unrounded) {  // the sum before fp32_to_bf16_roundtrip (cpu_runner.rs:2991)
+    float4* up = reinterpret_cast<float4*>(unrounded + (size_t)r * hidden + h);
+    up[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    up[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
   float o[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = bf16r(acc[e]);
@@ -2613,7 +2620,7 @@ __global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* y, const 
 
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* y, const float* w, int top_k, int hidden,
                                                      float* out, float* trace, const uint16_t* resid,
-                                                     uint16_t* next) {
+                                                     uint16_t* next, float* unrounded) {
   const int r = blockIdx.y;
   const int h = blockIdx.x * blockDim.x + threadIdx.x;
   if (h >= hidden) return;
@@ -2624,6 +2631,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* y, const f
     acc = acc + v * w[slot];
     if (trace) trace[slot * hidden + h] = v;
   }
+  if (unrounded) unrounded[(size_t)r * hidden + h] = acc;
   const float o = bf16r(acc);
   if (out) out[(size_t)r * hidden + h] = o;
   if (next) next[(size_t)r * hidden + h] = bf16_bits(bf16_to_f32(resid[(size_t)r * hidden + h]) + o);
@@ -2989,12 +2997,12 @@ hipError_t launch_route_gemv(const RouteArgs& r, const DispatchArgs& d, const Ge
 }
 
 hipError_t launch_down_combine(const GemmArgs& d, const float* weights, int top_k, float* out, float* trace_down,
-                               const uint16_t* resid, uint16_t* next, hipStream_t stream, hipEvent_t start,
-                               hipEvent_t stop) {
+                               const uint16_t* resid, uint16_t* next, float* unrounded, hipStream_t stream,
+                               hipEvent_t start, hipEvent_t stop) {
   if (d.w.blocks > (size_t)kTinyMaxBlocks || !d.residual || top_k < 1 || top_k > DownCombineGeom::kItems ||
       (next != nullptr && resid == nullptr))
     return hipErrorInvalidValue;
-  CombineArgs c{weights, top_k, out, trace_down, resid, next};
+  CombineArgs c{weights, top_k, out, trace_down, resid, next, unrounded};
   const dim3 grid((unsigned)d.w.tiles), block(DownCombineGeom::kThreads);
   if (start) hipExtLaunchKernelGGL(gemv_down_combine_kernel, grid, block, 0, stream, start, stop, 0, d, c);
   else hipLaunchKernelGGL(gemv_down_combine_kernel, grid, block, 0, stream, d, c);
@@ -3016,15 +3024,17 @@ hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream) {
 }
 
 hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int top_k, int hidden, float* out,
-                          float* trace_down, const uint16_t* resid, uint16_t* next, hipStream_t stream) {
+                          float* trace_down, const uint16_t* resid, uint16_t* next, float* unrounded,
+                          hipStream_t stream) {
   const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-  const bool aligned = hidden % 8 == 0 && a16(y) && a16(out) && a16(trace_down) && a16(resid) && a16(next);
+  const bool aligned =
+      hidden % 8 == 0 && a16(y) && a16(out) && a16(trace_down) && a16(resid) && a16(next) && a16(unrounded);
   if (aligned)
     hipLaunchKernelGGL(combine8_kernel, dim3(grid1d(hidden / 8, 256), m), dim3(256), 0, stream, y, weights, top_k,
-                       hidden, out, trace_down, resid, next);
+                       hidden, out, trace_down, resid, next, unrounded);
   else
     hipLaunchKernelGGL(combine_kernel, dim3(grid1d(hidden, 256), m), dim3(256), 0, stream, y, weights, top_k,
-                       hidden, out, trace_down, resid, next);
+                       hidden, out, trace_down, resid, next, unrounded);
   return hipGetLastError();
 }
 

@@ -1013,12 +1013,16 @@ int gossmx_weights_open_or_create(gossmx_ctx* ctx, const char* cache_root, const
   const RepackHeader expected = v3_header(blocks_name, shape, model_revision, source_hashes, n_hashes);
   const std::string dir = std::string(cache_root) + "/mxfp4/" + key;
   const std::string target = dir + "/weights.repack";
-  if (load_container(ctx, target.c_str(), &expected, out) == GOSSMX_OK) return GOSSMX_OK;
+  if (load_container(ctx, target.c_str(), &expected, out) == GOSSMX_OK) {
+    gossmx::count_repack_cache(true);
+    return GOSSMX_OK;
+  }
   if (int s = make_dirs(dir)) return s;
   const std::string lock = dir + "/repack.lock";
   bool owned = false;
   if (int s = acquire_lock(lock, target, expected, owned)) return s;
   int s = load_container(ctx, target.c_str(), &expected, out);
+  gossmx::count_repack_cache(s == GOSSMX_OK);
   if (s != GOSSMX_OK) {
     size_t got[3];
     s = from_safetensors(ctx, shards, n_shards, blocks_name, scales_name, out, got);

@@ -51,6 +51,11 @@ MEM_HOST = 0
 MEM_DEVICE = 1
 
 OPS = ("router_routing", "dispatch", "gate_up", "down", "weighting", "matmul", "post_attention_norm")
+ROLES = ("none", "router", "gate_up", "down")
+KERNELS = ("route", "gemv", "gemm", "exact", "combine")
+PHASE_UNKNOWN, PHASE_PREFILL, PHASE_DECODE = 0, 1, 2
+PHASES = ("unknown", "prefill", "decode")
+PROFILE_CAPACITY = 65536
 
 # The reference's activation records (lib.rs:732-742), 36 and 72 bytes.
 Q8_DTYPE = np.dtype([("scale", "<f4"), ("values", "i1", (32,))])
@@ -99,11 +104,30 @@ class MoeIo(C.Structure):
     _fields_ = [("x", C.c_void_p), ("m", C.c_size_t), ("injected_logits", C.c_void_p),
                 ("router_logits", C.c_void_p), ("selected", C.c_void_p), ("routing_weights", C.c_void_p),
                 ("output", C.c_void_p), ("route_order", C.c_void_p), ("trace_down", C.c_void_p),
-                ("memory", C.c_int), ("trace_gate_up", C.c_void_p), ("trace_swiglu", C.c_void_p)]
+                ("memory", C.c_int), ("trace_gate_up", C.c_void_p), ("trace_swiglu", C.c_void_p),
+                ("output_unrounded", C.c_void_p)]
 
 
 class ProfileRecord(C.Structure):
     _fields_ = [("op", C.c_int), ("launches", C.c_uint64), ("total_ms", C.c_double)]
+
+
+class ProfileEvent(C.Structure):
+    """gossmx_profile_event: one profiled stage (CpuExecutionProfileRecord)."""
+    _fields_ = [("sequence", C.c_uint64), ("op", C.c_int32), ("role", C.c_int32), ("kernel", C.c_int32),
+                ("layer", C.c_int32), ("phase", C.c_int32), ("memory", C.c_int32), ("m", C.c_uint32),
+                ("n", C.c_uint32), ("k", C.c_uint32), ("routes", C.c_uint32), ("rows_per_item", C.c_uint32),
+                ("reserved", C.c_uint32), ("start_ns", C.c_uint64), ("duration_ns", C.c_uint64),
+                ("scratch_bytes", C.c_uint64), ("resident_bytes", C.c_uint64)]
+
+
+class Stats(C.Structure):
+    """gossmx_stats: the process-wide projection, transfer and residency counters."""
+    _fields_ = [(name, C.c_uint64) for name in (
+        "projections_ok", "projections_failed", "projections_refused", "projections_rejected",
+        "weights_bias_uploaded_bytes", "activation_bytes", "output_bytes", "resident_bytes",
+        "resident_high_water_bytes", "resident_cap_bytes", "capacity_refusals", "repack_cache_hits",
+        "repack_cache_misses")] + [("circuit_open", C.c_int32), ("reserved", C.c_int32)]
 
 
 _lib = None
@@ -202,6 +226,12 @@ def load():
         "gossmx_profile_enable": (i32, [vp, i32]),
         "gossmx_profile_read": (i32, [vp, C.POINTER(ProfileRecord), sz, C.POINTER(sz)]),
         "gossmx_profile_reset": (i32, [vp]),
+        "gossmx_profile_tag": (i32, [vp, i32, i32]),
+        "gossmx_profile_events": (i32, [vp, C.POINTER(ProfileEvent), sz, C.POINTER(sz), C.POINTER(sz),
+                                        C.POINTER(u64)]),
+        "gossmx_stats_read": (i32, [C.POINTER(Stats)]),
+        "gossmx_stats_reset": (None, []),
+        "gossmx_set_resident_cap": (i32, [u64]),
         "gossmx_inject_fault": (i32, [vp, i32]),
         "gossmx_capture_begin": (i32, [vp]),
         "gossmx_capture_end": (i32, [vp, pp]),
@@ -251,6 +281,23 @@ def circuit_is_open() -> bool:
 
 def circuit_reset():
     load().gossmx_circuit_reset()
+
+
+def stats() -> dict:
+    """The process-wide counters (gossmx_stats_read): projections by result,
+    transfer bytes by direction, resident bytes and the cap."""
+    st = Stats()
+    _check(load().gossmx_stats_read(C.byref(st)))
+    return {name: int(getattr(st, name)) for name, _ in Stats._fields_ if name != "reserved"}
+
+
+def stats_reset():
+    load().gossmx_stats_reset()
+
+
+def set_resident_cap(nbytes: int):
+    """Caps the device bytes of live weights and layers (0: no cap)."""
+    _check(load().gossmx_set_resident_cap(int(nbytes)))
 
 
 def device_count() -> int:
@@ -311,6 +358,28 @@ class Context:
         n = C.c_size_t(0)
         _check(load().gossmx_profile_read(self._h, recs, len(OPS), C.byref(n)))
         return {OPS[r.op]: {"launches": int(r.launches), "total_ms": float(r.total_ms)} for r in recs[:n.value]}
+
+    def profile_tag(self, layer: int = -1, phase: int = PHASE_UNKNOWN):
+        _check(load().gossmx_profile_tag(self._h, layer, phase))
+
+    def profile_events(self, capacity: int | None = None) -> tuple[list[dict], int]:
+        """The per-stage records kept since the last reset, oldest first, and
+        the number dropped past the context's capacity."""
+        avail, written, dropped = C.c_size_t(0), C.c_size_t(0), C.c_uint64(0)
+        _check(load().gossmx_profile_events(self._h, None, 0, C.byref(written), C.byref(avail), C.byref(dropped)))
+        cap = avail.value if capacity is None else min(capacity, avail.value)
+        recs = (ProfileEvent * max(cap, 1))()
+        _check(load().gossmx_profile_events(self._h, recs, cap, C.byref(written), C.byref(avail), C.byref(dropped)))
+        out = []
+        for r in recs[:written.value]:
+            ev = {name: int(getattr(r, name)) for name, _ in ProfileEvent._fields_ if name != "reserved"}
+            ev["op"] = OPS[r.op]
+            ev["role"] = ROLES[r.role]
+            ev["kernel"] = KERNELS[r.kernel]
+            ev["phase"] = PHASES[r.phase]
+            ev["memory"] = "device" if r.memory == MEM_DEVICE else "host"
+            out.append(ev)
+        return out, int(dropped.value)
 
     def capture_begin(self):
         _check(load().gossmx_capture_begin(self._h))
@@ -594,10 +663,12 @@ class MoeLayer:
                                           down.handle, _ptr(db), C.byref(self._h)))
         self.gate_up, self.down = gate_up, down
 
-    def forward(self, x_bf16: np.ndarray, injected_logits: np.ndarray | None = None, trace: bool = False) -> dict:
+    def forward(self, x_bf16: np.ndarray, injected_logits: np.ndarray | None = None, trace: bool = False,
+                unrounded: bool = False) -> dict:
         """All outputs as arrays: router_logits, selected, routing_weights,
         output, route_order (+ trace_down, trace_gate_up, trace_swiglu: the
-        CpuExpertTrace vectors of every (row, rank)). The arrays are allocated
+        CpuExpertTrace vectors of every (row, rank); + output_unrounded: the
+        combine's sum before its bf16 round trip). The arrays are allocated
         uninitialized: a successful call writes every element."""
         x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
         m = x.shape[0]
@@ -613,11 +684,13 @@ class MoeLayer:
             res["trace_down"] = np.empty((m, K, H), np.float32)
             res["trace_gate_up"] = np.empty((m, K, 2 * self.intermediate), np.float32)
             res["trace_swiglu"] = np.empty((m, K, self.intermediate), np.float32)
+        if unrounded:
+            res["output_unrounded"] = np.empty((m, H), np.float32)
         inj = None if injected_logits is None else np.ascontiguousarray(injected_logits, dtype=np.float32)
         io = MoeIo(_ptr(x), m, _ptr(inj), _ptr(res["router_logits"]), _ptr(res["selected"]),
                    _ptr(res["routing_weights"]), _ptr(res["output"]), _ptr(res["route_order"]),
                    _ptr(res.get("trace_down")), MEM_HOST, _ptr(res.get("trace_gate_up")),
-                   _ptr(res.get("trace_swiglu")))
+                   _ptr(res.get("trace_swiglu")), _ptr(res.get("output_unrounded")))
         _check(load().gossmx_moe_forward(self.ctx.handle, self._h, C.byref(io)))
         return res
 
@@ -657,11 +730,11 @@ class MoeLayer:
                                                   float(epsilon), _ptr(next_residual)))
 
     def forward_device(self, x, m: int, output, injected_logits=None, router_logits=None, selected=None,
-                       routing_weights=None, route_order=None):
+                       routing_weights=None, route_order=None, output_unrounded=None):
         """Asynchronous forward on device pointers (ints or torch tensors);
         device-side errors surface at the next Context.synchronize()."""
         io = MoeIo(_ptr(x), m, _ptr(injected_logits), _ptr(router_logits), _ptr(selected), _ptr(routing_weights),
-                   _ptr(output), _ptr(route_order), None, MEM_DEVICE)
+                   _ptr(output), _ptr(route_order), None, MEM_DEVICE, None, None, _ptr(output_unrounded))
         _check(load().gossmx_moe_forward(self.ctx.handle, self._h, C.byref(io)))
 
     def moe_batch(self, inputs: np.ndarray, injected_logits: np.ndarray | None = None) -> list[MoeStep]:

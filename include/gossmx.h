@@ -255,6 +255,52 @@ int gossmx_mxfp4_scratch_requirement(const gossmx_matmul_problem* problem, size_
 int gossmx_circuit_is_open(void);
 void gossmx_circuit_reset(void);
 
+/* Process-wide accounting, the counters the Xe engine exports as metrics
+ * (crates/gpt-oss-xe/src/lib.rs:44-49: projection_total by result,
+ * transfer_bytes_total by direction, circuit_breaker, the expert cache's
+ * resident bytes; record_projection_metrics :785-825; XeResidencyStats
+ * :358-370). Projection calls (gossmx_mxfp4_matmul, gossmx_moe_forward,
+ * gossmx_moe_forward_residual, gossmx_moe_forward_noalloc) count by their
+ * return: ok; failed (GOSSMX_ERR_DEVICE, GOSSMX_ERR_OUT_OF_MEMORY,
+ * GOSSMX_ERR_INJECTED_FAULT: the caller's fallback reason "execution
+ * failure"); refused (GOSSMX_ERR_CIRCUIT_OPEN: the caller's fallback reason
+ * "fault"); rejected (every other status: argument, shape or non-finite data).
+ * A device-memory call counts when it returns; a device-side error that a
+ * later gossmx_synchronize reports does not change its count. Transfer bytes
+ * are the host<->device copies the library makes: weights, router and bias
+ * uploads (weights_bias_uploaded); the inputs of host-memory calls and the
+ * dense model's round trips (activations); their results (output). Resident
+ * bytes are the device memory held by live gossmx_weights and gossmx_layer
+ * objects (planes with their padding, router and biases); contexts' scratch is
+ * not included. */
+typedef struct gossmx_stats {
+  uint64_t projections_ok;
+  uint64_t projections_failed;
+  uint64_t projections_refused;
+  uint64_t projections_rejected;
+  uint64_t weights_bias_uploaded_bytes;
+  uint64_t activation_bytes;
+  uint64_t output_bytes;
+  uint64_t resident_bytes;
+  uint64_t resident_high_water_bytes;
+  uint64_t resident_cap_bytes;        /* 0: no cap */
+  uint64_t capacity_refusals;         /* creations refused by the cap */
+  uint64_t repack_cache_hits;         /* gossmx_weights_open_or_create found a valid repack */
+  uint64_t repack_cache_misses;       /* ... repacked from the SafeTensors shards */
+  int32_t circuit_open;
+  int32_t reserved;
+} gossmx_stats;
+int gossmx_stats_read(gossmx_stats* out);
+/* Zeroes the counters and sets the high-water mark to the bytes resident now;
+ * the cap and the resident bytes are kept. */
+void gossmx_stats_reset(void);
+/* Cap on the resident bytes (AttachConfig::max_resident_bytes,
+ * crates/gpt-oss-xe/src/lib.rs:239-250; 0 removes it). Weights and layer
+ * creation that would pass it fails with GOSSMX_ERR_OUT_OF_MEMORY before
+ * allocating anything and counts a capacity refusal; what is already resident
+ * stays, also when the new cap is below it. */
+int gossmx_set_resident_cap(uint64_t bytes);
+
 /* MoE layer (GPT-OSS): router [experts][hidden] bf16 + f32 bias, gate_up
  * [experts][2*intermediate][hidden/32] with gate/up rows interleaved even/odd
  * and f32 bias [experts][2*intermediate], down [experts][hidden][intermediate/32]
@@ -291,8 +337,12 @@ void gossmx_layer_destroy(gossmx_layer* layer);
  * [m][top_k][hidden] receives each rank's bf16-rounded down projection,
  * trace_gate_up [m][top_k][2 * intermediate] its bf16-rounded gate_up
  * projection and trace_swiglu [m][top_k][intermediate] its SwiGLU values
- * (CpuExpertTrace, cpu_runner.rs:2970-2984). All pointers are host or device
- * memory as `memory` says. */
+ * (CpuExpertTrace, cpu_runner.rs:2970-2984). output_unrounded [m][hidden] f32
+ * receives the weighted sum of the ranks before its bf16 round trip
+ * (fp32_to_bf16_roundtrip, cpu_runner.rs:2991), for callers that compare
+ * pre-round values; no counterpart field in CpuMoeStep. All pointers are host
+ * or device memory as `memory` says. Callers that zero-initialize the struct
+ * leave the trailing fields null. */
 typedef struct gossmx_moe_io {
   const uint16_t* x;
   size_t m;
@@ -306,6 +356,7 @@ typedef struct gossmx_moe_io {
   int memory;
   float* trace_gate_up;
   float* trace_swiglu;
+  float* output_unrounded;
 } gossmx_moe_io;
 
 int gossmx_moe_forward(gossmx_ctx* ctx, const gossmx_layer* layer, const gossmx_moe_io* io);
@@ -363,7 +414,61 @@ typedef struct gossmx_profile_record {
 int gossmx_profile_enable(gossmx_ctx* ctx, int enabled);
 /* Synchronizes, folds pending events into totals, writes GOSSMX_OP_COUNT records. */
 int gossmx_profile_read(gossmx_ctx* ctx, gossmx_profile_record* out, size_t capacity, size_t* written);
+/* Also clears the per-stage records below and their dropped count. */
 int gossmx_profile_reset(gossmx_ctx* ctx);
+
+/* Per-stage records of the profiled calls, a fixed-layout record per stage
+ * like CpuExecutionProfileRecord (cpu_profile.rs:121-150): the operation, the
+ * layer and phase the caller tagged, the shape, the projection role, the
+ * kernel family that ran, and the timing from the stage's events. A context
+ * keeps at most GOSSMX_PROFILE_CAPACITY records between resets; later stages
+ * still add to the totals of gossmx_profile_read and count as dropped. */
+enum {
+  GOSSMX_ROLE_NONE = 0,
+  GOSSMX_ROLE_ROUTER = 1,
+  GOSSMX_ROLE_GATE_UP = 2,
+  GOSSMX_ROLE_DOWN = 3
+};
+enum {
+  GOSSMX_KERNEL_ROUTE = 0,          /* router / selection / grouping kernels */
+  GOSSMX_KERNEL_GEMV = 1,           /* one work-group per (row block, route): few rows */
+  GOSSMX_KERNEL_GEMM = 2,           /* MFMA tiles; rows_per_item tells the geometry */
+  GOSSMX_KERNEL_EXACT = 3,          /* exact-BF16 expert projection */
+  GOSSMX_KERNEL_COMBINE = 4         /* routing-weight accumulation */
+};
+enum {
+  GOSSMX_PHASE_UNKNOWN = 0,
+  GOSSMX_PHASE_PREFILL = 1,
+  GOSSMX_PHASE_DECODE = 2
+};
+#define GOSSMX_PROFILE_CAPACITY 65536
+typedef struct gossmx_profile_event {
+  uint64_t sequence;        /* per context, from 0 after a reset */
+  int32_t op;               /* GOSSMX_OP_* */
+  int32_t role;             /* GOSSMX_ROLE_* */
+  int32_t kernel;           /* GOSSMX_KERNEL_* */
+  int32_t layer;            /* gossmx_profile_tag value; -1 untagged */
+  int32_t phase;            /* GOSSMX_PHASE_* from gossmx_profile_tag */
+  int32_t memory;           /* GOSSMX_MEM_HOST or GOSSMX_MEM_DEVICE */
+  uint32_t m;               /* activation rows of the call */
+  uint32_t n;               /* output columns of the stage (0: none) */
+  uint32_t k;               /* input columns of the stage */
+  uint32_t routes;          /* (row, expert) pairs of the call */
+  uint32_t rows_per_item;   /* GEMM work-item rows (0 off the GEMM) */
+  uint32_t reserved;
+  uint64_t start_ns;        /* from the first recorded stage after a reset */
+  uint64_t duration_ns;
+  uint64_t scratch_bytes;   /* the context's scratch buffers at the call */
+  uint64_t resident_bytes;  /* process resident bytes at the call */
+} gossmx_profile_event;
+/* Layer index and phase stamped on the following records (the model step sets
+ * them per layer; -1 and GOSSMX_PHASE_UNKNOWN by default). */
+int gossmx_profile_tag(gossmx_ctx* ctx, int layer, int phase);
+/* Synchronizes, then copies up to `capacity` records (oldest first) without
+ * consuming them; *available receives the count kept, *dropped those lost
+ * to the cap. */
+int gossmx_profile_events(gossmx_ctx* ctx, gossmx_profile_event* out, size_t capacity, size_t* written,
+                          size_t* available, uint64_t* dropped);
 
 /* HIP-graph capture of a sequence of calls on this context (no counterpart in
  * the reference; it removes the per-kernel launch gaps of a multi-layer step).

@@ -837,9 +837,9 @@ int oracle_swiglu(const float* gate_up, size_t intermediate, float alpha, float 
 }
 void oracle_stable_top_k(const float* v, size_t n, size_t k, uint32_t* out) { stable_top_k(v, n, k, out); }
 void oracle_softmax(const float* v, size_t n, float* out) { softmax(v, n, out); }
-void combine_rows(const float* y, const float* w, size_t m, size_t K, size_t H, float* out);
+void combine_rows(const float* y, const float* w, size_t m, size_t K, size_t H, float* out, float* unrounded);
 void oracle_combine(const float* y, const float* w, size_t m, size_t k, size_t h, float* out) {
-  combine_rows(y, w, m, k, h, out);
+  combine_rows(y, w, m, k, h, out, nullptr);
 }
 
 // The MoE block, CpuModel::moe_batch (cpu_runner.rs:2794-3013), with the
@@ -859,8 +859,9 @@ struct OracleLayer {
 // Weighted combine by source row and rank, then bf16 (cpu_runner.rs:2959-2999):
 // per row, output = 0.0; for rank 0..K-1 in order: weighted = y * weight (one
 // rounding), output += weighted (one rounding); then fp32_to_bf16_roundtrip.
-// y is [m][K][H] by (row, rank) slot, w [m][K].
-void combine_rows(const float* y, const float* w, size_t m, size_t K, size_t H, float* out) {
+// y is [m][K][H] by (row, rank) slot, w [m][K]. unrounded (nullable)
+// receives the sum before the round trip.
+void combine_rows(const float* y, const float* w, size_t m, size_t K, size_t H, float* out, float* unrounded) {
   for (size_t r = 0; r < m; ++r) {
     for (size_t h = 0; h < H; ++h) {
       float acc = 0.0f;
@@ -868,6 +869,7 @@ void combine_rows(const float* y, const float* w, size_t m, size_t K, size_t H, 
         const float weighted = y[(r * K + k) * H + h] * w[r * K + k];
         acc = acc + weighted;
       }
+      if (unrounded) unrounded[r * H + h] = acc;
       out[r * H + h] = bf16_round(acc);
     }
   }
@@ -899,6 +901,10 @@ int oracle_moe_batch_ex(const OracleLayer* L, const uint16_t* x, size_t m, const
                         float* logits, uint32_t* selected, float* weights, float* output, uint32_t* route_order,
                         float* trace_gate_up, float* trace_swiglu, float* trace_down, int auto_lane, int threads,
                         int projection);
+int oracle_moe_batch_full(const OracleLayer* L, const uint16_t* x, size_t m, const float* injected_logits,
+                          float* logits, uint32_t* selected, float* weights, float* output, uint32_t* route_order,
+                          float* trace_gate_up, float* trace_swiglu, float* trace_down, int auto_lane, int threads,
+                          int projection, float* output_unrounded);
 
 int oracle_moe_batch(const OracleLayer* L, const uint16_t* x, size_t m, const float* injected_logits, float* logits,
                      uint32_t* selected, float* weights, float* output, uint32_t* route_order, float* trace_gate_up,
@@ -917,6 +923,16 @@ int oracle_moe_batch_ex(const OracleLayer* L, const uint16_t* x, size_t m, const
                         float* logits, uint32_t* selected, float* weights, float* output, uint32_t* route_order,
                         float* trace_gate_up, float* trace_swiglu, float* trace_down, int auto_lane, int threads,
                         int projection) {
+  return oracle_moe_batch_full(L, x, m, injected_logits, logits, selected, weights, output, route_order,
+                               trace_gate_up, trace_swiglu, trace_down, auto_lane, threads, projection, nullptr);
+}
+
+// oracle_moe_batch_ex with the combine's sum before fp32_to_bf16_roundtrip
+// (cpu_runner.rs:2991) in output_unrounded (nullable).
+int oracle_moe_batch_full(const OracleLayer* L, const uint16_t* x, size_t m, const float* injected_logits,
+                          float* logits, uint32_t* selected, float* weights, float* output, uint32_t* route_order,
+                          float* trace_gate_up, float* trace_swiglu, float* trace_down, int auto_lane, int threads,
+                          int projection, float* output_unrounded) {
   if (projection < 0 || projection > 2) return INVALID_DIMENSIONS;
   if ((auto_lane == 4 && !host_has_avx2()) || (auto_lane == 8 && !host_has_avx512_vnni())) return UNAVAILABLE_BACKEND;
   const size_t E = L->experts, H = L->hidden, I = L->intermediate, K = L->top_k;
@@ -1041,7 +1057,7 @@ int oracle_moe_batch_ex(const OracleLayer* L, const uint16_t* x, size_t m, const
     }
     s = e_end;
   }
-  combine_rows(y.data(), wts.data(), m, K, H, output);
+  combine_rows(y.data(), wts.data(), m, K, H, output, output_unrounded);
   if (logits) std::memcpy(logits, lg.data(), m * E * 4);
   if (selected) std::memcpy(selected, sel.data(), m * K * 4);
   if (weights) std::memcpy(weights, wts.data(), m * K * 4);

@@ -116,6 +116,8 @@ def _declare(L):
         "oracle_combine": (None, [vp, vp, sz, sz, sz, vp]),
         "oracle_moe_batch": (i32, [C.POINTER(OracleLayer), vp, sz, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32]),
         "oracle_moe_batch_ex": (i32, [C.POINTER(OracleLayer), vp, sz, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32]),
+        "oracle_moe_batch_full": (i32, [C.POINTER(OracleLayer), vp, sz, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32,
+                                        i32, vp]),
         "oracle_stream_hash": (u64, [u64, u64, u64]),
         "oracle_gen_mxfp4": (None, [u64, u64, sz, sz, sz, vp]),
         "oracle_gen_bf16_normal": (None, [u64, u64, sz, f32, f32, vp]),
@@ -342,6 +344,7 @@ def moe_batch(layer: MoeLayerHost, x_bf16: np.ndarray, injected_logits=None, tra
         "routing_weights": np.zeros((m, K), np.float32),
         "output": np.zeros((m, H), np.float32),
         "route_order": np.zeros(m * K, np.uint32),
+        "output_unrounded": np.zeros((m, H), np.float32),  # the combine's sum before its bf16 round trip
     }
     if trace:
         res["gate_up"] = np.zeros((m, K, 2 * I), np.float32)
@@ -349,10 +352,10 @@ def moe_batch(layer: MoeLayerHost, x_bf16: np.ndarray, injected_logits=None, tra
         res["down"] = np.zeros((m, K, H), np.float32)
     inj = None if injected_logits is None else np.ascontiguousarray(injected_logits, dtype=np.float32)
     s = layer.struct()
-    st = lib().oracle_moe_batch_ex(C.byref(s), _p(x), m, _p(inj), _p(res["router_logits"]), _p(res["selected"]),
-                                   _p(res["routing_weights"]), _p(res["output"]), _p(res["route_order"]),
-                                   _p(res.get("gate_up")), _p(res.get("swiglu")), _p(res.get("down")),
-                                   lane, threads, projection)
+    st = lib().oracle_moe_batch_full(C.byref(s), _p(x), m, _p(inj), _p(res["router_logits"]), _p(res["selected"]),
+                                     _p(res["routing_weights"]), _p(res["output"]), _p(res["route_order"]),
+                                     _p(res.get("gate_up")), _p(res.get("swiglu")), _p(res.get("down")),
+                                     lane, threads, projection, _p(res["output_unrounded"]))
     res["status"] = st
     return res
 

@@ -124,6 +124,30 @@ pub mod ffi {
         pub memory: c_int,
         pub trace_gate_up: *mut f32,
         pub trace_swiglu: *mut f32,
+        /// The combine's sum before its bf16 round trip (nullable).
+        pub output_unrounded: *mut f32,
+    }
+
+    /// `gossmx_stats`: projections by result, transfer bytes by direction,
+    /// resident bytes and the cap (the Xe engine's metrics).
+    #[repr(C)]
+    #[derive(Debug, Clone, Copy, Default)]
+    pub struct GossmxStats {
+        pub projections_ok: u64,
+        pub projections_failed: u64,
+        pub projections_refused: u64,
+        pub projections_rejected: u64,
+        pub weights_bias_uploaded_bytes: u64,
+        pub activation_bytes: u64,
+        pub output_bytes: u64,
+        pub resident_bytes: u64,
+        pub resident_high_water_bytes: u64,
+        pub resident_cap_bytes: u64,
+        pub capacity_refusals: u64,
+        pub repack_cache_hits: u64,
+        pub repack_cache_misses: u64,
+        pub circuit_open: i32,
+        pub reserved: i32,
     }
 
     extern "C" {
@@ -187,6 +211,9 @@ pub mod ffi {
         pub fn gossmx_circuit_is_open() -> c_int;
         pub fn gossmx_circuit_reset();
         pub fn gossmx_inject_fault(ctx: *mut GossmxCtx, armed: c_int) -> c_int;
+        pub fn gossmx_stats_read(out: *mut GossmxStats) -> c_int;
+        pub fn gossmx_stats_reset();
+        pub fn gossmx_set_resident_cap(bytes: u64) -> c_int;
     }
 }
 
@@ -318,6 +345,23 @@ pub fn circuit_is_open() -> bool {
 pub fn reset_circuit() {
     // SAFETY: no arguments; writes an atomic.
     unsafe { ffi::gossmx_circuit_reset() }
+}
+
+/// The process-wide counters, for the caller's metrics exporter
+/// (`gpt_oss_xe_projection_total`, `_transfer_bytes_total`,
+/// `_expert_cache_resident_bytes`, crates/gpt-oss-xe/src/lib.rs:44-49).
+pub fn stats() -> Result<ffi::GossmxStats, HipError> {
+    let mut out = ffi::GossmxStats::default();
+    // SAFETY: out is a valid, writable gossmx_stats.
+    check(unsafe { ffi::gossmx_stats_read(&mut out) })?;
+    Ok(out)
+}
+
+/// Caps the device bytes of resident weights and layers
+/// (`AttachConfig::max_resident_bytes`); 0 removes the cap.
+pub fn set_resident_cap(bytes: u64) -> Result<(), HipError> {
+    // SAFETY: no pointers; writes an atomic.
+    check(unsafe { ffi::gossmx_set_resident_cap(bytes) })
 }
 
 /// Number of visible gfx950 devices.
@@ -778,6 +822,7 @@ impl HipMoeBackend {
             memory: ffi::MEM_HOST,
             trace_gate_up: nullable(&mut trace_gate_up),
             trace_swiglu: nullable(&mut trace_swiglu),
+            output_unrounded: ptr::null_mut(),
         };
         // SAFETY: every array has the size the header states for these m, e, k, h, i.
         check(unsafe { ffi::gossmx_moe_forward(self.ctx.raw, layer.raw, &io) })?;

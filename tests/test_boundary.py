@@ -48,6 +48,66 @@ def test_null_arguments_are_rejected():
     assert L.gossmx_inject_fault(None, 1) == G.ERR_INVALID_ARGUMENT
 
 
+def test_accounting_without_device():
+    # Projection calls count by result: argument failures are "rejected".
+    L = G.load()
+    before = G.stats()
+    assert L.gossmx_moe_forward(None, None, None) == G.ERR_INVALID_ARGUMENT
+    assert L.gossmx_moe_forward_noalloc(None, None, None) == G.ERR_INVALID_ARGUMENT
+    assert L.gossmx_mxfp4_matmul(None, None) == G.ERR_INVALID_ARGUMENT
+    after = G.stats()
+    assert after["projections_rejected"] - before["projections_rejected"] == 3
+    assert after["projections_ok"] == before["projections_ok"]
+    assert L.gossmx_stats_read(None) == G.ERR_INVALID_ARGUMENT
+    try:
+        G.set_resident_cap(1 << 30)
+        assert G.stats()["resident_cap_bytes"] == 1 << 30
+    finally:
+        G.set_resident_cap(0)
+    assert G.stats()["resident_cap_bytes"] == 0
+    G.stats_reset()
+    s = G.stats()
+    assert s["projections_rejected"] == 0 and s["resident_high_water_bytes"] == s["resident_bytes"]
+    assert L.gossmx_profile_tag(None, 0, G.PHASE_DECODE) == G.ERR_INVALID_ARGUMENT
+    assert L.gossmx_profile_events(None, None, 0, None, None, None) == G.ERR_INVALID_ARGUMENT
+
+
+def test_profile_event_layout_matches_the_header():
+    # Field offsets of gossmx_profile_event and gossmx_stats as the C compiler
+    # lays them out (gcc on the header).
+    import tempfile
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    src = '''#include <stddef.h>
+#include <stdio.h>
+#include "gossmx.h"
+#define F(T, f) printf("%s %s %zu\\n", #T, #f, offsetof(T, f));
+int main(void) {
+F(gossmx_profile_event, op) F(gossmx_profile_event, layer) F(gossmx_profile_event, m)
+F(gossmx_profile_event, rows_per_item) F(gossmx_profile_event, start_ns) F(gossmx_profile_event, resident_bytes)
+F(gossmx_stats, resident_bytes) F(gossmx_stats, repack_cache_misses) F(gossmx_stats, circuit_open)
+printf("sizes %zu %zu\\n", sizeof(gossmx_profile_event), sizeof(gossmx_stats));
+return 0; }
+'''
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "layout.c")
+        exe = os.path.join(d, "layout")
+        with open(c, "w") as fh:
+            fh.write(src)
+        subprocess.run(["gcc", "-std=c99", "-I", os.path.join(root, "include"), c, "-o", exe], check=True)
+        out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split("\n")
+    want = {}
+    for line in out:
+        parts = line.split()
+        if len(parts) == 3 and parts[0] != "sizes":
+            want[(parts[0], parts[1])] = int(parts[2])
+        elif parts and parts[0] == "sizes":
+            sizes = (int(parts[1]), int(parts[2]))
+    py = {"gossmx_profile_event": G.ProfileEvent, "gossmx_stats": G.Stats}
+    for (t, f), off in want.items():
+        assert getattr(py[t], f).offset == off, (t, f)
+    assert (C.sizeof(G.ProfileEvent), C.sizeof(G.Stats)) == sizes
+
+
 def test_circuit_breaker_without_device():
     assert not G.circuit_is_open()
     G.circuit_reset()

@@ -171,6 +171,37 @@ def test_small_model_device_flag_failure_opens_the_breaker(ctx, tiny):
     assert_bits(model.decode(want_tokens[0]), want_logits[1])
 
 
+def test_small_model_profile_records_carry_layer_and_phase(ctx, tiny):
+    # The model step tags its MoE calls with the layer index and the phase
+    # (CpuExecutionProfileRecord's layer and phase, cpu_profile.rs:121-150);
+    # its round trips count as activation and output transfers.
+    cfg, model, _ = tiny
+    model.reset()
+    ctx.profile(True)
+    ctx.profile_reset()
+    try:
+        s0 = G.stats()
+        logits = model.prefill(PROMPT)
+        prefill, _ = ctx.profile_events()
+        ctx.profile_reset()
+        model.decode(G.greedy_token(logits))
+        decode, dropped = ctx.profile_events()
+        s1 = G.stats()
+    finally:
+        ctx.profile(False)
+        ctx.profile_reset()
+        ctx.profile_tag()
+        model.reset()
+    assert dropped == 0
+    for events, phase, m in ((prefill, "prefill", len(PROMPT)), (decode, "decode", 1)):
+        assert {e["layer"] for e in events} == set(range(cfg["layers"]))
+        assert {e["phase"] for e in events} == {phase}
+        assert {e["m"] for e in events} == {m} and {e["memory"] for e in events} == {"device"}
+        assert {e["op"] for e in events} >= {"gate_up", "down"}
+    assert s1["projections_ok"] - s0["projections_ok"] == 2 * cfg["layers"]
+    assert s1["activation_bytes"] > s0["activation_bytes"] and s1["output_bytes"] > s0["output_bytes"]
+
+
 def test_small_model_follows_a_replaced_stream():
     # gossmx_ctx_set_stream between generations (the context's own stream is
     # destroyed): the model's copies, launches and MoE calls run on the new

@@ -462,6 +462,41 @@ def test_combine_order_pins(ctx, m, inject):
     close(layer)
 
 
+@pytest.mark.parametrize("experts,hidden,inter,top_k,m,projection", [
+    (8, 128, 96, 4, 1, G.PROJECTION_RESIDUAL_Q8),    # one row: the combine inside the down launch
+    (8, 128, 96, 4, 5, G.PROJECTION_RESIDUAL_Q8),    # combine8_kernel
+    (32, 256, 128, 4, 70, G.PROJECTION_RESIDUAL_Q8),
+    (4, 96, 64, 2, 3, G.PROJECTION_EXACT_BF16)])
+def test_output_unrounded_matches_oracle(ctx, experts, hidden, inter, top_k, m, projection):
+    """output_unrounded: the rank-order weighted sum before its bf16 round trip
+    (cpu_runner.rs:2991) equals the oracle's on every path, and rounds to
+    the output."""
+    host = O.synthetic_layer(47, 0, experts=experts, hidden=hidden, intermediate=inter, top_k=top_k)
+    x = O.gen_hidden(47, m, m, hidden)
+    want = O.moe_batch(host, x, projection=projection)
+    assert want["status"] == O.OK
+    layer = gpu_layer(ctx, host, projection)
+    got = layer.forward(x, unrounded=True)
+    assert_moe_equal(got, want)
+    assert (got["output_unrounded"].view(np.uint32) == want["output_unrounded"].view(np.uint32)).all()
+    assert (O.bf16_round_array(got["output_unrounded"]).view(np.uint32) == got["output"].view(np.uint32)).all()
+    # device memory, the pre-round output at a 4-byte offset: the scalar combine_kernel
+    if m > 1:
+        dx, dout, dunr = ctx.malloc(x.nbytes), ctx.malloc(m * hidden * 4), ctx.malloc(m * hidden * 4 + 16)
+        ctx.h2d(dx, x)
+        layer.forward_device(dx, m, dout, output_unrounded=dunr + 4)
+        ctx.synchronize()
+        unr = np.empty((m, hidden), np.float32)
+        out = np.empty((m, hidden), np.float32)
+        ctx.d2h(unr, dunr + 4)
+        ctx.d2h(out, dout)
+        assert (unr.view(np.uint32) == want["output_unrounded"].view(np.uint32)).all()
+        assert (out.view(np.uint32) == want["output"].view(np.uint32)).all()
+        for p in (dx, dout, dunr):
+            ctx.free(p)
+    close(layer)
+
+
 def test_all_experts_selected(ctx):
     host = O.synthetic_layer(5, 0, experts=4, hidden=64, intermediate=64, top_k=4)
     x = O.gen_hidden(5, 1, 9, 64)

@@ -680,3 +680,22 @@ def test_panel_lanes_finish_output_tails_with_scalar_rows():
                     continue
                 got = O.mxfp4_matmul_lane(x8, rows, blocks, act, m, bias, lane, 2, kind=kind)
                 assert (got.view(np.uint32) == want.view(np.uint32)).all(), (m, kind, lane)
+
+
+def test_output_unrounded_is_the_combine_sum_before_the_round_trip():
+    """moe_batch's output_unrounded: per row and column, the rank-order sum
+    from 0.0 of down output (the trace, pinned above) times routing weight,
+    before fp32_to_bf16_roundtrip (cpu_runner.rs:2959-2991); its bf16 round
+    is the output, and it differs from the output wherever the sum is not a
+    bf16 value."""
+    layer = O.synthetic_layer(51, 0, experts=6, hidden=64, intermediate=64, top_k=3)
+    x = O.gen_hidden(51, 1, 7, 64)
+    r = O.moe_batch(layer, x, trace=True)
+    assert r["status"] == O.OK
+    m, K, H = 7, 3, 64
+    want = np.zeros((m, H), np.float32)
+    for k in range(K):  # rank order, each product and each sum rounded to f32
+        want = (want + (r["down"][:, k, :] * r["routing_weights"][:, k:k + 1]).astype(np.float32)).astype(np.float32)
+    assert (r["output_unrounded"].view(np.uint32) == want.view(np.uint32)).all()
+    assert (O.bf16_round_array(r["output_unrounded"]).view(np.uint32) == r["output"].view(np.uint32)).all()
+    assert (r["output_unrounded"] != r["output"]).mean() > 0.9
