@@ -1043,13 +1043,14 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   const uint16_t* x = io->x;
   const float* injected = io->injected_logits;
   float* output = io->output;
+  uint16_t* output16 = nullptr;  // host memory: the output comes back as bf16 bits
   float* trace = io->trace_down;
   float* trace_gu = io->trace_gate_up;
   float* trace_sw = io->trace_swiglu;
   float* unrounded = io->output_unrounded;
   float* logits = (!host && io->router_logits) ? io->router_logits : logits_buf;
   if (host) {
-    if ((s = ensure(ctx, ctx->x, m * H * 2)) || (s = ensure(ctx, ctx->out, m * H * 4))) return s;
+    if ((s = ensure(ctx, ctx->x, m * H * 2)) || (s = ensure(ctx, ctx->out, m * H * 2))) return s;
     count_transfer(kTransferActivation, m * H * 2);
     HIP_TRY(hipMemcpyAsync(ctx->x.p, io->x, m * H * 2, hipMemcpyHostToDevice, ctx->stream), "H2D x");
     x = static_cast<const uint16_t*>(ctx->x.p);
@@ -1060,7 +1061,10 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
               "H2D logits");
       injected = static_cast<const float*>(ctx->injected.p);
     }
-    output = io->output ? static_cast<float*>(ctx->out.p) : nullptr;
+    // The output rows are bf16 values: they cross PCIe as bf16 bits (half the
+    // bytes) and are widened into the caller's f32 rows after the checks.
+    output16 = io->output ? static_cast<uint16_t*>(ctx->out.p) : nullptr;
+    output = nullptr;
     if (trace) {
       if ((s = ensure(ctx, ctx->trace, R * H * 4))) return s;
       trace = static_cast<float*>(ctx->trace.p);
@@ -1227,8 +1231,8 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
                      {GOSSMX_ROLE_DOWN, gemv ? GOSSMX_KERNEL_GEMV : GOSSMX_KERNEL_GEMM, n_down, (uint32_t)I,
                       gemv ? 0u : (uint32_t)chunk});
       if (down_combine)
-        HIP_TRY(launch_down_combine(d, weights, (int)K, output, trace, resid, next, unrounded, ctx->stream, sc.start,
-                                    sc.stop),
+        HIP_TRY(launch_down_combine(d, weights, (int)K, output, output16, trace, resid, next, unrounded, ctx->stream,
+                                    sc.start, sc.stop),
                 "down/combine launch");
       else if (use_gemv(m, B2, d.residual != 0))
         HIP_TRY(launch_gemv(kDown, d, (int)m, (int)max_work, ctx->stream, sc.start, sc.stop), "down launch");
@@ -1238,7 +1242,8 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   }
   if (!down_combine) {
     OpScope sc(ctx, GOSSMX_OP_WEIGHTING, {GOSSMX_ROLE_NONE, GOSSMX_KERNEL_COMBINE, n_down, (uint32_t)K, 0});
-    HIP_TRY(launch_combine(d.y, weights, (int)m, (int)K, (int)H, output, trace, resid, next, unrounded, ctx->stream),
+    HIP_TRY(launch_combine(d.y, weights, (int)m, (int)K, (int)H, output, output16, trace, resid, next, unrounded,
+                           ctx->stream),
             "combine launch");
   }
 
@@ -1249,10 +1254,11 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
     struct Piece {
       const void* src;
       void* dst;
-      size_t bytes;
+      size_t bytes;       // device bytes
+      bool widen = false;  // bf16 bits widened into f32 at dst
     };
     const Piece pieces[] = {
-        {output, io->output, io->output ? m * H * 4 : 0},
+        {output16, io->output, io->output ? m * H * 2 : 0, true},
         {next, next_residual, residual ? m * H * 2 : 0},
         {logits, io->router_logits, io->router_logits ? m * E * 4 : 0},
         {selected, io->selected, io->selected ? R * 4 : 0},
@@ -1289,7 +1295,13 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
     off = 16;
     for (const Piece& pc : pieces) {
       if (!pc.bytes) continue;
-      std::memcpy(pc.dst, ctx->h_stage + off, pc.bytes);
+      if (pc.widen) {
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(ctx->h_stage + off);
+        uint32_t* dst = static_cast<uint32_t*>(pc.dst);
+        for (size_t i = 0; i < pc.bytes / 2; ++i) dst[i] = (uint32_t)src[i] << 16;
+      } else {
+        std::memcpy(pc.dst, ctx->h_stage + off, pc.bytes);
+      }
       off += (pc.bytes + 15) / 16 * 16;
     }
   } else {

@@ -194,16 +194,17 @@ hipError_t launch_route_gemv(const RouteArgs& r, const DispatchArgs& d, const Ge
 // work item one route, top_k <= 4, blocks <= kTinyMaxBlocks): the outputs of
 // launch_gemv(kDown) followed by launch_combine with m = 1, without the y
 // buffer (d.y is not written).
-hipError_t launch_down_combine(const GemmArgs& d, const float* weights, int top_k, float* out, float* trace_down,
-                               const uint16_t* resid, uint16_t* next, float* unrounded, hipStream_t stream,
-                               hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+// out16 (nullable): the output as bf16 bits, beside or instead of out.
+hipError_t launch_down_combine(const GemmArgs& d, const float* weights, int top_k, float* out, uint16_t* out16,
+                               float* trace_down, const uint16_t* resid, uint16_t* next, float* unrounded,
+                               hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 // Exact-BF16 expert projection over the work list (mode kGateUp or kDown);
 // chunk <= kChunkMax.
 hipError_t launch_exact(GemmMode mode, const GemmArgs& a, int grid_work, hipStream_t stream);
 
 hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int top_k, int hidden, float* out,
-                          float* trace_down, const uint16_t* resid, uint16_t* next, float* unrounded,
-                          hipStream_t stream);
+                          uint16_t* out16, float* trace_down, const uint16_t* resid, uint16_t* next,
+                          float* unrounded, hipStream_t stream);
 hipError_t launch_prep_records(const uint8_t* records, int kind, size_t m, size_t blocks, size_t row_stride,
                                ActBuffers act, int* err, hipStream_t stream);
 hipError_t launch_repack(const uint8_t* src, int layout, TiledWeights w, hipStream_t stream);

@@ -2114,6 +2114,7 @@ struct CombineArgs {
   const float* weights;    // [top_k] routing weights by rank
   int top_k;
   float* out;              // [rows] f32 (bf16 values), or null
+  uint16_t* out16;         // [rows] the same values as bf16 bits, or null
   float* trace;            // [top_k][rows] down outputs by rank, or null
   const uint16_t* resid;   // [rows] bf16 residual stream, or null
   uint16_t* next;          // [rows] bf16(resid + out), or null
@@ -2226,6 +2227,7 @@ __global__ __launch_bounds__(DownCombineGeom::kThreads, 2) void gemv_down_combin
     for (int k = 0; k < c.top_k; ++k) acc = acc + s_y[k * kTileRows + nl] * c.weights[k];
     const float o = bf16r(acc);
     if (c.out != nullptr) c.out[row] = o;
+    if (c.out16 != nullptr) c.out16[row] = (uint16_t)(__float_as_uint(o) >> 16);
     if (c.unrounded != nullptr) c.unrounded[row] = acc;
     if (c.next != nullptr) c.next[row] = bf16_bits(bf16_to_f32(c.resid[row]) + o);
   }
@@ -2555,8 +2557,8 @@ __global__ __launch_bounds__(256) void tile_flags_kernel(TiledWeights w) {
 // decoder layer (add_residual, cpu_runner.rs:3732-3738): next =
 // bf16(resid + out). `out` may be null when only `next` is wanted.
 __global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* y, const float* w, int top_k, int hidden,
-                                                      float* out, float* trace, const uint16_t* resid,
-                                                      uint16_t* next, float* unrounded) {
+                                                      float* out, uint16_t* out16, float* trace,
+                                                      const uint16_t* resid, uint16_t* next, float* unrounded) {
   const int r = blockIdx.y;
   const int h = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
   if (h >= hidden) return;
@@ -2605,6 +2607,12 @@ __global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* y, const 
     op[0] = make_float4(o[0], o[1], o[2], o[3]);
     op[1] = make_float4(o[4], o[5], o[6], o[7]);
   }
+  if (out16) {  // the same values as bf16 bits (exact: every o is a bf16 value)
+    u32x4 ob;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ob[q] = (__float_as_uint(o[2 * q]) >> 16) | (__float_as_uint(o[2 * q + 1]) & 0xffff0000u);
+    *reinterpret_cast<u32x4*>(out16 + (size_t)r * hidden + h) = ob;
+  }
   if (next) {
     const u32x4 rp = *reinterpret_cast<const u32x4*>(resid + (size_t)r * hidden + h);
     u32x4 np;
@@ -2619,8 +2627,8 @@ __global__ __launch_bounds__(256) void combine8_kernel(const uint16_t* y, const 
 }
 
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* y, const float* w, int top_k, int hidden,
-                                                     float* out, float* trace, const uint16_t* resid,
-                                                     uint16_t* next, float* unrounded) {
+                                                     float* out, uint16_t* out16, float* trace,
+                                                     const uint16_t* resid, uint16_t* next, float* unrounded) {
   const int r = blockIdx.y;
   const int h = blockIdx.x * blockDim.x + threadIdx.x;
   if (h >= hidden) return;
@@ -2634,6 +2642,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* y, const f
   if (unrounded) unrounded[(size_t)r * hidden + h] = acc;
   const float o = bf16r(acc);
   if (out) out[(size_t)r * hidden + h] = o;
+  if (out16) out16[(size_t)r * hidden + h] = (uint16_t)(__float_as_uint(o) >> 16);
   if (next) next[(size_t)r * hidden + h] = bf16_bits(bf16_to_f32(resid[(size_t)r * hidden + h]) + o);
 }
 
@@ -2996,13 +3005,13 @@ hipError_t launch_route_gemv(const RouteArgs& r, const DispatchArgs& d, const Ge
   return hipGetLastError();
 }
 
-hipError_t launch_down_combine(const GemmArgs& d, const float* weights, int top_k, float* out, float* trace_down,
-                               const uint16_t* resid, uint16_t* next, float* unrounded, hipStream_t stream,
-                               hipEvent_t start, hipEvent_t stop) {
+hipError_t launch_down_combine(const GemmArgs& d, const float* weights, int top_k, float* out, uint16_t* out16,
+                               float* trace_down, const uint16_t* resid, uint16_t* next, float* unrounded,
+                               hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   if (d.w.blocks > (size_t)kTinyMaxBlocks || !d.residual || top_k < 1 || top_k > DownCombineGeom::kItems ||
       (next != nullptr && resid == nullptr))
     return hipErrorInvalidValue;
-  CombineArgs c{weights, top_k, out, trace_down, resid, next, unrounded};
+  CombineArgs c{weights, top_k, out, out16, trace_down, resid, next, unrounded};
   const dim3 grid((unsigned)d.w.tiles), block(DownCombineGeom::kThreads);
   if (start) hipExtLaunchKernelGGL(gemv_down_combine_kernel, grid, block, 0, stream, start, stop, 0, d, c);
   else hipLaunchKernelGGL(gemv_down_combine_kernel, grid, block, 0, stream, d, c);
@@ -3024,17 +3033,17 @@ hipError_t launch_tile_flags(TiledWeights w, hipStream_t stream) {
 }
 
 hipError_t launch_combine(const uint16_t* y, const float* weights, int m, int top_k, int hidden, float* out,
-                          float* trace_down, const uint16_t* resid, uint16_t* next, float* unrounded,
-                          hipStream_t stream) {
+                          uint16_t* out16, float* trace_down, const uint16_t* resid, uint16_t* next,
+                          float* unrounded, hipStream_t stream) {
   const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-  const bool aligned =
-      hidden % 8 == 0 && a16(y) && a16(out) && a16(trace_down) && a16(resid) && a16(next) && a16(unrounded);
+  const bool aligned = hidden % 8 == 0 && a16(y) && a16(out) && a16(out16) && a16(trace_down) && a16(resid) &&
+                       a16(next) && a16(unrounded);
   if (aligned)
     hipLaunchKernelGGL(combine8_kernel, dim3(grid1d(hidden / 8, 256), m), dim3(256), 0, stream, y, weights, top_k,
-                       hidden, out, trace_down, resid, next, unrounded);
+                       hidden, out, out16, trace_down, resid, next, unrounded);
   else
     hipLaunchKernelGGL(combine_kernel, dim3(grid1d(hidden, 256), m), dim3(256), 0, stream, y, weights, top_k,
-                       hidden, out, trace_down, resid, next, unrounded);
+                       hidden, out, out16, trace_down, resid, next, unrounded);
   return hipGetLastError();
 }
 
