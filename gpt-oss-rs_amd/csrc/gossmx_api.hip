@@ -1549,6 +1549,17 @@ static int run_selftest(gossmx_ctx* ctx, bool* scaled_ok) {
       }
     }
   }
+  // The device's f32 -> bf16 conversion against half's rounding.
+  for (int k = 0; k < kSelftestBf16; ++k) {
+    const uint32_t x = selftest_bf16_input(k);
+    uint16_t want;
+    if ((x & 0x7fffffffu) > 0x7f800000u) want = (uint16_t)((x >> 16) | 0x40u);
+    else if ((x & 0x8000u) && (x & 0x17fffu)) want = (uint16_t)((x >> 16) + 1u);
+    else want = (uint16_t)(x >> 16);
+    if (host[kSelftestBf16Base + k] != (float)want)
+      return fail(GOSSMX_ERR_UNSUPPORTED, "bf16 conversion of %#010x gave %#06x, expected %#06x", x,
+                  (unsigned)host[kSelftestBf16Base + k], want);
+  }
   // The device SwiGLU sigmoid table against the host libm expf on all 65,536
   // bf16 inputs (the reference's f32::exp is the host expf).
   std::vector<uint16_t> tab(65536);

@@ -219,7 +219,19 @@ hipError_t launch_build_sigmoid_table(uint16_t* tab, hipStream_t stream);
 // selftest_kernel).
 constexpr int kSelftestCodes = 8;
 constexpr int kSelftestDirty = 5 * 4 * 6;  // exponents x byte positions x neighbour patterns
-constexpr int kSelftestFloats = kSelftestCodes + 256 + kSelftestCodes + 16 * kSelftestDirty;
+// bf16 conversion cases: fixed edges (ties, NaN payloads, denormals, the
+// overflow boundary) and hashed bit patterns; input k is selftest_bf16_input(k).
+constexpr int kSelftestBf16 = 1024;
+constexpr int kSelftestBf16Base = kSelftestCodes + 256 + kSelftestCodes + 16 * kSelftestDirty;
+constexpr int kSelftestFloats = kSelftestBf16Base + kSelftestBf16;
+constexpr uint32_t kBf16Edges[] = {0x00000000u, 0x80000000u, 0x3f808000u, 0x3f818000u, 0x3f808001u, 0x3f80ffffu,
+                                   0x7f7f8000u, 0x7f7fffffu, 0x7f800000u, 0xff800000u, 0x7f800001u, 0x7fc00000u,
+                                   0xffc00001u, 0x7fa00000u, 0xff80ffffu, 0x00008000u, 0x00018000u, 0x807fffffu,
+                                   0x00400000u, 0xbf7f8000u};
+constexpr int kBf16EdgeCount = (int)(sizeof(kBf16Edges) / sizeof(kBf16Edges[0]));
+__host__ __device__ constexpr uint32_t selftest_bf16_input(int k) {
+  return k < kBf16EdgeCount ? kBf16Edges[k] : (uint32_t)k * 0x9E3779B1u + 0x7F4A7C15u;
+}
 hipError_t launch_selftest(float* out, hipStream_t stream);
 // The model's dense bf16 projections (16-lane dot order), up to three of the
 // same input in one launch: out_p[r * rows_p + o] = dot(w_p[o], x[r])

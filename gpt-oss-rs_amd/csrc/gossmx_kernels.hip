@@ -33,13 +33,12 @@ typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
 
 // bf16::from_f32 of half 2.7.1 (round to nearest even, NaN quieted), used by
 // fp32_to_bf16_roundtrip, cpu_runner.rs:3740-3744.
-__device__ __forceinline__ uint16_t bf16_bits(float f) {
-  const uint32_t x = __float_as_uint(f);
-  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x0040u);
-  const uint32_t round_bit = 0x8000u;
-  if ((x & round_bit) != 0 && (x & (3u * round_bit - 1u)) != 0) return (uint16_t)((x >> 16) + 1u);
-  return (uint16_t)(x >> 16);
-}
+// f32 -> bf16 as half 2.7.1's from_f32: round to nearest even, NaN kept with
+// its sign and upper payload and the quiet bit set ((x >> 16) | 0x40). gfx950's
+// conversion instruction (v_cvt_pk_bf16_f32, which the __bf16 cast compiles
+// to) gives exactly these bits: compared on every one of the 2^32 f32
+// patterns, and checked again by the context self-test on edge cases.
+__device__ __forceinline__ uint16_t bf16_bits(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 __device__ __forceinline__ float bf16r(float f) { return bf16_to_f32(bf16_bits(f)); }
 
@@ -207,6 +206,26 @@ __device__ __forceinline__ void residual_q8_store(float v, int l32, size_t row, 
   }
 }
 
+// Scale = max / 127 and inverse = 1 / scale (0 for a zero scale) of the N
+// blocks a half wave quantizes: the max is uniform over the half wave, so
+// lane j < N computes block j's pair once (the same correctly rounded
+// divisions) and every lane reads its blocks' pairs back by lane permute,
+// instead of every lane dividing for every block.
+template <int N>
+__device__ __forceinline__ void q8_scales_n(const float (&mx)[N], int l32, float (&sc)[N], float (&inv)[N]) {
+  float m = mx[0];
+#pragma unroll
+  for (int i = 1; i < N; ++i) m = (l32 % N) == i ? mx[i] : m;
+  const float sl = m / 127.0f;
+  const float il = sl == 0.0f ? 0.0f : 1.0f / sl;
+  const int base = threadIdx.x & 32;  // this half wave's first lane in the wave
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    sc[i] = __shfl(sl, base + i);
+    inv[i] = __shfl(il, base + i);
+  }
+}
+
 // residual_q8_store for N blocks per half wave at once (block i is item
 // hw + i * stride: activation row first_row + item / per_row, block
 // first_blk + item % per_row); blocks with live[i] false are computed on
@@ -215,25 +234,37 @@ template <int N, bool RESIDUAL>
 __device__ __forceinline__ void residual_q8_store_n(const float (&v)[N], const bool (&live)[N], int l32, int hw,
                                                     int stride, int per_row, size_t first_row, int blocks,
                                                     int first_blk, ActBuffers act) {
-  float mx[N], q[N], s[N], r[N], rq[N], rs[N];
+  float mx[N], q[N], s[N], r[N], rq[N], rs[N], inv[N];
 #pragma unroll
   for (int i = 0; i < N; ++i) mx[i] = half_wave_max(fabsf(v[i]));
+  if constexpr (N >= 4) {
+    q8_scales_n<N>(mx, l32, s, inv);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      s[i] = mx[i] / 127.0f;
+      inv[i] = s[i] == 0.0f ? 0.0f : 1.0f / s[i];
+    }
+  }
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    s[i] = mx[i] / 127.0f;
-    const float inv = s[i] == 0.0f ? 0.0f : 1.0f / s[i];
-    q[i] = fminf(fmaxf(roundf(v[i] * inv), -127.0f), 127.0f);
+    q[i] = fminf(fmaxf(roundf(v[i] * inv[i]), -127.0f), 127.0f);
     r[i] = RESIDUAL ? v[i] - q[i] * s[i] : 0.0f;  // quantize_q8: no residual block
     mx[i] = fabsf(r[i]);
   }
 #pragma unroll
   for (int i = 0; i < N; ++i) mx[i] = half_wave_max(mx[i]);
+  if constexpr (N >= 4) {
+    q8_scales_n<N>(mx, l32, rs, inv);
+  } else {
 #pragma unroll
-  for (int i = 0; i < N; ++i) {
-    rs[i] = mx[i] / 127.0f;
-    const float inv = rs[i] == 0.0f ? 0.0f : 1.0f / rs[i];
-    rq[i] = fminf(fmaxf(roundf(r[i] * inv), -127.0f), 127.0f);
+    for (int i = 0; i < N; ++i) {
+      rs[i] = mx[i] / 127.0f;
+      inv[i] = rs[i] == 0.0f ? 0.0f : 1.0f / rs[i];
+    }
   }
+#pragma unroll
+  for (int i = 0; i < N; ++i) rq[i] = fminf(fmaxf(roundf(r[i] * inv[i]), -127.0f), 127.0f);
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     if (!live[i]) continue;  // uniform per half wave
@@ -2845,6 +2876,8 @@ __global__ void selftest_kernel(float* out) {
       out[272 + 16 * c + 8 + i] = (float)hi[i];
     }
   }
+  for (int k = lane; k < kSelftestBf16; k += 64)
+    out[kSelftestBf16Base + k] = (float)bf16_bits(__uint_as_float(selftest_bf16_input(k)));
 }
 
 // ---------------------------------------------------------------------------
