@@ -1595,6 +1595,22 @@ int gossmx_selftest(gossmx_ctx* ctx) {
   return GOSSMX_OK;
 }
 
+int gossmx_selftest_bf16_exhaustive(gossmx_ctx* ctx, uint64_t* mismatches) {
+  if (!ctx || !mismatches) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
+  if (int s = set_device(ctx->device)) return s;
+  unsigned long long* dev = nullptr;
+  HIP_TRY(hipMalloc(&dev, sizeof(unsigned long long)), "hipMalloc(bf16 check)");
+  unsigned long long n = 0;
+  hipError_t e = hipMemcpyAsync(dev, &n, sizeof n, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = launch_bf16_exhaustive(dev, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(&n, dev, sizeof n, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  (void)hipFree(dev);
+  if (e != hipSuccess) return hip_fail(e, "bf16 check");
+  *mismatches = n;
+  return GOSSMX_OK;
+}
+
 int gossmx_ctx_fast_path(const gossmx_ctx* ctx, int* enabled) {
   if (!ctx || !enabled) return fail(GOSSMX_ERR_INVALID_ARGUMENT, "null argument");
   *enabled = ctx->fast_ok ? 1 : 0;

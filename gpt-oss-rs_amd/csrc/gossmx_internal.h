@@ -233,6 +233,9 @@ __host__ __device__ constexpr uint32_t selftest_bf16_input(int k) {
   return k < kBf16EdgeCount ? kBf16Edges[k] : (uint32_t)k * 0x9E3779B1u + 0x7F4A7C15u;
 }
 hipError_t launch_selftest(float* out, hipStream_t stream);
+// Every f32 bit pattern through bf16_bits against half's rounding restated
+// in software; mismatches are counted into *count (device, zeroed by the caller).
+hipError_t launch_bf16_exhaustive(unsigned long long* count, hipStream_t stream);
 // The model's dense bf16 projections (16-lane dot order), up to three of the
 // same input in one launch: out_p[r * rows_p + o] = dot(w_p[o], x[r])
 // (+ bias_p[o]) for r < m, o < rows_p; w bf16 [rows][cols], x f32 [m][cols],

@@ -3122,6 +3122,31 @@ hipError_t launch_build_sigmoid_table(uint16_t* tab, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// half 2.7.1's from_f32 restated with integer operations, the check's
+// reference for bf16_bits.
+__device__ __forceinline__ uint16_t bf16_bits_reference(float f) {
+  const uint32_t x = __float_as_uint(f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x0040u);
+  if ((x & 0x8000u) != 0 && (x & 0x17fffu) != 0) return (uint16_t)((x >> 16) + 1u);
+  return (uint16_t)(x >> 16);
+}
+
+__global__ __launch_bounds__(256) void bf16_exhaustive_kernel(uint32_t hi, unsigned long long* count) {
+  const uint32_t x = (hi << 24) | (blockIdx.x * 256u + threadIdx.x);
+  const float f = __uint_as_float(x);
+  const bool bad = bf16_bits(f) != bf16_bits_reference(f);
+  const unsigned long long n = __ballot(bad);
+  if (n != 0 && (threadIdx.x & 63) == 0) atomicAdd(count, (unsigned long long)__popcll(n));
+}
+
+hipError_t launch_bf16_exhaustive(unsigned long long* count, hipStream_t stream) {
+  for (uint32_t hi = 0; hi < 256; ++hi) {
+    hipLaunchKernelGGL(bf16_exhaustive_kernel, dim3(65536), dim3(256), 0, stream, hi, count);
+    if (hipError_t e = hipGetLastError()) return e;
+  }
+  return hipSuccess;
+}
+
 hipError_t launch_selftest(float* out, hipStream_t stream) {
   hipLaunchKernelGGL(selftest_kernel, dim3(1), dim3(64), 0, stream, out);
   return hipGetLastError();

@@ -238,6 +238,7 @@ def load():
         "gossmx_graph_launch": (i32, [vp, vp]),
         "gossmx_graph_destroy": (None, [vp]),
         "gossmx_selftest": (i32, [vp]),
+        "gossmx_selftest_bf16_exhaustive": (i32, [vp, C.POINTER(u64)]),
         "gossmx_model_create": (i32, [vp, C.POINTER(ModelConfig), vp, vp, vp, C.POINTER(DenseLayer), pp]),
         "gossmx_model_destroy": (None, [vp]),
         "gossmx_model_reset": (i32, [vp]),
@@ -339,6 +340,12 @@ class Context:
         False or FAULT_NONE (disarm)."""
         mode = int(armed) if not isinstance(armed, bool) else (FAULT_INJECTED if armed else FAULT_NONE)
         _check(load().gossmx_inject_fault(self._h, mode))
+
+    def bf16_exhaustive_mismatches(self) -> int:
+        """bf16 rounding on all 2^32 f32 patterns against half's rounding."""
+        n = C.c_uint64(0)
+        _check(load().gossmx_selftest_bf16_exhaustive(self._h, C.byref(n)))
+        return int(n.value)
 
     def fast_path(self) -> bool:
         """Whether the GEMMs may take the scaled-conversion fast path (the

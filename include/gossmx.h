@@ -508,6 +508,12 @@ int gossmx_inject_fault(gossmx_ctx* ctx, int armed);
  * table against the host expf. No counterpart in the reference;
  * GOSSMX_ERR_UNSUPPORTED with a message on any mismatch. */
 int gossmx_selftest(gossmx_ctx* ctx);
+/* The kernels round f32 to bf16 with gfx950's conversion instruction; this
+ * runs it on all 2^32 f32 bit patterns against half 2.7.1's rounding (nearest
+ * even, NaN quieted with its sign and upper payload kept) restated in integer
+ * operations, and counts the differences into *mismatches (0 expected). No
+ * counterpart in the reference; a diagnostic (about 0.1 s). */
+int gossmx_selftest_bf16_exhaustive(gossmx_ctx* ctx, uint64_t* mismatches);
 
 /* ---------------------------------------------------------------------------
  * The dense path around the block (crates/gpt-oss-model-runner/src/

@@ -642,6 +642,13 @@ def test_scratch_requirement_is_none_and_selftest_passes(ctx):
     close(layer)
 
 
+def test_bf16_rounding_matches_half_on_every_f32(ctx):
+    # The kernels' f32 -> bf16 rounding (gfx950's conversion instruction)
+    # against half 2.7.1's from_f32 restated in integer operations, on all
+    # 2^32 f32 bit patterns: nearest even, NaN quieted with sign and payload.
+    assert ctx.bf16_exhaustive_mismatches() == 0
+
+
 def test_profiler_counts_every_stage(ctx):
     """Every stage is timed once per call. Batches of at most 4 rows with a
     computed router run the router, selection and dispatch as one launch,
