@@ -521,8 +521,8 @@ def main() -> int:
                 ms_total = ms_eager
 
         # Host-memory mode (GOSSMX_MEM_HOST, the direct drop-in for Rust slices):
-        # every layer call copies x and the logits in and the outputs out, then
-        # synchronizes. PCIe-inclusive, reported beside value, never as value.
+        # every layer call copies x and the logits in and the outputs out (one
+        # copy each way), then synchronizes. PCIe-inclusive, reported beside value, never as value.
         # Python's cyclic collector is paused for the timed calls: a full
         # collection of the interpreter's objects (torch's included) takes tens of
         # ms and would land inside some call; a native caller has no such pause.
@@ -618,9 +618,10 @@ def main() -> int:
             result["host_memory"] = {
                 "ms_per_step": host_ms, "value": layer_tokens / (host_ms * 1e-3), "unit": "layer-tokens/s",
                 "steps": host_steps,
-                "note": ("GOSSMX_MEM_HOST calls (eager launches): x and logits copied in; every CpuMoeStep output "
-                         "(router logits, selection, routing weights, route order, output rows) and the device "
-                         "error flags copied out in one synchronization per layer"),
+                "note": ("GOSSMX_MEM_HOST calls (eager launches): x and logits in one copy from pinned staging; "
+                         "every CpuMoeStep output (router logits, selection, routing weights, route order, output "
+                         "rows) and the device error flags gathered on the device and copied out in one copy and "
+                         "one synchronization per layer"),
             }
         return result, x, state, graph
 

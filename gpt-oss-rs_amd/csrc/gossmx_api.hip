@@ -127,19 +127,20 @@ struct gossmx_ctx {
   hipEvent_t prof_base = nullptr;
   int tag_layer = -1, tag_phase = GOSSMX_PHASE_UNKNOWN;
   CallInfo call;  // the profiled call in progress
-  // Pinned host staging of the host-memory calls' outputs and the error flags,
-  // read back by one synchronization (grow-only).
+  // Pinned host staging of the host-memory MoE calls (grow-only): the inputs
+  // (one host-to-device copy), and the outputs with the error flags (one
+  // device-to-host copy and one synchronization).
+  char* h_in = nullptr;
+  size_t in_cap = 0;
   char* h_stage = nullptr;
   size_t stage_cap = 0;
-  // scratch
-  DevBuf x, injected, logits, selected, weights, act1v, act1s, bucket, route_tok, route_slot, work, act2v, act2s, y,
-      cnt, normw, next,
-      out, trace, trace_gu, trace_sw, rec, bias, mout, unrounded;
+  // scratch (x: the host-memory MoE call's input pack; out: its output pack)
+  DevBuf x, logits, selected, weights, act1v, act1s, bucket, route_tok, route_slot, work, act2v, act2s, y, cnt, out,
+      trace, trace_gu, trace_sw, rec, bias, mout, unrounded;
   template <class F>
   void each_buf(F f) {
-    for (DevBuf* b : {&x, &injected, &logits, &selected, &weights, &act1v, &act1s, &bucket, &route_tok, &route_slot,
-                      &work, &act2v, &act2s, &y, &cnt, &normw, &next, &out, &trace, &trace_gu, &trace_sw, &rec,
-                      &bias, &mout, &unrounded})
+    for (DevBuf* b : {&x, &logits, &selected, &weights, &act1v, &act1s, &bucket, &route_tok, &route_slot, &work,
+                      &act2v, &act2s, &y, &cnt, &out, &trace, &trace_gu, &trace_sw, &rec, &bias, &mout, &unrounded})
       f(*b);
   }
 };
@@ -190,6 +191,25 @@ int ensure(gossmx_ctx* ctx, DevBuf& b, size_t bytes) {
   b.cap = cap;
   return GOSSMX_OK;
 }
+
+// Grow-only pinned host staging. The stream is drained before a smaller
+// buffer is freed: a copy of an earlier call that ended in an error may still
+// read or write it.
+int ensure_pinned(gossmx_ctx* ctx, char** p, size_t* cap, size_t bytes) {
+  if (bytes <= *cap) return GOSSMX_OK;
+  if (*p) {
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    HIP_TRY(hipHostFree(*p), "hipHostFree");
+  }
+  *p = nullptr;
+  *cap = 0;
+  const size_t want = std::max<size_t>(bytes, 4096) * 5 / 4;
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(p), want), "pinned staging");
+  *cap = want;
+  return GOSSMX_OK;
+}
+
+constexpr size_t align16(size_t n) { return (n + 15) / 16 * 16; }
 
 // A fixed block of device memory that a call's scratch is carved from
 // (256-byte aligned pieces), instead of the context's grow-only buffers.
@@ -668,6 +688,7 @@ void gossmx_ctx_destroy(gossmx_ctx* ctx) {
   for (void* p : ctx->retired) (void)hipFree(p);
   if (ctx->err) (void)hipFree(ctx->err);
   if (ctx->sig_tab) (void)hipFree(ctx->sig_tab);
+  if (ctx->h_in) (void)hipHostFree(ctx->h_in);
   if (ctx->h_stage) (void)hipHostFree(ctx->h_stage);
   if (ctx->own_stream && ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
@@ -1049,21 +1070,23 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   float* trace_sw = io->trace_swiglu;
   float* unrounded = io->output_unrounded;
   float* logits = (!host && io->router_logits) ? io->router_logits : logits_buf;
+  // Host memory: the inputs (x, injected logits, norm weight) cross in one
+  // copy from pinned staging; the outputs and the error flags come back in
+  // one copy of a device pack (layout below).
+  const float* norm_dev = norm_weight;
   if (host) {
-    if ((s = ensure(ctx, ctx->x, m * H * 2)) || (s = ensure(ctx, ctx->out, m * H * 2))) return s;
-    count_transfer(kTransferActivation, m * H * 2);
-    HIP_TRY(hipMemcpyAsync(ctx->x.p, io->x, m * H * 2, hipMemcpyHostToDevice, ctx->stream), "H2D x");
-    x = static_cast<const uint16_t*>(ctx->x.p);
-    if (injected) {
-      if ((s = ensure(ctx, ctx->injected, m * E * 4))) return s;
-      count_transfer(kTransferActivation, m * E * 4);
-      HIP_TRY(hipMemcpyAsync(ctx->injected.p, io->injected_logits, m * E * 4, hipMemcpyHostToDevice, ctx->stream),
-              "H2D logits");
-      injected = static_cast<const float*>(ctx->injected.p);
-    }
-    // The output rows are bf16 values: they cross PCIe as bf16 bits (half the
-    // bytes) and are widened into the caller's f32 rows after the checks.
-    output16 = io->output ? static_cast<uint16_t*>(ctx->out.p) : nullptr;
+    const size_t x_bytes = m * H * 2, inj_bytes = injected ? m * E * 4 : 0, nw_bytes = residual ? H * 4 : 0;
+    const size_t off_inj = align16(x_bytes), off_nw = off_inj + align16(inj_bytes), in_bytes = off_nw + nw_bytes;
+    if ((s = ensure(ctx, ctx->x, in_bytes)) || (s = ensure_pinned(ctx, &ctx->h_in, &ctx->in_cap, in_bytes))) return s;
+    std::memcpy(ctx->h_in, io->x, x_bytes);
+    if (inj_bytes) std::memcpy(ctx->h_in + off_inj, io->injected_logits, inj_bytes);
+    if (nw_bytes) std::memcpy(ctx->h_in + off_nw, norm_weight, nw_bytes);
+    count_transfer(kTransferActivation, x_bytes + inj_bytes + nw_bytes);
+    HIP_TRY(hipMemcpyAsync(ctx->x.p, ctx->h_in, in_bytes, hipMemcpyHostToDevice, ctx->stream), "H2D inputs");
+    char* const in = static_cast<char*>(ctx->x.p);
+    x = reinterpret_cast<const uint16_t*>(in);
+    if (inj_bytes) injected = reinterpret_cast<const float*>(in + off_inj);
+    if (nw_bytes) norm_dev = reinterpret_cast<const float*>(in + off_nw);
     output = nullptr;
     if (trace) {
       if ((s = ensure(ctx, ctx->trace, R * H * 4))) return s;
@@ -1088,19 +1111,51 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   uint16_t* next = nullptr;
   const float* route_norm_w = nullptr;
   if (residual) {
-    const float* nw = norm_weight;
     next = next_residual;
-    if (host) {
-      if ((s = ensure(ctx, ctx->normw, H * 4)) || (s = ensure(ctx, ctx->next, m * H * 2))) return s;
-      count_transfer(kTransferActivation, H * 4);
-      HIP_TRY(hipMemcpyAsync(ctx->normw.p, norm_weight, H * 4, hipMemcpyHostToDevice, ctx->stream), "H2D norm");
-      nw = static_cast<const float*>(ctx->normw.p);
-      next = static_cast<uint16_t*>(ctx->next.p);
-    }
     resid = x;
     // The router kernel normalizes each row as it reads it; with injected
     // logits the selection kernels' quantization work-groups do.
-    route_norm_w = nw;
+    route_norm_w = norm_dev;
+  }
+  // The host-memory output pack: the error flags word (16 bytes), then each
+  // requested output at a 16-byte boundary. The output rows are bf16 values:
+  // they cross PCIe as bf16 bits (half the bytes) and are widened into the
+  // caller's f32 rows after the checks. The combine writes the rows and the
+  // next residual rows in place; pack_kernel copies the flags and the rest.
+  struct Piece {
+    const void* src;     // device source (null: written in place)
+    void* dst;           // the caller's buffer
+    size_t bytes = 0;    // device bytes
+    bool widen = false;  // bf16 bits widened into f32 at dst
+    size_t off = 0;      // in the pack
+  };
+  Piece pieces[kPackPieces];
+  int n_pieces = 0;
+  size_t pack_bytes = 16;
+  if (host) {
+    const Piece want[] = {
+        {nullptr, io->output, io->output ? m * H * 2 : 0, true},
+        {nullptr, next_residual, residual ? m * H * 2 : 0},
+        {logits, io->router_logits, io->router_logits ? m * E * 4 : 0},
+        {selected, io->selected, io->selected ? R * 4 : 0},
+        {weights, io->routing_weights, io->routing_weights ? R * 4 : 0},
+        {route_slot, io->route_order, io->route_order ? R * 4 : 0},
+        {trace, io->trace_down, io->trace_down ? R * H * 4 : 0},
+        {trace_gu, io->trace_gate_up, io->trace_gate_up ? R * 2 * I * 4 : 0},
+        {trace_sw, io->trace_swiglu, io->trace_swiglu ? R * I * 4 : 0},
+        {unrounded, io->output_unrounded, io->output_unrounded ? m * H * 4 : 0},
+    };
+    static_assert(sizeof(want) / sizeof(want[0]) == kPackPieces, "pack pieces");
+    for (const Piece& w : want) {
+      if (!w.bytes) continue;
+      pieces[n_pieces] = w;
+      pieces[n_pieces++].off = pack_bytes;
+      pack_bytes += align16(w.bytes);
+    }
+    if ((s = ensure(ctx, ctx->out, pack_bytes))) return s;
+    char* const pack = static_cast<char*>(ctx->out.p);
+    if (io->output) output16 = reinterpret_cast<uint16_t*>(pack + pieces[0].off);
+    if (residual) next = reinterpret_cast<uint16_t*>(pack + pieces[io->output ? 1 : 0].off);
   }
   int* n_work = work + 4 * max_work;
 
@@ -1248,61 +1303,35 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   }
 
   if (host) {
-    // Every requested output and the error flags come back in one stream
-    // sequence into pinned staging and one synchronization; the caller's
-    // buffers are written only when the flags are clear.
-    struct Piece {
-      const void* src;
-      void* dst;
-      size_t bytes;       // device bytes
-      bool widen = false;  // bf16 bits widened into f32 at dst
-    };
-    const Piece pieces[] = {
-        {output16, io->output, io->output ? m * H * 2 : 0, true},
-        {next, next_residual, residual ? m * H * 2 : 0},
-        {logits, io->router_logits, io->router_logits ? m * E * 4 : 0},
-        {selected, io->selected, io->selected ? R * 4 : 0},
-        {weights, io->routing_weights, io->routing_weights ? R * 4 : 0},
-        {da.route_slot, io->route_order, io->route_order ? R * 4 : 0},
-        {trace, io->trace_down, io->trace_down ? R * H * 4 : 0},
-        {trace_gu, io->trace_gate_up, io->trace_gate_up ? R * 2 * I * 4 : 0},
-        {trace_sw, io->trace_swiglu, io->trace_swiglu ? R * I * 4 : 0},
-        {unrounded, io->output_unrounded, io->output_unrounded ? m * H * 4 : 0},
-    };
-    size_t need = 16, payload = 0;
-    for (const Piece& pc : pieces) {
-      need += (pc.bytes + 15) / 16 * 16;
-      payload += pc.bytes;
+    // One gather, one copy, one synchronization; the caller's buffers are
+    // written only when the flags are clear.
+    PackArgs pa{};
+    pa.err = ctx->err;
+    pa.dst = static_cast<char*>(ctx->out.p);
+    size_t payload = 0;
+    for (int i = 0; i < n_pieces; ++i) {
+      payload += pieces[i].bytes;
+      if (!pieces[i].src) continue;
+      pa.src[pa.pieces] = pieces[i].src;
+      pa.off[pa.pieces] = pieces[i].off;
+      pa.words[pa.pieces++] = pieces[i].bytes / 4;
     }
     count_transfer(kTransferOutput, payload);
-    if (need > ctx->stage_cap) {
-      if (ctx->h_stage) HIP_TRY(hipHostFree(ctx->h_stage), "hipHostFree");
-      ctx->h_stage = nullptr;
-      ctx->stage_cap = 0;
-      HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ctx->h_stage), need), "pinned staging");
-      ctx->stage_cap = need;
-    }
-    int* flags = reinterpret_cast<int*>(ctx->h_stage);
-    HIP_TRY(hipMemcpyAsync(flags, ctx->err, sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "read error flags");
-    size_t off = 16;
-    for (const Piece& pc : pieces) {
-      if (!pc.bytes) continue;
-      HIP_TRY(hipMemcpyAsync(ctx->h_stage + off, pc.src, pc.bytes, hipMemcpyDeviceToHost, ctx->stream), "D2H output");
-      off += (pc.bytes + 15) / 16 * 16;
-    }
+    if ((s = ensure_pinned(ctx, &ctx->h_stage, &ctx->stage_cap, pack_bytes))) return s;
+    HIP_TRY(launch_pack(pa, ctx->stream), "pack launch");
+    HIP_TRY(hipMemcpyAsync(ctx->h_stage, ctx->out.p, pack_bytes, hipMemcpyDeviceToHost, ctx->stream), "D2H outputs");
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
-    if (*flags != 0) return device_flags_fail(ctx, *flags);
-    off = 16;
-    for (const Piece& pc : pieces) {
-      if (!pc.bytes) continue;
+    const int flags = *reinterpret_cast<const int*>(ctx->h_stage);
+    if (flags != 0) return device_flags_fail(ctx, flags);
+    for (int i = 0; i < n_pieces; ++i) {
+      const Piece& pc = pieces[i];
       if (pc.widen) {
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(ctx->h_stage + off);
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(ctx->h_stage + pc.off);
         uint32_t* dst = static_cast<uint32_t*>(pc.dst);
-        for (size_t i = 0; i < pc.bytes / 2; ++i) dst[i] = (uint32_t)src[i] << 16;
+        for (size_t j = 0; j < pc.bytes / 2; ++j) dst[j] = (uint32_t)src[j] << 16;
       } else {
-        std::memcpy(pc.dst, ctx->h_stage + off, pc.bytes);
+        std::memcpy(pc.dst, ctx->h_stage + pc.off, pc.bytes);
       }
-      off += (pc.bytes + 15) / 16 * 16;
     }
   } else {
     if (io->selected)

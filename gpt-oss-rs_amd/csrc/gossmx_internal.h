@@ -212,6 +212,20 @@ hipError_t launch_generate(uint64_t seed, uint64_t stream_id, TiledWeights w, hi
 hipError_t launch_export(TiledWeights w, uint8_t* dst, hipStream_t stream);
 hipError_t launch_fill_tiled_padding(TiledWeights w, hipStream_t stream);
 hipError_t launch_clear_ints(int* p, size_t n, hipStream_t stream);
+
+// Gathers a host-memory call's outputs into one device buffer for a single
+// device-to-host copy: dst[0] = the device error flags word, then each piece's
+// bytes (a multiple of 4) at its offset (a multiple of 16).
+constexpr int kPackPieces = 10;
+struct PackArgs {
+  const int* err;
+  char* dst;
+  const void* src[kPackPieces];
+  uint64_t off[kPackPieces];    // bytes into dst
+  uint64_t words[kPackPieces];  // 4-byte words
+  int pieces;
+};
+hipError_t launch_pack(const PackArgs& a, hipStream_t stream);
 hipError_t launch_build_sigmoid_table(uint16_t* tab, hipStream_t stream);
 // Self-test outputs (floats): kSelftestCodes conversion results, 256 MFMA
 // results, kSelftestCodes scaled results, then kSelftestDirty x 16 results of

@@ -18,6 +18,7 @@
 
 #include <hip/hip_ext.h>
 
+#include <algorithm>
 #include <cmath>
 
 namespace gossmx {
@@ -3108,6 +3109,30 @@ hipError_t launch_fill_tiled_padding(TiledWeights w, hipStream_t stream) {
   const size_t n = w.experts * (w.tiles * kTileRows - w.rows) * w.blocks;
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(fill_padding_kernel, dim3(grid1d(n, 256)), dim3(256), 0, stream, w);
+  return hipGetLastError();
+}
+
+// blockIdx.y = piece; work-groups along x stride through it (16 bytes per
+// thread where the piece allows, then the 4-byte tail).
+__global__ void pack_kernel(PackArgs a) {
+  const int pc = blockIdx.y;
+  if (pc == 0 && blockIdx.x == 0 && threadIdx.x == 0) reinterpret_cast<int*>(a.dst)[0] = *a.err;
+  if (pc >= a.pieces) return;
+  const size_t words = a.words[pc];
+  const uint32_t* src = static_cast<const uint32_t*>(a.src[pc]);
+  uint32_t* dst = reinterpret_cast<uint32_t*>(a.dst + a.off[pc]);
+  const size_t stride = (size_t)gridDim.x * blockDim.x, first = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t quads = (reinterpret_cast<uintptr_t>(src) & 15) ? 0 : words / 4;
+  for (size_t i = first; i < quads; i += stride)
+    reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+  for (size_t i = 4 * quads + first; i < words; i += stride) dst[i] = src[i];
+}
+
+hipError_t launch_pack(const PackArgs& a, hipStream_t stream) {
+  uint64_t most = 0;
+  for (int i = 0; i < a.pieces; ++i) most = std::max(most, a.words[i]);
+  const int gx = (int)std::min<uint64_t>(256, std::max<uint64_t>(1, (most / 4 + 255) / 256));
+  hipLaunchKernelGGL(pack_kernel, dim3(gx, std::max(1, a.pieces)), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
