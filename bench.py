@@ -620,8 +620,8 @@ def main() -> int:
                 "steps": host_steps,
                 "note": ("GOSSMX_MEM_HOST calls (eager launches): x and logits in one copy from pinned staging; "
                          "every CpuMoeStep output (router logits, selection, routing weights, route order, output "
-                         "rows) and the device error flags gathered on the device and copied out in one copy and "
-                         "one synchronization per layer"),
+                         "rows) and the device error flags written by the kernels into pinned host memory; one "
+                         "synchronization per layer"),
             }
         return result, x, state, graph
 

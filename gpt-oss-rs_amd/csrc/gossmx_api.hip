@@ -128,19 +128,19 @@ struct gossmx_ctx {
   int tag_layer = -1, tag_phase = GOSSMX_PHASE_UNKNOWN;
   CallInfo call;  // the profiled call in progress
   // Pinned host staging of the host-memory MoE calls (grow-only): the inputs
-  // (one host-to-device copy), and the outputs with the error flags (one
-  // device-to-host copy and one synchronization).
+  // (one host-to-device copy), and the outputs with the error flags (coherent
+  // memory the kernels write directly; one synchronization).
   char* h_in = nullptr;
   size_t in_cap = 0;
   char* h_stage = nullptr;
   size_t stage_cap = 0;
-  // scratch (x: the host-memory MoE call's input pack; out: its output pack)
-  DevBuf x, logits, selected, weights, act1v, act1s, bucket, route_tok, route_slot, work, act2v, act2s, y, cnt, out,
+  // scratch (x: the host-memory MoE call's input pack)
+  DevBuf x, logits, selected, weights, act1v, act1s, bucket, route_tok, route_slot, work, act2v, act2s, y, cnt,
       trace, trace_gu, trace_sw, rec, bias, mout, unrounded;
   template <class F>
   void each_buf(F f) {
     for (DevBuf* b : {&x, &logits, &selected, &weights, &act1v, &act1s, &bucket, &route_tok, &route_slot, &work,
-                      &act2v, &act2s, &y, &cnt, &out, &trace, &trace_gu, &trace_sw, &rec, &bias, &mout, &unrounded})
+                      &act2v, &act2s, &y, &cnt, &trace, &trace_gu, &trace_sw, &rec, &bias, &mout, &unrounded})
       f(*b);
   }
 };
@@ -193,9 +193,10 @@ int ensure(gossmx_ctx* ctx, DevBuf& b, size_t bytes) {
 }
 
 // Grow-only pinned host staging. The stream is drained before a smaller
-// buffer is freed: a copy of an earlier call that ended in an error may still
-// read or write it.
-int ensure_pinned(gossmx_ctx* ctx, char** p, size_t* cap, size_t bytes) {
+// buffer is freed: work of an earlier call that ended in an error may still
+// read or write it. `flags`: hipHostMalloc flags (coherent staging is written
+// by kernels directly).
+int ensure_pinned(gossmx_ctx* ctx, char** p, size_t* cap, size_t bytes, unsigned flags = hipHostMallocDefault) {
   if (bytes <= *cap) return GOSSMX_OK;
   if (*p) {
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
@@ -204,7 +205,7 @@ int ensure_pinned(gossmx_ctx* ctx, char** p, size_t* cap, size_t bytes) {
   *p = nullptr;
   *cap = 0;
   const size_t want = std::max<size_t>(bytes, 4096) * 5 / 4;
-  HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(p), want), "pinned staging");
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(p), want, flags), "pinned staging");
   *cap = want;
   return GOSSMX_OK;
 }
@@ -1117,11 +1118,12 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
     // logits the selection kernels' quantization work-groups do.
     route_norm_w = norm_dev;
   }
-  // The host-memory output pack: the error flags word (16 bytes), then each
-  // requested output at a 16-byte boundary. The output rows are bf16 values:
-  // they cross PCIe as bf16 bits (half the bytes) and are widened into the
-  // caller's f32 rows after the checks. The combine writes the rows and the
-  // next residual rows in place; pack_kernel copies the flags and the rest.
+  // The host-memory output pack, in the context's coherent pinned staging:
+  // the error flags word (16 bytes), then each requested output at a 16-byte
+  // boundary. The output rows are bf16 values: they cross PCIe as bf16 bits
+  // (half the bytes) and are widened into the caller's f32 rows after the
+  // checks. The combine writes the rows and the next residual rows there
+  // directly; pack_kernel writes the flags and the rest.
   struct Piece {
     const void* src;     // device source (null: written in place)
     void* dst;           // the caller's buffer
@@ -1152,8 +1154,9 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
       pieces[n_pieces++].off = pack_bytes;
       pack_bytes += align16(w.bytes);
     }
-    if ((s = ensure(ctx, ctx->out, pack_bytes))) return s;
-    char* const pack = static_cast<char*>(ctx->out.p);
+    if ((s = ensure_pinned(ctx, &ctx->h_stage, &ctx->stage_cap, pack_bytes, hipHostMallocCoherent))) return s;
+    char* pack = nullptr;
+    HIP_TRY(hipHostGetDevicePointer(reinterpret_cast<void**>(&pack), ctx->h_stage, 0), "hipHostGetDevicePointer");
     if (io->output) output16 = reinterpret_cast<uint16_t*>(pack + pieces[0].off);
     if (residual) next = reinterpret_cast<uint16_t*>(pack + pieces[io->output ? 1 : 0].off);
   }
@@ -1303,11 +1306,11 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
   }
 
   if (host) {
-    // One gather, one copy, one synchronization; the caller's buffers are
-    // written only when the flags are clear.
+    // One gather into the pinned pack, one synchronization; the caller's
+    // buffers are written only when the flags are clear.
     PackArgs pa{};
     pa.err = ctx->err;
-    pa.dst = static_cast<char*>(ctx->out.p);
+    HIP_TRY(hipHostGetDevicePointer(reinterpret_cast<void**>(&pa.dst), ctx->h_stage, 0), "hipHostGetDevicePointer");
     size_t payload = 0;
     for (int i = 0; i < n_pieces; ++i) {
       payload += pieces[i].bytes;
@@ -1317,9 +1320,7 @@ static int moe_forward_impl(gossmx_ctx* ctx, const gossmx_layer* L, const gossmx
       pa.words[pa.pieces++] = pieces[i].bytes / 4;
     }
     count_transfer(kTransferOutput, payload);
-    if ((s = ensure_pinned(ctx, &ctx->h_stage, &ctx->stage_cap, pack_bytes))) return s;
     HIP_TRY(launch_pack(pa, ctx->stream), "pack launch");
-    HIP_TRY(hipMemcpyAsync(ctx->h_stage, ctx->out.p, pack_bytes, hipMemcpyDeviceToHost, ctx->stream), "D2H outputs");
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     const int flags = *reinterpret_cast<const int*>(ctx->h_stage);
     if (flags != 0) return device_flags_fail(ctx, flags);
