@@ -1401,6 +1401,64 @@ __device__ __forceinline__ void group_update_pipelined(Acc<C>& tot, const char* 
 #undef GOSSMX_CHAIN
 }
 
+// A full fast step with NTG >= 2 token groups, software-pipelined by one
+// token group. Stage s = (block j, token group tg) issues the MFMAs of
+// (j, tg), then requests the LDS operands of stage s + 1, then runs the chain
+// of stage s - 1, whose MFMAs went out one stage earlier (two MFMAs and 16
+// chain instructions before their results are read), and in a block's last
+// stage converts the next block's weights. Every accumulator sees the same
+// operations in the same order as group_update.
+template <class C, bool RESIDUAL, int NTG>
+__device__ __forceinline__ void step_pipelined(Acc<C>& tot, const char* codes, const float2* scl, const WStep<C>& w,
+                                               const int lane, const int G) {
+  constexpr int T = C::kWaveTiles, NS = C::kStep * NTG;
+  const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  half8 aop[2];
+  float4 sc[3];
+  half8 bop[2][T];
+  f32x4 d[2][T];
+#define GOSSMX_A(S) \
+  (*reinterpret_cast<const half8*>(codes + slot_chunk<C>((S) / NTG, (S) % NTG) * 1024 + lane * 16))
+#define GOSSMX_S(S) (*reinterpret_cast<const float4*>(&scl[((S) / NTG) * C::kChunk + ((S) % NTG) * 8 + 2 * G]))
+#define GOSSMX_CVT(J, DST)                                                                              \
+  _Pragma("unroll") for (int t = 0; t < T; ++t)                                                       \
+      DST[t] = fp4x8_to_half8_scaled(w.v[(J) / 4][t][(J) % 4], e8m0_scale_operand(w.s[(J) / 4][t], (J) % 4));
+#define GOSSMX_CHAIN(S)                                                                                 \
+  _Pragma("unroll") for (int t = 0; t < T; ++t) {                                                     \
+    const float4 c = sc[(S) % 3];                                                                       \
+    const f32x4 r = d[(S) & 1][t];                                                                      \
+    float& p0 = tot[t][(S) % NTG][0];                                                                   \
+    float& p1 = tot[t][(S) % NTG][1];                                                                   \
+    p0 = p0 + r[0] * c.x;                                                                               \
+    if (RESIDUAL) p0 = p0 + r[1] * c.y;                                                                 \
+    p1 = p1 + r[2] * c.z;                                                                               \
+    if (RESIDUAL) p1 = p1 + r[3] * c.w;                                                                 \
+  }
+  aop[0] = GOSSMX_A(0);
+  sc[0] = GOSSMX_S(0);
+  GOSSMX_CVT(0, bop[0])
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      d[s & 1][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop[s & 1], bop[(s / NTG) & 1][t], zero, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + 1 < NS) {
+      aop[(s + 1) & 1] = GOSSMX_A(s + 1);
+      sc[(s + 1) % 3] = GOSSMX_S(s + 1);
+    }
+    if (s > 0) GOSSMX_CHAIN(s - 1)
+    if (s % NTG == NTG - 1 && s / NTG + 1 < C::kStep) GOSSMX_CVT(s / NTG + 1, bop[(s / NTG + 1) & 1])
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  GOSSMX_CHAIN(NS - 1)
+#undef GOSSMX_A
+#undef GOSSMX_S
+#undef GOSSMX_CVT
+#undef GOSSMX_CHAIN
+}
+
 // Shared GEMM epilogue: plain f32 stores, the down projection's bf16 rows,
 // or gate_up's SwiGLU and down-input quantization. `s_act` is LDS scratch of
 // at least count * (kGemmRows / 2 + 1) floats, free for reuse. Rows of tiles
@@ -1580,6 +1638,12 @@ template <class C, bool RESIDUAL, int NTG, bool FAST>
 __device__ __forceinline__ void step_update(const KLoop<C>& k, Acc<C>& tot, const char* codes, const float* scl,
                                             const WStep<C>& w, const int q) {
   const float2* s2 = reinterpret_cast<const float2*>(scl);
+  if constexpr (NTG >= 2 && FAST) {
+    if (C::kStep * q + C::kStep <= k.B) {
+      step_pipelined<C, RESIDUAL, NTG>(tot, codes, s2, w, k.lane, k.G);
+      return;
+    }
+  }
   if (C::kStep * q + C::kStep <= k.B) {
 #pragma unroll
     for (int g = 0; g < C::kGroups; ++g) {
