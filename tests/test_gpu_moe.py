@@ -497,6 +497,49 @@ def test_output_unrounded_matches_oracle(ctx, experts, hidden, inter, top_k, m, 
     close(layer)
 
 
+@pytest.mark.parametrize("experts,hidden,inter,top_k,m,projection", [
+    (8, 128, 96, 4, 1, G.PROJECTION_RESIDUAL_Q8),
+    (8, 128, 96, 4, 5, G.PROJECTION_RESIDUAL_Q8),
+    (32, 256, 128, 4, 40, G.PROJECTION_RESIDUAL_Q8),
+    (4, 96, 64, 2, 3, G.PROJECTION_EXACT_BF16)])
+def test_host_memory_every_output_in_one_call(ctx, experts, hidden, inter, top_k, m, projection):
+    """A host-memory call that asks for every output at once (routing, the
+    rows, the three traces and the pre-round output: nine pieces of the
+    pinned output pack, some of them not multiples of 16 bytes) returns each
+    bit for bit as the oracle's, and leaves the bytes around the caller's
+    buffers untouched."""
+    host = O.synthetic_layer(53, 0, experts=experts, hidden=hidden, intermediate=inter, top_k=top_k)
+    x = O.gen_hidden(53, m, m, hidden)
+    want = O.moe_batch(host, x, trace=True, projection=projection)
+    assert want["status"] == O.OK
+    layer = gpu_layer(ctx, host, projection)
+    got = layer.forward(x, trace=True, unrounded=True)
+    assert_moe_equal(got, want)
+    assert_traces_equal(got, want)
+    assert (got["output_unrounded"].view(np.uint32) == want["output_unrounded"].view(np.uint32)).all()
+    # the same call through the C ABI into canaried buffers
+    E, K, H, I = experts, top_k, hidden, inter
+    lib = G.load()
+    shapes = {"router_logits": (m * E, np.float32), "selected": (m * K, np.uint32),
+              "routing_weights": (m * K, np.float32), "output": (m * H, np.float32),
+              "route_order": (m * K, np.uint32), "trace_down": (m * K * H, np.float32),
+              "trace_gate_up": (m * K * 2 * I, np.float32), "trace_swiglu": (m * K * I, np.float32),
+              "output_unrounded": (m * H, np.float32)}
+    canary = 0x5A5A5A5A
+    bufs = {k: np.full(n + 2, canary, np.uint32).view(dt) for k, (n, dt) in shapes.items()}
+    inner = {k: b[1:-1] for k, b in bufs.items()}
+    io = G.MoeIo(G._ptr(x), m, None, G._ptr(inner["router_logits"]), G._ptr(inner["selected"]),
+                 G._ptr(inner["routing_weights"]), G._ptr(inner["output"]), G._ptr(inner["route_order"]),
+                 G._ptr(inner["trace_down"]), G.MEM_HOST, G._ptr(inner["trace_gate_up"]),
+                 G._ptr(inner["trace_swiglu"]), G._ptr(inner["output_unrounded"]))
+    assert lib.gossmx_moe_forward(ctx.handle, layer._h, G.C.byref(io)) == G.OK
+    for k, b in bufs.items():
+        raw = b.view(np.uint32)
+        assert raw[0] == canary and raw[-1] == canary, k
+        assert (inner[k].view(np.uint32) == got[k].reshape(-1).view(np.uint32)).all(), k
+    close(layer)
+
+
 def test_all_experts_selected(ctx):
     host = O.synthetic_layer(5, 0, experts=4, hidden=64, intermediate=64, top_k=4)
     x = O.gen_hidden(5, 1, 9, 64)
