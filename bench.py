@@ -21,8 +21,9 @@ BASELINE.md's CPU figures). Inputs and weights are resident before timing.
 
 With no --config (and no overrides) the line also carries configs[0]'s
 figures under "configs0": the same measurement of the 1-token workload
-(us_per_layer, value, roofline with its own traffic probe), run after the
-configs[1] measurement; `value` stays configs[1]'s.
+(us_per_layer, value, roofline with its own traffic probe, host-memory rate
+and CPU baseline), run after the configs[1] measurement; `value` stays
+configs[1]'s.
 
 Prints one JSON line. The per-kernel roofline uses the library's hipEvent
 profiler on the stream the kernels run on (the GEMM launches record their own
@@ -644,7 +645,12 @@ def main() -> int:
     if both:
         # The bs=1 half of the metric, timed the same way after
         # the configs[1] line's measurement; reported beside it, not in value.
-        r0, _, state0, graph0 = measure(dict(CONFIGS[0]), probe0, 0)
+        r0, x0, state0, graph0 = measure(dict(CONFIGS[0]), probe0, args.host_steps)
+        cb0 = None
+        if not args.no_cpu_baseline:
+            cb0 = cpu_baseline(dict(CONFIGS[0]), x0, state0, args.cpu_threads)
+            bits_ok = bits_ok and cb0["gpu_bits_equal"] and cb0["all_cores"]["bits_equal"] and \
+                cb0["forced_lane"]["bits_equal"] and cb0["last_layer_bits_equal"] is not False
         release(state0, graph0)
         result["configs0"] = {
             "workload": r0["config"]["workload"],
@@ -653,6 +659,7 @@ def main() -> int:
             "touched_experts": r0["config"]["touched_experts"],
             "hbm_gbps": r0["hbm_gbps"], "hbm_frac": r0["hbm_frac"],
             "roofline": r0["roofline"], "stage_ms_per_step": r0["stage_ms_per_step"],
+            "host_memory": r0.get("host_memory"), "cpu_baseline": cb0,
         }
     ctx.close()
     release_torch()
