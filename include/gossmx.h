@@ -267,9 +267,10 @@ void gossmx_circuit_reset(void);
  * "fault"); rejected (every other status: argument, shape or non-finite data).
  * A device-memory call counts when it returns; a device-side error that a
  * later gossmx_synchronize reports does not change its count. Transfer bytes
- * are the host<->device copies the library makes: weights, router and bias
- * uploads (weights_bias_uploaded); the inputs of host-memory calls and the
- * dense model's round trips (activations); their results (output). Resident
+ * are the bytes the library moves between host and device (copies, or kernel
+ * writes into its pinned staging): weights, router and bias uploads
+ * (weights_bias_uploaded); the inputs of host-memory calls and the dense
+ * model's round trips (activations); their results (output). Resident
  * bytes are the device memory held by live gossmx_weights and gossmx_layer
  * objects (planes with their padding, router and biases); contexts' scratch is
  * not included. */
