@@ -540,6 +540,48 @@ def test_host_memory_every_output_in_one_call(ctx, experts, hidden, inter, top_k
     close(layer)
 
 
+def forced_route_logits(counts, m, top_k):
+    """Injected logits whose top-k gives expert e exactly counts[e] routes:
+    each row takes the top_k experts with the most routes still to place
+    (ties by index; a valid assignment while no count exceeds the rows left),
+    ranked by descending logits 4, 3, 2, ... (bf16-exact); the other experts
+    get -4."""
+    E = len(counts)
+    need = np.array(counts, np.int64)
+    assert need.sum() == m * top_k and need.max() <= m
+    logits = np.full((m, E), -4.0, np.float32)
+    for r in range(m):
+        order = sorted(range(E), key=lambda e: (-need[e], e))[:top_k]
+        assert all(need[e] > 0 for e in order), "counts cannot be placed"
+        for rank, e in enumerate(order):
+            logits[r, e] = float(4 - rank)
+            need[e] -= 1
+    return logits
+
+
+@pytest.mark.parametrize("m,counts", [
+    (8, [8, 7, 1, 4, 4, 4, 3, 1]),                                      # 8-row items: a full bucket of 8
+    (9, [9, 9, 8, 6, 2, 1, 1, 0]),                                      # first 16-row-item batch: 8, 9 rows
+    (48, [16, 17, 8, 9, 15, 1, 7, 32, 33, 24, 0, 2, 3, 4, 5, 16]),      # 16-row items: 16, 17, 32, 33 rows
+    (512, [32, 33, 31, 64, 65, 63, 96, 97, 1, 8, 9, 16, 17, 24, 25, 40] + [89] * 15 + [92])])      # 32-row items
+def test_bucket_sizes_at_item_and_token_group_boundaries(ctx, m, counts):
+    """Expert buckets of exactly 8k and 8k + 1 rows and of exactly one chunk
+    and one chunk + 1 (every geometry's item size: 8, 16 and 32 rows), so
+    that full items, one-row partial items and single-token-group tails all
+    occur; bit for bit against the oracle."""
+    E = len(counts)
+    host = O.synthetic_layer(59, 0, experts=E, hidden=128, intermediate=96, top_k=4)
+    x = O.gen_hidden(59, m, m, 128)
+    logits = forced_route_logits(counts, m, 4)
+    want = O.moe_batch(host, x, injected_logits=logits)
+    assert want["status"] == O.OK
+    assert (np.bincount(want["selected"].reshape(-1), minlength=E) == np.array(counts)).all()
+    layer = gpu_layer(ctx, host)
+    got = layer.forward(x, injected_logits=logits)
+    assert_moe_equal(got, want)
+    close(layer)
+
+
 def test_all_experts_selected(ctx):
     host = O.synthetic_layer(5, 0, experts=4, hidden=64, intermediate=64, top_k=4)
     x = O.gen_hidden(5, 1, 9, 64)
